@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X switched-LoRA path (one JSON line on stdout).
+
+A step is one pass of the hot path over one batch: segment build (routing +
+aLoRA gating + adapter sort), then shrink and expand-add for every projection
+of the workload (one projection for the single-op shapes, 32 layers x 4 for
+the decoder-step shape).  K steps are captured in one HIP graph and timed with
+HIP events around its replay; inputs are resident in HBM and rotate over
+enough independent buffer sets (x, y, adapters) to exceed twice the 256 MB
+Infinity Cache, so every step reads from HBM.
+
+The roofline object is for the dominant kernel, timed the same way (a graph of
+K launches of that kernel alone, rotating buffers).  The CPU baseline is the
+reference's HF loop restated on torch-CPU, timed on the host cores.
+
+  python bench.py [--steps K] [--warmup W] [--config {0..4}] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "switched-LoRA tokens/sec + achieved HBM GB/s (% of 8 TB/s) on 1 MI355X"
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK = {"bf16": 2.5e15, "fp32": 157.3e12}
+MALL_BYTES = 256 << 20
+DEFAULT_STEPS = {0: 200, 1: 200, 2: 40, 3: 100, 4: 8}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=1, choices=[0, 1, 2, 3, 4])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--sets", type=int, default=None, help="buffer sets to rotate (default: > 2x MALL)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU: the switched-LoRA kernels run on one MI355X; "
+                                   "multi-GPU sharding is a design note only (run with --gpus 1)"}))
+        sys.exit(2)
+
+    import torch
+
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    from granite_switch_amd import _lib, switched, workloads
+
+    _lib.load()
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    cfg = args.config
+    K = args.steps if args.steps is not None else DEFAULT_STEPS[cfg]
+    W = args.warmup
+
+    routing = workloads.routing_for(cfg)
+    NA = workloads.num_adapters_for(cfg)
+    dtype = workloads.dtype_for(cfg)
+    dname = "fp32" if dtype == torch.float32 else "bf16"
+    e = 4 if dtype == torch.float32 else 2
+    specs = workloads.module_specs(cfg)
+    layers = 32 if cfg == 4 else 1
+    T = routing.num_tokens
+
+    # -- buffer sets ---------------------------------------------------------
+    def module_bytes(spec):
+        O = sum(spec.output_slices)
+        return (T * spec.hidden + T * O + len(spec.output_slices) * NA * spec.max_rank * spec.hidden
+                + NA * O * spec.max_rank) * e
+
+    set_bytes = layers * sum(module_bytes(s) for s in specs)
+    nsets = args.sets or max(1, min(64, math.ceil(2 * MALL_BYTES / set_bytes)))
+    log(f"config {cfg}: {workloads.NAMES[cfg]}; T={T}; {nsets} buffer set(s) of {set_bytes / 2**20:.1f} MiB")
+
+    sets = []       # sets[i][layer*len(specs)+k] = (ModuleData without slices, PackedAdapters)
+    cpu_sample = []
+    for i in range(nsets):
+        mods = []
+        for layer in range(layers):
+            for k, spec in enumerate(specs):
+                md = workloads.make_module(spec, T, NA, dtype, dev, seed=7919 * (cfg + 1) + 101 * layer + k + 1000003 * i)
+                pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, spec.ranks)
+                if i == 0 and layer == 0 and not args.no_cpu:
+                    cpu_sample.append((md.y.cpu(), md.x.cpu(), [a.cpu() for a in md.lora_A_slices],
+                                       [b.cpu() for b in md.lora_B_slices], spec.output_slices))
+                md.lora_A_slices = None
+                md.lora_B_slices = None
+                mods.append((md, pk))
+        sets.append(mods)
+    torch.cuda.synchronize()
+
+    ids_d = torch.tensor(routing.req_ids, device=dev)
+    pos_d = torch.tensor(routing.positions, device=dev)
+    cu_d = torch.tensor(routing.cu_seqlens, device=dev)
+    off_d = None if routing.act_offsets is None else torch.tensor(routing.act_offsets, device=dev)
+    segs = switched.build_segments(ids_d, NA, pos_d, cu_d, off_d)
+    zw = max(len(s.output_slices) * pk.max_rank for (_, pk), s in zip(sets[0][:len(specs)], specs))
+    z = torch.empty(max(T, 1), zw, dtype=dtype, device=dev)
+    ws_need = max(int(_lib.load().gs_shrink_workspace_bytes(T, s.hidden, len(s.output_slices), NA, sets[0][k][1].max_rank))
+                  for k, s in enumerate(specs))
+    switched.reserve_workspace(dev, ws_need)
+
+    def build():
+        switched.build_segments(ids_d, NA, pos_d, cu_d, off_d, out=segs)
+
+    def shrink(md, pk):
+        switched.shrink(md.x, segs, pk, z[:, : pk.num_slices * pk.max_rank])
+
+    def expand(md, pk):
+        switched.expand_add_(md.y, z[:, : pk.num_slices * pk.max_rank], segs, pk)
+
+    def step(i):
+        build()
+        for md, pk in sets[i % nsets]:
+            shrink(md, pk)
+            expand(md, pk)
+
+    # -- warm-up, capture, timed replay ---------------------------------------
+    for i in range(W):
+        step(i)
+    torch.cuda.synchronize()
+
+    def capture(fn):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        g.replay()                      # upload + one untimed run
+        torch.cuda.synchronize()
+        return g
+
+    def timed(g, n):
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        g.replay()
+        end.record()
+        end.synchronize()
+        return start.elapsed_time(end) / n       # ms per unit
+
+    g_steps = capture(lambda: [step(i) for i in range(K)])
+    ms_per_step = timed(g_steps, K)
+    log(f"step: {ms_per_step * 1e3:.2f} us over {K} graph-captured steps")
+
+    # -- host-side accounting --------------------------------------------------
+    from granite_switch_amd.switched import algorithmic_bytes, algorithmic_flops
+
+    eff = segs.eff_ids.cpu().numpy()
+    op_bytes = 0
+    op_flops = 0
+    per_kernel_bytes = {}
+    t_act = int((eff > 0).sum())
+    for k, spec in enumerate(specs):
+        pk = sets[0][k][1]
+        b = algorithmic_bytes(eff, pk, spec.ranks, e)
+        f = algorithmic_flops(eff, pk, spec.ranks)
+        op_bytes += layers * b
+        op_flops += layers * f
+        S, H, O = len(spec.output_slices), spec.hidden, sum(spec.output_slices)
+        used = np.unique(eff[eff > 0])
+        rsum = sum(spec.ranks[g - 1] for g in used)
+        zbytes = sum(S * spec.ranks[g - 1] for g in eff[eff > 0]) * e
+        per_kernel_bytes[f"shrink:{spec.name}"] = t_act * H * e + S * H * rsum * e + zbytes + 4 * t_act
+        per_kernel_bytes[f"expand:{spec.name}"] = O * rsum * e + 2 * t_act * O * e + zbytes + 4 * t_act
+    nseq = len(routing.cu_seqlens) - 1
+    per_kernel_bytes["build_segments"] = T * (8 + 8 + 4) + 4 * t_act + 12 * nseq + 4 * (NA + 1)
+
+    # -- per-kernel timing (graphs of K launches of one kernel) --------------
+    kern_us = {}
+    kern_launches = {"build_segments": 1}
+    g_b = capture(lambda: [build() for _ in range(K)])
+    kern_us["build_segments"] = timed(g_b, K) * 1e3
+    for k, spec in enumerate(specs):
+        mods = [sets[i][layer * len(specs) + k] for i in range(nsets) for layer in range(layers)]
+        n = max(K, len(mods)) if cfg != 4 else len(mods)
+        g_s = capture(lambda: [shrink(*mods[j % len(mods)]) for j in range(n)])
+        kern_us[f"shrink:{spec.name}"] = timed(g_s, n) * 1e3
+        g_e = capture(lambda: [expand(*mods[j % len(mods)]) for j in range(n)])
+        kern_us[f"expand:{spec.name}"] = timed(g_e, n) * 1e3
+        kern_launches[f"shrink:{spec.name}"] = layers
+        kern_launches[f"expand:{spec.name}"] = layers
+        del g_s, g_e
+    for name, us in kern_us.items():
+        log(f"kernel {name}: {us:.2f} us/launch, {per_kernel_bytes[name] / us / 1e3:.0f} GB/s algorithmic")
+    dom = max(kern_us, key=lambda n: kern_us[n] * kern_launches[n])
+    dom_gbs = per_kernel_bytes[dom] / (kern_us[dom] * 1e-6) / 1e9
+
+    # -- CPU baseline -----------------------------------------------------------
+    cpu = None
+    if not args.no_cpu and cpu_sample:
+        from oracle import baseline
+
+        ids_cpu = torch.tensor(eff.astype(np.int64))
+        med, runs, threads = baseline.time_modules(cpu_sample, ids_cpu, budget_s=12.0, min_runs=3)
+        step_cpu = med * layers
+        cpu = {
+            "value": T / step_cpu,
+            "unit": "tokens/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": (f"reference HF per-adapter loop (torch-CPU, {dname}) over "
+                       f"{'one layer (4 projections), scaled x32' if cfg == 4 else 'the full op'}; "
+                       f"median of {runs} runs; {baseline.cpu_model()}"),
+        }
+        log(f"cpu baseline: {med * 1e3:.2f} ms per sample pass on {threads} threads")
+
+    us_op = ms_per_step * 1e3
+    value = T / (ms_per_step * 1e-3)
+    op_gbs = op_bytes / (ms_per_step * 1e-3) / 1e9
+    wl_name = {0: "switched-LoRA single op fp32 2048->2048 T=512 (4x128) 4 adapters r8 aLoRA",
+               1: "switched-LoRA decode QKV 4096->6144 T=256 12 adapters r32 (20% not yet activated)",
+               2: "switched-LoRA chunked prefill gate_up 4096->25600 T=8192 (16 seqs) 12 adapters r32",
+               3: "switched-LoRA multiswitch down 12800->4096 T=4096 (64x64) 48 adapters r8-64",
+               4: "switched-LoRA side of a 32-layer Granite-8B-shaped step T=4144 24 adapters r32"}[cfg]
+    out = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dname,
+        "data": "synthetic (seeded; random-init adapters in the composed-checkpoint layout)",
+        "config": {"workload": wl_name, "tokens": T, "active_tokens": t_act, "adapters": NA,
+                   "projections": [f"{s.name} {s.hidden}->{sum(s.output_slices)}" for s in specs],
+                   "layers": layers, "buffer_sets": nsets},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": dom_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": dom_gbs / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes": per_kernel_bytes[dom], "avg_us": kern_us[dom]},
+        "cpu_baseline": cpu,
+        "us_per_op": us_op,
+        "op_algorithmic_bytes": op_bytes,
+        "op_hbm_gbs": op_gbs,
+        "op_hbm_frac": op_gbs / HBM_PEAK_GBS,
+        "op_mfma_frac": op_flops / (ms_per_step * 1e-3) / MFMA_PEAK[dname],
+        "kernels_us": kern_us,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,134 @@
+// Shared device and host helpers for the gfx950 switched-LoRA kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/granite_switch_amd.h"
+
+namespace gs {
+
+// ---------------------------------------------------------------------------
+// Host-side error reporting: every entry point returns a GS_* status and leaves
+// a human-readable message retrievable with gs_last_error().
+// ---------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+
+#define GS_CHECK_ARG(cond, ...)                 \
+  do {                                          \
+    if (!(cond)) {                              \
+      ::gs::set_error(__VA_ARGS__);             \
+      return GS_ERR_INVALID;                    \
+    }                                           \
+  } while (0)
+
+#define GS_CHECK_LAUNCH(what)                                                   \
+  do {                                                                          \
+    hipError_t e_ = hipGetLastError();                                          \
+    if (e_ != hipSuccess) {                                                     \
+      ::gs::set_error("%s: launch failed: %s", what, hipGetErrorString(e_));    \
+      return GS_ERR_HIP;                                                        \
+    }                                                                           \
+  } while (0)
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even float -> bf16 bits (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// Exclusive lane mask: bits of lanes below the calling lane (wave64).
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  int l = __lane_id();
+  return l == 0 ? 0ull : (~0ull >> (64 - l));
+}
+
+// 32x32 output tile, K=16 bf16 per step: D[i][j] += sum_k A[i][k] B[k][j].
+// Lane l supplies A[l%32][8*(l/32) .. +8) and B[8*(l/32) .. +8)[l%32].
+__device__ __forceinline__ f32x16 mfma32_bf16(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// 32x32 output tile, K=2 fp32 per step. Lane l supplies A[l%32][l/32] and B[l/32][l%32].
+__device__ __forceinline__ f32x16 mfma32_f32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Row of the 32x32 MFMA accumulator element v (0..15) held by lane l; the
+// column is l % 32.
+__device__ __forceinline__ int mfma32_row(int v, int l) { return ((v >> 2) << 3) + ((l >> 5) << 2) + (v & 3); }
+
+// ---------------------------------------------------------------------------
+// Segment work lists. Adapter g (1..NA) owns slots [seg[g-1], seg[g]) of the
+// adapter-sorted token permutation. A module skips adapters with rank 0 (not
+// applicable to it). Tiles are TM consecutive slots of one adapter. Every wave
+// computes the same answer, so no LDS or barrier is needed.
+// ---------------------------------------------------------------------------
+struct TileRef {
+  int g;        // global adapter id (0 = no tile: the workgroup exits)
+  int slot0;    // first slot of the tile
+  int nrows;    // rows in the tile (1..TM)
+};
+
+template <int TM>
+__device__ __forceinline__ TileRef find_tile(const int32_t* __restrict__ seg, const int32_t* __restrict__ ranks,
+                                             int num_adapters, int tile_id) {
+  TileRef ref{0, 0, 0};
+  const int l = __lane_id();
+  int carry = 0;
+  for (int g0 = 1; g0 <= num_adapters; g0 += 64) {
+    const int g = g0 + l;
+    int ntiles = 0;
+    int lo = 0, hi = 0;
+    if (g <= num_adapters) {
+      lo = seg[g - 1];
+      hi = seg[g];
+      ntiles = (ranks[g] > 0) ? (hi - lo + TM - 1) / TM : 0;
+    }
+    // inclusive scan over the wave
+    int incl = ntiles;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      int v = __shfl_up(incl, d, 64);
+      if (l >= d) incl += v;
+    }
+    const int excl = incl - ntiles;
+    const int total = __shfl(incl, 63, 64);
+    const bool mine = (ntiles > 0) && (tile_id >= carry + excl) && (tile_id < carry + incl);
+    const uint64_t bal = __ballot(mine);
+    if (bal) {
+      const int src = __ffsll(static_cast<long long>(bal)) - 1;
+      const int jj = tile_id - carry - __shfl(excl, src, 64);
+      const int slo = __shfl(lo, src, 64);
+      const int shi = __shfl(hi, src, 64);
+      ref.g = g0 + src;
+      ref.slot0 = slo + jj * TM;
+      ref.nrows = min(TM, shi - ref.slot0);
+      return ref;
+    }
+    carry += total;
+  }
+  return ref;
+}
+
+}  // namespace gs

@@ -1,0 +1,417 @@
+"""Per-token switched-LoRA on MI355X: segment metadata, packed adapters, apply.
+
+This is the ``y``-given form of the reference's switched-LoRA math
+(src/granite_switch/hf/core/lora.py:127-161 and :308-348):
+
+    y[t, slice s] += (x[t] . lora_A[a-1, 0]^T) . lora_B[a-1, 0]^T   for id a > 0
+
+with lora_B pre-scaled by alpha/r (src/granite_switch/composer/weight_transfer.py:
+564-568).  Three device steps, all launched on torch's current stream with no
+host synchronisation (so the whole thing can be captured in a HIP graph):
+
+  1. ``build_segments``  per-token ids (+ aLoRA activation offsets on ragged
+     packed batches) -> adapter-sorted token permutation and segment offsets;
+  2. ``shrink``           z[slot] = x[perm[slot]] . A_g^T   (bf16/fp32 MFMA)
+  3. ``expand_add``       y[perm[slot]] += z[slot] . B_g^T  (MFMA, in place)
+
+Base rows are never written.  Nothing here falls back to the CPU: the HIP
+library must be built.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.bfloat16: _lib.GS_DTYPE_BF16, torch.float32: _lib.GS_DTYPE_FP32}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; expected bfloat16 or float32") from None
+
+
+def _require_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("switched-LoRA tensors must live on the GPU")
+
+
+# ---------------------------------------------------------------------------
+# Segments
+# ---------------------------------------------------------------------------
+@dataclass
+class Segments:
+    """Adapter-sorted segments of one batch (built once, reused by every module).
+
+    eff_ids     [T] int32  effective per-token global id (0 = base)
+    seg_offsets [NA+1] int32: adapter g owns perm[seg_offsets[g-1]:seg_offsets[g]]
+    perm        [T] int32  token indices grouped by adapter, ascending within
+    """
+
+    eff_ids: torch.Tensor
+    seg_offsets: torch.Tensor
+    perm: torch.Tensor
+    num_tokens: int
+    num_adapters: int
+
+
+def _as_i64(t, device):
+    if t is None:
+        return None
+    if not isinstance(t, torch.Tensor):
+        t = torch.as_tensor(t)
+    return t.to(device=device, dtype=torch.int64).contiguous()
+
+
+def _as_i32(t, device):
+    if t is None:
+        return None
+    if not isinstance(t, torch.Tensor):
+        t = torch.as_tensor(t)
+    return t.to(device=device, dtype=torch.int32).contiguous()
+
+
+def build_segments(adapter_ids: torch.Tensor, num_adapters: int, positions=None, cu_seqlens=None,
+                   act_offsets=None, out: Segments | None = None) -> Segments:
+    """Gate per-token ids by aLoRA activation offsets and sort tokens by adapter.
+
+    adapter_ids: [T] requested adapter per token (0 = base, 1..num_adapters)
+    positions:   [T] absolute positions (chunked prefill / decode), or None
+                 (position = index inside the sequence)
+    cu_seqlens:  [B+1] sequence boundaries of the packed batch, or None
+    act_offsets: [B] activation offset per sequence: a token is adapted iff its
+                 position >= the offset (tokens before the invocation point are
+                 base only); None disables gating.
+    Integer tensors must already be on the GPU for graph capture (conversions
+    are skipped when dtypes already match).
+    """
+    _require_cuda(adapter_ids)
+    dev = adapter_ids.device
+    ids = _as_i64(adapter_ids.reshape(-1), dev)
+    T = ids.shape[0]
+    pos = _as_i64(positions, dev)
+    cu = _as_i32(cu_seqlens, dev)
+    off = _as_i64(act_offsets, dev)
+    if pos is not None and pos.numel() != T:
+        raise ValueError("positions must have one entry per token")
+    num_seqs = 1
+    if cu is not None:
+        num_seqs = cu.numel() - 1
+        if off is not None and off.numel() != num_seqs:
+            raise ValueError("act_offsets must have one entry per sequence")
+    elif off is not None and off.numel() != 1:
+        raise ValueError("act_offsets without cu_seqlens describes one sequence")
+    if out is None:
+        out = Segments(
+            eff_ids=torch.empty(T, dtype=torch.int32, device=dev),
+            seg_offsets=torch.empty(num_adapters + 1, dtype=torch.int32, device=dev),
+            perm=torch.empty(max(T, 1), dtype=torch.int32, device=dev),
+            num_tokens=T,
+            num_adapters=num_adapters,
+        )
+    _lib.call("gs_build_segments", ids.data_ptr(), _lib.ptr(pos), _lib.ptr(cu), _lib.ptr(off), T, num_seqs,
+              num_adapters, out.eff_ids.data_ptr(), out.seg_offsets.data_ptr(), out.perm.data_ptr(),
+              _lib.stream_ptr(dev))
+    return out
+
+
+def route_latest_wins(input_ids: torch.Tensor, control_tokens, id_offset: int = 1, cu_seqlens=None,
+                      start_ids=None) -> torch.Tensor:
+    """Latest-wins routing from control tokens (per sequence).
+
+    Semantics of src/granite_switch/vllm/switch/multi.py:348-525 as pinned by
+    tests/vllm/test_multi_switch_serving.py:141-153: a token equal to
+    control_tokens[k] fires id k + id_offset (id_offset=1: no base slot;
+    id_offset=0: slot 0 is a base-reset token); every position takes the id of
+    the latest control token at or before it, else ``start_ids[s]`` (the state
+    carried over from the sequence's cached prefix, 0 when None).
+    """
+    _require_cuda(input_ids)
+    dev = input_ids.device
+    ids = _as_i64(input_ids.reshape(-1), dev)
+    T = ids.shape[0]
+    ctl = _as_i64(control_tokens, dev)
+    cu = _as_i32(cu_seqlens, dev)
+    start = _as_i64(start_ids, dev)
+    num_seqs = 1 if cu is None else cu.numel() - 1
+    out = torch.empty(T, dtype=torch.int64, device=dev)
+    _lib.call("gs_route_latest_wins", ids.data_ptr(), _lib.ptr(cu), T, num_seqs, ctl.data_ptr(), ctl.numel(),
+              int(id_offset), _lib.ptr(start), out.data_ptr(), _lib.stream_ptr(dev))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Packed adapters (load time)
+# ---------------------------------------------------------------------------
+def _round8(r: int) -> int:
+    return ((r + 7) // 8) * 8
+
+
+@dataclass
+class PackedAdapters:
+    """One module's adapters in the layout the kernels read.
+
+    a_pack: rows of adapter g start at a_off[g] (elements): S*r_g rows of H,
+            row s*r_g + j = lora_A slice s, rank row j.
+    b_pack: adapter g at b_off[g]: [out_total, r_g] row-major, slices stacked
+            along out, rank contiguous, pre-scaled.
+    ranks[g]: r_g (true rank rounded up to a multiple of 8 with zero rows),
+            0 for g = 0 and for adapters that are not applicable here.
+    """
+
+    a_pack: torch.Tensor
+    b_pack: torch.Tensor
+    a_off: torch.Tensor
+    b_off: torch.Tensor
+    ranks: torch.Tensor
+    ranks_host: list
+    output_slices: tuple
+    hidden: int
+    num_adapters: int
+    max_rank: int
+
+    @property
+    def num_slices(self) -> int:
+        return len(self.output_slices)
+
+    @property
+    def out_total(self) -> int:
+        return int(sum(self.output_slices))
+
+    @property
+    def slice_bounds(self) -> list:
+        b = [0]
+        for s in self.output_slices:
+            b.append(b[-1] + int(s))
+        return b
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return self.a_pack.dtype
+
+    @staticmethod
+    def from_slices(lora_A_slices, lora_B_slices, adapter_ranks=None, applicable=None) -> "PackedAdapters":
+        """Pack checkpoint-layout adapters.
+
+        lora_A_slices[s]: [NA, 1, max_r, H]; lora_B_slices[s]: [NA, 1, O_s, max_r]
+        (the composed-checkpoint layout, src/granite_switch/composer/
+        weight_transfer.py:547-622).  ``adapter_ranks`` gives each adapter's
+        true rank (default max_r); only those rows/columns are packed, so the
+        bytes the kernels read are the true-rank bytes.  ``applicable``
+        defaults to the reference's rule: any nonzero lora_A value in the first
+        r rows of any slice (src/granite_switch/vllm/core/lora.py:353-362).
+        """
+        S = len(lora_A_slices)
+        if S != len(lora_B_slices) or S < 1 or S > _lib.GS_MAX_SLICES:
+            raise ValueError("lora_A_slices and lora_B_slices must have the same 1..8 slices")
+        A0 = lora_A_slices[0]
+        NA, _, max_r, H = A0.shape
+        dev, dt = A0.device, A0.dtype
+        out_slices = tuple(int(B.shape[2]) for B in lora_B_slices)
+        if adapter_ranks is None:
+            adapter_ranks = [max_r] * NA
+        if len(adapter_ranks) != NA:
+            raise ValueError("adapter_ranks must have one entry per adapter")
+        if applicable is None:
+            flags = torch.zeros(NA, dtype=torch.bool, device=dev)
+            rk = torch.tensor([int(r) for r in adapter_ranks], device=dev)
+            mask = torch.arange(max_r, device=dev)[None, :] < rk[:, None]
+            for A in lora_A_slices:
+                flags |= (A[:, 0].ne(0).any(dim=-1) & mask).any(dim=1)
+            applicable = flags.tolist()
+        a_parts, b_parts = [], []
+        a_off = [0] * (NA + 1)
+        b_off = [0] * (NA + 1)
+        ranks = [0] * (NA + 1)
+        arow = 0
+        belem = 0
+        O = sum(out_slices)
+        for a in range(NA):
+            r_true = int(adapter_ranks[a])
+            if not applicable[a] or r_true <= 0:
+                continue
+            if r_true > _lib.GS_MAX_RANK:
+                raise ValueError(f"rank {r_true} exceeds {_lib.GS_MAX_RANK}")
+            r = _round8(r_true)
+            g = a + 1
+            ranks[g] = r
+            a_off[g] = arow * H
+            b_off[g] = belem
+            for s in range(S):
+                A = lora_A_slices[s][a, 0, :min(r, r_true), :]
+                if A.shape[0] < r:
+                    A = torch.cat([A, torch.zeros(r - A.shape[0], H, dtype=dt, device=dev)])
+                a_parts.append(A)
+            Bs = []
+            for s in range(S):
+                B = lora_B_slices[s][a, 0, :, :min(r, r_true)]
+                if B.shape[1] < r:
+                    B = torch.cat([B, torch.zeros(B.shape[0], r - B.shape[1], dtype=dt, device=dev)], dim=1)
+                Bs.append(B)
+            b_parts.append(torch.cat(Bs, dim=0).reshape(-1))
+            arow += S * r
+            belem += O * r
+        if a_parts:
+            a_pack = torch.cat(a_parts).contiguous()
+            b_pack = torch.cat(b_parts).contiguous()
+        else:
+            a_pack = torch.zeros(8, H, dtype=dt, device=dev)
+            b_pack = torch.zeros(8 * O, dtype=dt, device=dev)
+        max_rank = max([8] + ranks)
+        return PackedAdapters(
+            a_pack=a_pack,
+            b_pack=b_pack,
+            a_off=torch.tensor(a_off, dtype=torch.int64, device=dev),
+            b_off=torch.tensor(b_off, dtype=torch.int64, device=dev),
+            ranks=torch.tensor(ranks, dtype=torch.int32, device=dev),
+            ranks_host=ranks,
+            output_slices=out_slices,
+            hidden=int(H),
+            num_adapters=int(NA),
+            max_rank=int(max_rank),
+        )
+
+
+# ---------------------------------------------------------------------------
+# Workspace (split-K partials + self-resetting counters), cached per device
+# ---------------------------------------------------------------------------
+_workspaces: dict = {}
+
+
+def shrink_workspace(num_tokens: int, hidden: int, num_slices: int, num_adapters: int, max_rank: int,
+                     device: torch.device) -> torch.Tensor:
+    """A zero-initialised workspace big enough for one shrink of this shape.
+
+    The counters inside are reset by the kernels themselves, so one buffer is
+    reused by every call on the device; calls on different streams that may
+    overlap in time must not share it.
+    """
+    need = int(_lib.load().gs_shrink_workspace_bytes(num_tokens, hidden, num_slices, num_adapters, max_rank))
+    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < need:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("shrink workspace must be allocated before graph capture (call reserve_workspace)")
+        ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def reserve_workspace(device: torch.device, nbytes: int) -> None:
+    """Pre-allocate the per-device shrink workspace (before graph capture)."""
+    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        _workspaces[key] = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------
+# Shrink / expand / fused apply
+# ---------------------------------------------------------------------------
+def shrink(x: torch.Tensor, segments: Segments, packed: PackedAdapters, z: torch.Tensor | None = None) -> torch.Tensor:
+    """z[slot, s*r_g + j] = x[perm[slot]] . A_{g,s}[j] (compact, slot-major)."""
+    _require_cuda(x)
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    if x2.dtype != packed.dtype:
+        raise TypeError("x and the packed adapters must share a dtype")
+    T, H = x2.shape
+    if H != packed.hidden or T != segments.num_tokens:
+        raise ValueError("x shape does not match the segments / adapters")
+    zw = packed.num_slices * packed.max_rank
+    if z is None:
+        z = torch.empty(max(T, 1), zw, dtype=x2.dtype, device=x2.device)
+    ws = shrink_workspace(T, H, packed.num_slices, packed.num_adapters, packed.max_rank, x2.device)
+    _lib.call("gs_shrink", _dtype_code(x2), x2.data_ptr(), x2.stride(0), T, H, packed.a_pack.data_ptr(),
+              packed.a_off.data_ptr(), packed.ranks.data_ptr(), packed.num_slices, packed.num_adapters,
+              packed.max_rank, segments.seg_offsets.data_ptr(), segments.perm.data_ptr(), z.data_ptr(), z.stride(0),
+              ws.data_ptr(), ws.numel(), _lib.stream_ptr(x2.device))
+    return z
+
+
+def expand_add_(y: torch.Tensor, z: torch.Tensor, segments: Segments, packed: PackedAdapters) -> torch.Tensor:
+    """y[perm[slot]] += z[slot] . B_g^T in place (rows of base tokens untouched)."""
+    _require_cuda(y, z)
+    if y.dtype != packed.dtype or z.dtype != packed.dtype:
+        raise TypeError("y, z and the packed adapters must share a dtype")
+    y2 = y.view(-1, y.shape[-1])
+    if y2.stride(-1) != 1:
+        raise ValueError("y must have unit column stride")
+    T, O = y2.shape
+    if O != packed.out_total or T != segments.num_tokens:
+        raise ValueError("y shape does not match the segments / adapters")
+    bounds = _i32_array(packed.slice_bounds)
+    _lib.call("gs_expand_add", _dtype_code(y2), y2.data_ptr(), y2.stride(0), T, O, bounds, packed.num_slices,
+              z.data_ptr(), z.stride(0), 0, None, packed.b_pack.data_ptr(), packed.b_off.data_ptr(),
+              packed.ranks.data_ptr(), packed.num_adapters, packed.max_rank, segments.seg_offsets.data_ptr(),
+              segments.perm.data_ptr(), _lib.stream_ptr(y2.device))
+    return y
+
+
+def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed: PackedAdapters,
+                   z: torch.Tensor | None = None) -> torch.Tensor:
+    """In place: y += switched-LoRA delta of x (shrink then expand)."""
+    z = shrink(x, segments, packed, z)
+    return expand_add_(y, z, segments, packed)
+
+
+def _i32_array(vals):
+    """Host int32 array for the C ABI's host-side table arguments."""
+    return (ctypes.c_int32 * len(vals))(*[int(v) for v in vals])
+
+
+def algorithmic_bytes(segments_host_ids, packed: PackedAdapters, true_ranks=None, elem_bytes: int = 2) -> int:
+    """Bytes the op must move at minimum, for the roofline.
+
+    x rows of active tokens + A and B of the adapters used (true rank) + read
+    and write of the active y rows + 4 bytes per token id.  ``segments_host_ids``
+    is the effective per-token id array on the host.
+    """
+    import numpy as np
+
+    ids = np.asarray(segments_host_ids)
+    S, H, O = packed.num_slices, packed.hidden, packed.out_total
+    ranks = packed.ranks_host if true_ranks is None else [0] + list(true_ranks)
+    act = ids[(ids > 0)]
+    act = act[np.array([ranks[int(g)] > 0 for g in act], dtype=bool)] if act.size else act
+    used = np.unique(act)
+    rsum = sum(int(ranks[int(g)]) for g in used)
+    t_act = int(act.size)
+    return (t_act * H * elem_bytes + S * H * rsum * elem_bytes + O * rsum * elem_bytes
+            + 2 * t_act * O * elem_bytes + 4 * ids.size)
+
+
+def algorithmic_flops(segments_host_ids, packed: PackedAdapters, true_ranks=None) -> int:
+    import numpy as np
+
+    ids = np.asarray(segments_host_ids)
+    S, H, O = packed.num_slices, packed.hidden, packed.out_total
+    ranks = packed.ranks_host if true_ranks is None else [0] + list(true_ranks)
+    tot = 0
+    for g in ids[ids > 0]:
+        r = int(ranks[int(g)])
+        tot += 2 * H * S * r + 2 * r * O
+    return int(tot)
+
+
+__all__ = [
+    "Segments",
+    "PackedAdapters",
+    "build_segments",
+    "route_latest_wins",
+    "shrink",
+    "expand_add_",
+    "switched_lora_",
+    "shrink_workspace",
+    "reserve_workspace",
+    "algorithmic_bytes",
+    "algorithmic_flops",
+]

@@ -1,0 +1,188 @@
+/*
+ * granite_switch_amd.h -- C ABI of the MI355X (gfx950) switched-LoRA library.
+ *
+ * One shared library, libgranite_switch_amd.so, built with hipcc for gfx950.
+ * Every entry point takes plain device pointers, sizes and a hipStream_t
+ * (passed as void*), launches on that stream, never synchronises, never
+ * allocates, and returns a GS_* status.  On failure gs_last_error() returns a
+ * message for the calling thread.  Tensors are row-major; "ld" arguments are
+ * row strides in ELEMENTS.  Token / adapter id convention is the reference's:
+ * 0 = base (no LoRA), 1..num_adapters = adapters.
+ *
+ * Element types (dtype argument): GS_DTYPE_BF16 or GS_DTYPE_FP32.  Compute is
+ * fp32-accumulated; bf16 paths use bf16 MFMA on gfx950, fp32 paths fp32 MFMA.
+ *
+ * Reference interfaces replaced (paths relative to the Granite Switch repo):
+ *   gs_build_segments      the per-adapter token grouping of the HF loop
+ *                          (src/granite_switch/hf/core/lora.py:127-135, 317-325)
+ *                          fed by latest-wins / aLoRA routing
+ *                          (src/granite_switch/vllm/switch/multi.py:516-518)
+ *   gs_route_latest_wins   control-token routing semantics of MultiSwitch
+ *                          (src/granite_switch/vllm/switch/multi.py:348-525)
+ *   gs_shrink, gs_expand_add, gs_switched_lora
+ *                          the shrink/expand/add of
+ *                          src/granite_switch/hf/core/lora.py:127-161, 308-348
+ *   gs_compute_bitmasks    torch.ops.granite_switch.compute_per_module_bitmasks
+ *                          (src/granite_switch/vllm/core/lora_kernel_meta.py:61-91,
+ *                          169-182) plus the remap gather at :294
+ *   gs_switch_lora_expand  torch.ops.granite_switch.switch_lora_expand
+ *                          (src/granite_switch/vllm/core/lora_ops.py:30-60,192-202;
+ *                          src/granite_switch/kernels/switch_lora_kernel.py:414-458)
+ *   gs_switch_lora_expand_swiglu
+ *                          torch.ops.granite_switch.switch_lora_expand_swiglu
+ *                          (lora_ops.py:82-113,204-214; switch_lora_kernel.py:809-857)
+ */
+#ifndef GRANITE_SWITCH_AMD_H_
+#define GRANITE_SWITCH_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GS_OK 0
+#define GS_ERR_INVALID 1     /* bad argument (shape, alignment, limit)            */
+#define GS_ERR_HIP 2         /* a HIP runtime call or kernel launch failed         */
+#define GS_ERR_WORKSPACE 3   /* workspace too small: see gs_shrink_workspace_bytes */
+
+#define GS_DTYPE_BF16 0
+#define GS_DTYPE_FP32 1
+
+#define GS_MAX_ADAPTERS 256  /* global adapter ids handled by the segment builder */
+#define GS_MAX_SLICES 8      /* output slices per projection (QKV = 3, gate_up = 2) */
+#define GS_MAX_RANK 512      /* largest LoRA rank (the reference's top tier)       */
+
+/* Library version (major*10000 + minor*100 + patch) and last error text. */
+int gs_version(void);
+const char* gs_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * Segment builder.
+ *
+ * eff_ids[t] = req_ids[t] if the token is activated, else 0, where a token t of
+ * sequence s (cu_seqlens[s] <= t < cu_seqlens[s+1]) at absolute position
+ * q = positions[t] (or t - cu_seqlens[s] when positions is NULL) is activated
+ * iff act_offsets == NULL or q >= act_offsets[s] (aLoRA: tokens before the
+ * invocation point are base only).  Ids outside [0, num_adapters] become 0.
+ *
+ * Then a stable counting sort of the active tokens by adapter:
+ *   seg_offsets[0] = 0, seg_offsets[g] = number of active tokens with id <= g;
+ *   perm[seg_offsets[g-1] .. seg_offsets[g]) = the tokens of adapter g in
+ *   ascending token order.  perm entries past seg_offsets[num_adapters] are
+ *   left untouched.
+ *
+ * req_ids [T] int64; positions [T] int64 or NULL; cu_seqlens [num_seqs+1]
+ * int32 or NULL (one sequence); act_offsets [num_seqs] int64 or NULL.
+ * Outputs: eff_ids [T] int32, seg_offsets [num_adapters+1] int32, perm [T] int32.
+ * Limits: 1 <= num_adapters <= GS_MAX_ADAPTERS; 0 <= T < 2^31.
+ * ---------------------------------------------------------------------- */
+int gs_build_segments(const int64_t* req_ids, const int64_t* positions, const int32_t* cu_seqlens,
+                      const int64_t* act_offsets, int64_t num_tokens, int32_t num_seqs, int32_t num_adapters,
+                      int32_t* eff_ids, int32_t* seg_offsets, int32_t* perm, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Latest-wins routing from control tokens (per sequence, across chunks).
+ *
+ * out_ids[t] = the adapter fired by the most recent control token at or before
+ * token t within its sequence, else start_ids[s] (the id in force at the end of
+ * the sequence's cached prefix; NULL = 0).  A token equal to
+ * control_tokens[k] fires id k + id_offset (id_offset = 1 for the layout with no
+ * base slot, 0 for the base-reset layout whose slot 0 re-selects base).
+ * input_ids [T] int64; cu_seqlens [num_seqs+1] int32 or NULL;
+ * control_tokens [num_control] int64; start_ids [num_seqs] int64 or NULL;
+ * out_ids [T] int64.  Limits: num_control <= GS_MAX_ADAPTERS + 1.
+ * ---------------------------------------------------------------------- */
+int gs_route_latest_wins(const int64_t* input_ids, const int32_t* cu_seqlens, int64_t num_tokens,
+                         int32_t num_seqs, const int64_t* control_tokens, int32_t num_control, int32_t id_offset,
+                         const int64_t* start_ids, int64_t* out_ids, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Per-module packed adapter weights (built once at load time by the host):
+ *   ranks [num_adapters+1] int32: rank of adapter g in this module, 0 if g is
+ *       not applicable here (ranks[0] = 0).  bf16 ranks must be multiples of 8.
+ *   a_pack + a_off[g]: S*r_g rows of `hidden` elements, row s*r_g + j is
+ *       lora_A of slice s, rank row j (the reference's w_ext tail order).
+ *   b_pack + b_off[g]: [out_total, r_g] row-major (slices concatenated along
+ *       out, rank contiguous -- the reference's lora_B_merged / lb_packed
+ *       layout), already scaled by alpha/r.
+ *   slice_bounds [S+1] int32 (host array): output column where each slice
+ *       starts; every slice width must be a multiple of 32.
+ * ---------------------------------------------------------------------- */
+
+/* Workspace for gs_shrink: split-K partial tiles plus self-resetting tile
+ * counters.  The counter region (the first gs_shrink_counter_bytes bytes of
+ * the workspace) must be zero before the first call; each call leaves it
+ * zero again.  Calls that share one workspace must not overlap in time. */
+int64_t gs_shrink_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t num_slices, int32_t num_adapters,
+                                  int32_t max_rank);
+int64_t gs_shrink_counter_bytes(int64_t num_tokens, int32_t num_slices, int32_t num_adapters, int32_t max_rank);
+
+/* z[slot, s*r_g + j] = sum_k x[perm[slot], k] * lora_A_{g,s}[j, k] for every
+ * active slot (slot < seg_offsets[num_adapters]) whose adapter is applicable.
+ * x [T, hidden] (ld ldx); z [T, ldz] with ldz >= S*max_rank; same dtype. */
+int gs_shrink(int32_t dtype, const void* x, int64_t ldx, int64_t num_tokens, int32_t hidden, const void* a_pack,
+              const int64_t* a_off, const int32_t* ranks, int32_t num_slices, int32_t num_adapters,
+              int32_t max_rank, const int32_t* seg_offsets, const int32_t* perm, void* z, int64_t ldz,
+              void* workspace, int64_t workspace_bytes, void* stream);
+
+/* y[perm[slot], n] = round(y + sum_k z[row, zcol + k] * B_g[n, k]) for every
+ * active slot and output column n, k < r_g, where n lies in slice s,
+ * zcol = z_off[g] + s*r_g, and row = perm[slot] if z_by_token else slot.
+ * Rows of base tokens and of non-applicable adapters are not touched.
+ * z_off [num_adapters+1] int32 or NULL (all zero). */
+int gs_expand_add(int32_t dtype, void* y, int64_t ldy, int64_t num_tokens, int32_t out_total,
+                  const int32_t* slice_bounds, int32_t num_slices, const void* z, int64_t ldz, int32_t z_by_token,
+                  const int32_t* z_off, const void* b_pack, const int64_t* b_off, const int32_t* ranks,
+                  int32_t num_adapters, int32_t max_rank, const int32_t* seg_offsets, const int32_t* perm,
+                  void* stream);
+
+/* gs_shrink followed by gs_expand_add (compact z): the whole switched-LoRA
+ * delta fused into y.  z [T, S*max_rank] scratch of the same dtype. */
+int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t num_tokens,
+                     int32_t hidden, int32_t out_total, const int32_t* slice_bounds, int32_t num_slices,
+                     const void* a_pack, const int64_t* a_off, const void* b_pack, const int64_t* b_off,
+                     const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* seg_offsets,
+                     const int32_t* perm, void* z, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Reference op: per-module tile bitmasks and kernel-local ids.
+ * bitmasks[m, tile] (int64, [num_modules, ceil(M/block_m)]) has bit (loc-1) set
+ * iff some token of the tile has kernel-local id loc = remap_t[clamp(id,0,NA), m]
+ * > 0 (loc 64 sets the sign bit); the tail tile is padded with id 0.
+ * remapped (int64 [num_modules, M], NULL to skip) = remap_t[clamp(id), m].
+ * adapter_indices [M] with element size idx_bytes (4 or 8);
+ * remap_tables_t [NA+1, num_modules] int64.  1 <= block_m <= 1024.
+ * ---------------------------------------------------------------------- */
+int gs_compute_bitmasks(const void* adapter_indices, int32_t idx_bytes, int64_t M, const int64_t* remap_tables_t,
+                        int32_t na_plus_1, int32_t num_modules, int32_t block_m, int64_t* bitmasks,
+                        int64_t* remapped, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Reference op: in-place expand over x_ext (bf16), reference semantics.
+ * x_ext [M, >= N + shrink cols] with strides (stride_m, stride_n) in elements;
+ * adapter_indices [M] kernel-local ids (element size idx_bytes 4 or 8);
+ * bitmask [ceil(M/32)] int64 with stride stride_bm; lb_packed bf16 (tiers
+ * concatenated, each [NA_r, N, r]); tile_slice [ceil(N/block_n)] int32;
+ * slice_col_r [S, 6] int32; na[6] = NA_16..NA_512 (host array).
+ * Requires block_n % 32 == 0 and N % 32 == 0.
+ * ---------------------------------------------------------------------- */
+int gs_switch_lora_expand(void* x_ext, int64_t stride_m, int64_t stride_n, int64_t M, const void* adapter_indices,
+                          int32_t idx_bytes, const int64_t* bitmask, int64_t stride_bm, const void* lb_packed,
+                          const int32_t* tile_slice, const int32_t* slice_col_r, const int32_t* na, int32_t S,
+                          int32_t block_n, int32_t N, void* stream);
+
+/* Reference op: out[M, H] = silu(gate + dgate) * (up + dup), always written.
+ * gate = x_ext[:, 0:H], up = x_ext[:, H:2H]; out dtype bf16 with strides
+ * (stride_om, stride_on).  S must be 2 and N = 2H.  H % 32 == 0. */
+int gs_switch_lora_expand_swiglu(void* out, int64_t stride_om, int64_t stride_on, const void* x_ext,
+                                 int64_t stride_m, int64_t stride_n, int64_t M, const void* adapter_indices,
+                                 int32_t idx_bytes, const int64_t* bitmask, int64_t stride_bm,
+                                 const void* lb_packed, const int32_t* slice_col_r, const int32_t* na, int32_t S,
+                                 int32_t block_n, int32_t H, int32_t N, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GRANITE_SWITCH_AMD_H_ */

@@ -1,0 +1,235 @@
+"""GPU parity of the reference-form ops and layer wrappers.
+
+* ``torch.ops.granite_switch.switch_lora_expand`` / ``..._swiglu`` vs the
+  oracle's restatement of the reference kernels, on the same bf16 x_ext;
+* vLLM-form ``SwitchedLoRALinear`` (fused w_ext GEMM + expand, segment path and
+  op path) vs the switched-LoRA math;
+* HF-form layers vs the HF loop restated in the oracle.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from granite_switch_amd import hf_layers, meta, ops, switched, vllm_layers
+from oracle import lora as olora
+from oracle import mapping as omap
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _close(got, ref, tol, what):
+    err = np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64))
+    bad = err > tol + tol * np.abs(ref)
+    assert not bad.any(), f"{what}: {int(bad.sum())} bad, max abs err {err.max():.3e}"
+
+
+def _make_vllm_layer(dev, K, slices, ranks, seed, fuse_swiglu=False, bias=False, zero=()):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    base = torch.nn.Linear(K, sum(slices), bias=bias).to(device=dev, dtype=torch.bfloat16)
+    with torch.no_grad():
+        base.weight.copy_(torch.randn(sum(slices), K, generator=g, device=dev) / K ** 0.5)
+    max_r = max(ranks)
+    layer = vllm_layers.SwitchedLoRALinear(base, len(ranks), max_r, num_slices=len(slices),
+                                           output_slices=slices if len(slices) > 1 else None, fuse_swiglu=fuse_swiglu)
+    A_sl = [layer.lora_A] if len(slices) == 1 else list(layer.lora_A_slices)
+    B_sl = [layer.lora_B] if len(slices) == 1 else list(layer.lora_B_slices)
+    with torch.no_grad():
+        for s in range(len(slices)):
+            for a, r in enumerate(ranks):
+                if a in zero:
+                    continue
+                A_sl[s].data[a, 0, :r] = (torch.randn(r, K, generator=g, device=dev) / K ** 0.5).to(torch.bfloat16)
+                B_sl[s].data[a, 0, :, :r] = (torch.randn(slices[s], r, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    A_np = [_np(a) for a in A_sl]
+    B_np = [_np(b) for b in B_sl]
+    W = _np(base.weight)
+    layer.finalize_weights(ranks)
+    return layer, W, A_np, B_np
+
+
+def _ctx_for(dev, layer, ids):
+    fm = meta.FusedLoRAKernelMeta(dev)
+    fm.register_remap_tables(layer.remap_table.unsqueeze(0), [(layer.in_features, layer._N_total, layer._num_applicable)])
+    ctx = meta.LoRAContext()
+    fm.prepare_and_store(ids, ctx)
+    return ctx
+
+
+@pytest.mark.parametrize("slices,ranks", [((4096, 1024, 1024), [32] * 12), ((2048,), [8, 16, 32, 64, 128, 16]),
+                                          ((512, 256), [16, 512, 8])])
+def test_vllm_layer_segment_and_op_paths(dev, slices, ranks):
+    K, T = 1024, 300
+    _say(f"vllm layer slices={slices} ranks={ranks}")
+    layer, W, A, B = _make_vllm_layer(dev, K, slices, ranks, seed=5, zero=(1,))
+    g = torch.Generator(device=dev).manual_seed(8)
+    x = torch.randn(T, K, generator=g, device=dev).to(torch.bfloat16)
+    ids = torch.randint(0, len(ranks) + 1, (T,), generator=g, device=dev)
+    ctx = _ctx_for(dev, layer, ids)
+    layer._lora_ctx = ctx
+    out_seg, _ = layer(x)                       # segment path
+    out_seg = out_seg.clone()
+    seg = ctx.segments
+    ctx.segments = None
+    out_op, _ = layer(x)                        # reference op path (bitmask tiles)
+    ctx.segments = seg
+    torch.cuda.synchronize()
+    ids_h = ids.cpu().numpy()
+    eff = ids_h.copy()
+    eff[eff == 2] = 0                           # adapter 2 (index 1) is not applicable
+    xb = _np(x)
+    ref = olora.switched_lora_apply(xb @ W.T, xb, eff, A, B, slices, ranks, "f64")
+    _close(_np(out_seg), ref, 2e-2, "segment path")
+    _close(_np(out_op), ref, 2e-2, "op path")
+    # both paths read the same bf16 shrink columns; they differ by at most 1 ulp of the output
+    d = (out_seg.float() - out_op.float()).abs()
+    assert (d <= 2 ** -7 * out_op.float().abs().clamp_min(1.0)).all()
+
+
+def test_switch_lora_expand_op_matches_oracle(dev):
+    """The op alone, on a fixed bf16 x_ext, vs the oracle's restatement of the Triton kernel."""
+    slices, ranks, K, T = (256, 128, 128), [16, 32, 16, 64, 8], 512, 200
+    layer, W, A, B = _make_vllm_layer(dev, K, slices, ranks, seed=9)
+    g = torch.Generator(device=dev).manual_seed(10)
+    x = torch.randn(T, K, generator=g, device=dev).to(torch.bfloat16)
+    ids = torch.randint(0, len(ranks) + 1, (T,), generator=g, device=dev)
+    ctx = _ctx_for(dev, layer, ids)
+    x_ext = torch.mm(x, layer.w_ext.T)
+    x_ext0 = _np(x_ext)
+    loc = ctx.remapped_indices[0]
+    for idx in (loc, loc.to(torch.int32)):
+        xe = x_ext.clone()
+        ops.op("switch_lora_expand")(xe, idx, ctx.per_module_bitmasks[0], layer._lb_packed, layer.tile_to_slice,
+                                      layer.slice_col_r, *layer._na, layer._S, layer._block_n, layer._N_total)
+        torch.cuda.synchronize()
+        ref = olora.switch_lora_expand_xext(x_ext0, loc.cpu().numpy(), ctx.per_module_bitmasks[0].cpu().numpy(),
+                                            _np(layer._lb_packed), layer.tile_to_slice.cpu().numpy(),
+                                            layer.slice_col_r.cpu().numpy(), layer._na, layer._S, layer._block_n,
+                                            layer._N_total)
+        _close(_np(xe), ref, 2e-2, "switch_lora_expand")
+        base = (loc == 0).cpu().numpy()
+        assert np.array_equal(_np(xe)[base], x_ext0[base]), "base rows touched"
+        # shrink columns are never written
+        assert np.array_equal(_np(xe)[:, layer._N_total:], x_ext0[:, layer._N_total:])
+
+
+def test_switch_lora_expand_zero_bitmask_skips(dev):
+    slices, ranks, K, T = (128,), [16, 16], 256, 64
+    layer, W, A, B = _make_vllm_layer(dev, K, slices, ranks, seed=12)
+    x = torch.randn(T, K, device=dev).to(torch.bfloat16)
+    x_ext = torch.mm(x, layer.w_ext.T)
+    ids = torch.ones(T, dtype=torch.int64, device=dev)
+    bm = torch.zeros(2, dtype=torch.int64, device=dev)          # says: no adapter anywhere
+    xe = x_ext.clone()
+    ops.op("switch_lora_expand")(xe, ids, bm, layer._lb_packed, layer.tile_to_slice, layer.slice_col_r, *layer._na,
+                                  layer._S, layer._block_n, layer._N_total)
+    torch.cuda.synchronize()
+    assert torch.equal(xe, x_ext)
+
+
+@pytest.mark.parametrize("with_ctx", [True, False])
+def test_swiglu_path(dev, with_ctx):
+    H, K, T = 1280, 512, 150
+    ranks = [32, 16, 32]
+    layer, W, A, B = _make_vllm_layer(dev, K, (H, H), ranks, seed=13, fuse_swiglu=True)
+    g = torch.Generator(device=dev).manual_seed(14)
+    x = torch.randn(T, K, generator=g, device=dev).to(torch.bfloat16)
+    ids = torch.randint(0, 4, (T,), generator=g, device=dev)
+    if with_ctx:
+        layer._lora_ctx = _ctx_for(dev, layer, ids)
+    else:
+        layer._lora_ctx = None
+    out, _ = layer(x)
+    torch.cuda.synchronize()
+    xb = _np(x)
+    eff = ids.cpu().numpy() if with_ctx else np.zeros(T, np.int64)
+    corr = olora.switched_lora_apply(xb @ W.T, xb, eff, A, B, (H, H), ranks, "f64")
+    gte, up = corr[:, :H], corr[:, H:]
+    ref = gte / (1 + np.exp(-gte)) * up
+    _close(_np(out), ref, 3e-2, "swiglu")
+    assert out.is_contiguous() and out.shape == (T, H)
+
+
+def test_swiglu_op_matches_oracle(dev):
+    H, K, T = 256, 256, 97
+    ranks = [16, 64]
+    layer, W, A, B = _make_vllm_layer(dev, K, (H, H), ranks, seed=15, fuse_swiglu=True)
+    x = torch.randn(T, K, device=dev).to(torch.bfloat16)
+    ids = torch.randint(0, 3, (T,), device=dev)
+    ctx = _ctx_for(dev, layer, ids)
+    x_ext = torch.mm(x, layer.w_ext.T)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    ops.op("switch_lora_expand_swiglu")(out, x_ext, ctx.remapped_indices[0], ctx.per_module_bitmasks[0],
+                                         layer._lb_packed, layer.slice_col_r, *layer._na, 2, 32, H, 2 * H)
+    torch.cuda.synchronize()
+    ref = olora.expand_swiglu_xext(_np(x_ext), ctx.remapped_indices[0].cpu().numpy(),
+                                   ctx.per_module_bitmasks[0].cpu().numpy(), _np(layer._lb_packed),
+                                   layer.slice_col_r.cpu().numpy(), layer._na, 2, H, 2 * H)
+    _close(_np(out), ref, 2e-2, "swiglu op")
+
+
+@pytest.mark.parametrize("merged", [False, True])
+def test_hf_layers_match_hf_loop(dev, merged):
+    K, NA, R = 384, 5, 16
+    torch.manual_seed(0)
+    if merged:
+        slices = (256, 128, 128)
+        layer = hf_layers.MergedSwitchedLoRALinear(K, slices, NA, R).to(dev)
+        A_sl, B_sl = list(layer.lora_A_slices), list(layer.lora_B_slices)
+    else:
+        slices = (320,)
+        layer = hf_layers.SwitchedLoRALinear(K, 320, NA, R).to(dev)
+        A_sl, B_sl = [layer.lora_A], [layer.lora_B]
+    with torch.no_grad():
+        for B in B_sl:
+            B.copy_(torch.randn_like(B) * 0.1)
+    x = torch.randn(3, 40, K, device=dev)
+    ids = torch.randint(0, NA + 1, (3, 40), device=dev)
+    out = layer(x, ids)
+    base = layer.base_layer(x)
+    torch.cuda.synchronize()
+    ref = olora.switched_lora_apply(_np(base).reshape(-1, sum(slices)), _np(x).reshape(-1, K),
+                                    ids.cpu().numpy().reshape(-1), [_np(a) for a in A_sl], [_np(b) for b in B_sl],
+                                    slices, None, "fp32")
+    _close(_np(out).reshape(-1, sum(slices)), ref, 1e-4, "hf layer")
+    # frozen pack gives the same answer; context-passing indices too
+    layer.freeze()
+    layer._adapter_indices = ids
+    out2 = layer(x)
+    torch.cuda.synchronize()
+    assert torch.allclose(out2, out, atol=1e-6, rtol=1e-6)
+    # all-base == base layer exactly
+    out3 = layer(x, torch.zeros_like(ids))
+    assert torch.equal(out3, layer.base_layer(x))
+
+
+def test_custom_ops_under_torch_compile(dev):
+    remap_t = torch.tensor([[0, 1, 2, 3, 4], [0, 1, 0, 2, 0]], dtype=torch.int64, device=dev).T.contiguous()
+    ids = torch.randint(0, 5, (200,), device=dev)
+
+    def fn(a, r):
+        return torch.ops.granite_switch.compute_per_module_bitmasks(a, r)
+
+    eager = fn(ids, remap_t)
+    compiled = torch.compile(fn, fullgraph=True)(ids, remap_t)
+    assert torch.equal(compiled, eager)
+    assert np.array_equal(eager.cpu().numpy(), omap.compute_bitmasks(ids.cpu().numpy(), remap_t.cpu().numpy(), 32))
+
+
+def test_segment_op_surface(dev):
+    ids = torch.tensor([0, 2, 1, 2, 0, 1], device=dev)
+    eff, seg, perm = ops.op("build_segments")(ids, 3, None, None, None)
+    torch.cuda.synchronize()
+    assert seg.cpu().tolist() == [0, 2, 4, 4]
+    assert perm.cpu().tolist()[:4] == [2, 5, 1, 3]
+    _ = switched

@@ -1,0 +1,207 @@
+"""CPU tests: the C ABI library loads and exports its header, host-side logic.
+
+No kernel is launched here: the only library calls are ones whose argument
+validation rejects them before any HIP call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import glob
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from granite_switch_amd import _lib, kernels, switched, vllm_layers, workloads
+from oracle import mapping as omap
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        txt = open(h).read()
+        txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+        for m in re.finditer(r"^\s*(?:const\s+)?[\w\*\s]+?\b(gs_\w+)\s*\(", txt, flags=re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.load()
+    names = _header_functions()
+    assert len(names) >= 10
+    for n in sorted(names):
+        assert hasattr(lib, n), f"missing export {n}"
+    assert set(_lib.SIGNATURES) == names, "ctypes signatures out of sync with the header"
+    assert lib.gs_version() >= 100
+
+
+def test_library_shares_torchs_hip_runtime():
+    _lib.load()
+    maps = open("/proc/self/maps").read()
+    hip = {l.split()[-1] for l in maps.splitlines() if "libamdhip64" in l}
+    assert len(hip) == 1, hip
+
+
+def test_validation_errors_without_launch():
+    with pytest.raises(_lib.GraniteSwitchError) as e:
+        _lib.call("gs_build_segments", None, None, None, None, 4, 1, 0, None, None, None, None)
+    assert e.value.status == _lib.GS_ERR_INVALID and "num_adapters" in str(e.value)
+    with pytest.raises(_lib.GraniteSwitchError) as e:
+        _lib.call("gs_shrink", 0, None, 16, 4, 12, None, None, None, 1, 4, 16, None, None, None, 16, None, 0, None)
+    assert "hidden" in str(e.value)
+    with pytest.raises(_lib.GraniteSwitchError) as e:
+        _lib.call("gs_expand_add", 0, None, 64, 4, 48, (ctypes.c_int32 * 2)(0, 48), 1, None, 16, 0, None, None,
+                  None, None, 4, 16, None, None, None)
+    assert "multiple of 32" in str(e.value)
+    na = (ctypes.c_int32 * 6)(65, 0, 0, 0, 0, 0)
+    with pytest.raises(_lib.GraniteSwitchError) as e:
+        _lib.call("gs_switch_lora_expand", None, 64, 1, 4, None, 8, None, 1, None, None, None, na, 1, 32, 32, None)
+    assert "64-bit tile mask" in str(e.value)
+    with pytest.raises(_lib.GraniteSwitchError) as e:
+        _lib.call("gs_compute_bitmasks", None, 2, 4, None, 2, 1, 32, None, None, None)
+    assert "idx_bytes" in str(e.value)
+
+
+def test_workspace_plan_is_consistent():
+    lib = _lib.load()
+    small = lib.gs_shrink_workspace_bytes(256, 4096, 3, 12, 32)
+    big = lib.gs_shrink_workspace_bytes(8192, 4096, 2, 12, 32)
+    assert small > 0 and big > 0
+    assert lib.gs_shrink_counter_bytes(256, 3, 12, 32) % 256 == 0
+
+
+# -- host mirrors of the reference API ---------------------------------------
+def test_kernels_promote_rank_matches_reference_table(kats):
+    for rank, expected in kats["promote_rank"]["cases"]:
+        assert kernels.promote_rank(rank) == expected
+    for r in kats["promote_rank"]["raises"]:
+        with pytest.raises(ValueError):
+            kernels.promote_rank(r)
+    assert kernels.get_switch_lora_expand_config() == {"block_m": 32, "block_n": 32, "num_warps": 4, "num_stages": 1}
+
+
+def test_build_w_ext_row_order():
+    W = torch.arange(6.0).reshape(2, 3)
+    A16 = torch.arange(2 * 2 * 16 * 3, dtype=torch.float32).reshape(2, 2, 16, 3)
+    A32 = -torch.arange(1 * 2 * 32 * 3, dtype=torch.float32).reshape(1, 2, 32, 3)
+    w = kernels.build_w_ext(W, {32: A32, 16: A16})
+    assert w.shape == (2 + 64 + 64, 3)
+    assert torch.equal(w[:2], W)
+    assert torch.equal(w[2:2 + 16], A16[0, 0])          # tier 16, adapter 0, slice 0
+    assert torch.equal(w[2 + 16:2 + 32], A16[0, 1])     # ... slice 1
+    assert torch.equal(w[2 + 32:2 + 48], A16[1, 0])     # adapter 1
+    assert torch.equal(w[66:98], A32[0, 0])              # tier 32 after tier 16
+
+
+def _fill(layer, ranks, seed=0, zero=()):
+    g = torch.Generator().manual_seed(seed)
+    A_sl = [layer.lora_A] if layer.num_slices == 1 else list(layer.lora_A_slices)
+    B_sl = [layer.lora_B] if layer.num_slices == 1 else list(layer.lora_B_slices)
+    with torch.no_grad():
+        for s in range(layer.num_slices):
+            for a, r in enumerate(ranks):
+                if a in zero:
+                    continue
+                A_sl[s].data[a, 0, :r] = torch.randn(r, A_sl[s].shape[3], generator=g)
+                B_sl[s].data[a, 0, :, :r] = torch.randn(B_sl[s].shape[2], r, generator=g)
+    return [a.data.clone().numpy() for a in A_sl], [b.data.clone().numpy() for b in B_sl]
+
+
+def test_vllm_finalize_tables_match_oracle():
+    """finalize_weights on CPU tensors reproduces the reference's tables."""
+    slices = (64, 32, 32)
+    ranks = [32, 8, 16, 16, 32]
+    base = torch.nn.Linear(48, sum(slices), bias=False)
+    layer = vllm_layers.SwitchedLoRALinear(base, len(ranks), 32, num_slices=3, output_slices=slices)
+    A, B = _fill(layer, ranks, zero=(4,))
+    W = base.weight.data.clone().numpy()
+    layer.finalize_weights(ranks)
+    applicable = omap.applicability(A, ranks)
+    remap, order, eff = omap.build_remap(applicable, ranks)
+    na, tile_slice, scr, tiers = omap.finalize_tables(slices, order, eff, 32)
+    assert layer.remap_table.tolist() == remap.tolist()
+    assert layer._na == na
+    assert layer.tile_to_slice.tolist() == tile_slice.tolist()
+    assert layer.slice_col_r.tolist() == scr.tolist()
+    np.testing.assert_array_equal(layer.w_ext.numpy(), omap.build_w_ext(W, A, tiers))
+    np.testing.assert_array_equal(layer._lb_packed.numpy(), omap.build_lb_packed(B, tiers))
+    # per-global-adapter tables of the segment path
+    for g in range(1, len(ranks) + 1):
+        if remap[g] == 0:
+            assert layer._seg_ranks[g] == 0
+        else:
+            assert layer._seg_ranks[g] == eff[g - 1]
+    # checkpoint tensors are released
+    assert all(p.numel() == 0 for p in layer.lora_A_slices)
+
+
+def test_vllm_block_n_alignment_assert():
+    base = torch.nn.Linear(16, 96 + 65, bias=False)
+    layer = vllm_layers.SwitchedLoRALinear(base, 1, 16, num_slices=2, output_slices=(96, 65))
+    _fill(layer, [16])
+    with pytest.raises(AssertionError, match="block_n=.*must divide"):
+        layer.finalize_weights([16])
+
+
+def test_packed_adapters_layout_cpu():
+    slices = (32, 64)
+    NA, H, maxr = 3, 24, 16
+    ranks = [8, 16, 12]
+    g = torch.Generator().manual_seed(1)
+    A = [torch.randn(NA, 1, maxr, H, generator=g) for _ in slices]
+    B = [torch.randn(NA, 1, o, maxr, generator=g) for o in slices]
+    for s in range(2):
+        for a, r in enumerate(ranks):
+            A[s][a, 0, r:] = 0
+            B[s][a, 0, :, r:] = 0
+    pk = switched.PackedAdapters.from_slices(A, B, ranks)
+    assert pk.ranks.tolist() == [0, 8, 16, 16]       # 12 rounded up to 16 with zero rows
+    for a in range(NA):
+        gi = a + 1
+        r = pk.ranks_host[gi]
+        rows = pk.a_pack.view(-1)[pk.a_off[gi]: pk.a_off[gi] + 2 * r * H].view(2 * r, H)
+        for s in range(2):
+            assert torch.equal(rows[s * r:(s + 1) * r, :], A[s][a, 0, :r])
+        bm = pk.b_pack[pk.b_off[gi]: pk.b_off[gi] + 96 * r].view(96, r)
+        assert torch.equal(bm, torch.cat([B[0][a, 0, :, :r], B[1][a, 0, :, :r]]))
+    assert pk.slice_bounds == [0, 32, 96]
+
+
+def test_non_applicable_adapter_is_skipped_in_pack():
+    A = [torch.zeros(2, 1, 16, 8)]
+    B = [torch.ones(2, 1, 32, 16)]
+    A[0][0, 0, :16] = 1.0
+    pk = switched.PackedAdapters.from_slices(A, B, [16, 16])
+    assert pk.ranks.tolist() == [0, 16, 0]
+
+
+# -- workloads ---------------------------------------------------------------
+def test_workload_routing_shapes():
+    r1 = workloads.routing_for(1)
+    eff1 = omap.alora_effective_ids(r1.req_ids, r1.positions, r1.cu_seqlens, r1.act_offsets)
+    assert r1.num_tokens == 256 and (eff1 == 0).sum() == round(0.2 * 256)
+    r2 = workloads.routing_for(2)
+    lens = np.diff(r2.cu_seqlens)
+    assert r2.num_tokens == 8192 and lens.size == 16 and lens.min() >= 1
+    r3 = workloads.routing_for(3)
+    assert r3.num_tokens == 4096 and r3.act_offsets is None and r3.req_ids.max() <= 48
+    r4 = workloads.routing_for(4)
+    assert r4.num_tokens == 48 + 16 * 256
+    r0 = workloads.routing_for(0)
+    assert r0.num_tokens == 512
+
+
+def test_workload_module_on_cpu():
+    spec = workloads.ModuleSpec("t", 64, (32, 32), [8, 16], 16)
+    md = workloads.make_module(spec, 10, 2, torch.float32, "cpu", seed=3)
+    assert md.x.shape == (10, 64) and md.y.shape == (10, 64)
+    # rows past the true rank are zero (stored padded to max_r)
+    assert torch.all(md.lora_A_slices[0][0, 0, 8:] == 0) and torch.all(md.lora_B_slices[1][0, 0, :, 8:] == 0)
+    # B is pre-scaled by alpha/r: std ~ 0.02 * 16/r
+    assert md.lora_B_slices[0][1, 0].std().item() < 0.05
