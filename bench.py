@@ -113,8 +113,8 @@ def main():
     cu_d = torch.tensor(routing.cu_seqlens, device=dev)
     off_d = None if routing.act_offsets is None else torch.tensor(routing.act_offsets, device=dev)
     segs = switched.build_segments(ids_d, NA, pos_d, cu_d, off_d)
-    zw = max(len(s.output_slices) * pk.max_rank for (_, pk), s in zip(sets[0][:len(specs)], specs))
-    z = torch.empty(max(T, 1), zw, dtype=dtype, device=dev)
+    zbuf = [torch.empty(max(T, 1), len(s.output_slices) * sets[0][k][1].max_rank, dtype=dtype, device=dev)
+            for k, s in enumerate(specs)]
     ws_need = max(int(_lib.load().gs_shrink_workspace_bytes(T, s.hidden, len(s.output_slices), NA, sets[0][k][1].max_rank))
                   for k, s in enumerate(specs))
     switched.reserve_workspace(dev, ws_need)
@@ -122,17 +122,19 @@ def main():
     def build():
         switched.build_segments(ids_d, NA, pos_d, cu_d, off_d, out=segs)
 
-    def shrink(md, pk):
-        switched.shrink(md.x, segs, pk, z[:, : pk.num_slices * pk.max_rank])
+    def pair(k, md, pk):
+        switched.switched_lora_(md.y, md.x, segs, pk, zbuf[k])
 
-    def expand(md, pk):
-        switched.expand_add_(md.y, z[:, : pk.num_slices * pk.max_rank], segs, pk)
+    def shrink(k, md, pk):
+        switched.shrink(md.x, segs, pk, zbuf[k])
+
+    def expand(k, md, pk):
+        switched.expand_add_(md.y, zbuf[k], segs, pk)
 
     def step(i):
         build()
-        for md, pk in sets[i % nsets]:
-            shrink(md, pk)
-            expand(md, pk)
+        for j, (md, pk) in enumerate(sets[i % nsets]):
+            pair(j % len(specs), md, pk)
 
     # -- warm-up, capture, timed replay ---------------------------------------
     for i in range(W):
@@ -184,24 +186,33 @@ def main():
     nseq = len(routing.cu_seqlens) - 1
     per_kernel_bytes["build_segments"] = T * (8 + 8 + 4) + 4 * t_act + 12 * nseq + 4 * (NA + 1)
 
-    # -- per-kernel timing (graphs of K launches of one kernel) --------------
+    # -- per-kernel timing (graphs of n launches of one kernel) -------------
+    # switched_lora = the shrink and expand kernels of one projection (the
+    # production pair); shrink alone also runs the split-K reduce when the
+    # hidden dimension is split; expand alone reads a materialised z.
     kern_us = {}
     kern_launches = {"build_segments": 1}
     g_b = capture(lambda: [build() for _ in range(K)])
     kern_us["build_segments"] = timed(g_b, K) * 1e3
+    ks_split = {}
     for k, spec in enumerate(specs):
         mods = [sets[i][layer * len(specs) + k] for i in range(nsets) for layer in range(layers)]
         n = max(K, len(mods)) if cfg != 4 else len(mods)
-        g_s = capture(lambda: [shrink(*mods[j % len(mods)]) for j in range(n)])
-        kern_us[f"shrink:{spec.name}"] = timed(g_s, n) * 1e3
-        g_e = capture(lambda: [expand(*mods[j % len(mods)]) for j in range(n)])
-        kern_us[f"expand:{spec.name}"] = timed(g_e, n) * 1e3
-        kern_launches[f"shrink:{spec.name}"] = layers
-        kern_launches[f"expand:{spec.name}"] = layers
-        del g_s, g_e
+        for kind, fn in (("switched_lora", pair), ("shrink", shrink), ("expand", expand)):
+            g_k = capture(lambda: [fn(k, *mods[j % len(mods)]) for j in range(n)])
+            kern_us[f"{kind}:{spec.name}"] = timed(g_k, n) * 1e3
+            kern_launches[f"{kind}:{spec.name}"] = layers
+            del g_k
+        pk0 = sets[0][k][1]
+        ks_split[spec.name] = int(_lib.load().gs_shrink_workspace_bytes(T, spec.hidden, len(spec.output_slices), NA,
+                                                                          pk0.max_rank)) > 256
+        per_kernel_bytes[f"switched_lora:{spec.name}"] = (per_kernel_bytes[f"shrink:{spec.name}"]
+                                                          + per_kernel_bytes[f"expand:{spec.name}"])
     for name, us in kern_us.items():
         log(f"kernel {name}: {us:.2f} us/launch, {per_kernel_bytes[name] / us / 1e3:.0f} GB/s algorithmic")
-    dom = max(kern_us, key=lambda n: kern_us[n] * kern_launches[n])
+    singles = [n for n in kern_us if n.startswith("expand:") or n == "build_segments"
+               or (n.startswith("shrink:") and not ks_split[n.split(":", 1)[1]])]
+    dom = max(singles, key=lambda n: kern_us[n] * kern_launches[n])
     dom_gbs = per_kernel_bytes[dom] / (kern_us[dom] * 1e-6) / 1e9
 
     # -- CPU baseline -----------------------------------------------------------

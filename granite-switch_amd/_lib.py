@@ -39,7 +39,6 @@ SIGNATURES = {
     "gs_route_latest_wins": (c_i32, [c_void_p, c_void_p, c_i64, c_i32, c_void_p, c_i32, c_i32, c_void_p, c_void_p,
                                      c_void_p]),
     "gs_shrink_workspace_bytes": (c_i64, [c_i64, c_i32, c_i32, c_i32, c_i32]),
-    "gs_shrink_counter_bytes": (c_i64, [c_i64, c_i32, c_i32, c_i32]),
     "gs_shrink": (c_i32, [c_i32, c_void_p, c_i64, c_i64, c_i32, c_void_p, c_void_p, c_void_p, c_i32, c_i32, c_i32,
                           c_void_p, c_void_p, c_void_p, c_i64, c_void_p, c_i64, c_void_p]),
     "gs_expand_add": (c_i32, [c_i32, c_void_p, c_i64, c_i64, c_i32, c_void_p, c_i32, c_void_p, c_i64, c_i32, c_void_p,

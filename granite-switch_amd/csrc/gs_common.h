@@ -74,6 +74,16 @@ __device__ __forceinline__ f32x16 mfma32_f32(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also
+// orders global memory, which on gfx9 waits for every outstanding global load
+// and store of the wave -- including prefetches meant to stay in flight across
+// the barrier.  Use this one where the barrier protects LDS data only.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Row of the 32x32 MFMA accumulator element v (0..15) held by lane l; the
 // column is l % 32.
 __device__ __forceinline__ int mfma32_row(int v, int l) { return ((v >> 2) << 3) + ((l >> 5) << 2) + (v & 3); }
@@ -88,22 +98,27 @@ struct TileRef {
   int g;        // global adapter id (0 = no tile: the workgroup exits)
   int slot0;    // first slot of the tile
   int nrows;    // rows in the tile (1..TM)
+  int rank;     // the adapter's rank in this module
+  int64_t off;  // offs[g] (the adapter's weight offset), fetched in the same pass
 };
 
 template <int TM>
 __device__ __forceinline__ TileRef find_tile(const int32_t* __restrict__ seg, const int32_t* __restrict__ ranks,
-                                             int num_adapters, int tile_id) {
-  TileRef ref{0, 0, 0};
+                                             const int64_t* __restrict__ offs, int num_adapters, int tile_id) {
+  TileRef ref{0, 0, 0, 0, 0};
   const int l = __lane_id();
   int carry = 0;
   for (int g0 = 1; g0 <= num_adapters; g0 += 64) {
     const int g = g0 + l;
     int ntiles = 0;
-    int lo = 0, hi = 0;
+    int lo = 0, hi = 0, rk = 0;
+    int64_t of = 0;
     if (g <= num_adapters) {
       lo = seg[g - 1];
       hi = seg[g];
-      ntiles = (ranks[g] > 0) ? (hi - lo + TM - 1) / TM : 0;
+      rk = ranks[g];
+      of = offs[g];
+      ntiles = (rk > 0) ? (hi - lo + TM - 1) / TM : 0;
     }
     // inclusive scan over the wave
     int incl = ntiles;
@@ -124,6 +139,8 @@ __device__ __forceinline__ TileRef find_tile(const int32_t* __restrict__ seg, co
       ref.g = g0 + src;
       ref.slot0 = slo + jj * TM;
       ref.nrows = min(TM, shi - ref.slot0);
+      ref.rank = __shfl(rk, src, 64);
+      ref.off = __shfl(of, src, 64);
       return ref;
     }
     carry += total;

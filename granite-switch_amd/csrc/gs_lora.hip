@@ -4,6 +4,13 @@
 // owns a tile of up to 32 consecutive slots of ONE adapter, so every MFMA is a
 // dense product with one adapter's weights -- no per-row adapter masks and no
 // repeated passes over the adapters present in a tile.
+//
+// No workgroup ever waits for or reads data produced by another workgroup of
+// the same launch.  When the shrink splits the hidden dimension over several
+// workgroups (split-K, needed to spread a decode-sized A over all CUs) it
+// writes fp32 partial sums; the consumer -- the expand kernel, or a small
+// reduce kernel when z itself is asked for -- adds the partials in a fixed
+// order, so results are deterministic and need no cross-XCD fences.
 #include "gs_common.h"
 
 namespace gs {
@@ -36,17 +43,32 @@ struct Elt<false> {
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ u32x4 sel16(bool keep, const u32x4& v) {
+  return keep ? v : u32x4{0u, 0u, 0u, 0u};
+}
 
-// 4 pieces of 16 bytes starting at element k of a row, zero where piece start >= kend.
+// Straight-line loads.  Every load below is issued unconditionally from a
+// clamped, in-bounds address and masked afterwards with a select: with no
+// branches around memory instructions the compiler can count the loads in
+// flight, so a prefetch really overlaps the work on the previous batch
+// instead of being drained by a conservative wait.
+
+// The 4 pieces of 16 bytes a lane loads from a row for the batch starting at
+// element kb: piece p covers elements kb + (2p + h)*P .. +P, so the two lane
+// halves of a row read adjacent pieces (32 contiguous bytes per row and
+// access).  Pieces at or past kend (or all, when !valid) read element kclamp
+// instead and become zero.  The MFMA pairs x and A elements by (piece, lane
+// half, element), the same for both operands, so any fixed mapping of k is a
+// correct contraction.
 template <bool BF16>
-__device__ __forceinline__ void load_row4(const void* row, int64_t k, int64_t kend, bool valid, u32x4 out[4]) {
+__device__ __forceinline__ void load_row4(const char* row, int64_t kb, int h, int64_t kend, int64_t kclamp, bool valid,
+                                          u32x4 out[4]) {
   constexpr int P = Elt<BF16>::kPerPiece;
-  const char* base = static_cast<const char*>(row);
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    const int64_t kp = k + p * P;
-    if (valid && kp < kend) out[p] = ld16(base + kp * Elt<BF16>::kSize);
-    else out[p] = u32x4{0u, 0u, 0u, 0u};
+    const int64_t kp = kb + (2 * p + h) * P;
+    const bool ok = valid && kp < kend;
+    out[p] = sel16(ok, ld16(row + (ok ? kp : kclamp) * Elt<BF16>::kSize));
   }
 }
 
@@ -59,27 +81,29 @@ __device__ __forceinline__ f32x16 mfma_batch(const u32x4 xa[4], const u32x4 wb[4
   } else {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const float* a = reinterpret_cast<const float*>(&xa[t]);
-      const float* b = reinterpret_cast<const float*>(&wb[t]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc = mfma32_f32(a[e], b[e], acc);
+      const f32x4 a = __builtin_bit_cast(f32x4, xa[t]);
+      const f32x4 b = __builtin_bit_cast(f32x4, wb[t]);
+      acc = mfma32_f32(a.x, b.x, acc);
+      acc = mfma32_f32(a.y, b.y, acc);
+      acc = mfma32_f32(a.z, b.z, acc);
+      acc = mfma32_f32(a.w, b.w, acc);
     }
   }
   return acc;
 }
 
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+}
+
 // ----------------------------------------------------------------------------
-// Shrink.  Grid (max_tiles, n_chunks, KS).  A workgroup computes the partial
-// product of one tile (32 slots) x 128 output columns (4 n-blocks of 32) over
-// the k-chunk [ks*KC, ks*KC+KC); its 4 waves split that chunk in 4 and are
-// reduced through LDS in a fixed order.  With KS > 1 the partial tile goes to
-// the workspace; the last workgroup of the tile (a self-resetting counter
-// decides) sums the KS partials in ks order and writes z, so the result does
-// not depend on scheduling.
+// Shrink.  Grid (max_tiles, n_chunks, KS).  A workgroup computes one tile
+// (32 slots) x NB n-blocks of 32 output columns over the k-chunk
+// [ks*KC, ks*KC+KC); its 4 waves split that chunk in 4, stream it in
+// double-buffered batches, and are reduced through LDS in a fixed order.
+// KS == 1 writes z in the element type; KS > 1 writes the fp32 partial of
+// chunk ks to part[ks][slot][col].
 // ----------------------------------------------------------------------------
-constexpr int kShrinkNB = 4;
-constexpr int kShrinkCols = 32 * kShrinkNB;            // 128
-constexpr int kTileFloats = kTM * kShrinkCols;         // 4096
 constexpr int kOutPad = 4;
 
 struct ShrinkParams {
@@ -93,13 +117,13 @@ struct ShrinkParams {
   int NA;
   const int32_t* seg;
   const int32_t* perm;
-  void* z;
+  void* z;                // KS == 1
   int64_t ldz;
-  float* part;
-  int* counters;
+  float* part;            // KS > 1: [KS][T][zw]
+  int64_t part_stride;    // T * zw
+  int zw;
   int KS;
   int KC;
-  int n_chunks;
 };
 
 template <bool BF16>
@@ -110,12 +134,9 @@ __device__ __forceinline__ void store_z16(void* z, int64_t ldz, int slot, int co
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       if (col + half * 8 < ncols) {
-        uint32_t w[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          w[e] = static_cast<uint32_t>(f32_to_bf16_bits(v[half * 8 + 2 * e])) |
-                 (static_cast<uint32_t>(f32_to_bf16_bits(v[half * 8 + 2 * e + 1])) << 16);
-        st16(zr + half * 8, u32x4{w[0], w[1], w[2], w[3]});
+        const float* w = v + half * 8;
+        st16(zr + half * 8, u32x4{pack_bf16x2(w[0], w[1]), pack_bf16x2(w[2], w[3]), pack_bf16x2(w[4], w[5]),
+                                  pack_bf16x2(w[6], w[7])});
       }
     }
   } else {
@@ -127,17 +148,17 @@ __device__ __forceinline__ void store_z16(void* z, int64_t ldz, int slot, int co
   }
 }
 
-template <bool BF16>
+template <bool BF16, int NB>
 __global__ __launch_bounds__(kThreads) void shrink_kernel(ShrinkParams p) {
-  __shared__ float red[2][kShrinkNB][16][64];           // 32 KB: cross-wave reduction
-  __shared__ int s_last;
-  float(*tile_s)[kShrinkCols + kOutPad] = reinterpret_cast<float(*)[kShrinkCols + kOutPad]>(&red[0][0][0][0]);
+  constexpr int COLS = 32 * NB;
+  __shared__ float red[2][NB][16][64];                 // cross-wave reduction
+  __shared__ float tile_s[kTM][COLS + kOutPad];        // row-major result
 
-  const TileRef tr = find_tile<kTM>(p.seg, p.ranks, p.NA, blockIdx.x);
+  const TileRef tr = find_tile<kTM>(p.seg, p.ranks, p.a_off, p.NA, blockIdx.x);
   if (tr.g == 0) return;
-  const int r = p.ranks[tr.g];
+  const int r = tr.rank;
   const int ncols = p.S * r;
-  const int col0 = blockIdx.y * kShrinkCols;
+  const int col0 = blockIdx.y * COLS;
   if (col0 >= ncols) return;
 
   const int tid = threadIdx.x;
@@ -145,138 +166,160 @@ __global__ __launch_bounds__(kThreads) void shrink_kernel(ShrinkParams p) {
   const int l = tid & 63;
   const int i = l & 31;
   const int h = l >> 5;
+  constexpr int B = Elt<BF16>::kBatch;
 
   const int64_t k_lo = static_cast<int64_t>(blockIdx.z) * p.KC;
   const int64_t k_hi = min(static_cast<int64_t>(p.H), k_lo + p.KC);
   const int wk = p.KC / 4;
   const int64_t wk_lo = k_lo + static_cast<int64_t>(wave) * wk;
   const int64_t wk_hi = min(k_hi, wk_lo + wk);
+  const int nbat = wk_hi > wk_lo ? static_cast<int>((wk_hi - wk_lo + B - 1) / B) : 0;
 
+  // rows: tokens of the tile (rows past the tile re-read its first token) and
+  // the adapter's A rows for this workgroup's columns (clamped likewise)
   const bool row_ok = i < tr.nrows;
-  const int token = row_ok ? p.perm[tr.slot0 + i] : 0;
+  const int token = p.perm[tr.slot0 + (row_ok ? i : 0)];
   const char* xrow = static_cast<const char*>(p.x) + (static_cast<int64_t>(token) * p.ldx) * Elt<BF16>::kSize;
-  const char* arow[kShrinkNB];
-  bool n_ok[kShrinkNB];
-  const int64_t a_base = p.a_off[tr.g];
+  const char* arow[NB];
+  bool n_ok[NB];
 #pragma unroll
-  for (int nb = 0; nb < kShrinkNB; ++nb) {
+  for (int nb = 0; nb < NB; ++nb) {
     const int n = col0 + 32 * nb + i;
     n_ok[nb] = n < ncols;
-    arow[nb] = static_cast<const char*>(p.a_pack) + (a_base + static_cast<int64_t>(n_ok[nb] ? n : 0) * p.H) * Elt<BF16>::kSize;
+    arow[nb] = static_cast<const char*>(p.a_pack) + (tr.off + static_cast<int64_t>(n_ok[nb] ? n : ncols - 1) * p.H) * Elt<BF16>::kSize;
   }
-  int nblk = (ncols - col0 + 31) / 32;
-  if (nblk > kShrinkNB) nblk = kShrinkNB;
 
-  f32x16 acc[kShrinkNB];
+  f32x16 acc[NB];
 #pragma unroll
-  for (int nb = 0; nb < kShrinkNB; ++nb) acc[nb] = f32x16{};
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x16{};
 
-  constexpr int B = Elt<BF16>::kBatch;
-  for (int64_t kb = wk_lo; kb < wk_hi; kb += B) {
-    const int64_t kk = kb + h * (B / 2);
-    u32x4 xv[4];
-    load_row4<BF16>(xrow, kk, wk_hi, row_ok, xv);
+  auto load = [&](int b, u32x4 (&xv)[4], u32x4 (&av)[NB][4]) {
+    const int64_t kb = wk_lo + static_cast<int64_t>(b) * B;
 #pragma unroll
-    for (int nb = 0; nb < kShrinkNB; ++nb) {
-      if (nb < nblk) {
-        u32x4 av[4];
-        load_row4<BF16>(arow[nb], kk, wk_hi, n_ok[nb], av);
-        acc[nb] = mfma_batch<BF16>(xv, av, acc[nb]);
+    for (int nb = 0; nb < NB; ++nb) load_row4<BF16>(arow[nb], kb, h, wk_hi, wk_lo, n_ok[nb], av[nb]);
+    load_row4<BF16>(xrow, kb, h, wk_hi, wk_lo, row_ok, xv);
+  };
+  if (nbat > 0) {
+    u32x4 xc[4], ac[NB][4];
+    load(0, xc, ac);
+    for (int b = 0; b + 1 < nbat; ++b) {
+      u32x4 xn[4], an[NB][4];
+      load(b + 1, xn, an);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma_batch<BF16>(xc, ac[nb], acc[nb]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        xc[q] = xn[q];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) ac[nb][q] = an[nb][q];
       }
     }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma_batch<BF16>(xc, ac[nb], acc[nb]);
   }
 
   // Fixed-order cross-wave reduction: (w0 + w2) + (w1 + w3).
   if (wave >= 2) {
 #pragma unroll
-    for (int nb = 0; nb < kShrinkNB; ++nb)
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) red[wave - 2][nb][v][l] = acc[nb][v];
   }
-  __syncthreads();
+  lds_barrier();
   if (wave < 2) {
 #pragma unroll
-    for (int nb = 0; nb < kShrinkNB; ++nb)
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[nb][v] += red[wave][nb][v][l];
   }
-  __syncthreads();
+  lds_barrier();
   if (wave == 1) {
 #pragma unroll
-    for (int nb = 0; nb < kShrinkNB; ++nb)
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) red[0][nb][v][l] = acc[nb][v];
   }
-  __syncthreads();
+  lds_barrier();
   if (wave == 0) {
 #pragma unroll
-    for (int nb = 0; nb < kShrinkNB; ++nb)
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[nb][v] += red[0][nb][v][l];
+      for (int v = 0; v < 16; ++v) tile_s[mfma32_row(v, l)][32 * nb + i] = acc[nb][v] + red[0][nb][v][l];
   }
-  __syncthreads();
-  // wave 0 scatters the MFMA layout into a row-major [32][128] tile
-  if (wave == 0) {
-#pragma unroll
-    for (int nb = 0; nb < kShrinkNB; ++nb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) tile_s[mfma32_row(v, l)][32 * nb + i] = acc[nb][v];
-  }
-  __syncthreads();
+  lds_barrier();
 
   // each thread owns 16 consecutive columns of one row
-  const int row = tid >> 3;
-  const int cx = (tid & 7) * 16;
-  float vals[16];
+  constexpr int TPR = COLS / 16;
+  for (int idx = tid; idx < kTM * TPR; idx += kThreads) {
+    const int row = idx / TPR;
+    const int cx = (idx % TPR) * 16;
+    if (row >= tr.nrows) continue;
+    float vals[16];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) vals[e] = tile_s[row][cx + e];
-
-  if (p.KS == 1) {
-    if (row < tr.nrows) store_z16<BF16>(p.z, p.ldz, tr.slot0 + row, col0 + cx, ncols, vals);
-    return;
-  }
-
-  const int64_t pair = static_cast<int64_t>(blockIdx.x) * p.n_chunks + blockIdx.y;
-  float* part_base = p.part + pair * p.KS * kTileFloats;
-  {
-    f32x4* dst = reinterpret_cast<f32x4*>(part_base + static_cast<int64_t>(blockIdx.z) * kTileFloats + tid * 16);
+    for (int e = 0; e < 16; ++e) vals[e] = tile_s[row][cx + e];
+    const int slot = tr.slot0 + row;
+    const int col = col0 + cx;
+    if (p.KS == 1) {
+      store_z16<BF16>(p.z, p.ldz, slot, col, ncols, vals);
+    } else {
+      float* dst = p.part + static_cast<int64_t>(blockIdx.z) * p.part_stride + static_cast<int64_t>(slot) * p.zw + col;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dst[q] = f32x4{vals[4 * q], vals[4 * q + 1], vals[4 * q + 2], vals[4 * q + 3]};
-  }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const int prev = atomicAdd(&p.counters[pair], 1);
-    s_last = (prev == p.KS - 1) ? 1 : 0;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  float sum[16];
-#pragma unroll
-  for (int e = 0; e < 16; ++e) sum[e] = 0.f;
-  for (int ks = 0; ks < p.KS; ++ks) {
-    const f32x4* src = reinterpret_cast<const f32x4*>(part_base + static_cast<int64_t>(ks) * kTileFloats + tid * 16);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f32x4 v = __builtin_nontemporal_load(src + q);
-      sum[4 * q] += v.x;
-      sum[4 * q + 1] += v.y;
-      sum[4 * q + 2] += v.z;
-      sum[4 * q + 3] += v.w;
+      for (int q = 0; q < 4; ++q)
+        if (col + 4 * q < ncols) *reinterpret_cast<f32x4*>(dst + 4 * q) = f32x4{vals[4 * q], vals[4 * q + 1], vals[4 * q + 2], vals[4 * q + 3]};
     }
   }
-  if (row < tr.nrows) store_z16<BF16>(p.z, p.ldz, tr.slot0 + row, col0 + cx, ncols, sum);
-  if (tid == 0) atomicExch(&p.counters[pair], 0);
+}
+
+// z[slot][col] = sum_ks part[ks][slot][col] (fixed order), for active slots.
+template <bool BF16>
+__global__ __launch_bounds__(kThreads) void reduce_parts_kernel(const float* __restrict__ part, int64_t part_stride,
+                                                               int KS, int zw, const int32_t* __restrict__ seg,
+                                                               int NA, void* z, int64_t ldz) {
+  const int64_t e8 = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * 8;   // 8 elements
+  const int64_t slot = e8 / zw;
+  const int col = static_cast<int>(e8 % zw);
+  if (slot >= seg[NA]) return;
+  // all partial loads in flight at once (KS <= 16), summed in ks order
+  f32x4 a[16], b[16];
+#pragma unroll
+  for (int ks = 0; ks < 16; ++ks) {
+    if (ks < KS) {
+      const f32x4* src = reinterpret_cast<const f32x4*>(part + ks * part_stride + slot * zw + col);
+      a[ks] = src[0];
+      b[ks] = src[1];
+    }
+  }
+  float s[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s[e] = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < 16; ++ks) {
+    if (ks < KS) {
+      s[0] += a[ks].x; s[1] += a[ks].y; s[2] += a[ks].z; s[3] += a[ks].w;
+      s[4] += b[ks].x; s[5] += b[ks].y; s[6] += b[ks].z; s[7] += b[ks].w;
+    }
+  }
+  if constexpr (BF16) {
+    uint16_t* zr = static_cast<uint16_t*>(z) + slot * ldz + col;
+    st16(zr, u32x4{pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3]), pack_bf16x2(s[4], s[5]), pack_bf16x2(s[6], s[7])});
+  } else {
+    float* zr = static_cast<float*>(z) + slot * ldz + col;
+    *reinterpret_cast<f32x4*>(zr) = f32x4{s[0], s[1], s[2], s[3]};
+    *reinterpret_cast<f32x4*>(zr + 4) = f32x4{s[4], s[5], s[6], s[7]};
+  }
 }
 
 // ----------------------------------------------------------------------------
-// Expand.  Grid (n_tiles, max_tiles).  A workgroup owns one tile (32 slots of
-// one adapter) x NT output columns; each wave computes NBW 32x32 blocks of the
-// delta with MFMA over the adapter's rank, the blocks go through LDS to a
-// row-major tile, and every thread read-modify-writes 16 consecutive y columns
-// of one token row (loaded before the MFMA work to hide the latency).  Only the
-// tile's token rows are touched.
+// Expand.  Grid (ceil(n_sub / ni), max_tiles).  A workgroup owns one tile (32
+// slots of one adapter) and walks ni consecutive column sub-tiles of NT
+// columns.  The tile's shrink values for every slice (z rows, or the sum of
+// the split-K partials rounded to the element type exactly like a
+// materialised z) are staged in LDS once.  Per sub-tile each wave computes NBW
+// 32x32 delta blocks with MFMA over the adapter's rank (all KSTEP k-groups of
+// B held in registers, PRE of them), the blocks go through LDS to a row-major
+// tile, and every thread read-modify-writes 16 consecutive y columns of one
+// token row.  The next sub-tile's B and y loads are issued before the current
+// one is computed.  Only the tile's token rows are written.
 // ----------------------------------------------------------------------------
 struct SliceInfo {
   int S;
@@ -288,174 +331,281 @@ struct ExpandParams {
   int64_t ldy;
   int out_total;
   SliceInfo si;
-  const void* z;
+  const void* z;          // nparts == 0
   int64_t ldz;
   int z_by_token;
   const int32_t* z_off;
+  const float* part;      // nparts > 0: [nparts][T][zw] fp32
+  int64_t part_stride;
+  int zw;
+  int nparts;
   const void* b_pack;
   const int64_t* b_off;
   const int32_t* ranks;
   int NA;
+  int max_rank;
+  int ni;                 // column sub-tiles per workgroup
   const int32_t* seg;
   const int32_t* perm;
 };
 
+// y piece (16 bytes = 8 bf16 / 4 fp32) + delta, rounded once, stored back.
 template <bool BF16>
-__device__ __forceinline__ void load_y16(const void* y, int64_t off, u32x4 out[4]) {
-  const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const char*>(y) + off * Elt<BF16>::kSize);
-  if constexpr (BF16) {
-    out[0] = __builtin_nontemporal_load(p);
-    out[1] = __builtin_nontemporal_load(p + 1);
-  } else {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) out[q] = __builtin_nontemporal_load(p + q);
-  }
-}
-
-template <bool BF16>
-__device__ __forceinline__ void add_store_y16(void* y, int64_t off, const u32x4 in[4], const float* d) {
+__device__ __forceinline__ void add_store_y(void* y, int64_t off, const u32x4& in, const float* d) {
   u32x4* p = reinterpret_cast<u32x4*>(static_cast<char*>(y) + off * Elt<BF16>::kSize);
   if constexpr (BF16) {
+    uint32_t o[4];
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const uint32_t* w = reinterpret_cast<const uint32_t*>(&in[half]);
-      uint32_t o[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float lo = bf16_bits_to_f32(static_cast<uint16_t>(w[e] & 0xffffu)) + d[half * 8 + 2 * e];
-        const float hi = bf16_bits_to_f32(static_cast<uint16_t>(w[e] >> 16)) + d[half * 8 + 2 * e + 1];
-        o[e] = static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
-      }
-      __builtin_nontemporal_store(u32x4{o[0], o[1], o[2], o[3]}, p + half);
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t w = in[e];
+      const float lo = bf16_bits_to_f32(static_cast<uint16_t>(w & 0xffffu)) + d[2 * e];
+      const float hi = bf16_bits_to_f32(static_cast<uint16_t>(w >> 16)) + d[2 * e + 1];
+      o[e] = pack_bf16x2(lo, hi);
     }
+    *p = u32x4{o[0], o[1], o[2], o[3]};
   } else {
+    const f32x4 f = __builtin_bit_cast(f32x4, in);
+    *p = __builtin_bit_cast(u32x4, f32x4{f.x + d[0], f.y + d[1], f.z + d[2], f.w + d[3]});
+  }
+}
+
+// Shrink values of the tile for all slices, 4 elements per item: item it
+// covers row it / (zwa/4) and columns c4 .. c4+3 of the row's S*r values
+// (slice c4 / r).  Split-K partials are loaded kPartGroup at a time and
+// summed in ks order; values are rounded to the element type when stored to
+// LDS, exactly as a materialised z would have been.
+constexpr int kPartGroup = 8;
+
+template <bool BF16>
+__device__ __forceinline__ void z_stage(const ExpandParams& p, const TileRef& tr, int r, int zo, char* zs, int zs_ld) {
+  const int zwa = p.si.S * r;                 // this adapter's shrink width
+  const int per_row = zwa >> 2;
+  const int items = kTM * per_row;
+  for (int it = threadIdx.x; it < items; it += kThreads) {
+    const int row = it / per_row;
+    const int c4 = (it - row * per_row) * 4;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (row < tr.nrows) {
+      const int slot = tr.slot0 + row;
+      if (p.nparts > 0) {
+        const float* src = p.part + static_cast<int64_t>(slot) * p.zw + c4;
+        for (int ks0 = 0; ks0 < p.nparts; ks0 += kPartGroup) {
+          f32x4 a[kPartGroup];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float* f = reinterpret_cast<const float*>(&in[q]);
-      const f32x4 o = f32x4{f[0] + d[4 * q], f[1] + d[4 * q + 1], f[2] + d[4 * q + 2], f[3] + d[4 * q + 3]};
-      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), p + q);
+          for (int u = 0; u < kPartGroup; ++u)
+            if (ks0 + u < p.nparts) a[u] = *reinterpret_cast<const f32x4*>(src + (ks0 + u) * p.part_stride);
+#pragma unroll
+          for (int u = 0; u < kPartGroup; ++u) {
+            if (ks0 + u < p.nparts) {
+              v[0] += a[u].x;
+              v[1] += a[u].y;
+              v[2] += a[u].z;
+              v[3] += a[u].w;
+            }
+          }
+        }
+      } else {
+        const int64_t zrow = p.z_by_token ? static_cast<int64_t>(p.perm[slot]) : static_cast<int64_t>(slot);
+        const char* zr = static_cast<const char*>(p.z) + (zrow * p.ldz + zo + c4) * Elt<BF16>::kSize;
+        if constexpr (BF16) {
+          const uint2 w = *reinterpret_cast<const uint2*>(zr);
+          v[0] = bf16_bits_to_f32(static_cast<uint16_t>(w.x & 0xffffu));
+          v[1] = bf16_bits_to_f32(static_cast<uint16_t>(w.x >> 16));
+          v[2] = bf16_bits_to_f32(static_cast<uint16_t>(w.y & 0xffffu));
+          v[3] = bf16_bits_to_f32(static_cast<uint16_t>(w.y >> 16));
+        } else {
+          const f32x4 a = *reinterpret_cast<const f32x4*>(zr);
+          v[0] = a.x;
+          v[1] = a.y;
+          v[2] = a.z;
+          v[3] = a.w;
+        }
+      }
+    }
+    char* dst = zs + (static_cast<int64_t>(row) * zs_ld + c4) * Elt<BF16>::kSize;
+    if constexpr (BF16) {
+      *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    } else {
+      *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
     }
   }
 }
 
-template <bool BF16, int NBW>
+template <bool BF16, int NBW, int PRE>
 __global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
-  constexpr int NT = 4 * NBW * 32;           // columns per workgroup
-  constexpr int TPR = NT / 16;               // threads per row in the RMW
-  constexpr int RPP = kThreads / TPR;        // rows per RMW pass
-  constexpr int PASSES = kTM / RPP;
+  constexpr int NT = 4 * NBW * 32;           // columns per sub-tile
+  // read-modify-write mapping: each lane owns one 16-byte piece per row it
+  // touches, consecutive lanes consecutive pieces, so every wave access
+  // covers whole row segments
+  constexpr int EPL = 16 / Elt<BF16>::kSize;  // elements per 16-byte piece
+  constexpr int LPR = NT / EPL;               // lanes per row
+  constexpr int RPI = kThreads / LPR;         // rows per workgroup-wide access
+  constexpr int PASSES = kTM / RPI;           // rows per thread
+  constexpr int KSTEP = BF16 ? 16 : 8;       // k per MFMA group (both lane halves)
+  constexpr int KHALF = KSTEP / 2;
   __shared__ float dtile[kTM][NT + kOutPad];
+  extern __shared__ __align__(16) char zs[];   // [32][S*max_rank + 8] element type
 
-  const TileRef tr = find_tile<kTM>(p.seg, p.ranks, p.NA, blockIdx.y);
+  const TileRef tr = find_tile<kTM>(p.seg, p.ranks, p.b_off, p.NA, blockIdx.y);
   if (tr.g == 0) return;
-  const int r = p.ranks[tr.g];
-  const int n_tile0 = blockIdx.x * NT;
-  if (n_tile0 >= p.out_total) return;
+  const int r = tr.rank;
+  const int n_sub = (p.out_total + NT - 1) / NT;
+  const int sub0 = blockIdx.x * p.ni;
+  if (sub0 >= n_sub) return;
+  const int nsub = min(p.ni, n_sub - sub0);
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int l = tid & 63;
   const int i = l & 31;
   const int h = l >> 5;
+  const int zs_ld = p.si.S * p.max_rank + 8;
+  const int zo = (p.z_off != nullptr) ? p.z_off[tr.g] : 0;
+  const int cx = (tid % LPR) * EPL;
+  const int nchunk = (r + PRE * KSTEP - 1) / (PRE * KSTEP);   // 1 unless the rank exceeds PRE k-groups
 
-  // 1. issue the y loads of this thread's RMW rows
-  u32x4 yv[PASSES][4];
-  int64_t yoff[PASSES];
-  bool yok[PASSES];
-  const int cx = (tid % TPR) * 16;
+  // token rows of this thread's read-modify-write (rows past the tile re-read
+  // the tile's first token; their stores are masked)
+  int64_t yrow[PASSES];
+  bool rok[PASSES];
 #pragma unroll
   for (int ps = 0; ps < PASSES; ++ps) {
-    const int row = ps * RPP + tid / TPR;
-    yok[ps] = row < tr.nrows && (n_tile0 + cx) < p.out_total;
-    const int tok = yok[ps] ? p.perm[tr.slot0 + row] : 0;
-    yoff[ps] = static_cast<int64_t>(tok) * p.ldy + n_tile0 + cx;
-    if (yok[ps]) load_y16<BF16>(p.y, yoff[ps], yv[ps]);
+    const int row = ps * RPI + tid / LPR;
+    rok[ps] = row < tr.nrows;
+    yrow[ps] = static_cast<int64_t>(p.perm[tr.slot0 + (rok[ps] ? row : 0)]) * p.ldy;
   }
 
-  // 2. delta blocks with MFMA
-  const bool row_ok = i < tr.nrows;
-  const int slot = tr.slot0 + (row_ok ? i : 0);
-  const int64_t zrow = p.z_by_token ? static_cast<int64_t>(p.perm[slot]) : static_cast<int64_t>(slot);
-  const int zo = (p.z_off != nullptr) ? p.z_off[tr.g] : 0;
-  const int64_t b_base = p.b_off[tr.g];
+  auto load_y = [&](int sub, u32x4 (&yv)[PASSES]) {
+    const int64_t col = min(static_cast<int64_t>(sub) * NT + cx, static_cast<int64_t>(p.out_total) - EPL);
 #pragma unroll
-  for (int q = 0; q < NBW; ++q) {
-    const int nbl = wave * NBW + q;
-    const int n0 = n_tile0 + 32 * nbl;
-    f32x16 acc = f32x16{};
-    if (n0 < p.out_total) {
+    for (int ps = 0; ps < PASSES; ++ps)
+      yv[ps] = ld16(static_cast<const char*>(p.y) + (yrow[ps] + col) * Elt<BF16>::kSize);
+  };
+  // B k-groups [kc*PRE, kc*PRE + PRE) of this wave's n-blocks in sub-tile sub
+  auto load_b = [&](int sub, int kc, u32x4 (&bp)[NBW][PRE]) {
+#pragma unroll
+    for (int q = 0; q < NBW; ++q) {
+      const int n = min(sub * NT + 32 * (wave * NBW + q) + i, p.out_total - 1);
+      const char* br = static_cast<const char*>(p.b_pack) + (tr.off + static_cast<int64_t>(n) * r) * Elt<BF16>::kSize;
+#pragma unroll
+      for (int st = 0; st < PRE; ++st) {
+        const int k0 = (kc * PRE + st) * KSTEP + KHALF * h;
+        const bool kin = k0 < r;
+        bp[q][st] = sel16(kin, ld16(br + (kin ? k0 : 0) * Elt<BF16>::kSize));
+      }
+    }
+  };
+
+  u32x4 yc[PASSES], bc[NBW][PRE];
+  load_b(sub0, 0, bc);
+  load_y(sub0, yc);
+  z_stage<BF16>(p, tr, r, zo, zs, zs_ld);
+  lds_barrier();
+
+  auto compute = [&](int sub, u32x4 (&bcur)[NBW][PRE], u32x4 (&ycur)[PASSES]) {
+    const int n_tile0 = sub * NT;
+    f32x16 acc[NBW];
+#pragma unroll
+    for (int q = 0; q < NBW; ++q) {
+      const int n0 = n_tile0 + 32 * (wave * NBW + q);
       int s = 0;
       while (s + 1 < p.si.S && n0 >= p.si.bounds[s + 1]) ++s;
-      const int n = n0 + i;
-      const char* zr = static_cast<const char*>(p.z) + (zrow * p.ldz + zo + s * r) * Elt<BF16>::kSize;
-      const char* br = static_cast<const char*>(p.b_pack) + (b_base + static_cast<int64_t>(n) * r) * Elt<BF16>::kSize;
-      // The k loops are uniform across the wave (MFMA is a whole-wave
-      // instruction); a lane half whose k range passed r feeds zeros.
-      if constexpr (BF16) {
-        for (int kb = 0; kb < r; kb += 16) {
-          const int k0 = kb + 8 * h;
-          const bool kin = k0 < r;
-          const u32x4 za = (row_ok && kin) ? ld16(zr + k0 * 2) : u32x4{0u, 0u, 0u, 0u};
-          const u32x4 bb = kin ? ld16(br + k0 * 2) : u32x4{0u, 0u, 0u, 0u};
-          acc = mfma32_bf16(za, bb, acc);
-        }
-      } else {
-        for (int kb = 0; kb < r; kb += 8) {
-          const int k0 = kb + 4 * h;
-          const bool kin = k0 < r;
-          f32x4 za = f32x4{0.f, 0.f, 0.f, 0.f}, bb = f32x4{0.f, 0.f, 0.f, 0.f};
-          if (kin) {
-            if (row_ok) za = *reinterpret_cast<const f32x4*>(zr + k0 * 4);
-            bb = *reinterpret_cast<const f32x4*>(br + k0 * 4);
+      const char* zrow_s = zs + (static_cast<int64_t>(i) * zs_ld + s * r) * Elt<BF16>::kSize;
+      acc[q] = f32x16{};
+      for (int kc = 0; kc < nchunk; ++kc) {
+        u32x4 bx[PRE];
+        if (kc == 0) {
+#pragma unroll
+          for (int st = 0; st < PRE; ++st) bx[st] = bcur[q][st];
+        } else {
+          // ranks above PRE k-groups: the later groups are loaded here
+          const int n = min(n0 + i, p.out_total - 1);
+          const char* br = static_cast<const char*>(p.b_pack) + (tr.off + static_cast<int64_t>(n) * r) * Elt<BF16>::kSize;
+#pragma unroll
+          for (int st = 0; st < PRE; ++st) {
+            const int k0 = (kc * PRE + st) * KSTEP + KHALF * h;
+            const bool kin = k0 < r;
+            bx[st] = sel16(kin, ld16(br + (kin ? k0 : 0) * Elt<BF16>::kSize));
           }
-          acc = mfma32_f32(za.x, bb.x, acc);
-          acc = mfma32_f32(za.y, bb.y, acc);
-          acc = mfma32_f32(za.z, bb.z, acc);
-          acc = mfma32_f32(za.w, bb.w, acc);
+        }
+#pragma unroll
+        for (int st = 0; st < PRE; ++st) {
+          const int k0 = (kc * PRE + st) * KSTEP + KHALF * h;
+          const bool kin = k0 < r;
+          const u32x4 za = sel16(kin, *reinterpret_cast<const u32x4*>(zrow_s + (kin ? k0 : 0) * Elt<BF16>::kSize));
+          if constexpr (BF16) {
+            acc[q] = mfma32_bf16(za, bx[st], acc[q]);
+          } else {
+            const f32x4 zf = __builtin_bit_cast(f32x4, za);
+            const f32x4 bf = __builtin_bit_cast(f32x4, bx[st]);
+            acc[q] = mfma32_f32(zf.x, bf.x, acc[q]);
+            acc[q] = mfma32_f32(zf.y, bf.y, acc[q]);
+            acc[q] = mfma32_f32(zf.z, bf.z, acc[q]);
+            acc[q] = mfma32_f32(zf.w, bf.w, acc[q]);
+          }
         }
       }
     }
 #pragma unroll
-    for (int v = 0; v < 16; ++v) dtile[mfma32_row(v, l)][32 * nbl + i] = acc[v];
-  }
-  __syncthreads();
+    for (int q = 0; q < NBW; ++q)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) dtile[mfma32_row(v, l)][32 * (wave * NBW + q) + i] = acc[q][v];
+    lds_barrier();
+    const int64_t col = static_cast<int64_t>(n_tile0) + cx;
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) {
+      const int row = ps * RPI + tid / LPR;
+      float d[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) d[e] = dtile[row][cx + e];
+      if (rok[ps] && col < p.out_total) add_store_y<BF16>(p.y, yrow[ps] + col, ycur[ps], d);
+    }
+    lds_barrier();                          // dtile is rewritten by the next sub-tile
+  };
 
-  // 3. read-modify-write y
+  for (int it = 0; it + 1 < nsub; ++it) {
+    u32x4 yn[PASSES], bn[NBW][PRE];
+    load_b(sub0 + it + 1, 0, bn);
+    load_y(sub0 + it + 1, yn);
+    compute(sub0 + it, bc, yc);
 #pragma unroll
-  for (int ps = 0; ps < PASSES; ++ps) {
-    if (!yok[ps]) continue;
-    const int row = ps * RPP + tid / TPR;
-    float d[16];
+    for (int ps = 0; ps < PASSES; ++ps) yc[ps] = yn[ps];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) d[e] = dtile[row][cx + e];
-    add_store_y16<BF16>(p.y, yoff[ps], yv[ps], d);
+    for (int q = 0; q < NBW; ++q)
+#pragma unroll
+      for (int st = 0; st < PRE; ++st) bc[q][st] = bn[q][st];
   }
+  compute(sub0 + nsub - 1, bc, yc);
 }
 
 // ----------------------------------------------------------------------------
-// Host-side planning (shared by the workspace query and the launch).
+// Host-side planning (shared by the workspace query and the launches).
 // ----------------------------------------------------------------------------
 struct ShrinkPlan {
-  int max_tiles, n_chunks, KS, KC;
-  int64_t counter_bytes, part_bytes;
+  int max_tiles, n_chunks, KS, KC, zw, NB;
+  int64_t part_bytes;
 };
 
 static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, bool bf16) {
   ShrinkPlan pl{};
   pl.max_tiles = max_tiles_for(T, NA);
-  pl.n_chunks = (S * max_rank + kShrinkCols - 1) / kShrinkCols;
+  pl.zw = S * max_rank;
+  const int nblk = (pl.zw + 31) / 32;         // 32-column blocks of the widest adapter
+  pl.NB = nblk >= 4 ? 4 : nblk;
+  pl.n_chunks = (pl.zw + 32 * pl.NB - 1) / (32 * pl.NB);
   const int unit = 4 * (bf16 ? Elt<true>::kBatch : Elt<false>::kBatch);   // k per workgroup step
   const int units = (H + unit - 1) / unit;
+  // aim for ~1024 workgroups; the tile count is an upper bound (T/32 + NA)
   const int64_t wgs = static_cast<int64_t>(pl.max_tiles) * pl.n_chunks;
   int ks = static_cast<int>((1024 + wgs - 1) / (wgs > 0 ? wgs : 1));
   if (ks < 1) ks = 1;
+  if (ks > 16) ks = 16;
   if (ks > units) ks = units;
   const int per = (units + ks - 1) / ks;
   pl.KC = per * unit;
   pl.KS = (H + pl.KC - 1) / pl.KC;
   if (pl.KS < 1) pl.KS = 1;
-  pl.counter_bytes = ((static_cast<int64_t>(pl.max_tiles) * pl.n_chunks * 4 + 255) / 256) * 256;
-  pl.part_bytes = pl.KS > 1 ? static_cast<int64_t>(pl.max_tiles) * pl.n_chunks * pl.KS * kTileFloats * 4 : 0;
+  pl.part_bytes = pl.KS > 1 ? static_cast<int64_t>(pl.KS) * T * pl.zw * 4 : 0;
   return pl;
 }
 
@@ -463,25 +613,16 @@ static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, boo
 
 using namespace gs;
 
-extern "C" {
+namespace {
 
-int64_t gs_shrink_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t num_slices, int32_t num_adapters,
-                                  int32_t max_rank) {
-  if (num_tokens <= 0 || hidden <= 0) return 256;
-  const ShrinkPlan pl = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, true);
-  const ShrinkPlan pf = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, false);
-  const int64_t a = pl.counter_bytes + pl.part_bytes, b = pf.counter_bytes + pf.part_bytes;
-  return a > b ? a : b;
+// LDS of the expand: the row-major delta tile plus the tile's shrink values.
+size_t expand_lds_bytes(bool bf16, int S, int max_rank) {
+  return static_cast<size_t>(kTM) * (static_cast<size_t>(S) * max_rank + 8) * (bf16 ? 2 : 4);
 }
+constexpr size_t kMaxDynLds = 120 * 1024;
 
-int64_t gs_shrink_counter_bytes(int64_t num_tokens, int32_t num_slices, int32_t num_adapters, int32_t max_rank) {
-  if (num_tokens <= 0) return 256;
-  const ShrinkPlan pl = plan_shrink(num_tokens, 256, num_slices, num_adapters, max_rank, true);
-  return pl.counter_bytes;
-}
-
-static int check_common(const char* who, int32_t dtype, int64_t T, int32_t num_slices, int32_t num_adapters,
-                        int32_t max_rank) {
+int check_common(const char* who, int32_t dtype, int64_t T, int32_t num_slices, int32_t num_adapters,
+                 int32_t max_rank) {
   GS_CHECK_ARG(dtype == GS_DTYPE_BF16 || dtype == GS_DTYPE_FP32, "%s: dtype=%d", who, dtype);
   GS_CHECK_ARG(T >= 0 && T < (int64_t(1) << 31), "%s: num_tokens out of range", who);
   GS_CHECK_ARG(num_slices >= 1 && num_slices <= GS_MAX_SLICES, "%s: num_slices=%d", who, num_slices);
@@ -491,28 +632,18 @@ static int check_common(const char* who, int32_t dtype, int64_t T, int32_t num_s
   return GS_OK;
 }
 
-int gs_shrink(int32_t dtype, const void* x, int64_t ldx, int64_t num_tokens, int32_t hidden, const void* a_pack,
-              const int64_t* a_off, const int32_t* ranks, int32_t num_slices, int32_t num_adapters,
-              int32_t max_rank, const int32_t* seg_offsets, const int32_t* perm, void* z, int64_t ldz,
-              void* workspace, int64_t workspace_bytes, void* stream) {
-  int rc = check_common("gs_shrink", dtype, num_tokens, num_slices, num_adapters, max_rank);
-  if (rc != GS_OK) return rc;
-  const bool bf16 = dtype == GS_DTYPE_BF16;
-  const int vec = bf16 ? 8 : 4;
+int check_shrink(int32_t dtype, const void* x, int64_t ldx, int32_t hidden, const void* a_pack) {
+  const int vec = dtype == GS_DTYPE_BF16 ? 8 : 4;
   GS_CHECK_ARG(hidden > 0 && hidden % 8 == 0, "gs_shrink: hidden=%d must be a positive multiple of 8", hidden);
   GS_CHECK_ARG(ldx >= hidden && ldx % vec == 0, "gs_shrink: ldx=%lld", (long long)ldx);
-  GS_CHECK_ARG(ldz >= int64_t(num_slices) * max_rank && ldz % vec == 0, "gs_shrink: ldz=%lld", (long long)ldz);
-  GS_CHECK_ARG(aligned16(x) && aligned16(a_pack) && aligned16(z), "gs_shrink: x, a_pack and z must be 16-byte aligned");
-  if (num_tokens == 0) return GS_OK;
-  const ShrinkPlan pl = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, bf16);
-  GS_CHECK_ARG(pl.max_tiles <= 65535 * 64, "gs_shrink: too many tiles");
-  if (pl.KS > 1) {
-    if (workspace == nullptr || workspace_bytes < pl.counter_bytes + pl.part_bytes || !aligned16(workspace)) {
-      set_error("gs_shrink: workspace of %lld bytes needed (got %lld)", (long long)(pl.counter_bytes + pl.part_bytes),
-                (long long)workspace_bytes);
-      return GS_ERR_WORKSPACE;
-    }
-  }
+  GS_CHECK_ARG(aligned16(x) && aligned16(a_pack), "gs_shrink: x and a_pack must be 16-byte aligned");
+  return GS_OK;
+}
+
+ShrinkParams make_shrink_params(const ShrinkPlan& pl, const void* x, int64_t ldx, int32_t hidden, const void* a_pack,
+                                const int64_t* a_off, const int32_t* ranks, int32_t S, int32_t NA,
+                                const int32_t* seg, const int32_t* perm, void* z, int64_t ldz, void* workspace,
+                                int64_t T) {
   ShrinkParams p{};
   p.x = x;
   p.ldx = ldx;
@@ -520,21 +651,157 @@ int gs_shrink(int32_t dtype, const void* x, int64_t ldx, int64_t num_tokens, int
   p.a_pack = a_pack;
   p.a_off = a_off;
   p.ranks = ranks;
-  p.S = num_slices;
-  p.NA = num_adapters;
-  p.seg = seg_offsets;
+  p.S = S;
+  p.NA = NA;
+  p.seg = seg;
   p.perm = perm;
   p.z = z;
   p.ldz = ldz;
-  p.counters = static_cast<int*>(workspace);
-  p.part = pl.KS > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + pl.counter_bytes) : nullptr;
+  p.part = pl.KS > 1 ? static_cast<float*>(workspace) : nullptr;
+  p.part_stride = T * pl.zw;
+  p.zw = pl.zw;
   p.KS = pl.KS;
   p.KC = pl.KC;
-  p.n_chunks = pl.n_chunks;
+  return p;
+}
+
+int check_workspace(const ShrinkPlan& pl, const void* workspace, int64_t workspace_bytes) {
+  if (pl.KS > 1 && (workspace == nullptr || workspace_bytes < pl.part_bytes || !aligned16(workspace))) {
+    set_error("gs_shrink: workspace of %lld bytes needed (got %lld)", (long long)pl.part_bytes,
+              (long long)workspace_bytes);
+    return GS_ERR_WORKSPACE;
+  }
+  return GS_OK;
+}
+
+template <bool BF16>
+void launch_shrink_t(const ShrinkPlan& pl, const ShrinkParams& p, hipStream_t st) {
   dim3 grid(pl.max_tiles, pl.n_chunks, pl.KS);
-  if (bf16) hipLaunchKernelGGL(shrink_kernel<true>, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), p);
-  else hipLaunchKernelGGL(shrink_kernel<false>, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), p);
+  if (pl.NB == 4) hipLaunchKernelGGL((shrink_kernel<BF16, 4>), grid, dim3(kThreads), 0, st, p);
+  else if (pl.NB == 3) hipLaunchKernelGGL((shrink_kernel<BF16, 3>), grid, dim3(kThreads), 0, st, p);
+  else if (pl.NB == 2) hipLaunchKernelGGL((shrink_kernel<BF16, 2>), grid, dim3(kThreads), 0, st, p);
+  else hipLaunchKernelGGL((shrink_kernel<BF16, 1>), grid, dim3(kThreads), 0, st, p);
+}
+
+void launch_shrink(bool bf16, const ShrinkPlan& pl, const ShrinkParams& p, hipStream_t st) {
+  if (bf16) launch_shrink_t<true>(pl, p, st);
+  else launch_shrink_t<false>(pl, p, st);
+}
+
+int prepare_expand(ExpandParams& p, const char* who, int32_t dtype, void* y, int64_t ldy, int64_t T,
+                   int32_t out_total, const int32_t* slice_bounds, int32_t num_slices, const void* b_pack,
+                   const int64_t* b_off, const int32_t* ranks, int32_t NA, int32_t max_rank, const int32_t* seg,
+                   const int32_t* perm) {
+  const int vec = dtype == GS_DTYPE_BF16 ? 8 : 4;
+  GS_CHECK_ARG(out_total > 0 && out_total % 32 == 0, "%s: out_total=%d must be a multiple of 32", who, out_total);
+  GS_CHECK_ARG(slice_bounds != nullptr, "%s: slice_bounds is NULL", who);
+  GS_CHECK_ARG(slice_bounds[0] == 0 && slice_bounds[num_slices] == out_total, "%s: slice_bounds must span [0,out_total]", who);
+  for (int s = 0; s < num_slices; ++s)
+    GS_CHECK_ARG(slice_bounds[s + 1] > slice_bounds[s] && (slice_bounds[s + 1] - slice_bounds[s]) % 32 == 0,
+                 "%s: slice %d width must be a positive multiple of 32", who, s);
+  GS_CHECK_ARG(ldy >= out_total && ldy % vec == 0, "%s: ldy=%lld", who, (long long)ldy);
+  GS_CHECK_ARG(aligned16(y) && aligned16(b_pack), "%s: y and b_pack must be 16-byte aligned", who);
+  GS_CHECK_ARG(max_tiles_for(T, NA) <= 65535, "%s: num_tokens too large for one launch", who);
+  GS_CHECK_ARG(expand_lds_bytes(dtype == GS_DTYPE_BF16, num_slices, max_rank) <= kMaxDynLds,
+               "%s: num_slices * max_rank = %d too large for the LDS-staged expand", who, num_slices * max_rank);
+  p.y = y;
+  p.ldy = ldy;
+  p.out_total = out_total;
+  p.si.S = num_slices;
+  for (int s = 0; s <= num_slices; ++s) p.si.bounds[s] = slice_bounds[s];
+  p.b_pack = b_pack;
+  p.b_off = b_off;
+  p.ranks = ranks;
+  p.NA = NA;
+  p.max_rank = max_rank;
+  p.seg = seg;
+  p.perm = perm;
+  return GS_OK;
+}
+
+template <bool BF16, int NBW, int PRE>
+void launch_expand_t(dim3 grid, size_t lds, const ExpandParams& p, hipStream_t st) {
+  auto kern = expand_kernel<BF16, NBW, PRE>;
+  if (lds > 64 * 1024) (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, st, p);
+}
+
+template <bool BF16, int NBW>
+void launch_expand_pre(dim3 grid, size_t lds, const ExpandParams& p, hipStream_t st) {
+  constexpr int KSTEP = BF16 ? 16 : 8;
+  const int need = (p.max_rank + KSTEP - 1) / KSTEP;
+  if (need <= 2) launch_expand_t<BF16, NBW, 2>(grid, lds, p, st);
+  else if (need <= 4) launch_expand_t<BF16, NBW, 4>(grid, lds, p, st);
+  else launch_expand_t<BF16, NBW, 8>(grid, lds, p, st);
+}
+
+void launch_expand(bool bf16, int64_t T, ExpandParams p, hipStream_t st) {
+  const int max_tiles = max_tiles_for(T, p.NA);
+  // wider column tiles halve the z / partial reads per output byte
+  const bool wide = T >= 2048 || p.nparts > 1;
+  const int NT = wide ? 256 : 128;
+  const int n_sub = (p.out_total + NT - 1) / NT;
+  // enough sub-tiles per workgroup that ~4096 workgroups cover the grid, and
+  // at least 2 (so the prefetch has something to overlap) once that still
+  // leaves over 1024 workgroups
+  int ni = static_cast<int>((static_cast<int64_t>(n_sub) * max_tiles + 4095) / 4096);
+  if (ni < 2 && static_cast<int64_t>(n_sub) * max_tiles >= 2 * 1024) ni = 2;
+  if (ni < 1) ni = 1;
+  if (ni > n_sub) ni = n_sub;
+  p.ni = ni;
+  dim3 grid((n_sub + ni - 1) / ni, max_tiles);
+  const size_t lds = expand_lds_bytes(bf16, p.si.S, p.max_rank);
+  if (bf16) {
+    if (wide) launch_expand_pre<true, 2>(grid, lds, p, st);
+    else launch_expand_pre<true, 1>(grid, lds, p, st);
+  } else {
+    if (wide) launch_expand_pre<false, 2>(grid, lds, p, st);
+    else launch_expand_pre<false, 1>(grid, lds, p, st);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t gs_shrink_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t num_slices, int32_t num_adapters,
+                                  int32_t max_rank) {
+  if (num_tokens <= 0 || hidden <= 0) return 256;
+  const ShrinkPlan pl = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, true);
+  const ShrinkPlan pf = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, false);
+  int64_t b = pl.part_bytes > pf.part_bytes ? pl.part_bytes : pf.part_bytes;
+  return b < 256 ? 256 : b;
+}
+
+int gs_shrink(int32_t dtype, const void* x, int64_t ldx, int64_t num_tokens, int32_t hidden, const void* a_pack,
+              const int64_t* a_off, const int32_t* ranks, int32_t num_slices, int32_t num_adapters,
+              int32_t max_rank, const int32_t* seg_offsets, const int32_t* perm, void* z, int64_t ldz,
+              void* workspace, int64_t workspace_bytes, void* stream) {
+  int rc = check_common("gs_shrink", dtype, num_tokens, num_slices, num_adapters, max_rank);
+  if (rc != GS_OK) return rc;
+  rc = check_shrink(dtype, x, ldx, hidden, a_pack);
+  if (rc != GS_OK) return rc;
+  const bool bf16 = dtype == GS_DTYPE_BF16;
+  GS_CHECK_ARG(ldz >= int64_t(num_slices) * max_rank && ldz % 8 == 0 && aligned16(z), "gs_shrink: ldz=%lld / z alignment",
+               (long long)ldz);
+  if (num_tokens == 0) return GS_OK;
+  const ShrinkPlan pl = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, bf16);
+  rc = check_workspace(pl, workspace, workspace_bytes);
+  if (rc != GS_OK) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const ShrinkParams p = make_shrink_params(pl, x, ldx, hidden, a_pack, a_off, ranks, num_slices, num_adapters,
+                                            seg_offsets, perm, z, ldz, workspace, num_tokens);
+  launch_shrink(bf16, pl, p, st);
   GS_CHECK_LAUNCH("gs_shrink");
+  if (pl.KS > 1) {
+    const int64_t n8 = (num_tokens * pl.zw) / 8;
+    const unsigned blocks = static_cast<unsigned>((n8 + kThreads - 1) / kThreads);
+    if (bf16) hipLaunchKernelGGL(reduce_parts_kernel<true>, dim3(blocks), dim3(kThreads), 0, st, p.part, p.part_stride,
+                                 pl.KS, pl.zw, seg_offsets, num_adapters, z, ldz);
+    else hipLaunchKernelGGL(reduce_parts_kernel<false>, dim3(blocks), dim3(kThreads), 0, st, p.part, p.part_stride,
+                            pl.KS, pl.zw, seg_offsets, num_adapters, z, ldz);
+    GS_CHECK_LAUNCH("gs_shrink (reduce)");
+  }
   return GS_OK;
 }
 
@@ -545,47 +812,18 @@ int gs_expand_add(int32_t dtype, void* y, int64_t ldy, int64_t num_tokens, int32
                   void* stream) {
   int rc = check_common("gs_expand_add", dtype, num_tokens, num_slices, num_adapters, max_rank);
   if (rc != GS_OK) return rc;
-  const bool bf16 = dtype == GS_DTYPE_BF16;
-  const int vec = bf16 ? 8 : 4;
-  GS_CHECK_ARG(out_total > 0 && out_total % 32 == 0, "gs_expand_add: out_total=%d must be a multiple of 32", out_total);
-  GS_CHECK_ARG(slice_bounds != nullptr, "gs_expand_add: slice_bounds is NULL");
-  GS_CHECK_ARG(slice_bounds[0] == 0 && slice_bounds[num_slices] == out_total, "gs_expand_add: slice_bounds must span [0,out_total]");
-  for (int s = 0; s < num_slices; ++s)
-    GS_CHECK_ARG(slice_bounds[s + 1] > slice_bounds[s] && (slice_bounds[s + 1] - slice_bounds[s]) % 32 == 0,
-                 "gs_expand_add: slice %d width must be a positive multiple of 32", s);
-  GS_CHECK_ARG(ldy >= out_total && ldy % vec == 0, "gs_expand_add: ldy=%lld", (long long)ldy);
-  GS_CHECK_ARG(ldz % vec == 0, "gs_expand_add: ldz=%lld", (long long)ldz);
-  GS_CHECK_ARG(aligned16(y) && aligned16(z) && aligned16(b_pack), "gs_expand_add: y, z and b_pack must be 16-byte aligned");
-  if (num_tokens == 0) return GS_OK;
   ExpandParams p{};
-  p.y = y;
-  p.ldy = ldy;
-  p.out_total = out_total;
-  p.si.S = num_slices;
-  for (int s = 0; s <= num_slices; ++s) p.si.bounds[s] = slice_bounds[s];
+  rc = prepare_expand(p, "gs_expand_add", dtype, y, ldy, num_tokens, out_total, slice_bounds, num_slices, b_pack, b_off,
+                      ranks, num_adapters, max_rank, seg_offsets, perm);
+  if (rc != GS_OK) return rc;
+  GS_CHECK_ARG(ldz % 8 == 0 && aligned16(z), "gs_expand_add: ldz=%lld / z alignment", (long long)ldz);
+  if (num_tokens == 0) return GS_OK;
   p.z = z;
   p.ldz = ldz;
   p.z_by_token = z_by_token;
   p.z_off = z_off;
-  p.b_pack = b_pack;
-  p.b_off = b_off;
-  p.ranks = ranks;
-  p.NA = num_adapters;
-  p.seg = seg_offsets;
-  p.perm = perm;
-  const int max_tiles = max_tiles_for(num_tokens, num_adapters);
-  GS_CHECK_ARG(max_tiles <= 65535, "gs_expand_add: num_tokens too large for one launch");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool wide = num_tokens >= 2048;
-  const int NT = wide ? 256 : 128;
-  dim3 grid((out_total + NT - 1) / NT, max_tiles);
-  if (bf16) {
-    if (wide) hipLaunchKernelGGL((expand_kernel<true, 2>), grid, dim3(kThreads), 0, st, p);
-    else hipLaunchKernelGGL((expand_kernel<true, 1>), grid, dim3(kThreads), 0, st, p);
-  } else {
-    if (wide) hipLaunchKernelGGL((expand_kernel<false, 2>), grid, dim3(kThreads), 0, st, p);
-    else hipLaunchKernelGGL((expand_kernel<false, 1>), grid, dim3(kThreads), 0, st, p);
-  }
+  p.nparts = 0;
+  launch_expand(dtype == GS_DTYPE_BF16, num_tokens, p, static_cast<hipStream_t>(stream));
   GS_CHECK_LAUNCH("gs_expand_add");
   return GS_OK;
 }
@@ -595,12 +833,37 @@ int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t
                      const void* a_pack, const int64_t* a_off, const void* b_pack, const int64_t* b_off,
                      const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* seg_offsets,
                      const int32_t* perm, void* z, void* workspace, int64_t workspace_bytes, void* stream) {
-  const int64_t ldz = static_cast<int64_t>(num_slices) * max_rank;
-  int rc = gs_shrink(dtype, x, ldx, num_tokens, hidden, a_pack, a_off, ranks, num_slices, num_adapters, max_rank,
-                     seg_offsets, perm, z, ldz, workspace, workspace_bytes, stream);
+  int rc = check_common("gs_switched_lora", dtype, num_tokens, num_slices, num_adapters, max_rank);
   if (rc != GS_OK) return rc;
-  return gs_expand_add(dtype, y, ldy, num_tokens, out_total, slice_bounds, num_slices, z, ldz, 0, nullptr, b_pack,
-                       b_off, ranks, num_adapters, max_rank, seg_offsets, perm, stream);
+  rc = check_shrink(dtype, x, ldx, hidden, a_pack);
+  if (rc != GS_OK) return rc;
+  ExpandParams ep{};
+  rc = prepare_expand(ep, "gs_switched_lora", dtype, y, ldy, num_tokens, out_total, slice_bounds, num_slices, b_pack,
+                      b_off, ranks, num_adapters, max_rank, seg_offsets, perm);
+  if (rc != GS_OK) return rc;
+  GS_CHECK_ARG(aligned16(z), "gs_switched_lora: z must be 16-byte aligned");
+  if (num_tokens == 0) return GS_OK;
+  const bool bf16 = dtype == GS_DTYPE_BF16;
+  const ShrinkPlan pl = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, bf16);
+  rc = check_workspace(pl, workspace, workspace_bytes);
+  if (rc != GS_OK) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t ldz = static_cast<int64_t>(num_slices) * max_rank;
+  const ShrinkParams sp = make_shrink_params(pl, x, ldx, hidden, a_pack, a_off, ranks, num_slices, num_adapters,
+                                             seg_offsets, perm, z, ldz, workspace, num_tokens);
+  launch_shrink(bf16, pl, sp, st);
+  GS_CHECK_LAUNCH("gs_switched_lora (shrink)");
+  ep.z = z;
+  ep.ldz = ldz;
+  ep.z_by_token = 0;
+  ep.z_off = nullptr;
+  ep.part = sp.part;
+  ep.part_stride = sp.part_stride;
+  ep.zw = sp.zw;
+  ep.nparts = pl.KS > 1 ? pl.KS : 0;
+  launch_expand(bf16, num_tokens, ep, st);
+  GS_CHECK_LAUNCH("gs_switched_lora (expand)");
+  return GS_OK;
 }
 
 }  // extern "C"

@@ -27,10 +27,12 @@ void set_error(const char* fmt, ...) {
 // ---------------------------------------------------------------------------
 constexpr int kBuildThreads = 1024;
 constexpr int kBuildWaves = kBuildThreads / 64;
+constexpr int kBuildRegChunks = 8;      // chunks of 1024 tokens whose ids stay in registers
+constexpr int kCuCap = 2048;            // sequences whose boundaries are staged in LDS
 
-__device__ __forceinline__ int find_seq(const int32_t* __restrict__ cu, int num_seqs, int t) {
-  // largest s with cu[s] <= t (cu is non-decreasing, cu[0] = 0)
-  int lo = 0, hi = num_seqs - 1;
+// largest s with cu[s] <= t (cu non-decreasing, cu[0] = 0), over n = num_seqs entries
+__device__ __forceinline__ int find_seq(const int32_t* cu, int n, int t) {
+  int lo = 0, hi = n - 1;
   while (lo < hi) {
     int mid = (lo + hi + 1) >> 1;
     if (cu[mid] <= t) lo = mid; else hi = mid - 1;
@@ -38,42 +40,78 @@ __device__ __forceinline__ int find_seq(const int32_t* __restrict__ cu, int num_
   return lo;
 }
 
-__global__ __launch_bounds__(kBuildThreads) void build_segments_kernel(
-    const int64_t* __restrict__ req, const int64_t* __restrict__ pos, const int32_t* __restrict__ cu,
-    const int64_t* __restrict__ act_off, int T, int num_seqs, int NA, int32_t* __restrict__ eff,
-    int32_t* __restrict__ seg, int32_t* __restrict__ perm) {
+struct BuildArgs {
+  const int64_t* req;
+  const int64_t* pos;
+  const int32_t* cu;
+  const int64_t* act_off;
+  int T;
+  int num_seqs;
+  int NA;
+  int32_t* eff;
+  int32_t* seg;
+  int32_t* perm;
+};
+
+__device__ __forceinline__ int effective_id(const BuildArgs& a, const int32_t* cu_lds, int t) {
+  int64_t id = a.req[t];
+  if (a.act_off != nullptr) {
+    int s = 0;
+    if (a.cu != nullptr) s = cu_lds != nullptr ? find_seq(cu_lds, a.num_seqs, t) : find_seq(a.cu, a.num_seqs, t);
+    const int64_t q = (a.pos != nullptr) ? a.pos[t]
+                                         : static_cast<int64_t>(t - (a.cu != nullptr ? (cu_lds ? cu_lds[s] : a.cu[s]) : 0));
+    if (q < a.act_off[s]) id = 0;
+  }
+  if (id < 0 || id > a.NA) id = 0;
+  return static_cast<int>(id);
+}
+
+__global__ __launch_bounds__(kBuildThreads) void build_segments_kernel(BuildArgs a) {
   __shared__ int hist[GS_MAX_ADAPTERS + 1];
   __shared__ int cursor[GS_MAX_ADAPTERS + 1];
   __shared__ int wcnt[kBuildWaves][GS_MAX_ADAPTERS + 1];
+  __shared__ int32_t cu_s[kCuCap];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
-  const int lane = tid & 63;
+  const int NA = a.NA;
+  const int T = a.T;
 
   for (int i = tid; i <= NA; i += kBuildThreads) {
     hist[i] = 0;
     for (int w = 0; w < kBuildWaves; ++w) wcnt[w][i] = 0;
   }
-  __syncthreads();
+  const bool cu_in_lds = a.cu != nullptr && a.act_off != nullptr && a.num_seqs <= kCuCap;
+  if (cu_in_lds)
+    for (int i = tid; i < a.num_seqs; i += kBuildThreads) cu_s[i] = a.cu[i];
+  lds_barrier();
+  const int32_t* cu_lds = cu_in_lds ? cu_s : nullptr;
 
-  // Pass 1: effective ids + histogram.
-  for (int t = tid; t < T; t += kBuildThreads) {
-    int64_t id = req[t];
-    if (act_off != nullptr) {
-      const int s = (cu != nullptr) ? find_seq(cu, num_seqs, t) : 0;
-      const int64_t q = (pos != nullptr) ? pos[t] : static_cast<int64_t>(t - (cu != nullptr ? cu[s] : 0));
-      if (q < act_off[s]) id = 0;
+  // Pass 1: effective ids + histogram; the first chunks keep their ids in registers.
+  int ereg[kBuildRegChunks];
+#pragma unroll
+  for (int c = 0; c < kBuildRegChunks; ++c) {
+    const int t = c * kBuildThreads + tid;
+    ereg[c] = 0;
+    if (t < T) {
+      const int id = effective_id(a, cu_lds, t);
+      ereg[c] = id;
+      a.eff[t] = id;
+      if (id > 0) atomicAdd(&hist[id], 1);
     }
-    if (id < 0 || id > NA) id = 0;
-    eff[t] = static_cast<int32_t>(id);
+  }
+  for (int t = kBuildRegChunks * kBuildThreads + tid; t < T; t += kBuildThreads) {
+    const int id = effective_id(a, cu_lds, t);
+    a.eff[t] = id;
     if (id > 0) atomicAdd(&hist[id], 1);
   }
-  __syncthreads();
+  lds_barrier();
 
   // Exclusive scan of hist[1..NA] by wave 0 -> cursor, seg.
   if (wave == 0) {
+    const int lane = tid & 63;
     int carry = 0;
-    if (lane == 0) seg[0] = 0;
+    if (lane == 0) a.seg[0] = 0;
     for (int g0 = 1; g0 <= NA; g0 += 64) {
       const int g = g0 + lane;
       const int v = (g <= NA) ? hist[g] : 0;
@@ -85,20 +123,28 @@ __global__ __launch_bounds__(kBuildThreads) void build_segments_kernel(
       }
       if (g <= NA) {
         cursor[g] = carry + incl - v;
-        seg[g] = carry + incl;
+        a.seg[g] = carry + incl;
       }
       carry += __shfl(incl, 63, 64);
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   int nbits = 0;
   while ((1 << nbits) <= NA) ++nbits;
 
-  // Pass 2: stable scatter, chunk by chunk.
-  for (int base = 0; base < T; base += kBuildThreads) {
-    const int t = base + tid;
-    const int id = (t < T) ? eff[t] : 0;  // written by this same thread in pass 1
+  // Pass 2: stable scatter, chunk by chunk in token order.
+  const int nchunks = (T + kBuildThreads - 1) / kBuildThreads;
+  for (int c = 0; c < nchunks; ++c) {
+    const int t = c * kBuildThreads + tid;
+    int id = 0;
+    if (c < kBuildRegChunks) {
+#pragma unroll
+      for (int u = 0; u < kBuildRegChunks; ++u)
+        if (u == c) id = ereg[u];
+    } else if (t < T) {
+      id = a.eff[t];    // written by this same thread in pass 1
+    }
     const bool active = id > 0;
     uint64_t match = __ballot(active);
     for (int b = 0; b < nbits; ++b) {
@@ -108,13 +154,13 @@ __global__ __launch_bounds__(kBuildThreads) void build_segments_kernel(
     }
     const uint64_t below = match & lanemask_lt();
     if (active && below == 0) wcnt[wave][id] = __popcll(match);
-    __syncthreads();
+    lds_barrier();
     if (active) {
-      int p = cursor[id] + __popcll(below);
-      for (int w = 0; w < wave; ++w) p += wcnt[w][id];
-      perm[p] = t;
+      int pp = cursor[id] + __popcll(below);
+      for (int w = 0; w < wave; ++w) pp += wcnt[w][id];
+      a.perm[pp] = t;
     }
-    __syncthreads();
+    lds_barrier();
     for (int g = tid + 1; g <= NA; g += kBuildThreads) {
       int add = 0;
       for (int w = 0; w < kBuildWaves; ++w) {
@@ -123,7 +169,7 @@ __global__ __launch_bounds__(kBuildThreads) void build_segments_kernel(
       }
       cursor[g] += add;
     }
-    __syncthreads();
+    lds_barrier();
   }
 }
 
@@ -144,7 +190,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_latest_wins_kernel(
   const int lane = tid & 63;
   const int wave = tid >> 6;
   for (int i = tid; i < num_control; i += kRouteThreads) ctl_s[i] = ctl[i];
-  __syncthreads();
+  lds_barrier();
   const int lo = (cu != nullptr) ? cu[s] : 0;
   const int hi = (cu != nullptr) ? cu[s + 1] : T;
   // carry: (index of last control token so far, its fired id); index -1 = none
@@ -178,7 +224,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_latest_wins_kernel(
       wave_max[wave] = sidx;
       wave_id[wave] = sid;
     }
-    __syncthreads();
+    lds_barrier();
     // combine with earlier waves of this chunk, then with the carry
     for (int w = 0; w < wave; ++w) {
       if (wave_max[w] > sidx) {
@@ -199,7 +245,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_latest_wins_kernel(
         cid = wave_id[w];
       }
     }
-    __syncthreads();
+    lds_barrier();
     carry_idx = cidx;
     carry_id = cid;
   }
@@ -270,9 +316,9 @@ int gs_build_segments(const int64_t* req_ids, const int64_t* positions, const in
   GS_CHECK_ARG(num_tokens == 0 || (req_ids && eff_ids && perm), "gs_build_segments: NULL token array");
   GS_CHECK_ARG(act_offsets == nullptr || cu_seqlens == nullptr || num_seqs >= 1,
                "gs_build_segments: num_seqs=%d with cu_seqlens", num_seqs);
-  hipLaunchKernelGGL(build_segments_kernel, dim3(1), dim3(kBuildThreads), 0, static_cast<hipStream_t>(stream),
-                     req_ids, positions, cu_seqlens, act_offsets, static_cast<int>(num_tokens),
-                     cu_seqlens ? num_seqs : 1, num_adapters, eff_ids, seg_offsets, perm);
+  BuildArgs a{req_ids, positions, cu_seqlens, act_offsets, static_cast<int>(num_tokens), cu_seqlens ? num_seqs : 1,
+              num_adapters, eff_ids, seg_offsets, perm};
+  hipLaunchKernelGGL(build_segments_kernel, dim3(1), dim3(kBuildThreads), 0, static_cast<hipStream_t>(stream), a);
   GS_CHECK_LAUNCH("gs_build_segments");
   return GS_OK;
 }

@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void xext_expand_kernel(XextArgs a, uint16_t* 
   }
 #pragma unroll
   for (int v = 0; v < 16; ++v) dtile[mfma32_row(v, l)][32 * wave + i] = acc[v];
-  __syncthreads();
+  lds_barrier();
 
   const int row = tid >> 3;
   const int cx = (tid & 7) * 16;
@@ -156,7 +156,7 @@ __global__ __launch_bounds__(256) void xext_swiglu_kernel(XextArgs a, uint16_t* 
       du[mfma32_row(v, l)][32 * wave + i] = au[v];
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   const int row = tid >> 3;
   const int cx = (tid & 7) * 16;

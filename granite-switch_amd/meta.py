@@ -50,7 +50,7 @@ class FusedLoRAKernelMeta(nn.Module):
     def __init__(self, device: torch.device):
         super().__init__()
         self.device = device
-        self._remap_tables_t = None
+        self.register_buffer("_remap_tables_t", None, persistent=False)
         self._module_cfg_keys = None
 
     def register_remap_tables(self, all_remap_tables: torch.Tensor, module_cfg_keys: list) -> None:
@@ -63,7 +63,7 @@ class FusedLoRAKernelMeta(nn.Module):
         assert all_remap_tables.max() <= 64, (
             f"int64 bitmask supports at most 64 kernel-local adapters per module, "
             f"got {all_remap_tables.max().item()}")
-        self.register_buffer("_remap_tables_t", all_remap_tables.T.contiguous(), persistent=False)
+        self._remap_tables_t = all_remap_tables.T.contiguous()
         self._module_cfg_keys = module_cfg_keys
 
     def prepare_and_store(self, adapter_indices: torch.Tensor, ctx: LoRAContext, positions=None, cu_seqlens=None,

@@ -280,18 +280,18 @@ class PackedAdapters:
 
 
 # ---------------------------------------------------------------------------
-# Workspace (split-K partials + self-resetting counters), cached per device
+# Workspace (split-K partial sums), cached per device
 # ---------------------------------------------------------------------------
 _workspaces: dict = {}
 
 
 def shrink_workspace(num_tokens: int, hidden: int, num_slices: int, num_adapters: int, max_rank: int,
                      device: torch.device) -> torch.Tensor:
-    """A zero-initialised workspace big enough for one shrink of this shape.
+    """A workspace big enough for the split-K partials of one shrink of this shape.
 
-    The counters inside are reset by the kernels themselves, so one buffer is
-    reused by every call on the device; calls on different streams that may
-    overlap in time must not share it.
+    One buffer per device is reused by every call (stream order keeps calls on
+    one stream apart); calls on different streams that may overlap in time
+    must not share it.
     """
     need = int(_lib.load().gs_shrink_workspace_bytes(num_tokens, hidden, num_slices, num_adapters, max_rank))
     key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
@@ -358,9 +358,36 @@ def expand_add_(y: torch.Tensor, z: torch.Tensor, segments: Segments, packed: Pa
 
 def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed: PackedAdapters,
                    z: torch.Tensor | None = None) -> torch.Tensor:
-    """In place: y += switched-LoRA delta of x (shrink then expand)."""
-    z = shrink(x, segments, packed, z)
-    return expand_add_(y, z, segments, packed)
+    """In place: y += switched-LoRA delta of x (shrink then expand, two launches).
+
+    ``z`` is optional scratch [T, S*max_rank] of y's dtype (allocated when
+    omitted); when the shrink is split over the hidden dimension the expand
+    reads the fp32 partials from the workspace and z is not written.
+    """
+    _require_cuda(x, y)
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    y2 = y.view(-1, y.shape[-1])
+    if y2.stride(-1) != 1:
+        raise ValueError("y must have unit column stride")
+    if x2.dtype != packed.dtype or y2.dtype != packed.dtype:
+        raise TypeError("x, y and the packed adapters must share a dtype")
+    T, H = x2.shape
+    if H != packed.hidden or T != segments.num_tokens or y2.shape != (T, packed.out_total):
+        raise ValueError("x / y shapes do not match the segments / adapters")
+    zw = packed.num_slices * packed.max_rank
+    if z is None:
+        z = torch.empty(max(T, 1), zw, dtype=x2.dtype, device=x2.device)
+    elif z.stride(-1) != 1 or z.shape[-1] < zw or (T and z.stride(0) != zw):
+        raise ValueError("z must be a contiguous [T, S*max_rank] buffer")
+    ws = shrink_workspace(T, H, packed.num_slices, packed.num_adapters, packed.max_rank, x2.device)
+    _lib.call("gs_switched_lora", _dtype_code(x2), x2.data_ptr(), x2.stride(0), y2.data_ptr(), y2.stride(0), T, H,
+              packed.out_total, _i32_array(packed.slice_bounds), packed.num_slices, packed.a_pack.data_ptr(),
+              packed.a_off.data_ptr(), packed.b_pack.data_ptr(), packed.b_off.data_ptr(), packed.ranks.data_ptr(),
+              packed.num_adapters, packed.max_rank, segments.seg_offsets.data_ptr(), segments.perm.data_ptr(),
+              z.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(x2.device))
+    return y
 
 
 def _i32_array(vals):

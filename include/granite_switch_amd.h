@@ -110,13 +110,14 @@ int gs_route_latest_wins(const int64_t* input_ids, const int32_t* cu_seqlens, in
  *       starts; every slice width must be a multiple of 32.
  * ---------------------------------------------------------------------- */
 
-/* Workspace for gs_shrink: split-K partial tiles plus self-resetting tile
- * counters.  The counter region (the first gs_shrink_counter_bytes bytes of
- * the workspace) must be zero before the first call; each call leaves it
- * zero again.  Calls that share one workspace must not overlap in time. */
+/* Workspace for gs_shrink / gs_switched_lora: fp32 split-K partial sums.
+ * The hidden dimension is split over several workgroups when there are too
+ * few tiles to fill the GPU; each writes its own partial and the consumer adds
+ * them in a fixed order (deterministic, no cross-workgroup synchronisation).
+ * No initialisation is needed.  Calls that share a workspace must not overlap
+ * in time (stream order is enough). */
 int64_t gs_shrink_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t num_slices, int32_t num_adapters,
                                   int32_t max_rank);
-int64_t gs_shrink_counter_bytes(int64_t num_tokens, int32_t num_slices, int32_t num_adapters, int32_t max_rank);
 
 /* z[slot, s*r_g + j] = sum_k x[perm[slot], k] * lora_A_{g,s}[j, k] for every
  * active slot (slot < seg_offsets[num_adapters]) whose adapter is applicable.
@@ -137,8 +138,10 @@ int gs_expand_add(int32_t dtype, void* y, int64_t ldy, int64_t num_tokens, int32
                   int32_t num_adapters, int32_t max_rank, const int32_t* seg_offsets, const int32_t* perm,
                   void* stream);
 
-/* gs_shrink followed by gs_expand_add (compact z): the whole switched-LoRA
- * delta fused into y.  z [T, S*max_rank] scratch of the same dtype. */
+/* The whole switched-LoRA delta added into y in two launches: the shrink,
+ * then the expand reading the shrink's output directly (split-K partials are
+ * summed while they are staged, so z is only written when the shrink is not
+ * split).  z [T, S*max_rank] scratch of the same dtype. */
 int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t num_tokens,
                      int32_t hidden, int32_t out_total, const int32_t* slice_bounds, int32_t num_slices,
                      const void* a_pack, const int64_t* a_off, const void* b_pack, const int64_t* b_off,

@@ -73,7 +73,7 @@ def test_workspace_plan_is_consistent():
     small = lib.gs_shrink_workspace_bytes(256, 4096, 3, 12, 32)
     big = lib.gs_shrink_workspace_bytes(8192, 4096, 2, 12, 32)
     assert small > 0 and big > 0
-    assert lib.gs_shrink_counter_bytes(256, 3, 12, 32) % 256 == 0
+    assert lib.gs_shrink_workspace_bytes(0, 4096, 3, 12, 32) == 256
 
 
 # -- host mirrors of the reference API ---------------------------------------
