@@ -76,6 +76,26 @@ def _na_array(na) -> ctypes.Array:
     return (ctypes.c_int32 * 6)(*[int(v) for v in na])
 
 
+def _check_tables(who, x_ext, lb_packed, slice_col_r, na, S, N) -> None:
+    """Shape checks the kernels rely on (host metadata only, no device sync).
+
+    x_ext must hold the base columns plus every tier's shrink columns, and
+    lb_packed every tier's [NA_r, N, r] block, in the layout finalize_weights
+    produces (src/granite_switch/vllm/core/lora.py:435-492).
+    """
+    if len(na) != 6:
+        raise ValueError(f"{who}: na must have 6 tier counts")
+    shrink_cols = sum(int(n) * int(S) * r for n, r in zip(na, SUPPORTED_RANKS))
+    if x_ext.dim() != 2 or x_ext.shape[1] < int(N) + shrink_cols:
+        raise ValueError(f"{who}: x_ext has {x_ext.shape[-1]} columns, needs N + shrink columns = "
+                         f"{int(N) + shrink_cols}")
+    lb_need = sum(int(n) * int(N) * r for n, r in zip(na, SUPPORTED_RANKS))
+    if lb_packed.numel() < lb_need:
+        raise ValueError(f"{who}: lb_packed holds {lb_packed.numel()} elements, needs {lb_need}")
+    if slice_col_r.numel() < int(S) * 6:
+        raise ValueError(f"{who}: slice_col_r must be [S, 6]")
+
+
 def switch_lora_expand(x_ext: torch.Tensor, adapter_indices: torch.Tensor, bitmask: torch.Tensor,
                        lb_packed: torch.Tensor, tile_slice: torch.Tensor, slice_col_r: torch.Tensor, na: tuple,
                        S: int, block_n: int, N: int) -> None:
@@ -94,6 +114,9 @@ def switch_lora_expand(x_ext: torch.Tensor, adapter_indices: torch.Tensor, bitma
     M = x_ext.shape[0]
     if adapter_indices.numel() < M or bitmask.numel() < (M + BLOCK_M - 1) // BLOCK_M:
         raise ValueError("switch_lora_expand: adapter_indices / bitmask shorter than x_ext's rows")
+    _check_tables("switch_lora_expand", x_ext, lb_packed, slice_col_r, na, S, N)
+    if tile_slice.numel() < (int(N) + int(block_n) - 1) // int(block_n):
+        raise ValueError("switch_lora_expand: tile_slice has fewer than ceil(N / block_n) entries")
     ids = adapter_indices if adapter_indices.stride(-1) == 1 else adapter_indices.contiguous()
     _lib.call("gs_switch_lora_expand", x_ext.data_ptr(), x_ext.stride(0), x_ext.stride(1), M, ids.data_ptr(),
               _idx_bytes(ids), bitmask.data_ptr(), bitmask.stride(0), lb_packed.data_ptr(),
@@ -114,6 +137,9 @@ def switch_lora_expand_swiglu(out: torch.Tensor, x_ext: torch.Tensor, adapter_in
     M = x_ext.shape[0]
     if out.shape[0] < M or out.shape[1] < H:
         raise ValueError("switch_lora_expand_swiglu: out is smaller than [M, H]")
+    if adapter_indices.numel() < M or bitmask.numel() < (M + BLOCK_M - 1) // BLOCK_M:
+        raise ValueError("switch_lora_expand_swiglu: adapter_indices / bitmask shorter than x_ext's rows")
+    _check_tables("switch_lora_expand_swiglu", x_ext, lb_packed, slice_col_r, na, S, N)
     ids = adapter_indices if adapter_indices.stride(-1) == 1 else adapter_indices.contiguous()
     _lib.call("gs_switch_lora_expand_swiglu", out.data_ptr(), out.stride(0), out.stride(1), x_ext.data_ptr(),
               x_ext.stride(0), x_ext.stride(1), M, ids.data_ptr(), _idx_bytes(ids), bitmask.data_ptr(),

@@ -326,9 +326,12 @@ def shrink(x: torch.Tensor, segments: Segments, packed: PackedAdapters, z: torch
     T, H = x2.shape
     if H != packed.hidden or T != segments.num_tokens:
         raise ValueError("x shape does not match the segments / adapters")
+    _check_segments(segments, packed)
     zw = packed.num_slices * packed.max_rank
     if z is None:
         z = torch.empty(max(T, 1), zw, dtype=x2.dtype, device=x2.device)
+    elif z.dtype != x2.dtype or z.stride(-1) != 1 or z.dim() != 2 or z.shape[0] < T or z.shape[1] < zw:
+        raise ValueError("z must be a [T, >= S*max_rank] buffer of x's dtype with unit column stride")
     ws = shrink_workspace(T, H, packed.num_slices, packed.num_adapters, packed.max_rank, x2.device)
     _lib.call("gs_shrink", _dtype_code(x2), x2.data_ptr(), x2.stride(0), T, H, packed.a_pack.data_ptr(),
               packed.a_off.data_ptr(), packed.ranks.data_ptr(), packed.num_slices, packed.num_adapters,
@@ -348,6 +351,10 @@ def expand_add_(y: torch.Tensor, z: torch.Tensor, segments: Segments, packed: Pa
     T, O = y2.shape
     if O != packed.out_total or T != segments.num_tokens:
         raise ValueError("y shape does not match the segments / adapters")
+    _check_segments(segments, packed)
+    zw = packed.num_slices * packed.max_rank
+    if z.dim() != 2 or z.stride(-1) != 1 or z.shape[0] < T or z.shape[1] < zw:
+        raise ValueError("z must be a [T, >= S*max_rank] buffer with unit column stride")
     bounds = _i32_array(packed.slice_bounds)
     _lib.call("gs_expand_add", _dtype_code(y2), y2.data_ptr(), y2.stride(0), T, O, bounds, packed.num_slices,
               z.data_ptr(), z.stride(0), 0, None, packed.b_pack.data_ptr(), packed.b_off.data_ptr(),
@@ -376,6 +383,7 @@ def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed:
     T, H = x2.shape
     if H != packed.hidden or T != segments.num_tokens or y2.shape != (T, packed.out_total):
         raise ValueError("x / y shapes do not match the segments / adapters")
+    _check_segments(segments, packed)
     zw = packed.num_slices * packed.max_rank
     if z is None:
         z = torch.empty(max(T, 1), zw, dtype=x2.dtype, device=x2.device)
@@ -388,6 +396,15 @@ def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed:
               packed.num_adapters, packed.max_rank, segments.seg_offsets.data_ptr(), segments.perm.data_ptr(),
               z.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(x2.device))
     return y
+
+
+def _check_segments(segments: Segments, packed: PackedAdapters) -> None:
+    """The kernels read seg_offsets[0..NA] and perm[0..T): both must match the pack."""
+    if segments.num_adapters != packed.num_adapters or segments.seg_offsets.numel() != packed.num_adapters + 1:
+        raise ValueError(f"segments were built for {segments.num_adapters} adapters, the pack holds "
+                         f"{packed.num_adapters}")
+    if segments.perm.numel() < segments.num_tokens:
+        raise ValueError("segments.perm is shorter than the token count")
 
 
 def _i32_array(vals):

@@ -269,8 +269,10 @@ class SwitchedLoRALinear(nn.Module):
         base_out = x_ext[:, :self._N_total]
         ctx = self._lora_ctx
         if ctx is not None and ctx.adapter_indices is not None and self._num_applicable > 0:
-            if getattr(ctx, "segments", None) is not None:
-                self._run_segment_expand(x_ext, ctx.segments)
+            segs = getattr(ctx, "segments", None)
+            if (segs is not None and segs.num_tokens == x.shape[0]
+                    and segs.num_adapters == self.num_adapters):
+                self._run_segment_expand(x_ext, segs)
             else:
                 M = x.shape[0]
                 self._run_expand(x_ext, ctx.remapped_indices[self._module_idx, :M], ctx)

@@ -221,7 +221,7 @@ def test_custom_ops_under_torch_compile(dev):
         return torch.ops.granite_switch.compute_per_module_bitmasks(a, r)
 
     eager = fn(ids, remap_t)
-    compiled = torch.compile(fn, fullgraph=True)(ids, remap_t)
+    compiled = torch.compile(fn, fullgraph=True, backend="aot_eager")(ids, remap_t)
     assert torch.equal(compiled, eager)
     assert np.array_equal(eager.cpu().numpy(), omap.compute_bitmasks(ids.cpu().numpy(), remap_t.cpu().numpy(), 32))
 
