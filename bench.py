@@ -117,13 +117,21 @@ def main():
             for k, s in enumerate(specs)]
     ws_need = max(int(_lib.load().gs_shrink_workspace_bytes(T, s.hidden, len(s.output_slices), NA, sets[0][k][1].max_rank))
                   for k, s in enumerate(specs))
+    nseq_r = len(routing.cu_seqlens) - 1
+    small = all(switched.small_eligible(sets[0][k][1], T, nseq_r) for k in range(len(specs))) and layers == 1
+    if small:
+        ws_need = max([ws_need] + [switched.small_workspace_bytes(sets[0][k][1], T) for k in range(len(specs))])
     switched.reserve_workspace(dev, ws_need)
+    log(f"path: {'small-batch (two launches, routing inside the kernels)' if small else 'segments'}")
 
     def build():
         switched.build_segments(ids_d, NA, pos_d, cu_d, off_d, out=segs)
 
     def pair(k, md, pk):
-        switched.switched_lora_(md.y, md.x, segs, pk, zbuf[k])
+        if small:
+            switched.switched_lora_routed_(md.y, md.x, ids_d, pk, pos_d, cu_d, off_d)
+        else:
+            switched.switched_lora_(md.y, md.x, segs, pk, zbuf[k], path="segments")
 
     def shrink(k, md, pk):
         switched.shrink(md.x, segs, pk, zbuf[k])
@@ -132,7 +140,8 @@ def main():
         switched.expand_add_(md.y, zbuf[k], segs, pk)
 
     def step(i):
-        build()
+        if not small:
+            build()
         for j, (md, pk) in enumerate(sets[i % nsets]):
             pair(j % len(specs), md, pk)
 

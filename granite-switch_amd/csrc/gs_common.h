@@ -88,6 +88,78 @@ __device__ __forceinline__ void lds_barrier() {
 // column is l % 32.
 __device__ __forceinline__ int mfma32_row(int v, int l) { return ((v >> 2) << 3) + ((l >> 5) << 2) + (v & 3); }
 
+// ----------------------------------------------------------------------------
+// Element traits.  A "batch" is the k-span one lane pair covers with four
+// 16-byte loads per row: 64 bf16 or 32 fp32 (each lane half loads 64 bytes).
+// ----------------------------------------------------------------------------
+template <bool BF16>
+struct Elt;
+template <>
+struct Elt<true> {
+  static constexpr int kBatch = 64;       // k per batch
+  static constexpr int kPerPiece = 8;     // elements per 16-byte piece
+  static constexpr int kSize = 2;
+};
+template <>
+struct Elt<false> {
+  static constexpr int kBatch = 32;
+  static constexpr int kPerPiece = 4;
+  static constexpr int kSize = 4;
+};
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ u32x4 sel16(bool keep, const u32x4& v) {
+  return keep ? v : u32x4{0u, 0u, 0u, 0u};
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+}
+
+// y piece (16 bytes = 8 bf16 / 4 fp32) + delta, rounded once, stored back.
+template <bool BF16>
+__device__ __forceinline__ void add_store_y(void* y, int64_t off, const u32x4& in, const float* d) {
+  u32x4* p = reinterpret_cast<u32x4*>(static_cast<char*>(y) + off * Elt<BF16>::kSize);
+  if constexpr (BF16) {
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t w = in[e];
+      const float lo = bf16_bits_to_f32(static_cast<uint16_t>(w & 0xffffu)) + d[2 * e];
+      const float hi = bf16_bits_to_f32(static_cast<uint16_t>(w >> 16)) + d[2 * e + 1];
+      o[e] = pack_bf16x2(lo, hi);
+    }
+    *p = u32x4{o[0], o[1], o[2], o[3]};
+  } else {
+    const f32x4 f = __builtin_bit_cast(f32x4, in);
+    *p = __builtin_bit_cast(u32x4, f32x4{f.x + d[0], f.y + d[1], f.z + d[2], f.w + d[3]});
+  }
+}
+
+// acc += one 16-byte piece of each operand (bf16: K=16 over both lane halves;
+// fp32: four K=2 steps).  Both operands pair their elements by (lane half,
+// element), so any fixed assignment of k to pieces is a correct contraction.
+template <bool BF16>
+__device__ __forceinline__ f32x16 mfma_piece(const u32x4& a, const u32x4& b, f32x16 acc) {
+  if constexpr (BF16) {
+    return mfma32_bf16(a, b, acc);
+  } else {
+    const f32x4 x = __builtin_bit_cast(f32x4, a);
+    const f32x4 w = __builtin_bit_cast(f32x4, b);
+    acc = mfma32_f32(x.x, w.x, acc);
+    acc = mfma32_f32(x.y, w.y, acc);
+    acc = mfma32_f32(x.z, w.z, acc);
+    return mfma32_f32(x.w, w.w, acc);
+  }
+}
+
+// Output slices of a projection: slice s covers columns [bounds[s], bounds[s+1]).
+struct SliceInfo {
+  int S;
+  int bounds[GS_MAX_SLICES + 1];
+};
+
 // ---------------------------------------------------------------------------
 // Segment work lists. Adapter g (1..NA) owns slots [seg[g-1], seg[g]) of the
 // adapter-sorted token permutation. A module skips adapters with rank 0 (not

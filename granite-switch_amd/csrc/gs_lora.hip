@@ -22,31 +22,6 @@ __host__ __device__ inline int max_tiles_for(int64_t T, int NA) {
   return static_cast<int>((T + kTM - 1) / kTM + (NA < T ? NA : T));
 }
 
-// ----------------------------------------------------------------------------
-// Element traits.  A "batch" is the k-span one lane pair covers with four
-// 16-byte loads per row: 64 bf16 or 32 fp32 (each lane half loads 64 bytes).
-// ----------------------------------------------------------------------------
-template <bool BF16>
-struct Elt;
-template <>
-struct Elt<true> {
-  static constexpr int kBatch = 64;       // k per batch
-  static constexpr int kPerPiece = 8;     // elements per 16-byte piece
-  static constexpr int kSize = 2;
-};
-template <>
-struct Elt<false> {
-  static constexpr int kBatch = 32;
-  static constexpr int kPerPiece = 4;
-  static constexpr int kSize = 4;
-};
-
-__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
-__device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
-__device__ __forceinline__ u32x4 sel16(bool keep, const u32x4& v) {
-  return keep ? v : u32x4{0u, 0u, 0u, 0u};
-}
-
 // Straight-line loads.  Every load below is issued unconditionally from a
 // clamped, in-bounds address and masked afterwards with a select: with no
 // branches around memory instructions the compiler can count the loads in
@@ -90,10 +65,6 @@ __device__ __forceinline__ f32x16 mfma_batch(const u32x4 xa[4], const u32x4 wb[4
     }
   }
   return acc;
-}
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
 }
 
 // ----------------------------------------------------------------------------
@@ -321,11 +292,6 @@ __global__ __launch_bounds__(kThreads) void reduce_parts_kernel(const float* __r
 // token row.  The next sub-tile's B and y loads are issued before the current
 // one is computed.  Only the tile's token rows are written.
 // ----------------------------------------------------------------------------
-struct SliceInfo {
-  int S;
-  int bounds[GS_MAX_SLICES + 1];
-};
-
 struct ExpandParams {
   void* y;
   int64_t ldy;
@@ -348,26 +314,6 @@ struct ExpandParams {
   const int32_t* seg;
   const int32_t* perm;
 };
-
-// y piece (16 bytes = 8 bf16 / 4 fp32) + delta, rounded once, stored back.
-template <bool BF16>
-__device__ __forceinline__ void add_store_y(void* y, int64_t off, const u32x4& in, const float* d) {
-  u32x4* p = reinterpret_cast<u32x4*>(static_cast<char*>(y) + off * Elt<BF16>::kSize);
-  if constexpr (BF16) {
-    uint32_t o[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t w = in[e];
-      const float lo = bf16_bits_to_f32(static_cast<uint16_t>(w & 0xffffu)) + d[2 * e];
-      const float hi = bf16_bits_to_f32(static_cast<uint16_t>(w >> 16)) + d[2 * e + 1];
-      o[e] = pack_bf16x2(lo, hi);
-    }
-    *p = u32x4{o[0], o[1], o[2], o[3]};
-  } else {
-    const f32x4 f = __builtin_bit_cast(f32x4, in);
-    *p = __builtin_bit_cast(u32x4, f32x4{f.x + d[0], f.y + d[1], f.z + d[2], f.w + d[3]});
-  }
-}
 
 // Shrink values of the tile for all slices, 4 elements per item: item it
 // covers row it / (zwa/4) and columns c4 .. c4+3 of the row's S*r values

@@ -176,6 +176,8 @@ class PackedAdapters:
     hidden: int
     num_adapters: int
     max_rank: int
+    a_off_host: list = None     # host copies of a_off / b_off (the small-batch path passes them by value)
+    b_off_host: list = None
 
     @property
     def num_slices(self) -> int:
@@ -276,6 +278,8 @@ class PackedAdapters:
             hidden=int(H),
             num_adapters=int(NA),
             max_rank=int(max_rank),
+            a_off_host=list(a_off),
+            b_off_host=list(b_off),
         )
 
 
@@ -283,6 +287,18 @@ class PackedAdapters:
 # Workspace (split-K partial sums), cached per device
 # ---------------------------------------------------------------------------
 _workspaces: dict = {}
+
+
+def _workspace(device: torch.device, need: int) -> torch.Tensor:
+    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < need:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("switched-LoRA workspace must be allocated before graph capture "
+                               "(call reserve_workspace)")
+        ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
 
 
 def shrink_workspace(num_tokens: int, hidden: int, num_slices: int, num_adapters: int, max_rank: int,
@@ -294,14 +310,28 @@ def shrink_workspace(num_tokens: int, hidden: int, num_slices: int, num_adapters
     must not share it.
     """
     need = int(_lib.load().gs_shrink_workspace_bytes(num_tokens, hidden, num_slices, num_adapters, max_rank))
-    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
-    ws = _workspaces.get(key)
-    if ws is None or ws.numel() < need:
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("shrink workspace must be allocated before graph capture (call reserve_workspace)")
-        ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=device)
-        _workspaces[key] = ws
-    return ws
+    return _workspace(device, need)
+
+
+def small_workspace_bytes(packed: "PackedAdapters", num_tokens: int) -> int:
+    """Workspace bytes of the small-batch path for this module and batch size."""
+    return int(_lib.load().gs_small_workspace_bytes(_DTYPES[packed.dtype], num_tokens, packed.hidden,
+                                                    packed.num_slices, packed.num_adapters, packed.max_rank,
+                                                    packed.out_total, _i32_array(packed.slice_bounds)))
+
+
+def small_eligible(packed: "PackedAdapters", num_tokens: int, num_seqs: int = 1) -> bool:
+    """True when the two-launch small-batch path handles this module and batch.
+
+    It needs the adapters' host-side offset tables (``PackedAdapters.from_slices``
+    keeps them) and decode-sized shapes: T <= 1024, <= 64 adapters, max rank
+    <= 64, slice widths multiples of 128.
+    """
+    if packed.a_off_host is None or packed.b_off_host is None or not packed.ranks_host:
+        return False
+    return bool(_lib.load().gs_small_eligible(int(num_tokens), int(num_seqs), packed.num_slices,
+                                              _i32_array(packed.slice_bounds), packed.num_adapters,
+                                              packed.max_rank))
 
 
 def reserve_workspace(device: torch.device, nbytes: int) -> None:
@@ -363,14 +393,7 @@ def expand_add_(y: torch.Tensor, z: torch.Tensor, segments: Segments, packed: Pa
     return y
 
 
-def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed: PackedAdapters,
-                   z: torch.Tensor | None = None) -> torch.Tensor:
-    """In place: y += switched-LoRA delta of x (shrink then expand, two launches).
-
-    ``z`` is optional scratch [T, S*max_rank] of y's dtype (allocated when
-    omitted); when the shrink is split over the hidden dimension the expand
-    reads the fp32 partials from the workspace and z is not written.
-    """
+def _xy2(x: torch.Tensor, y: torch.Tensor, packed: PackedAdapters):
     _require_cuda(x, y)
     x2 = x.reshape(-1, x.shape[-1])
     if x2.stride(-1) != 1:
@@ -380,10 +403,76 @@ def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed:
         raise ValueError("y must have unit column stride")
     if x2.dtype != packed.dtype or y2.dtype != packed.dtype:
         raise TypeError("x, y and the packed adapters must share a dtype")
+    if x2.shape[1] != packed.hidden or y2.shape != (x2.shape[0], packed.out_total):
+        raise ValueError("x / y shapes do not match the adapters")
+    return x2, y2
+
+
+def _call_small(x2, y2, packed, eff_ids=None, req=None, pos=None, cu=None, off=None, num_seqs=1):
+    T = x2.shape[0]
+    ws = _workspace(x2.device, small_workspace_bytes(packed, T))
+    i64 = lambda v: (ctypes.c_int64 * len(v))(*[int(u) for u in v])
+    _lib.call("gs_switched_lora_small", _dtype_code(x2), _lib.ptr(req), _lib.ptr(pos), _lib.ptr(cu), _lib.ptr(off),
+              int(num_seqs), _lib.ptr(eff_ids), x2.data_ptr(), x2.stride(0), y2.data_ptr(), y2.stride(0), T,
+              packed.hidden, packed.out_total, _i32_array(packed.slice_bounds), packed.num_slices,
+              packed.a_pack.data_ptr(), i64(packed.a_off_host), packed.b_pack.data_ptr(), i64(packed.b_off_host),
+              _i32_array(packed.ranks_host), packed.num_adapters, packed.max_rank, ws.data_ptr(), ws.numel(),
+              _lib.stream_ptr(x2.device))
+
+
+def switched_lora_routed_(y: torch.Tensor, x: torch.Tensor, adapter_ids: torch.Tensor, packed: PackedAdapters,
+                          positions=None, cu_seqlens=None, act_offsets=None) -> torch.Tensor:
+    """In place: y += switched-LoRA delta of x, routed straight from the per-token ids.
+
+    ``adapter_ids`` / ``positions`` / ``cu_seqlens`` / ``act_offsets`` have the
+    meaning of ``build_segments``.  Decode-sized batches (``small_eligible``)
+    run in two launches that gate and group the tokens themselves; larger ones
+    build segments first and run ``switched_lora_``.
+    """
+    x2, y2 = _xy2(x, y, packed)
+    dev = x2.device
+    ids = _as_i64(adapter_ids.reshape(-1), dev)
+    T = ids.shape[0]
+    if T != x2.shape[0]:
+        raise ValueError("adapter_ids must have one entry per token")
+    pos = _as_i64(positions, dev)
+    cu = _as_i32(cu_seqlens, dev)
+    off = _as_i64(act_offsets, dev)
+    if pos is not None and pos.numel() != T:
+        raise ValueError("positions must have one entry per token")
+    num_seqs = 1 if cu is None else cu.numel() - 1
+    if off is not None and off.numel() != num_seqs:
+        raise ValueError("act_offsets must have one entry per sequence")
+    if small_eligible(packed, T, num_seqs):
+        _call_small(x2, y2, packed, req=ids, pos=pos, cu=cu if off is not None else None, off=off,
+                    num_seqs=num_seqs if off is not None else 1)
+        return y
+    segs = build_segments(ids, packed.num_adapters, pos, cu, off)
+    return switched_lora_(y, x, segs, packed)
+
+
+def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed: PackedAdapters,
+                   z: torch.Tensor | None = None, path: str = "auto") -> torch.Tensor:
+    """In place: y += switched-LoRA delta of x (two launches).
+
+    ``path="auto"``: decode-sized batches (``small_eligible``) take the
+    small-batch kernels, which group tokens from ``segments.eff_ids``
+    themselves; larger ones the segment kernels.  ``"small"`` / ``"segments"``
+    force one of the two.  On the segment path ``z`` is optional scratch
+    [T, S*max_rank] of y's dtype (allocated when omitted) -- when the shrink
+    is split over the hidden dimension the expand reads the fp32 partials from
+    the workspace and z is not written.
+    """
+    if path not in ("auto", "small", "segments"):
+        raise ValueError(f"unknown path {path!r}")
+    x2, y2 = _xy2(x, y, packed)
     T, H = x2.shape
-    if H != packed.hidden or T != segments.num_tokens or y2.shape != (T, packed.out_total):
-        raise ValueError("x / y shapes do not match the segments / adapters")
+    if T != segments.num_tokens:
+        raise ValueError("x / y shapes do not match the segments")
     _check_segments(segments, packed)
+    if path == "small" or (path == "auto" and T and small_eligible(packed, T)):
+        _call_small(x2, y2, packed, eff_ids=segments.eff_ids)
+        return y
     zw = packed.num_slices * packed.max_rank
     if z is None:
         z = torch.empty(max(T, 1), zw, dtype=x2.dtype, device=x2.device)
@@ -454,6 +543,9 @@ __all__ = [
     "shrink",
     "expand_add_",
     "switched_lora_",
+    "switched_lora_routed_",
+    "small_eligible",
+    "small_workspace_bytes",
     "shrink_workspace",
     "reserve_workspace",
     "algorithmic_bytes",

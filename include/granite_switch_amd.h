@@ -22,6 +22,10 @@
  *   gs_shrink, gs_expand_add, gs_switched_lora
  *                          the shrink/expand/add of
  *                          src/granite_switch/hf/core/lora.py:127-161, 308-348
+ *   gs_switched_lora_small the same shrink/expand/add for decode-sized batches,
+ *                          with the per-adapter token grouping of
+ *                          src/granite_switch/hf/core/lora.py:127-135 done
+ *                          inside the two kernels
  *   gs_compute_bitmasks    torch.ops.granite_switch.compute_per_module_bitmasks
  *                          (src/granite_switch/vllm/core/lora_kernel_meta.py:61-91,
  *                          169-182) plus the remap gather at :294
@@ -147,6 +151,37 @@ int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t
                      const void* a_pack, const int64_t* a_off, const void* b_pack, const int64_t* b_off,
                      const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* seg_offsets,
                      const int32_t* perm, void* z, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Small-batch switched-LoRA in two launches, no segment build (decode-sized
+ * batches).  Same result as gs_build_segments + gs_switched_lora: every
+ * workgroup gates and lists the tokens of its own adapter from the routing
+ * input, so no metadata kernel runs first.
+ *
+ * Routing input, one of:
+ *   eff_ids [T] int32 -- ids already gated (e.g. gs_build_segments' eff_ids);
+ *   req_ids [T] int64 (+ positions, cu_seqlens, act_offsets, num_seqs with the
+ *   meaning of gs_build_segments) when eff_ids is NULL.
+ * a_off, b_off [num_adapters+1] int64 and ranks [num_adapters+1] int32 are
+ * HOST arrays here (load-time constants of the module; they travel in the
+ * kernel arguments), with the layout described above.
+ * Limits (gs_small_eligible): T <= 1024, num_seqs <= 1024,
+ * num_adapters <= 64, max_rank <= 64, every slice width a multiple of 128.
+ * workspace: gs_small_workspace_bytes(...) bytes, 16-byte aligned, no
+ * initialisation; calls sharing it must not overlap in time.
+ * ---------------------------------------------------------------------- */
+int gs_small_eligible(int64_t num_tokens, int32_t num_seqs, int32_t num_slices, const int32_t* slice_bounds,
+                      int32_t num_adapters, int32_t max_rank);
+int64_t gs_small_workspace_bytes(int32_t dtype, int64_t num_tokens, int32_t hidden, int32_t num_slices,
+                                 int32_t num_adapters, int32_t max_rank, int32_t out_total,
+                                 const int32_t* slice_bounds);
+int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t* positions,
+                           const int32_t* cu_seqlens, const int64_t* act_offsets, int32_t num_seqs,
+                           const int32_t* eff_ids, const void* x, int64_t ldx, void* y, int64_t ldy,
+                           int64_t num_tokens, int32_t hidden, int32_t out_total, const int32_t* slice_bounds,
+                           int32_t num_slices, const void* a_pack, const int64_t* a_off, const void* b_pack,
+                           const int64_t* b_off, const int32_t* ranks, int32_t num_adapters, int32_t max_rank,
+                           void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Reference op: per-module tile bitmasks and kernel-local ids.

@@ -1,0 +1,183 @@
+"""GPU parity of the two-launch small-batch (decode) path.
+
+The small path groups tokens inside its kernels, either from pre-gated ids
+(``switched_lora_`` with segments) or from the raw routing
+(``switched_lora_routed_``: requested ids + positions + sequence boundaries +
+aLoRA offsets).  Checked against the CPU oracle at the target tolerance
+(bf16 |got - ref| <= 2e-2 + 2e-2*|ref|, fp32 1e-5 + 1e-5*|ref|, ``ref`` the
+float64 math rounded once), against the segment path, and for bit-identical
+base rows.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from granite_switch_amd import switched, workloads
+from oracle import lora as olora
+from oracle import mapping as omap
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.bfloat16: 2e-2, torch.float32: 1e-5}
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _close(got, ref, tol, what):
+    err = np.abs(np.asarray(got, np.float64) - ref)
+    bad = err > tol + tol * np.abs(ref)
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements out of tolerance, max abs err {err.max():.3e}"
+
+
+def _oracle(md, eff, dtype, mode="exact"):
+    dt = "bf16" if dtype == torch.bfloat16 else "fp32"
+    return olora.switched_lora_apply(_np(md.y), _np(md.x), eff, [_np(a) for a in md.lora_A_slices],
+                                     [_np(b) for b in md.lora_B_slices], md.spec.output_slices, md.spec.ranks, dt,
+                                     mode)
+
+
+def _check(md, y, eff, dtype):
+    ref = _oracle(md, eff, dtype)
+    _close(_np(y), ref, TOL[dtype], "small path vs oracle")
+    base = eff == 0
+    assert np.array_equal(_np(y)[base], _np(md.y)[base]), "base rows were modified"
+
+
+@pytest.mark.parametrize("config", [0, 1])
+def test_small_routed_configs(dev, config):
+    """Configs 0 and 1 from the raw routing (gating inside the kernels)."""
+    wl = workloads.make_workload(config, dev)
+    md, r = wl.modules[0], wl.routing
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, md.spec.ranks)
+    assert switched.small_eligible(pk, r.num_tokens, len(r.cu_seqlens) - 1)
+    _say(f"small routed config={config} T={r.num_tokens}")
+    y = md.y.clone()
+    switched.switched_lora_routed_(y, md.x, torch.tensor(r.req_ids, device=dev), pk,
+                                   torch.tensor(r.positions, device=dev), torch.tensor(r.cu_seqlens, device=dev),
+                                   torch.tensor(r.act_offsets, device=dev))
+    torch.cuda.synchronize()
+    eff = omap.alora_effective_ids(r.req_ids, r.positions, r.cu_seqlens, r.act_offsets)
+    _check(md, y, eff, wl.dtype)
+    # the HF loop's own rounding sequence too
+    _close(_np(y), _oracle(md, eff, wl.dtype, "hf"), TOL[wl.dtype], "small path vs HF-rounding oracle")
+
+
+@pytest.mark.parametrize("config", [0, 1])
+def test_small_matches_segment_path(dev, config):
+    """Small path (eff ids from the builder) vs the segment path on the same inputs."""
+    wl = workloads.make_workload(config, dev)
+    md, r = wl.modules[0], wl.routing
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, md.spec.ranks)
+    segs = switched.build_segments(torch.tensor(r.req_ids, device=dev), wl.num_adapters,
+                                   torch.tensor(r.positions, device=dev), torch.tensor(r.cu_seqlens, device=dev),
+                                   torch.tensor(r.act_offsets, device=dev))
+    y_small = md.y.clone()
+    y_seg = md.y.clone()
+    switched.switched_lora_(y_small, md.x, segs, pk, path="small")
+    switched.switched_lora_(y_seg, md.x, segs, pk, path="segments")
+    torch.cuda.synchronize()
+    eff = segs.eff_ids.cpu().numpy()
+    _check(md, y_small, eff, wl.dtype)
+    _check(md, y_seg, eff, wl.dtype)
+    # both round one fp32 delta per element; split-K orders differ, so allow 1 ulp of the output
+    d = (y_small.float() - y_seg.float()).abs()
+    ulp = 2.0 ** -7 if wl.dtype == torch.bfloat16 else 2.0 ** -20
+    assert bool((d <= ulp * y_seg.float().abs().clamp_min(1.0)).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,NA,ranks,slices,H,seed", [
+    (1000, 3, [16, 64, 8], (256, 128), 1024, 1),        # ~250 tokens per adapter: 8 row tiles each
+    (333, 5, [8, 24, 40, 64, 16], (128,), 1000, 2),     # ranks not multiples of 16, H not a k-chunk multiple
+    (7, 2, [32, 32], (128, 128, 256), 4096, 3),         # tiny batch
+    (1024, 64, [32] * 64, (256,), 512, 4),              # every limit at once
+])
+def test_small_shapes(dev, dtype, T, NA, ranks, slices, H, seed):
+    spec = workloads.ModuleSpec("t", H, slices, ranks, max(ranks))
+    md = workloads.make_module(spec, T, NA, dtype, dev, seed=seed)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, ranks)
+    assert switched.small_eligible(pk, T)
+    rng = np.random.default_rng(seed)
+    ids = rng.integers(-1, NA + 2, size=T)           # includes out-of-range ids (-> base)
+    _say(f"small shapes dtype={dtype} T={T} NA={NA} ranks={ranks[:6]} slices={slices} H={H}")
+    y = md.y.clone()
+    switched.switched_lora_routed_(y, md.x, torch.tensor(ids, device=dev), pk)
+    torch.cuda.synchronize()
+    eff = np.where((ids < 0) | (ids > NA), 0, ids)
+    _check(md, y, eff, dtype)
+
+
+def test_small_ragged_gating_and_nonapplicable(dev):
+    """Packed ragged sequences, cached prefixes (absolute positions), an adapter that is not applicable."""
+    T, NA = 700, 6
+    spec = workloads.ModuleSpec("t", 768, (384, 128), [16, 32, 8, 64, 24, 40], 64)
+    md = workloads.make_module(spec, T, NA, torch.bfloat16, dev, seed=21)
+    for A in md.lora_A_slices:
+        A[2].zero_()                                  # adapter 3 not applicable here
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, spec.ranks)
+    assert pk.ranks_host[3] == 0
+    rng = np.random.default_rng(21)
+    cuts = np.sort(rng.choice(np.arange(1, T), size=39, replace=False))
+    cu = np.concatenate([[0], cuts, [T]]).astype(np.int32)
+    lens = np.diff(cu)
+    cached = rng.integers(0, 300, size=lens.size)
+    pos = np.concatenate([c + np.arange(n) for c, n in zip(cached, lens)]).astype(np.int64)
+    offs = rng.integers(0, 400, size=lens.size).astype(np.int64)
+    req = rng.integers(0, NA + 1, size=T)
+    for with_pos in (True, False):
+        y = md.y.clone()
+        switched.switched_lora_routed_(y, md.x, torch.tensor(req, device=dev), pk,
+                                       torch.tensor(pos, device=dev) if with_pos else None,
+                                       torch.tensor(cu, device=dev), torch.tensor(offs, device=dev))
+        torch.cuda.synchronize()
+        eff = omap.alora_effective_ids(req, pos if with_pos else None, cu, offs)
+        eff[eff == 3] = 0                             # non-applicable -> base, as the reference remaps it
+        _say(f"ragged gating with_pos={with_pos}: active {int((eff > 0).sum())}")
+        _check(md, y, eff, torch.bfloat16)
+
+
+def test_small_all_base_and_no_tokens_for_some_adapters(dev):
+    spec = workloads.ModuleSpec("t", 512, (256,), [16, 16, 16], 16)
+    md = workloads.make_module(spec, 90, 3, torch.bfloat16, dev, seed=5)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, spec.ranks)
+    y = md.y.clone()
+    switched.switched_lora_routed_(y, md.x, torch.zeros(90, dtype=torch.int64, device=dev), pk)
+    torch.cuda.synchronize()
+    assert torch.equal(y, md.y)
+    ids = np.where(np.arange(90) % 3 == 0, 2, 0)     # only adapter 2 present
+    y = md.y.clone()
+    switched.switched_lora_routed_(y, md.x, torch.tensor(ids, device=dev), pk)
+    torch.cuda.synchronize()
+    _check(md, y, ids, torch.bfloat16)
+
+
+def test_small_graph_replays(dev):
+    """The routed two-launch op captured in a HIP graph; every replay equals eager, bit for bit."""
+    wl = workloads.make_workload(1, dev)
+    md, r = wl.modules[0], wl.routing
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, md.spec.ranks)
+    args = (torch.tensor(r.req_ids, device=dev), pk, torch.tensor(r.positions, device=dev),
+            torch.tensor(r.cu_seqlens, device=dev), torch.tensor(r.act_offsets, device=dev))
+    y_eager = md.y.clone()
+    switched.switched_lora_routed_(y_eager, md.x, *args)
+    torch.cuda.synchronize()
+    y = md.y.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        switched.switched_lora_routed_(y, md.x, *args)
+    for rep in range(3):
+        y.copy_(md.y)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        _say(f"small graph replay {rep}")
+        assert torch.equal(y, y_eager), f"replay {rep} differs from eager"
