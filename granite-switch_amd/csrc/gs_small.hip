@@ -22,8 +22,7 @@
 // the element type exactly as a materialised z would be, then MFMAs with
 // lora_B and read-modify-writes only its adapter's token rows of y.
 //
-// Workspace: part [KS][NA][cap][zw] fp32, then cnt [NA] int32 (padded to a
-// multiple of 64 entries), then lists [NA][cap] int32.
+// Workspace: part [KS][NA][cap][zw] fp32, then lists [NA][cap] int32.
 #include "gs_common.h"
 
 namespace gs {
@@ -36,6 +35,9 @@ constexpr int kSmMaxAdapters = 64;           // adapters whose tables ride in th
 constexpr int kSmMaxRank = 64;               // largest (padded) rank of this path
 constexpr int kSmU = kSmMaxTokens / kSmT;    // tokens per thread in the routing pass
 constexpr int kPartGrp = 8;                  // split-K partials loaded together by the expand
+constexpr int kTokBits = 11;                 // token-list entry: (count << kTokBits) | token
+constexpr int kTokMask = (1 << kTokBits) - 1;
+static_assert(kSmMaxTokens < kTokMask, "token ids must fit below the list marker");
 
 // Per-adapter weight offsets and ranks, passed by value (load-time constants of
 // the module) so no workgroup waits on a table load before its weight loads.
@@ -61,68 +63,123 @@ struct RouteLds {
   int tok[kSmMaxTokens];
   int32_t cu[kSmMaxTokens];
   int64_t off[kSmMaxTokens];
+  int wreq[4];
   int wcnt[kSmU * 4];
 };
 
-// Lists adapter g's tokens (ascending) in s.tok and returns their count.
-// Called by all threads of the workgroup; ends with a barrier.
-__device__ int route_tokens(const SmallRoute& r, int g, RouteLds& s) {
+// Routing in two halves so the caller can issue its weight loads in between.
+// route_load: token t = u*256 + tid of every thread; loads the ids (and the
+// raw routing), stages sequence boundaries and activation offsets in LDS, and
+// returns whether any token REQUESTS adapter g (before gating; exact for
+// pre-gated ids) -- workgroup-uniform, read after one barrier.
+struct RouteRegs {
+  int id[kSmU];
+};
+
+__device__ bool route_load(const SmallRoute& r, int g, RouteLds& s, RouteRegs& rr) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  int id[kSmU];
+  int64_t rq[kSmU], q[kSmU];
   if (r.eff != nullptr) {
 #pragma unroll
     for (int u = 0; u < kSmU; ++u) {
       const int t = u * kSmT + tid;
-      id[u] = t < r.T ? r.eff[t] : 0;
+      rq[u] = t < r.T ? r.eff[t] : 0;
     }
   } else {
-    int64_t rq[kSmU], q[kSmU];
 #pragma unroll
     for (int u = 0; u < kSmU; ++u) {
       const int t = u * kSmT + tid;
       rq[u] = t < r.T ? r.req[t] : 0;
       q[u] = (t < r.T && r.pos != nullptr) ? r.pos[t] : 0;
     }
-    const bool gate = r.act_off != nullptr;
-    const int ns = (gate && r.cu != nullptr) ? r.num_seqs : 1;
-    if (gate) {
-      if (r.cu != nullptr) {
-        for (int k = tid; k < ns; k += kSmT) {
+  }
+  const bool gate = r.eff == nullptr && r.act_off != nullptr;
+  const int ns = (gate && r.cu != nullptr) ? r.num_seqs : 1;
+  if (gate) {
+    if (r.cu != nullptr) {
+#pragma unroll
+      for (int u = 0; u < kSmU; ++u) {
+        const int k = u * kSmT + tid;
+        if (k < ns) {
           s.cu[k] = r.cu[k];
           s.off[k] = r.act_off[k];
         }
-      } else if (tid == 0) {
-        s.cu[0] = 0;
-        s.off[0] = r.act_off[0];
       }
+    } else if (tid == 0) {
+      s.cu[0] = 0;
+      s.off[0] = r.act_off[0];
     }
-    lds_barrier();
+  }
+  bool req_g = false;
+#pragma unroll
+  for (int u = 0; u < kSmU; ++u) req_g |= (u * kSmT + tid < r.T) && rq[u] == g;
+  const uint64_t any = __ballot(req_g);
+  if (lane == 0) s.wreq[wave] = any != 0;
+  lds_barrier();
+  const bool used = (s.wreq[0] | s.wreq[1] | s.wreq[2] | s.wreq[3]) != 0;
+  // gating (sequence of token t: the largest sq with cu[sq] <= t, by a
+  // fixed-step search whose per-token chains interleave)
+  int sq[kSmU];
+#pragma unroll
+  for (int u = 0; u < kSmU; ++u) sq[u] = 0;
+  if (gate) {
+    // First guess: token t is sequence t (a decode batch, one token per
+    // sequence); it is right iff cu[t] <= t < cu[t+1].  Lanes whose guess
+    // fails run a fixed-step search (one LDS read per token slot and step,
+    // all issued before any is compared; clamped indices stay in bounds).
+    bool ok[kSmU];
+    bool all_ok = true;
 #pragma unroll
     for (int u = 0; u < kSmU; ++u) {
       const int t = u * kSmT + tid;
-      int64_t v = rq[u];
-      if (gate && t < r.T) {
-        // sequence of token t: the largest s with cu[s] <= t
-        int lo = 0, hi = ns - 1;
-        while (lo < hi) {
-          const int mid = (lo + hi + 1) >> 1;
-          if (s.cu[mid] <= t) lo = mid;
-          else hi = mid - 1;
+      const int gs = min(t, ns - 1);
+      const int c0 = s.cu[gs];
+      const int c1 = gs + 1 < ns ? s.cu[gs + 1] : 0x7fffffff;
+      ok[u] = t >= r.T || (c0 <= t && t < c1);
+      sq[u] = ok[u] ? gs : 0;
+      all_ok = all_ok && ok[u];
+    }
+    if (!all_ok) {
+#pragma unroll
+      for (int step = kSmMaxTokens / 2; step > 0; step >>= 1) {
+        if (step < ns) {
+          int c[kSmU];
+#pragma unroll
+          for (int u = 0; u < kSmU; ++u) c[u] = s.cu[min(sq[u] + step, ns - 1)];
+#pragma unroll
+          for (int u = 0; u < kSmU; ++u)
+            sq[u] = (!ok[u] && sq[u] + step < ns && c[u] <= u * kSmT + tid) ? sq[u] + step : sq[u];
         }
-        const int64_t qq = r.pos != nullptr ? q[u] : static_cast<int64_t>(t - s.cu[lo]);
-        if (qq < s.off[lo]) v = 0;
       }
-      if (v < 0 || v > r.NA) v = 0;
-      id[u] = static_cast<int>(v);
     }
   }
-  uint64_t bal[kSmU];
 #pragma unroll
   for (int u = 0; u < kSmU; ++u) {
     const int t = u * kSmT + tid;
-    bal[u] = __ballot(t < r.T && id[u] == g);
+    int64_t v = rq[u];
+    if (gate && t < r.T) {
+      const int64_t qq = r.pos != nullptr ? q[u] : static_cast<int64_t>(t - s.cu[sq[u]]);
+      if (qq < s.off[sq[u]]) v = 0;
+    }
+    if (t >= r.T || v < 0 || v > r.NA) v = 0;
+    rr.id[u] = static_cast<int>(v);
+  }
+  return used;
+}
+
+// route_list: lists adapter g's tokens (ascending) in s.tok and returns their
+// count; position = earlier (u, wave) chunks' counts + matches in lower lanes.
+// Called by all threads of the workgroup; ends with a barrier.
+__device__ int route_list(int g, RouteLds& s, const RouteRegs& rr) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  uint64_t bal[kSmU];
+#pragma unroll
+  for (int u = 0; u < kSmU; ++u) {
+    bal[u] = __ballot(rr.id[u] == g);
     if (lane == 0) s.wcnt[u * 4 + wave] = __popcll(bal[u]);
   }
   lds_barrier();
@@ -138,15 +195,14 @@ __device__ int route_tokens(const SmallRoute& r, int g, RouteLds& s) {
   }
 #pragma unroll
   for (int u = 0; u < kSmU; ++u) {
-    const int t = u * kSmT + tid;
-    if (t < r.T && id[u] == g) s.tok[before[u] + __popcll(bal[u] & lanemask_lt())] = t;
+    if (rr.id[u] == g) s.tok[before[u] + __popcll(bal[u] & lanemask_lt())] = u * kSmT + tid;
   }
   lds_barrier();
   return total;
 }
 
 // ----------------------------------------------------------------------------
-// Shrink.  1-D grid over (adapter, k-chunk, 32-column block).  The 4 waves
+// Shrink.  Grid (32-column block, k-chunk, adapter).  The 4 waves
 // split the k-chunk; each holds its share of the adapter's 32 lora_A rows in
 // registers (NPW 16-byte pieces per lane) for every 32-token row tile.
 // ----------------------------------------------------------------------------
@@ -160,8 +216,7 @@ struct SmallShrinkParams {
   int KS;
   int NCB;
   float* part;    // [KS][NA][cap][zw]
-  int32_t* cnt;   // [NA] tokens per adapter
-  int32_t* lists; // [NA][cap] the adapter's tokens, ascending
+  int32_t* lists; // [NA][cap] the adapter's tokens, ascending (see the shrink)
   int cap;
   int zw;
   SmallTab tab;
@@ -176,32 +231,29 @@ __global__ __launch_bounds__(kSmT) void shrink_small_kernel(SmallShrinkParams p)
   constexpr int ES = Elt<BF16>::kSize;
   constexpr int KW = NPW * 2 * P;   // k per wave
 
-  int L = blockIdx.x;
-  const int cb = L % p.NCB;
-  L /= p.NCB;
-  const int kc = L % p.KS;
-  const int g = L / p.KS + 1;
-  // the routing loads go out before the adapter's table entry is needed
-  const int n_g = route_tokens(p.rt, g, rl);
-  const int r = p.tab.rank[g];
-  const int ncols = p.S * r;
-  if (r == 0 || cb * 32 >= ncols) return;
-  if (kc == 0 && cb == 0) {
-    // the expand reads the token list instead of routing again
-    if (threadIdx.x == 0) p.cnt[g - 1] = n_g;
-    for (int j = threadIdx.x; j < n_g; j += kSmT) p.lists[static_cast<int64_t>(g - 1) * p.cap + j] = rl.tok[j];
-  }
-  if (n_g == 0) return;
-
+  const int cb = blockIdx.x;
+  const int kc = blockIdx.y;
+  const int g = blockIdx.z + 1;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int l = tid & 63;
   const int i = l & 31;
   const int h = l >> 5;
+  // Trip 1: the routing loads (and the adapter's table entry, a kernel
+  // argument).
+  RouteRegs rr;
+  const bool requested = route_load(p.rt, g, rl, rr);
+  const int r = p.tab.rank[g];
+  const int ncols = p.S * r;
+  const bool active = r > 0 && cb * 32 < ncols;
+  // Trip 2 starts here: lora_A of this workgroup's 32 shrink columns and its
+  // waves' k ranges, issued while the tokens are gated and listed -- only if
+  // some token requested the adapter, so an adapter absent from the batch
+  // reads no weights.
   const int64_t k_lo = (static_cast<int64_t>(kc) * 4 + wave) * KW;
   const int64_t k_hi = min(static_cast<int64_t>(p.H), k_lo + KW);
   const int n = cb * 32 + i;
-  const bool n_ok = n < ncols;
+  const bool n_ok = active && requested && n < ncols;
   const char* arow =
       static_cast<const char*>(p.a_pack) + (p.tab.off[g] + static_cast<int64_t>(n_ok ? n : 0) * p.H) * ES;
   u32x4 av[NPW];
@@ -211,6 +263,18 @@ __global__ __launch_bounds__(kSmT) void shrink_small_kernel(SmallShrinkParams p)
     av[pp] = u32x4{0u, 0u, 0u, 0u};
     if (n_ok && kp < k_hi) av[pp] = ld16(arow + kp * ES);
   }
+  const int n_g = route_list(g, rl, rr);
+  if (!active) return;
+  if (kc == 0 && cb == 0) {
+    // The expand reads the token list instead of routing again.  Each entry
+    // is (count << kTokBits) | token; the first 32 entries are always written
+    // (token kTokMask past the count), so an expand workgroup learns the count
+    // from its own first-tile entries.
+    const int nw = n_g > 32 ? n_g : 32;
+    for (int j = tid; j < nw; j += kSmT)
+      p.lists[static_cast<int64_t>(g - 1) * p.cap + j] = (n_g << kTokBits) | (j < n_g ? rl.tok[j] : kTokMask);
+  }
+  if (n_g == 0) return;
 
   for (int rt0 = 0; rt0 < n_g; rt0 += 32) {
     const int row = rt0 + i;
@@ -252,16 +316,15 @@ __global__ __launch_bounds__(kSmT) void shrink_small_kernel(SmallShrinkParams p)
 }
 
 // ----------------------------------------------------------------------------
-// Expand.  1-D grid over (adapter, column tile of NT = 128*NBW columns, inside
-// one slice).  Each wave owns NBW 32-column blocks and holds their lora_B rows
+// Expand.  Grid (column tile of NT = 128*NBW columns inside one slice,
+// adapter).  Each wave owns NBW 32-column blocks and holds their lora_B rows
 // for the whole rank in registers.  Per 32-token row tile: the partial sums
 // become the tile's shrink rows in LDS, y rows are loaded, the MFMA deltas go
 // through LDS to a row-major tile, and each thread adds and stores 16-byte
 // pieces of its token rows.
 // ----------------------------------------------------------------------------
 struct SmallExpandParams {
-  const int32_t* cnt;     // [NA] written by the shrink
-  const int32_t* lists;   // [NA][cap]
+  const int32_t* lists;   // [NA][cap] written by the shrink
   int NA;
   void* y;
   int64_t ldy;
@@ -291,32 +354,39 @@ __global__ __launch_bounds__(kSmT) void expand_small_kernel(SmallExpandParams p)
   __shared__ __align__(16) char zs[32 * ZLD * ES];
   __shared__ float dtile[32][NT + 4];
 
-  const int nt = blockIdx.x % p.NNT;
-  const int g = blockIdx.x / p.NNT + 1;
-  const int r = p.tab.rank[g];
-  if (r == 0) return;
+  const int nt = blockIdx.x;
+  const int g = blockIdx.y + 1;
   const int tid = threadIdx.x;
-  const int32_t* list = p.lists + static_cast<int64_t>(g - 1) * p.cap;
-  // one trip: the adapter's token count and the first row tile of its list
-  // (entries past the count are masked below)
-  const int n_g = p.cnt[g - 1];
-  constexpr int RPI0 = kSmT / LPR;
-  int tokp[32 / RPI0];
-#pragma unroll
-  for (int ps = 0; ps < 32 / RPI0; ++ps) tokp[ps] = list[ps * RPI0 + tid / LPR];
-  if (n_g == 0) return;
-
   const int wave = tid >> 6;
   const int l = tid & 63;
   const int i = l & 31;
   const int h = l >> 5;
+  const int32_t* list = p.lists + static_cast<int64_t>(g - 1) * p.cap;
+  // Trip 1: this thread's entries of the first row tile.  Every entry also
+  // carries the adapter's token count, so the exit test below depends on
+  // these loads and they are issued before it.
+  int ent[PASSES];
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) ent[ps] = list[ps * RPI + tid / LPR];
+  const int r = p.tab.rank[g];
+  const int n_g = __builtin_amdgcn_readfirstlane(ent[0] >> kTokBits);
+  if (r == 0 || n_g == 0) return;
+
   const int n_tile0 = nt * NT;
-  int s = 0;
-  while (s + 1 < p.si.S && n_tile0 >= p.si.bounds[s + 1]) ++s;
+  int s = 0;                             // slice of this column tile
+#pragma unroll
+  for (int k = 1; k < GS_MAX_SLICES; ++k)
+    if (k < p.si.S && n_tile0 >= p.si.bounds[k]) s = k;
   const int zc0 = s * r;                 // this slice's columns in the adapter's shrink row
   const int64_t goff = static_cast<int64_t>(g - 1) * p.cap;
+  const int64_t kstride = static_cast<int64_t>(p.NA) * p.cap * p.zw;
+  const int cx = (tid % LPR) * EPL;
+  const int per_row = r >> 2;            // 4-element items per shrink row
+  const int nitems = 32 * per_row;       // <= 2 items per thread (rank <= 64)
 
-  // lora_B rows of this wave's column blocks, all k-groups of the rank
+  // Trip 2 (first tile): lora_B rows of this wave's column blocks (all
+  // k-groups of the rank), the first kPartGrp split-K partials of the tile's
+  // shrink rows, and the tile's y rows -- all in flight before any is used.
   u32x4 bv[NBW][KG];
 #pragma unroll
   for (int q = 0; q < NBW; ++q) {
@@ -330,15 +400,7 @@ __global__ __launch_bounds__(kSmT) void expand_small_kernel(SmallExpandParams p)
     }
   }
 
-  const int cx = (tid % LPR) * EPL;
-  const int per_row = r >> 2;            // 4-element items per shrink row
-  const int nitems = 32 * per_row;       // <= 2 items per thread (rank <= 64)
-  const int64_t kstride = static_cast<int64_t>(p.NA) * p.cap * p.zw;
-  for (int rt0 = 0; rt0 < n_g; rt0 += 32) {
-    // shrink rows of the tile: partial sums in ks order, rounded like a stored
-    // z.  The first kPartGrp partials per item and the tile's y rows are all
-    // in flight before anything is added, so the tile costs one memory trip
-    // (plus one per further group of partials).
+  auto tile = [&](const int rt0) {
     const float* src[2];
     bool iok[2];
 #pragma unroll
@@ -357,7 +419,6 @@ __global__ __launch_bounds__(kSmT) void expand_small_kernel(SmallExpandParams p)
         a[j][u] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (iok[j] && u < p.KS) a[j][u] = *reinterpret_cast<const f32x4*>(src[j] + u * kstride);
       }
-    // y rows of the tile (token rows only)
     u32x4 yv[PASSES];
     int64_t yoff[PASSES];
     bool rok[PASSES];
@@ -365,21 +426,25 @@ __global__ __launch_bounds__(kSmT) void expand_small_kernel(SmallExpandParams p)
     for (int ps = 0; ps < PASSES; ++ps) {
       const int row = ps * RPI + tid / LPR;
       rok[ps] = rt0 + row < n_g;
-      yoff[ps] = static_cast<int64_t>(rok[ps] ? tokp[ps] : 0) * p.ldy + n_tile0 + cx;
+      yoff[ps] = static_cast<int64_t>(rok[ps] ? (ent[ps] & kTokMask) : 0) * p.ldy + n_tile0 + cx;
       yv[ps] = u32x4{0u, 0u, 0u, 0u};
       if (rok[ps]) yv[ps] = ld16(static_cast<const char*>(p.y) + yoff[ps] * ES);
     }
+    // shrink rows: partials summed in ks order, rounded like a stored z
     f32x4 sum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-    for (int ks0 = 0; ks0 < p.KS; ks0 += kPartGrp) {
-      if (ks0 > 0) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-          for (int u = 0; u < kPartGrp; ++u) {
-            a[j][u] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (iok[j] && ks0 + u < p.KS) a[j][u] = *reinterpret_cast<const f32x4*>(src[j] + (ks0 + u) * kstride);
-          }
-      }
+      for (int u = 0; u < kPartGrp; ++u)
+        if (u < p.KS) sum[j] += a[j][u];
+    for (int ks0 = kPartGrp; ks0 < p.KS; ks0 += kPartGrp) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int u = 0; u < kPartGrp; ++u) {
+          a[j][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (iok[j] && ks0 + u < p.KS) a[j][u] = *reinterpret_cast<const f32x4*>(src[j] + (ks0 + u) * kstride);
+        }
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -431,15 +496,17 @@ __global__ __launch_bounds__(kSmT) void expand_small_kernel(SmallExpandParams p)
         add_store_y<BF16>(p.y, yoff[ps], yv[ps], d);
       }
     }
-    if (rt0 + 32 < n_g) {
-      // token list entries of the next row tile
+  };
+
+  tile(0);
+  for (int rt0 = 32; rt0 < n_g; rt0 += 32) {
+    lds_barrier();   // zs / dtile are reused by this tile
 #pragma unroll
-      for (int ps = 0; ps < PASSES; ++ps) {
-        const int row = rt0 + 32 + ps * RPI + tid / LPR;
-        tokp[ps] = row < n_g ? list[row] : 0;
-      }
+    for (int ps = 0; ps < PASSES; ++ps) {
+      const int row = rt0 + ps * RPI + tid / LPR;
+      ent[ps] = row < n_g ? list[row] : 0;
     }
-    lds_barrier();   // zs / dtile are reused by the next row tile
+    tile(rt0);
   }
 }
 
@@ -448,7 +515,7 @@ __global__ __launch_bounds__(kSmT) void expand_small_kernel(SmallExpandParams p)
 // ----------------------------------------------------------------------------
 struct SmallPlan {
   int NPW, KS, NCB, cap, zw, NBW, NNT;
-  int64_t part_bytes, cnt_bytes, ws_bytes;
+  int64_t part_bytes, ws_bytes;
 };
 
 constexpr int kSmTargetShrinkWgs = 192;
@@ -479,24 +546,23 @@ SmallPlan plan_small(int64_t T, int H, int S, int NA, int max_rank, bool bf16, i
   pl.NBW = all256 ? 2 : 1;
   pl.NNT = out_total / (128 * pl.NBW);
   pl.part_bytes = static_cast<int64_t>(pl.KS) * NA * pl.cap * pl.zw * 4;
-  pl.cnt_bytes = static_cast<int64_t>((NA + 63) / 64) * 64 * 4;
-  pl.ws_bytes = pl.part_bytes + pl.cnt_bytes + static_cast<int64_t>(NA) * pl.cap * 4;
+  pl.ws_bytes = pl.part_bytes + static_cast<int64_t>(NA) * pl.cap * 4;
   return pl;
 }
 
 template <bool BF16>
 void launch_small(const SmallPlan& pl, const SmallShrinkParams& sp, const SmallExpandParams& ep, int NA,
                   hipStream_t st) {
-  const unsigned g1 = static_cast<unsigned>(NA * pl.KS * pl.NCB);
+  const dim3 g1(static_cast<unsigned>(pl.NCB), static_cast<unsigned>(pl.KS), static_cast<unsigned>(NA));
   switch (pl.NPW) {
-    case 16: hipLaunchKernelGGL((shrink_small_kernel<BF16, 16>), dim3(g1), dim3(kSmT), 0, st, sp); break;
-    case 8: hipLaunchKernelGGL((shrink_small_kernel<BF16, 8>), dim3(g1), dim3(kSmT), 0, st, sp); break;
-    case 4: hipLaunchKernelGGL((shrink_small_kernel<BF16, 4>), dim3(g1), dim3(kSmT), 0, st, sp); break;
-    default: hipLaunchKernelGGL((shrink_small_kernel<BF16, 2>), dim3(g1), dim3(kSmT), 0, st, sp); break;
+    case 16: hipLaunchKernelGGL((shrink_small_kernel<BF16, 16>), g1, dim3(kSmT), 0, st, sp); break;
+    case 8: hipLaunchKernelGGL((shrink_small_kernel<BF16, 8>), g1, dim3(kSmT), 0, st, sp); break;
+    case 4: hipLaunchKernelGGL((shrink_small_kernel<BF16, 4>), g1, dim3(kSmT), 0, st, sp); break;
+    default: hipLaunchKernelGGL((shrink_small_kernel<BF16, 2>), g1, dim3(kSmT), 0, st, sp); break;
   }
-  const unsigned g2 = static_cast<unsigned>(NA * pl.NNT);
-  if (pl.NBW == 2) hipLaunchKernelGGL((expand_small_kernel<BF16, 2>), dim3(g2), dim3(kSmT), 0, st, ep);
-  else hipLaunchKernelGGL((expand_small_kernel<BF16, 1>), dim3(g2), dim3(kSmT), 0, st, ep);
+  const dim3 g2(static_cast<unsigned>(pl.NNT), static_cast<unsigned>(NA));
+  if (pl.NBW == 2) hipLaunchKernelGGL((expand_small_kernel<BF16, 2>), g2, dim3(kSmT), 0, st, ep);
+  else hipLaunchKernelGGL((expand_small_kernel<BF16, 1>), g2, dim3(kSmT), 0, st, ep);
 }
 
 }  // namespace
@@ -586,15 +652,12 @@ int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t*
   sp.KS = pl.KS;
   sp.NCB = pl.NCB;
   sp.part = static_cast<float*>(workspace);
-  int32_t* cnt = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + pl.part_bytes);
-  int32_t* lists = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + pl.part_bytes + pl.cnt_bytes);
-  sp.cnt = cnt;
+  int32_t* lists = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + pl.part_bytes);
   sp.lists = lists;
   sp.cap = pl.cap;
   sp.zw = pl.zw;
   sp.tab = at;
   SmallExpandParams ep{};
-  ep.cnt = cnt;
   ep.lists = lists;
   ep.NA = num_adapters;
   ep.y = y;
