@@ -118,18 +118,20 @@ def main():
     ws_need = max(int(_lib.load().gs_shrink_workspace_bytes(T, s.hidden, len(s.output_slices), NA, sets[0][k][1].max_rank))
                   for k, s in enumerate(specs))
     nseq_r = len(routing.cu_seqlens) - 1
-    small = all(switched.small_eligible(sets[0][k][1], T, nseq_r) for k in range(len(specs))) and layers == 1
+    small = all(switched.small_preferred(sets[0][k][1], T, nseq_r) for k in range(len(specs))) and layers == 1
     if small:
-        ws_need = max([ws_need] + [switched.small_workspace_bytes(sets[0][k][1], T) for k in range(len(specs))])
+        switched.reserve_small_workspace(dev, max(switched.small_workspace_bytes(sets[0][k][1], T)
+                                                  for k in range(len(specs))))
+        switched.small_reset(dev)
     switched.reserve_workspace(dev, ws_need)
-    log(f"path: {'small-batch (two launches, routing inside the kernels)' if small else 'segments'}")
+    log(f"path: {'small-batch (one launch, routing inside the kernel)' if small else 'segments'}")
 
     def build():
         switched.build_segments(ids_d, NA, pos_d, cu_d, off_d, out=segs)
 
     def pair(k, md, pk):
         if small:
-            switched.switched_lora_routed_(md.y, md.x, ids_d, pk, pos_d, cu_d, off_d)
+            switched.switched_lora_routed_(md.y, md.x, ids_d, pk, pos_d, cu_d, off_d, path="small")
         else:
             switched.switched_lora_(md.y, md.x, segs, pk, zbuf[k], path="segments")
 
@@ -196,18 +198,22 @@ def main():
     per_kernel_bytes["build_segments"] = T * (8 + 8 + 4) + 4 * t_act + 12 * nseq + 4 * (NA + 1)
 
     # -- per-kernel timing (graphs of n launches of one kernel) -------------
+    # Small path: the step is one fused kernel per projection.  Segment path:
     # switched_lora = the shrink and expand kernels of one projection (the
     # production pair); shrink alone also runs the split-K reduce when the
     # hidden dimension is split; expand alone reads a materialised z.
     kern_us = {}
-    kern_launches = {"build_segments": 1}
-    g_b = capture(lambda: [build() for _ in range(K)])
-    kern_us["build_segments"] = timed(g_b, K) * 1e3
+    kern_launches = {}
     ks_split = {}
+    if not small:
+        kern_launches["build_segments"] = 1
+        g_b = capture(lambda: [build() for _ in range(K)])
+        kern_us["build_segments"] = timed(g_b, K) * 1e3
     for k, spec in enumerate(specs):
         mods = [sets[i][layer * len(specs) + k] for i in range(nsets) for layer in range(layers)]
         n = max(K, len(mods)) if cfg != 4 else len(mods)
-        for kind, fn in (("switched_lora", pair), ("shrink", shrink), ("expand", expand)):
+        kinds = (("small_fused", pair),) if small else (("switched_lora", pair), ("shrink", shrink), ("expand", expand))
+        for kind, fn in kinds:
             g_k = capture(lambda: [fn(k, *mods[j % len(mods)]) for j in range(n)])
             kern_us[f"{kind}:{spec.name}"] = timed(g_k, n) * 1e3
             kern_launches[f"{kind}:{spec.name}"] = layers
@@ -217,9 +223,13 @@ def main():
                                                                           pk0.max_rank)) > 256
         per_kernel_bytes[f"switched_lora:{spec.name}"] = (per_kernel_bytes[f"shrink:{spec.name}"]
                                                           + per_kernel_bytes[f"expand:{spec.name}"])
+        per_kernel_bytes[f"small_fused:{spec.name}"] = algorithmic_bytes(eff, pk0, spec.ranks, e)
+    if small:
+        if switched.small_status(dev) != 0:
+            raise RuntimeError(f"small-batch kernel reported error word {switched.small_status(dev)}")
     for name, us in kern_us.items():
         log(f"kernel {name}: {us:.2f} us/launch, {per_kernel_bytes[name] / us / 1e3:.0f} GB/s algorithmic")
-    singles = [n for n in kern_us if n.startswith("expand:") or n == "build_segments"
+    singles = [n for n in kern_us if n.startswith("expand:") or n == "build_segments" or n.startswith("small_fused:")
                or (n.startswith("shrink:") and not ks_split[n.split(":", 1)[1]])]
     dom = max(singles, key=lambda n: kern_us[n] * kern_launches[n])
     dom_gbs = per_kernel_bytes[dom] / (kern_us[dom] * 1e-6) / 1e9

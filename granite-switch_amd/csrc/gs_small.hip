@@ -1,28 +1,49 @@
-// Small-batch (decode-sized) switched-LoRA for gfx950: the whole op in two
-// launches, with no separate segment build.
+// Small-batch (decode-sized) switched-LoRA for gfx950: the whole op in ONE
+// launch, with no separate segment build.
 //
-// Both grids are adapter-major and static: a workgroup owns ONE adapter g and
-// a slice of its work (shrink: a k-chunk x 32 shrink columns; expand: a
-// column tile of y).  A shrink workgroup first lists the batch's tokens of
-// adapter g itself: every thread gates a few tokens exactly like
-// gs_build_segments does (ids outside [0, NA] are base; aLoRA: a token before
-// its sequence's activation offset is base), and one ballot per token chunk
-// plus a 16-entry prefix in LDS gives the list in ascending token order -- the
-// order of the reference HF loop.  That costs one round trip to memory (the
-// ids, cache-resident after the first workgroup), after which all of its
-// lora_A and x loads are issued at once.  One shrink workgroup per adapter
-// also stores the list and its length, so an expand workgroup reads them in
-// one cache-hot trip and then issues its lora_B, partial-sum and y loads
-// together.  Each kernel is therefore launch + two memory trips + its stores,
-// and an adapter with no tokens in the batch reads no weights.
+// The grid is 1-D: NP producer workgroups, then NC consumer workgroups.
+//   producer (cb, kc, g): the shrink of adapter g's 32-column block cb over the
+//     k-chunk kc, written as fp32 partial sums;
+//   consumer (nt, g): the expand of adapter g into the NT-column tile nt of y
+//     (inside one slice), which adds the partials of its slice in ks order.
+// Every workgroup gates and lists the tokens of its own adapter from the
+// routing input (ids outside [0, NA] are base; aLoRA: a token before its
+// sequence's activation offset is base), with one ballot per token chunk and a
+// 16-entry prefix in LDS, giving the list in ascending token order -- the
+// iteration order of the reference HF loop.
 //
-// The shrink splits the hidden dimension into KS chunks and writes fp32
-// partial sums at part[ks][g-1][j][col], j = the token's rank among adapter
-// g's tokens.  The expand sums them in ks order (deterministic) and rounds to
-// the element type exactly as a materialised z would be, then MFMAs with
-// lora_B and read-modify-writes only its adapter's token rows of y.
+// Hand-off inside the launch: tagged partials.  Each adapter g has an epoch
+// word E_g and a done count in the sync buffer.  Every workgroup of adapter g
+// reads E_g when it starts; a producer stores each partial as one 64-bit pair
+// (tag = E_g + 1, fp32 bits) with agent-coherent stores (sc1: written through
+// past the XCD's L2), and a consumer issues its lora_B and y loads first, then
+// polls its partials with agent-coherent 64-bit loads until every tag equals
+// E_g + 1 (a pair is read in one access, so a value is never taken without its
+// tag).  Once it has its partials, a consumer adds 1 to g's done count; the
+// consumer that completes the count stores E_g + 1 and a zero count for the
+// next launch.  That is safe: every workgroup of g that writes partials is
+// waited for by some consumer of g, so it has read E_g by then, and every
+// consumer of g has read E_g before counting itself done.  No counters on the
+// critical path, no cache writeback or invalidate, no device-scope fence.
+// Adapter g's partials live in a fixed region of the workspace whatever the
+// module's shape, so a stale pair there carries a tag of an earlier epoch of
+// the same g and never the current one (until the 32-bit epoch wraps).
 //
-// Workspace: part [KS][NA][cap][zw] fp32, then lists [NA][cap] int32.
+// Forward progress: producers have the lowest workgroup ids and never wait, and
+// workgroups are dispatched in id order, so a waiting consumer never holds a
+// slot a producer still needs.  The wait is nevertheless bounded: after
+// timeout_ticks of the 100 MHz wall clock a consumer sets bit 0 of the error
+// word and goes on, so every wave of the grid always ends.
+//
+// MFMA shapes: 16x16x32 bf16 (16x16x4 fp32) throughout, so each global load
+// instruction reads 64 contiguous bytes of 16 rows (4 lanes per row) instead
+// of 32 bytes of 32 rows.
+//
+// Workspace: kSmMaxAdapters equal regions, adapter g's holding its tagged
+// partials [KS][cap][zw] uint64; used by nothing else.
+// Sync buffer (int32 words): [2] error word; [32*g] epoch and [32*g + 1] done
+// count of adapter g (one 128-byte line per adapter).  Both buffers are
+// zeroed once before the first call.
 #include "gs_common.h"
 
 namespace gs {
@@ -34,15 +55,16 @@ constexpr int kSmMaxTokens = 1024;           // largest batch of this path
 constexpr int kSmMaxAdapters = 64;           // adapters whose tables ride in the kernel arguments
 constexpr int kSmMaxRank = 64;               // largest (padded) rank of this path
 constexpr int kSmU = kSmMaxTokens / kSmT;    // tokens per thread in the routing pass
-constexpr int kPartGrp = 8;                  // split-K partials loaded together by the expand
-constexpr int kTokBits = 11;                 // token-list entry: (count << kTokBits) | token
-constexpr int kTokMask = (1 << kTokBits) - 1;
-static_assert(kSmMaxTokens < kTokMask, "token ids must fit below the list marker");
+constexpr int kKsGrp = 4;                    // split-K partials a consumer polls together
+constexpr int kErrTimeout = 1;               // error word bits
+constexpr int kSyncErrWord = 2;              // int32 index of the error word
+constexpr int kSyncLine = 32;                // int32 words per adapter (epoch, done count)
 
 // Per-adapter weight offsets and ranks, passed by value (load-time constants of
 // the module) so no workgroup waits on a table load before its weight loads.
 struct SmallTab {
-  int64_t off[kSmMaxAdapters + 1];
+  int64_t a_off[kSmMaxAdapters + 1];
+  int64_t b_off[kSmMaxAdapters + 1];
   int32_t rank[kSmMaxAdapters + 1];
 };
 
@@ -67,68 +89,108 @@ struct RouteLds {
   int wcnt[kSmU * 4];
 };
 
-// Routing in two halves so the caller can issue its weight loads in between.
-// route_load: token t = u*256 + tid of every thread; loads the ids (and the
-// raw routing), stages sequence boundaries and activation offsets in LDS, and
-// returns whether any token REQUESTS adapter g (before gating; exact for
-// pre-gated ids) -- workgroup-uniform, read after one barrier.
+// Routing in three steps so the caller can issue its weight loads between the
+// routing loads and their first use (loads return in order, so a wait for the
+// routing loads does not wait for weight loads issued after them).
 struct RouteRegs {
+  int64_t rq[kSmU];     // requested ids (req path)
+  int32_t e32[kSmU];    // pre-gated ids (eff path), widened only when used
+  int64_t q[kSmU];
+  int32_t cu[kSmU];
+  int64_t off[kSmU];
   int id[kSmU];
 };
 
-__device__ bool route_load(const SmallRoute& r, int g, RouteLds& s, RouteRegs& rr) {
+__device__ __forceinline__ bool route_gated(const SmallRoute& r) { return r.eff == nullptr && r.act_off != nullptr; }
+__device__ __forceinline__ int route_nseq(const SmallRoute& r) {
+  return (route_gated(r) && r.cu != nullptr) ? r.num_seqs : 1;
+}
+
+// Step 1: issue the routing loads for tokens t = u*256 + tid.  The pointer
+// checks are uniform and sit outside the loops; inside, every load is issued
+// unconditionally from a clamped in-bounds index (T >= 1, ns >= 1), so the
+// loads stay in flight together.  Entries past T / ns are masked by the users.
+__device__ __forceinline__ void route_issue(const SmallRoute& r, RouteRegs& rr) {
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  int64_t rq[kSmU], q[kSmU];
+  const int tl = r.T - 1;
   if (r.eff != nullptr) {
 #pragma unroll
     for (int u = 0; u < kSmU; ++u) {
-      const int t = u * kSmT + tid;
-      rq[u] = t < r.T ? r.eff[t] : 0;
+      rr.e32[u] = r.eff[min(u * kSmT + tid, tl)];
+      rr.rq[u] = 0;
     }
   } else {
 #pragma unroll
     for (int u = 0; u < kSmU; ++u) {
-      const int t = u * kSmT + tid;
-      rq[u] = t < r.T ? r.req[t] : 0;
-      q[u] = (t < r.T && r.pos != nullptr) ? r.pos[t] : 0;
+      rr.rq[u] = r.req[min(u * kSmT + tid, tl)];
+      rr.e32[u] = 0;
     }
   }
-  const bool gate = r.eff == nullptr && r.act_off != nullptr;
-  const int ns = (gate && r.cu != nullptr) ? r.num_seqs : 1;
-  if (gate) {
+  if (r.eff == nullptr && r.pos != nullptr) {
+#pragma unroll
+    for (int u = 0; u < kSmU; ++u) rr.q[u] = r.pos[min(u * kSmT + tid, tl)];
+  } else {
+#pragma unroll
+    for (int u = 0; u < kSmU; ++u) rr.q[u] = 0;
+  }
+  if (route_gated(r)) {
+    const int nl = route_nseq(r) - 1;
+#pragma unroll
+    for (int u = 0; u < kSmU; ++u) rr.off[u] = r.act_off[min(u * kSmT + tid, nl)];
     if (r.cu != nullptr) {
 #pragma unroll
-      for (int u = 0; u < kSmU; ++u) {
-        const int k = u * kSmT + tid;
-        if (k < ns) {
-          s.cu[k] = r.cu[k];
-          s.off[k] = r.act_off[k];
-        }
-      }
-    } else if (tid == 0) {
-      s.cu[0] = 0;
-      s.off[0] = r.act_off[0];
+      for (int u = 0; u < kSmU; ++u) rr.cu[u] = r.cu[min(u * kSmT + tid, nl)];
+    } else {
+#pragma unroll
+      for (int u = 0; u < kSmU; ++u) rr.cu[u] = 0;
     }
+  } else {
+#pragma unroll
+    for (int u = 0; u < kSmU; ++u) {
+      rr.off[u] = 0;
+      rr.cu[u] = 0;
+    }
+  }
+}
+
+// Step 2: stage sequence boundaries and offsets in LDS, gate every token, and
+// return whether any token REQUESTS adapter g (before gating; exact for
+// pre-gated ids) -- workgroup-uniform.  Ends with a barrier.
+__device__ __forceinline__ bool route_gate(const SmallRoute& r, int g, RouteLds& s, RouteRegs& rr) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const bool gate = route_gated(r);
+  const int ns = route_nseq(r);
+  if (gate) {
+#pragma unroll
+    for (int u = 0; u < kSmU; ++u) {
+      const int k = u * kSmT + tid;
+      if (k < ns) {
+        s.cu[k] = rr.cu[u];
+        s.off[k] = rr.off[u];
+      }
+    }
+  }
+  if (r.eff != nullptr) {
+#pragma unroll
+    for (int u = 0; u < kSmU; ++u) rr.rq[u] = rr.e32[u];
   }
   bool req_g = false;
 #pragma unroll
-  for (int u = 0; u < kSmU; ++u) req_g |= (u * kSmT + tid < r.T) && rq[u] == g;
+  for (int u = 0; u < kSmU; ++u) req_g |= (u * kSmT + tid < r.T) && rr.rq[u] == g;
   const uint64_t any = __ballot(req_g);
   if (lane == 0) s.wreq[wave] = any != 0;
   lds_barrier();
   const bool used = (s.wreq[0] | s.wreq[1] | s.wreq[2] | s.wreq[3]) != 0;
-  // gating (sequence of token t: the largest sq with cu[sq] <= t, by a
-  // fixed-step search whose per-token chains interleave)
+  // sequence of token t: the largest sq with cu[sq] <= t.  First guess: token t
+  // is sequence t (a decode batch, one token per sequence), right iff
+  // cu[t] <= t < cu[t+1].  Lanes whose guess fails run a fixed-step search
+  // (one LDS read per token slot and step; clamped indices stay in bounds).
   int sq[kSmU];
 #pragma unroll
   for (int u = 0; u < kSmU; ++u) sq[u] = 0;
   if (gate) {
-    // First guess: token t is sequence t (a decode batch, one token per
-    // sequence); it is right iff cu[t] <= t < cu[t+1].  Lanes whose guess
-    // fails run a fixed-step search (one LDS read per token slot and step,
-    // all issued before any is compared; clamped indices stay in bounds).
     bool ok[kSmU];
     bool all_ok = true;
 #pragma unroll
@@ -158,9 +220,9 @@ __device__ bool route_load(const SmallRoute& r, int g, RouteLds& s, RouteRegs& r
 #pragma unroll
   for (int u = 0; u < kSmU; ++u) {
     const int t = u * kSmT + tid;
-    int64_t v = rq[u];
+    int64_t v = rr.rq[u];
     if (gate && t < r.T) {
-      const int64_t qq = r.pos != nullptr ? q[u] : static_cast<int64_t>(t - s.cu[sq[u]]);
+      const int64_t qq = r.pos != nullptr ? rr.q[u] : static_cast<int64_t>(t - s.cu[sq[u]]);
       if (qq < s.off[sq[u]]) v = 0;
     }
     if (t >= r.T || v < 0 || v > r.NA) v = 0;
@@ -169,10 +231,10 @@ __device__ bool route_load(const SmallRoute& r, int g, RouteLds& s, RouteRegs& r
   return used;
 }
 
-// route_list: lists adapter g's tokens (ascending) in s.tok and returns their
-// count; position = earlier (u, wave) chunks' counts + matches in lower lanes.
-// Called by all threads of the workgroup; ends with a barrier.
-__device__ int route_list(int g, RouteLds& s, const RouteRegs& rr) {
+// Step 3: list adapter g's tokens (ascending) in s.tok and return their count;
+// position = earlier (u, wave) chunks' counts + matches in lower lanes.
+// Ends with a barrier.
+__device__ __forceinline__ int route_list(int g, RouteLds& s, const RouteRegs& rr) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -201,13 +263,29 @@ __device__ int route_list(int g, RouteLds& s, const RouteRegs& rr) {
   return total;
 }
 
-// ----------------------------------------------------------------------------
-// Shrink.  Grid (32-column block, k-chunk, adapter).  The 4 waves
-// split the k-chunk; each holds its share of the adapter's 32 lora_A rows in
-// registers (NPW 16-byte pieces per lane) for every 32-token row tile.
-// ----------------------------------------------------------------------------
-struct SmallShrinkParams {
+// 16x16 MFMA, K = 32 bf16 (one 16-byte piece per lane) or 4 x K = 4 fp32.
+// Lane l supplies row (l % 16) of the A operand and column (l % 16) of the B
+// operand, elements [8*(l/16), +8) of K (bf16).  Both operands pair their
+// elements by (lane group, element), so any fixed assignment of k to pieces is
+// a correct contraction.  Result: lane l holds D[4*(l/16) + e][l % 16], e < 4.
+template <bool BF16>
+__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, f32x4 acc) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc,
+                                                   0, 0, 0);
+  } else {
+    const f32x4 x = __builtin_bit_cast(f32x4, a);
+    const f32x4 w = __builtin_bit_cast(f32x4, b);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, w.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, w.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, w.z, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, w.w, acc, 0, 0, 0);
+  }
+}
+
+struct FusedParams {
   SmallRoute rt;
+  // shrink side
   const void* x;
   int64_t ldx;
   int H;
@@ -215,326 +293,429 @@ struct SmallShrinkParams {
   int S;
   int KS;
   int NCB;
-  float* part;    // [KS][NA][cap][zw]
-  int32_t* lists; // [NA][cap] the adapter's tokens, ascending (see the shrink)
+  int NP;                 // producer workgroups (the first NP ids)
+  uint64_t* part;         // tagged partials: region (g-1) at part + (g-1)*region, [KS][cap][zw]
+  int64_t region;
   int cap;
   int zw;
-  SmallTab tab;
-};
-
-template <bool BF16, int NPW>
-__global__ __launch_bounds__(kSmT) void shrink_small_kernel(SmallShrinkParams p) {
-  __shared__ RouteLds rl;
-  __shared__ float red[3][16][64];
-  __shared__ float tile_s[32][32 + 4];
-  constexpr int P = Elt<BF16>::kPerPiece;
-  constexpr int ES = Elt<BF16>::kSize;
-  constexpr int KW = NPW * 2 * P;   // k per wave
-
-  const int cb = blockIdx.x;
-  const int kc = blockIdx.y;
-  const int g = blockIdx.z + 1;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int l = tid & 63;
-  const int i = l & 31;
-  const int h = l >> 5;
-  // Trip 1: the routing loads (and the adapter's table entry, a kernel
-  // argument).
-  RouteRegs rr;
-  const bool requested = route_load(p.rt, g, rl, rr);
-  const int r = p.tab.rank[g];
-  const int ncols = p.S * r;
-  const bool active = r > 0 && cb * 32 < ncols;
-  // Trip 2 starts here: lora_A of this workgroup's 32 shrink columns and its
-  // waves' k ranges, issued while the tokens are gated and listed -- only if
-  // some token requested the adapter, so an adapter absent from the batch
-  // reads no weights.
-  const int64_t k_lo = (static_cast<int64_t>(kc) * 4 + wave) * KW;
-  const int64_t k_hi = min(static_cast<int64_t>(p.H), k_lo + KW);
-  const int n = cb * 32 + i;
-  const bool n_ok = active && requested && n < ncols;
-  const char* arow =
-      static_cast<const char*>(p.a_pack) + (p.tab.off[g] + static_cast<int64_t>(n_ok ? n : 0) * p.H) * ES;
-  u32x4 av[NPW];
-#pragma unroll
-  for (int pp = 0; pp < NPW; ++pp) {
-    const int64_t kp = k_lo + (2 * pp + h) * P;
-    av[pp] = u32x4{0u, 0u, 0u, 0u};
-    if (n_ok && kp < k_hi) av[pp] = ld16(arow + kp * ES);
-  }
-  const int n_g = route_list(g, rl, rr);
-  if (!active) return;
-  if (kc == 0 && cb == 0) {
-    // The expand reads the token list instead of routing again.  Each entry
-    // is (count << kTokBits) | token; the first 32 entries are always written
-    // (token kTokMask past the count), so an expand workgroup learns the count
-    // from its own first-tile entries.
-    const int nw = n_g > 32 ? n_g : 32;
-    for (int j = tid; j < nw; j += kSmT)
-      p.lists[static_cast<int64_t>(g - 1) * p.cap + j] = (n_g << kTokBits) | (j < n_g ? rl.tok[j] : kTokMask);
-  }
-  if (n_g == 0) return;
-
-  for (int rt0 = 0; rt0 < n_g; rt0 += 32) {
-    const int row = rt0 + i;
-    const bool row_ok = row < n_g;
-    const int token = rl.tok[row_ok ? row : rt0];
-    const char* xrow = static_cast<const char*>(p.x) + static_cast<int64_t>(token) * p.ldx * ES;
-    u32x4 xv[NPW];
-#pragma unroll
-    for (int pp = 0; pp < NPW; ++pp) {
-      const int64_t kp = k_lo + (2 * pp + h) * P;
-      xv[pp] = u32x4{0u, 0u, 0u, 0u};
-      if (row_ok && kp < k_hi) xv[pp] = ld16(xrow + kp * ES);
-    }
-    f32x16 acc = f32x16{};
-#pragma unroll
-    for (int pp = 0; pp < NPW; ++pp) acc = mfma_piece<BF16>(xv[pp], av[pp], acc);
-
-    // fixed-order cross-wave sum: ((w0 + w1) + w2) + w3
-    if (wave > 0) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) red[wave - 1][v][l] = acc[v];
-    }
-    lds_barrier();
-    if (wave == 0) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) tile_s[mfma32_row(v, l)][i] = ((acc[v] + red[0][v][l]) + red[1][v][l]) + red[2][v][l];
-    }
-    lds_barrier();
-    const int srow = tid >> 3;
-    const int c4 = (tid & 7) * 4;
-    if (rt0 + srow < n_g && cb * 32 + c4 < ncols) {
-      float* dst = p.part +
-                   ((static_cast<int64_t>(kc) * p.rt.NA + (g - 1)) * p.cap + rt0 + srow) * p.zw + cb * 32 + c4;
-      *reinterpret_cast<f32x4*>(dst) =
-          f32x4{tile_s[srow][c4], tile_s[srow][c4 + 1], tile_s[srow][c4 + 2], tile_s[srow][c4 + 3]};
-    }
-    lds_barrier();   // red / tile_s are reused by the next row tile
-  }
-}
-
-// ----------------------------------------------------------------------------
-// Expand.  Grid (column tile of NT = 128*NBW columns inside one slice,
-// adapter).  Each wave owns NBW 32-column blocks and holds their lora_B rows
-// for the whole rank in registers.  Per 32-token row tile: the partial sums
-// become the tile's shrink rows in LDS, y rows are loaded, the MFMA deltas go
-// through LDS to a row-major tile, and each thread adds and stores 16-byte
-// pieces of its token rows.
-// ----------------------------------------------------------------------------
-struct SmallExpandParams {
-  const int32_t* lists;   // [NA][cap] written by the shrink
-  int NA;
+  // expand side
   void* y;
   int64_t ldy;
   int out_total;
   SliceInfo si;
   const void* b_pack;
-  const float* part;
-  int KS;
-  int cap;
-  int zw;
-  int NNT;          // column tiles per adapter
+  int NNT;                // column tiles per adapter
+  // hand-off
+  int32_t* sync;
+  int64_t timeout_ticks;
   SmallTab tab;
 };
 
-template <bool BF16, int NBW>
-__global__ __launch_bounds__(kSmT) void expand_small_kernel(SmallExpandParams p) {
-  constexpr int NT = 4 * NBW * 32;
-  constexpr int ES = Elt<BF16>::kSize;
-  constexpr int EPL = 16 / ES;          // elements per 16-byte piece
-  constexpr int LPR = NT / EPL;         // lanes per y row
-  constexpr int RPI = kSmT / LPR;       // rows per workgroup-wide access
-  constexpr int PASSES = 32 / RPI;
-  constexpr int KSTEP = BF16 ? 16 : 8;  // rank per MFMA group (both lane halves)
-  constexpr int KHALF = KSTEP / 2;
-  constexpr int KG = kSmMaxRank / KSTEP;
-  constexpr int ZLD = kSmMaxRank + 8;   // elements per LDS shrink row
-  __shared__ __align__(16) char zs[32 * ZLD * ES];
-  __shared__ float dtile[32][NT + 4];
+// Slice of column tile nt (tiles never straddle a slice).
+template <int NT>
+__device__ __forceinline__ int tile_slice(const SliceInfo& si, int nt) {
+  const int n0 = nt * NT;
+  int s = 0;
+#pragma unroll
+  for (int k = 1; k < GS_MAX_SLICES; ++k)
+    if (k < si.S && n0 >= si.bounds[k]) s = k;
+  return s;
+}
 
-  const int nt = blockIdx.x;
-  const int g = blockIdx.y + 1;
+constexpr int kZld = kSmMaxRank + 8;         // elements per LDS shrink row
+constexpr int kHalf = 128;                   // y columns per delta staging pass
+
+template <bool BF16>
+struct FusedLds {
+  RouteLds rt;
+  uint32_t epoch;
+  union {
+    float red[3][16][64];                    // producer: cross-wave sums
+    struct {                                 // consumer
+      __attribute__((aligned(16))) char zs[32 * kZld * Elt<BF16>::kSize];
+      float dtile[32][kHalf + 4];
+    } co;
+  } u;
+};
+
+// Adapter g's epoch at the start of this launch (thread 0 only).
+__device__ __forceinline__ uint32_t read_epoch(const FusedParams& p, int g) {
+  return static_cast<uint32_t>(
+      __hip_atomic_load(p.sync + kSyncLine * g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// ----------------------------------------------------------------------------
+// Producer: the 4 waves split the k-chunk; each holds its share of the
+// adapter's 32 lora_A rows (two 16-row blocks) in registers, NPW 16-byte
+// pieces per lane and block, and streams x rows in 32-token chunks (two
+// 16-row tiles).  The waves' sums are added in a fixed order in LDS and wave 0
+// stores the tagged partials straight from its registers.
+// ----------------------------------------------------------------------------
+template <bool BF16, int NPW, int NT, bool SPEC>
+__device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16>& L, int bid) {
+  constexpr int P = Elt<BF16>::kPerPiece;
+  constexpr int ES = Elt<BF16>::kSize;
+  constexpr int KSTEP = 4 * P;      // k per piece over the 4 lane groups
+  constexpr int KW = NPW * KSTEP;   // k per wave
+  const int cb = bid % p.NCB;
+  const int rem = bid / p.NCB;
+  const int kc = rem % p.KS;
+  const int g = rem / p.KS + 1;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int l = tid & 63;
-  const int i = l & 31;
-  const int h = l >> 5;
-  const int32_t* list = p.lists + static_cast<int64_t>(g - 1) * p.cap;
-  // Trip 1: this thread's entries of the first row tile.  Every entry also
-  // carries the adapter's token count, so the exit test below depends on
-  // these loads and they are issued before it.
-  int ent[PASSES];
-#pragma unroll
-  for (int ps = 0; ps < PASSES; ++ps) ent[ps] = list[ps * RPI + tid / LPR];
+  const int i16 = l & 15;
+  const int q4 = l >> 4;
   const int r = p.tab.rank[g];
-  const int n_g = __builtin_amdgcn_readfirstlane(ent[0] >> kTokBits);
-  if (r == 0 || n_g == 0) return;
-
-  const int n_tile0 = nt * NT;
-  int s = 0;                             // slice of this column tile
+  const int ncols = p.S * r;
+  const bool active = r > 0 && cb * 32 < ncols;
+  const int64_t k_lo = (static_cast<int64_t>(kc) * 4 + wave) * KW;
+  const int64_t k_hi = min(static_cast<int64_t>(p.H), k_lo + KW);
+  int n[2];
+  bool nok[2];
+  const char* arow[2];
 #pragma unroll
-  for (int k = 1; k < GS_MAX_SLICES; ++k)
-    if (k < p.si.S && n_tile0 >= p.si.bounds[k]) s = k;
-  const int zc0 = s * r;                 // this slice's columns in the adapter's shrink row
-  const int64_t goff = static_cast<int64_t>(g - 1) * p.cap;
-  const int64_t kstride = static_cast<int64_t>(p.NA) * p.cap * p.zw;
-  const int cx = (tid % LPR) * EPL;
-  const int per_row = r >> 2;            // 4-element items per shrink row
-  const int nitems = 32 * per_row;       // <= 2 items per thread (rank <= 64)
-
-  // Trip 2 (first tile): lora_B rows of this wave's column blocks (all
-  // k-groups of the rank), the first kPartGrp split-K partials of the tile's
-  // shrink rows, and the tile's y rows -- all in flight before any is used.
-  u32x4 bv[NBW][KG];
-#pragma unroll
-  for (int q = 0; q < NBW; ++q) {
-    const int n = n_tile0 + 32 * (wave * NBW + q) + i;
-    const char* br = static_cast<const char*>(p.b_pack) + (p.tab.off[g] + static_cast<int64_t>(n) * r) * ES;
-#pragma unroll
-    for (int kg = 0; kg < KG; ++kg) {
-      const int k0 = kg * KSTEP + KHALF * h;
-      bv[q][kg] = u32x4{0u, 0u, 0u, 0u};
-      if (k0 < r) bv[q][kg] = ld16(br + k0 * ES);
-    }
+  for (int c2 = 0; c2 < 2; ++c2) {
+    n[c2] = cb * 32 + 16 * c2 + i16;
+    nok[c2] = active && n[c2] < ncols;
+    // rows past the adapter's columns (and adapters with rank 0, whose offset
+    // is 0) read row 0 of the block and are masked
+    arow[c2] = static_cast<const char*>(p.a_pack) +
+               (p.tab.a_off[g] + static_cast<int64_t>(nok[c2] ? n[c2] : 0) * p.H) * ES;
   }
 
-  auto tile = [&](const int rt0) {
-    const float* src[2];
-    bool iok[2];
+  if (tid == 0) L.epoch = read_epoch(p, g);
+  RouteRegs rr;
+  route_issue(p.rt, rr);
+  u32x4 av[2][NPW];
+  if constexpr (SPEC) {
+    // lora_A in the same memory trip as the routing loads: unconditional loads
+    // from clamped addresses, so the wait for the routing loads below does not
+    // also wait for these
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int it = tid + j * kSmT;
-      const int row = it / per_row;
-      const int c4 = (it - row * per_row) * 4;
-      iok[j] = it < nitems && rt0 + row < n_g;
-      src[j] = p.part + (goff + rt0 + (iok[j] ? row : 0)) * p.zw + zc0 + (iok[j] ? c4 : 0);
-    }
-    f32x4 a[2][kPartGrp];
+    for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int u = 0; u < kPartGrp; ++u) {
-        a[j][u] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (iok[j] && u < p.KS) a[j][u] = *reinterpret_cast<const f32x4*>(src[j] + u * kstride);
+      for (int pp = 0; pp < NPW; ++pp) {
+        const int64_t kp = k_lo + pp * KSTEP + q4 * P;
+        const bool ok = nok[c2] && kp < k_hi;
+        av[c2][pp] = sel16(ok, ld16(arow[c2] + (ok ? kp : 0) * ES));
       }
-    u32x4 yv[PASSES];
+  }
+  const bool requested = route_gate(p.rt, g, L.rt, rr);
+  if constexpr (!SPEC) {
+    // only adapters some token asked for read their weights
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+      for (int pp = 0; pp < NPW; ++pp) {
+        const int64_t kp = k_lo + pp * KSTEP + q4 * P;
+        av[c2][pp] = u32x4{0u, 0u, 0u, 0u};
+        if (requested && nok[c2] && kp < k_hi) av[c2][pp] = ld16(arow[c2] + kp * ES);
+      }
+  }
+  const int n_g = route_list(g, L.rt, rr);
+  if (!active || n_g == 0) return;
+  const uint64_t tag = static_cast<uint64_t>(L.epoch + 1u) << 32;
+  uint64_t* part = p.part + static_cast<int64_t>(g - 1) * p.region;
+
+  for (int rt0 = 0; rt0 < n_g; rt0 += 32) {
+    u32x4 xv[2][NPW];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int slot = rt0 + 16 * rt + i16;
+      const bool rok = slot < n_g;
+      const char* xrow = static_cast<const char*>(p.x) + static_cast<int64_t>(L.rt.tok[rok ? slot : rt0]) * p.ldx * ES;
+#pragma unroll
+      for (int pp = 0; pp < NPW; ++pp) {
+        const int64_t kp = k_lo + pp * KSTEP + q4 * P;
+        xv[rt][pp] = u32x4{0u, 0u, 0u, 0u};
+        if (rok && kp < k_hi) xv[rt][pp] = ld16(xrow + kp * ES);
+      }
+    }
+    // acc[rt][c2]: token slots rt0 + 16*rt + 4*q4 + e, column n[c2]
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) {
+        acc[rt][c2] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int pp = 0; pp < NPW; ++pp) acc[rt][c2] = mfma16<BF16>(xv[rt][pp], av[c2][pp], acc[rt][c2]);
+      }
+
+    // fixed-order cross-wave sum: ((w0 + w1) + w2) + w3
+    if (wave > 0) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) L.u.red[wave - 1][v][l] = acc[v >> 3][(v >> 2) & 1][v & 3];
+    }
+    lds_barrier();
+    if (wave == 0) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int rt = v >> 3, c2 = (v >> 2) & 1, e = v & 3;
+        const int slot = rt0 + 16 * rt + 4 * q4 + e;
+        const float val = ((acc[rt][c2][e] + L.u.red[0][v][l]) + L.u.red[1][v][l]) + L.u.red[2][v][l];
+        if (nok[c2] && slot < n_g)
+          __hip_atomic_store(part + (static_cast<int64_t>(kc) * p.cap + slot) * p.zw + n[c2],
+                             tag | __float_as_uint(val), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    lds_barrier();   // red is reused by the next row chunk
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Consumer: each wave owns NQ 16-column blocks of the tile (block q*4 + wave)
+// and holds their lora_B rows for the whole rank in registers.  Per 32-token
+// row chunk: y rows are loaded, the tagged partials are polled and summed in
+// ks order into the chunk's shrink rows in LDS (rounded like a stored z), the
+// MFMA deltas go through LDS in 128-column halves, and each thread adds and
+// stores 16-byte pieces of its token rows.
+// ----------------------------------------------------------------------------
+template <bool BF16, int NQ, bool SPEC>
+__device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16>& L, int cid) {
+  constexpr int NT = 64 * NQ;
+  constexpr int NH = NQ / 2;            // 128-column halves
+  constexpr int P = Elt<BF16>::kPerPiece;
+  constexpr int ES = Elt<BF16>::kSize;
+  constexpr int KSTEP = 4 * P;          // rank per MFMA (over the 4 lane groups)
+  constexpr int KG = kSmMaxRank / KSTEP;
+  constexpr int EPL = 16 / ES;          // y elements per 16-byte piece
+  constexpr int LPR = kHalf / EPL;      // lanes per y row in a half
+  constexpr int RPP = kSmT / LPR;       // y rows per workgroup-wide access
+  constexpr int PASSES = 32 / RPP;
+  constexpr int EPT = 4;                // shrink elements per thread and batch
+  constexpr int NEB = 32 * kSmMaxRank / (kSmT * EPT);   // batches (rank <= 64)
+
+  const int nt = cid % p.NNT;
+  const int g = cid / p.NNT + 1;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int l = tid & 63;
+  const int i16 = l & 15;
+  const int q4 = l >> 4;
+  const int r = p.tab.rank[g];
+  const int n_tile0 = nt * NT;
+  const int s = tile_slice<NT>(p.si, nt);
+  const int zc0 = s * r;                 // this slice's columns in the adapter's shrink row
+
+  if (tid == 0) L.epoch = read_epoch(p, g);
+  RouteRegs rr;
+  route_issue(p.rt, rr);
+  // lora_B rows of this wave's column blocks (n < out_total always; rank 0
+  // reads element 0 of the pack and is masked)
+  u32x4 bv[NQ][KG];
+  const char* brow[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int n = n_tile0 + 16 * (q * 4 + wave) + i16;
+    brow[q] = static_cast<const char*>(p.b_pack) + (p.tab.b_off[g] + static_cast<int64_t>(n) * r) * ES;
+  }
+  if constexpr (SPEC) {
+    // unconditional loads from clamped addresses (see the producer)
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+      for (int kg = 0; kg < KG; ++kg) {
+        const int k0 = kg * KSTEP + q4 * P;
+        const bool ok = k0 < r;
+        bv[q][kg] = sel16(ok, ld16(brow[q] + (ok ? k0 : 0) * ES));
+      }
+  }
+  const bool requested = route_gate(p.rt, g, L.rt, rr);
+  if constexpr (!SPEC) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+      for (int kg = 0; kg < KG; ++kg) {
+        const int k0 = kg * KSTEP + q4 * P;
+        bv[q][kg] = u32x4{0u, 0u, 0u, 0u};
+        if (requested && k0 < r) bv[q][kg] = ld16(brow[q] + k0 * ES);
+      }
+  }
+  const int n_g = route_list(g, L.rt, rr);
+  if (r == 0 || n_g == 0) return;       // no producer wrote partials for it
+  const uint32_t epoch = L.epoch;
+  const uint32_t want = epoch + 1u;
+  const uint64_t* part = p.part + static_cast<int64_t>(g - 1) * p.region;
+  const int64_t kstride = static_cast<int64_t>(p.cap) * p.zw;
+  int32_t* sync_g = p.sync + kSyncLine * g;
+  int done_before = -1;
+  const int cx = (tid % LPR) * EPL;
+
+  for (int rt0 = 0; rt0 < n_g; rt0 += 32) {
+    // y pieces of this row chunk (issued before the wait)
+    u32x4 yv[NH][PASSES];
     int64_t yoff[PASSES];
     bool rok[PASSES];
 #pragma unroll
     for (int ps = 0; ps < PASSES; ++ps) {
-      const int row = ps * RPI + tid / LPR;
-      rok[ps] = rt0 + row < n_g;
-      yoff[ps] = static_cast<int64_t>(rok[ps] ? (ent[ps] & kTokMask) : 0) * p.ldy + n_tile0 + cx;
-      yv[ps] = u32x4{0u, 0u, 0u, 0u};
-      if (rok[ps]) yv[ps] = ld16(static_cast<const char*>(p.y) + yoff[ps] * ES);
+      const int row = rt0 + ps * RPP + tid / LPR;
+      rok[ps] = row < n_g;
+      yoff[ps] = static_cast<int64_t>(rok[ps] ? L.rt.tok[row] : 0) * p.ldy + n_tile0 + cx;
+#pragma unroll
+      for (int hf = 0; hf < NH; ++hf) {
+        yv[hf][ps] = u32x4{0u, 0u, 0u, 0u};
+        if (rok[ps]) yv[hf][ps] = ld16(static_cast<const char*>(p.y) + (yoff[ps] + hf * kHalf) * ES);
+      }
     }
-    // shrink rows: partials summed in ks order, rounded like a stored z
-    f32x4 sum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+
+    // shrink rows of the chunk: element m of batch eb of this thread is
+    // (row, c) = divmod(tid + 256*(EPT*eb + m), r); partials polled kKsGrp at
+    // a time and summed in ks order, then rounded like a stored z
+    for (int eb = 0; eb < NEB; ++eb) {
+      if (kSmT * EPT * eb >= 32 * r) break;
+      float sum[EPT];
+      const uint64_t* src[EPT];
+      bool eok[EPT];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int m = 0; m < EPT; ++m) {
+        const int e = tid + kSmT * (EPT * eb + m);
+        const int row = e / r;
+        const int c = e - row * r;
+        eok[m] = e < 32 * r && rt0 + row < n_g;
+        src[m] = part + static_cast<int64_t>(rt0 + (eok[m] ? row : 0)) * p.zw + zc0 + (eok[m] ? c : 0);
+        sum[m] = 0.f;
+      }
+      for (int ks0 = 0; ks0 < p.KS; ks0 += kKsGrp) {
+        uint64_t pv[EPT][kKsGrp];
+        const int64_t t_start = wall_clock64();
+        for (;;) {
+          bool ready = true;
 #pragma unroll
-      for (int u = 0; u < kPartGrp; ++u)
-        if (u < p.KS) sum[j] += a[j][u];
-    for (int ks0 = kPartGrp; ks0 < p.KS; ks0 += kPartGrp) {
+          for (int m = 0; m < EPT; ++m)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+            for (int u = 0; u < kKsGrp; ++u) {
+              pv[m][u] = static_cast<uint64_t>(want) << 32;
+              if (eok[m] && ks0 + u < p.KS)
+                pv[m][u] = __hip_atomic_load(src[m] + (ks0 + u) * kstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
 #pragma unroll
-        for (int u = 0; u < kPartGrp; ++u) {
-          a[j][u] = f32x4{0.f, 0.f, 0.f, 0.f};
-          if (iok[j] && ks0 + u < p.KS) a[j][u] = *reinterpret_cast<const f32x4*>(src[j] + (ks0 + u) * kstride);
+          for (int m = 0; m < EPT; ++m)
+#pragma unroll
+            for (int u = 0; u < kKsGrp; ++u) ready = ready && static_cast<uint32_t>(pv[m][u] >> 32) == want;
+          if (ready) break;
+          if (wall_clock64() - t_start > p.timeout_ticks) {
+            __hip_atomic_fetch_or(p.sync + kSyncErrWord, kErrTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
         }
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+        for (int m = 0; m < EPT; ++m)
 #pragma unroll
-        for (int u = 0; u < kPartGrp; ++u)
-          if (ks0 + u < p.KS) sum[j] += a[j][u];
-    }
+          for (int u = 0; u < kKsGrp; ++u)
+            if (ks0 + u < p.KS) sum[m] += __uint_as_float(static_cast<uint32_t>(pv[m][u]));
+      }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int it = tid + j * kSmT;
-      if (it < nitems) {
-        const int row = it / per_row;
-        const int c4 = (it - row * per_row) * 4;
-        char* dst = zs + (row * ZLD + c4) * ES;
-        if constexpr (BF16) {
-          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(sum[j].x, sum[j].y), pack_bf16x2(sum[j].z, sum[j].w));
-        } else {
-          *reinterpret_cast<f32x4*>(dst) = sum[j];
+      for (int m = 0; m < EPT; ++m) {
+        const int e = tid + kSmT * (EPT * eb + m);
+        if (e < 32 * r) {
+          const int row = e / r;
+          const int c = e - row * r;
+          char* dst = L.u.co.zs + (row * kZld + c) * ES;
+          if constexpr (BF16) *reinterpret_cast<uint16_t*>(dst) = f32_to_bf16_bits(sum[m]);
+          else *reinterpret_cast<float*>(dst) = sum[m];
         }
       }
     }
     lds_barrier();
+    // every thread has its last partials: count this consumer done (the
+    // returned count is only looked at when the workgroup ends)
+    if (tid == 0 && rt0 + 32 >= n_g)
+      done_before = __hip_atomic_fetch_add(sync_g + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-    f32x16 acc[NBW];
+    // D[t][n] = sum_k z[t][k] B[n][k]; acc[rt][q]: token 16*rt + 4*q4 + e of
+    // the chunk, column n_tile0 + 16*(q*4 + wave) + i16
+    f32x4 acc[2][NQ];
 #pragma unroll
-    for (int q = 0; q < NBW; ++q) {
-      acc[q] = f32x16{};
+    for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-      for (int kg = 0; kg < KG; ++kg) {
-        if (kg * KSTEP < r) {
-          const int k0 = kg * KSTEP + KHALF * h;
-          u32x4 za = u32x4{0u, 0u, 0u, 0u};
-          if (k0 < r) za = *reinterpret_cast<const u32x4*>(zs + (i * ZLD + k0) * ES);
-          acc[q] = mfma_piece<BF16>(za, bv[q][kg], acc[q]);
+      for (int q = 0; q < NQ; ++q) acc[rt][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kg = 0; kg < KG; ++kg) {
+      if (kg * KSTEP < r) {
+        const int k0 = kg * KSTEP + q4 * P;
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          const bool kin = k0 < r;
+          const u32x4 za =
+              sel16(kin, *reinterpret_cast<const u32x4*>(L.u.co.zs + ((16 * rt + i16) * kZld + (kin ? k0 : 0)) * ES));
+#pragma unroll
+          for (int q = 0; q < NQ; ++q) acc[rt][q] = mfma16<BF16>(za, bv[q][kg], acc[rt][q]);
         }
       }
     }
 #pragma unroll
-    for (int q = 0; q < NBW; ++q)
+    for (int hf = 0; hf < NH; ++hf) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) dtile[mfma32_row(v, l)][32 * (wave * NBW + q) + i] = acc[q][v];
-    lds_barrier();
+      for (int qq = 0; qq < 2; ++qq) {
+        const int q = 2 * hf + qq;
+        const int col = 16 * (qq * 4 + wave) + i16;      // within the half
 #pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) {
-      if (rok[ps]) {
-        const int row = ps * RPI + tid / LPR;
-        float d[EPL];
+        for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) d[e] = dtile[row][cx + e];
-        add_store_y<BF16>(p.y, yoff[ps], yv[ps], d);
+          for (int e = 0; e < 4; ++e) L.u.co.dtile[16 * rt + 4 * q4 + e][col] = acc[rt][q][e];
       }
-    }
-  };
-
-  tile(0);
-  for (int rt0 = 32; rt0 < n_g; rt0 += 32) {
-    lds_barrier();   // zs / dtile are reused by this tile
+      lds_barrier();
 #pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) {
-      const int row = rt0 + ps * RPI + tid / LPR;
-      ent[ps] = row < n_g ? list[row] : 0;
+      for (int ps = 0; ps < PASSES; ++ps) {
+        if (rok[ps]) {
+          const int row = ps * RPP + tid / LPR;
+          float d[EPL];
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) d[e] = L.u.co.dtile[row][cx + e];
+          add_store_y<BF16>(p.y, yoff[ps] + hf * kHalf, yv[hf][ps], d);
+        }
+      }
+      lds_barrier();   // dtile / zs are reused
     }
-    tile(rt0);
   }
+  if (done_before == p.NNT - 1) {
+    // the last consumer of g: the next launch uses the next epoch
+    __hip_atomic_store(sync_g + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(sync_g, static_cast<int32_t>(epoch + 1u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+template <bool BF16, int NPW, int NQ, bool SPEC>
+__global__ __launch_bounds__(kSmT) void small_fused_kernel(FusedParams p) {
+  __shared__ FusedLds<BF16> lds;
+  const int bid = static_cast<int>(blockIdx.x);
+  if (bid < p.NP) produce<BF16, NPW, 64 * NQ, SPEC>(p, lds, bid);
+  else consume<BF16, NQ, SPEC>(p, lds, bid - p.NP);
 }
 
 // ----------------------------------------------------------------------------
 // Host-side plan.
 // ----------------------------------------------------------------------------
 struct SmallPlan {
-  int NPW, KS, NCB, cap, zw, NBW, NNT;
-  int64_t part_bytes, ws_bytes;
+  int NPW, KS, NCB, cap, zw, NQ, NNT;
+  int64_t region_bytes;       // one adapter's tagged partials
 };
 
-constexpr int kSmTargetShrinkWgs = 192;
+// about this many producer workgroups: fewer means fewer split-K partials for
+// each consumer to wait for and add, more means more loads in flight
+#ifndef GS_SMALL_TARGET_PRODUCERS
+#define GS_SMALL_TARGET_PRODUCERS 128
+#endif
+constexpr int kSmTargetShrinkWgs = GS_SMALL_TARGET_PRODUCERS;
+constexpr int64_t kDefaultTimeoutTicks = 2000000;   // 20 ms of the 100 MHz wall clock
+constexpr int64_t kSyncBytes = 4 * kSyncLine * (kSmMaxAdapters + 1);
 
 SmallPlan plan_small(int64_t T, int H, int S, int NA, int max_rank, bool bf16, int out_total,
                      const int32_t* slice_bounds) {
   SmallPlan pl{};
   pl.zw = S * max_rank;
   pl.NCB = (pl.zw + 31) / 32;
-  const int kpair = bf16 ? 16 : 8;       // k covered by one piece of each lane half
-  // smallest k-split (fewest partials for the expand to add) that still gives
-  // about kSmTargetShrinkWgs workgroups, with at most 2 partial groups
-  int npw = 16;
+  const int kstep = bf16 ? 32 : 16;      // k of one piece over the 4 lane groups
+  // largest pieces per wave (fewest partials for the consumers to add) that
+  // still gives about kSmTargetShrinkWgs producers
+  int npw = 8;
   int ks = 1;
   for (;;) {
-    ks = (H + 4 * npw * kpair - 1) / (4 * npw * kpair);
-    if (static_cast<int64_t>(NA) * pl.NCB * ks >= kSmTargetShrinkWgs || npw == 2) break;
-    const int ks_next = (H + 2 * npw * kpair - 1) / (2 * npw * kpair);
-    if (ks_next > 2 * kPartGrp) break;
+    ks = (H + 4 * npw * kstep - 1) / (4 * npw * kstep);
+    if (static_cast<int64_t>(NA) * pl.NCB * ks >= kSmTargetShrinkWgs || npw == 4) break;
     npw >>= 1;
   }
   pl.NPW = npw;
@@ -543,26 +724,30 @@ SmallPlan plan_small(int64_t T, int H, int S, int NA, int max_rank, bool bf16, i
   bool all256 = true;
   for (int s = 0; s < S; ++s)
     if ((slice_bounds[s + 1] - slice_bounds[s]) % 256 != 0) all256 = false;
-  pl.NBW = all256 ? 2 : 1;
-  pl.NNT = out_total / (128 * pl.NBW);
-  pl.part_bytes = static_cast<int64_t>(pl.KS) * NA * pl.cap * pl.zw * 4;
-  pl.ws_bytes = pl.part_bytes + static_cast<int64_t>(NA) * pl.cap * 4;
+  pl.NQ = all256 ? 4 : 2;
+  pl.NNT = out_total / (64 * pl.NQ);
+  pl.region_bytes = static_cast<int64_t>(pl.KS) * pl.cap * pl.zw * 8;
   return pl;
 }
 
-template <bool BF16>
-void launch_small(const SmallPlan& pl, const SmallShrinkParams& sp, const SmallExpandParams& ep, int NA,
-                  hipStream_t st) {
-  const dim3 g1(static_cast<unsigned>(pl.NCB), static_cast<unsigned>(pl.KS), static_cast<unsigned>(NA));
+template <bool BF16, int NQ, bool SPEC>
+void launch_fused_nq(const SmallPlan& pl, const FusedParams& fp, unsigned grid, hipStream_t st) {
   switch (pl.NPW) {
-    case 16: hipLaunchKernelGGL((shrink_small_kernel<BF16, 16>), g1, dim3(kSmT), 0, st, sp); break;
-    case 8: hipLaunchKernelGGL((shrink_small_kernel<BF16, 8>), g1, dim3(kSmT), 0, st, sp); break;
-    case 4: hipLaunchKernelGGL((shrink_small_kernel<BF16, 4>), g1, dim3(kSmT), 0, st, sp); break;
-    default: hipLaunchKernelGGL((shrink_small_kernel<BF16, 2>), g1, dim3(kSmT), 0, st, sp); break;
+    case 8: hipLaunchKernelGGL((small_fused_kernel<BF16, 8, NQ, SPEC>), dim3(grid), dim3(kSmT), 0, st, fp); break;
+    default: hipLaunchKernelGGL((small_fused_kernel<BF16, 4, NQ, SPEC>), dim3(grid), dim3(kSmT), 0, st, fp); break;
   }
-  const dim3 g2(static_cast<unsigned>(pl.NNT), static_cast<unsigned>(NA));
-  if (pl.NBW == 2) hipLaunchKernelGGL((expand_small_kernel<BF16, 2>), g2, dim3(kSmT), 0, st, ep);
-  else hipLaunchKernelGGL((expand_small_kernel<BF16, 1>), g2, dim3(kSmT), 0, st, ep);
+}
+
+template <bool BF16, bool SPEC>
+void launch_fused_spec(const SmallPlan& pl, const FusedParams& fp, unsigned grid, hipStream_t st) {
+  if (pl.NQ == 4) launch_fused_nq<BF16, 4, SPEC>(pl, fp, grid, st);
+  else launch_fused_nq<BF16, 2, SPEC>(pl, fp, grid, st);
+}
+
+template <bool BF16>
+void launch_fused(const SmallPlan& pl, const FusedParams& fp, unsigned grid, bool spec, hipStream_t st) {
+  if (spec) launch_fused_spec<BF16, true>(pl, fp, grid, st);
+  else launch_fused_spec<BF16, false>(pl, fp, grid, st);
 }
 
 }  // namespace
@@ -593,8 +778,10 @@ int64_t gs_small_workspace_bytes(int32_t dtype, int64_t num_tokens, int32_t hidd
   if (num_tokens <= 0 || hidden <= 0 || slice_bounds == nullptr) return 256;
   const SmallPlan pl = plan_small(num_tokens, hidden, num_slices, num_adapters, max_rank, dtype == GS_DTYPE_BF16,
                                   out_total, slice_bounds);
-  return pl.ws_bytes < 256 ? 256 : pl.ws_bytes;
+  return kSmMaxAdapters * pl.region_bytes;
 }
+
+int64_t gs_small_sync_bytes(void) { return kSyncBytes; }
 
 int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t* positions,
                            const int32_t* cu_seqlens, const int64_t* act_offsets, int32_t num_seqs,
@@ -602,7 +789,8 @@ int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t*
                            int64_t num_tokens, int32_t hidden, int32_t out_total, const int32_t* slice_bounds,
                            int32_t num_slices, const void* a_pack, const int64_t* a_off, const void* b_pack,
                            const int64_t* b_off, const int32_t* ranks, int32_t num_adapters, int32_t max_rank,
-                           void* workspace, int64_t workspace_bytes, void* stream) {
+                           void* workspace, int64_t workspace_bytes, int32_t* sync, int64_t sync_bytes,
+                           int32_t speculate, void* stream) {
   const char* who = "gs_switched_lora_small";
   GS_CHECK_ARG(dtype == GS_DTYPE_BF16 || dtype == GS_DTYPE_FP32, "%s: dtype=%d", who, dtype);
   const int nseq = (cu_seqlens != nullptr) ? num_seqs : 1;
@@ -624,57 +812,54 @@ int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t*
     GS_CHECK_ARG(a_off[g] >= 0 && a_off[g] % 8 == 0 && b_off[g] >= 0 && b_off[g] % 8 == 0,
                  "%s: adapter %d offsets must be non-negative multiples of 8", who, g);
   }
+  GS_CHECK_ARG(sync != nullptr && (reinterpret_cast<uintptr_t>(sync) & 7u) == 0, "%s: sync must be 8-byte aligned",
+               who);
+  GS_CHECK_ARG(sync_bytes >= kSyncBytes, "%s: sync buffer of %lld bytes needed (got %lld)", who,
+               (long long)kSyncBytes, (long long)sync_bytes);
   if (num_tokens == 0) return GS_OK;
   const bool bf16 = dtype == GS_DTYPE_BF16;
   const SmallPlan pl = plan_small(num_tokens, hidden, num_slices, num_adapters, max_rank, bf16, out_total,
                                   slice_bounds);
-  if (workspace_bytes < pl.ws_bytes) {
-    set_error("%s: workspace of %lld bytes needed (got %lld)", who, (long long)pl.ws_bytes,
+  // adapter regions are a fixed fraction of the workspace, whatever the shape
+  const int64_t region_bytes = (workspace_bytes / kSmMaxAdapters) & ~int64_t(15);
+  if (region_bytes < pl.region_bytes) {
+    set_error("%s: workspace of %lld bytes needed (got %lld)", who, (long long)(kSmMaxAdapters * pl.region_bytes),
               (long long)workspace_bytes);
     return GS_ERR_WORKSPACE;
   }
-  SmallRoute rt{eff_ids != nullptr ? nullptr : req_ids, positions, cu_seqlens, act_offsets, eff_ids,
-                static_cast<int>(num_tokens), nseq, num_adapters};
-  SmallTab at{}, bt{};
+  FusedParams fp{};
+  fp.rt = SmallRoute{eff_ids != nullptr ? nullptr : req_ids, positions, cu_seqlens, act_offsets, eff_ids,
+                     static_cast<int>(num_tokens), nseq, num_adapters};
   for (int g = 0; g <= num_adapters; ++g) {
-    at.off[g] = a_off[g];
-    at.rank[g] = ranks[g];
-    bt.off[g] = b_off[g];
-    bt.rank[g] = ranks[g];
+    fp.tab.a_off[g] = a_off[g];
+    fp.tab.b_off[g] = b_off[g];
+    fp.tab.rank[g] = ranks[g];
   }
-  SmallShrinkParams sp{};
-  sp.rt = rt;
-  sp.x = x;
-  sp.ldx = ldx;
-  sp.H = hidden;
-  sp.a_pack = a_pack;
-  sp.S = num_slices;
-  sp.KS = pl.KS;
-  sp.NCB = pl.NCB;
-  sp.part = static_cast<float*>(workspace);
-  int32_t* lists = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + pl.part_bytes);
-  sp.lists = lists;
-  sp.cap = pl.cap;
-  sp.zw = pl.zw;
-  sp.tab = at;
-  SmallExpandParams ep{};
-  ep.lists = lists;
-  ep.NA = num_adapters;
-  ep.y = y;
-  ep.ldy = ldy;
-  ep.out_total = out_total;
-  ep.si.S = num_slices;
-  for (int s = 0; s <= num_slices; ++s) ep.si.bounds[s] = slice_bounds[s];
-  ep.b_pack = b_pack;
-  ep.part = static_cast<const float*>(workspace);
-  ep.KS = pl.KS;
-  ep.cap = pl.cap;
-  ep.zw = pl.zw;
-  ep.NNT = pl.NNT;
-  ep.tab = bt;
+  fp.x = x;
+  fp.ldx = ldx;
+  fp.H = hidden;
+  fp.a_pack = a_pack;
+  fp.S = num_slices;
+  fp.KS = pl.KS;
+  fp.NCB = pl.NCB;
+  fp.NP = pl.NCB * pl.KS * num_adapters;
+  fp.part = static_cast<uint64_t*>(workspace);
+  fp.region = region_bytes / 8;
+  fp.cap = pl.cap;
+  fp.zw = pl.zw;
+  fp.y = y;
+  fp.ldy = ldy;
+  fp.out_total = out_total;
+  fp.si.S = num_slices;
+  for (int s = 0; s <= num_slices; ++s) fp.si.bounds[s] = slice_bounds[s];
+  fp.b_pack = b_pack;
+  fp.NNT = pl.NNT;
+  fp.sync = sync;
+  fp.timeout_ticks = kDefaultTimeoutTicks;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (bf16) launch_small<true>(pl, sp, ep, num_adapters, st);
-  else launch_small<false>(pl, sp, ep, num_adapters, st);
+  const unsigned grid = static_cast<unsigned>(fp.NP + pl.NNT * num_adapters);
+  if (bf16) launch_fused<true>(pl, fp, grid, speculate != 0, st);
+  else launch_fused<false>(pl, fp, grid, speculate != 0, st);
   GS_CHECK_LAUNCH(who);
   return GS_OK;
 }

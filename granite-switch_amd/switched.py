@@ -321,7 +321,7 @@ def small_workspace_bytes(packed: "PackedAdapters", num_tokens: int) -> int:
 
 
 def small_eligible(packed: "PackedAdapters", num_tokens: int, num_seqs: int = 1) -> bool:
-    """True when the two-launch small-batch path handles this module and batch.
+    """True when the one-launch small-batch kernel can run this module and batch.
 
     It needs the adapters' host-side offset tables (``PackedAdapters.from_slices``
     keeps them) and decode-sized shapes: T <= 1024, <= 64 adapters, max rank
@@ -334,12 +334,95 @@ def small_eligible(packed: "PackedAdapters", num_tokens: int, num_seqs: int = 1)
                                               packed.max_rank))
 
 
+def small_preferred(packed: "PackedAdapters", num_tokens: int, num_seqs: int = 1) -> bool:
+    """The ``auto`` path choice: the small-batch kernel when it is eligible and
+    the batch averages at most one 32-token row tile per adapter (decode); the
+    segment kernels otherwise, which spread longer per-adapter runs over more
+    workgroups."""
+    return small_eligible(packed, num_tokens, num_seqs) and num_tokens <= max(64, 32 * packed.num_adapters)
+
+
 def reserve_workspace(device: torch.device, nbytes: int) -> None:
     """Pre-allocate the per-device shrink workspace (before graph capture)."""
     key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         _workspaces[key] = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+
+
+# The small-batch kernel's state, one set per device: its sync buffer (the
+# error word and each adapter's epoch and done count) and its workspace of
+# epoch-tagged partials.  Both start zeroed; the workspace is used by nothing
+# else, so it only ever holds tags of earlier epochs.
+_sync_buffers: dict = {}
+_small_workspaces: dict = {}
+_ERR_WORD = 2
+_SYNC_LINE = 32
+
+
+def _dev_key(device: torch.device):
+    return (device.type, device.index if device.index is not None else torch.cuda.current_device())
+
+
+def small_sync_buffer(device: torch.device) -> torch.Tensor:
+    """The per-device sync buffer of the small-batch kernel (int32 words)."""
+    key = _dev_key(device)
+    buf = _sync_buffers.get(key)
+    if buf is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("switched-LoRA sync buffer must be allocated before graph capture "
+                               "(call reserve_small_workspace or run once eagerly)")
+        buf = torch.zeros(int(_lib.load().gs_small_sync_bytes()) // 4, dtype=torch.int32, device=device)
+        _sync_buffers[key] = buf
+    return buf
+
+
+def small_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """The per-device workspace of the small-batch kernel (at least ``nbytes``)."""
+    key = _dev_key(device)
+    ws = _small_workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("switched-LoRA small-batch workspace must be allocated before graph capture "
+                               "(call reserve_small_workspace or run once eagerly)")
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _small_workspaces[key] = ws
+    return ws
+
+
+def reserve_small_workspace(device: torch.device, nbytes: int) -> None:
+    """Pre-allocate the small-batch kernel's workspace and sync buffer (before graph capture)."""
+    small_sync_buffer(device)
+    small_workspace(device, nbytes)
+
+
+def small_status(device: torch.device) -> int:
+    """Error word of the small-batch kernel on ``device`` (synchronises).
+
+    0 = every call so far handed off cleanly; bit 0 = an expand workgroup gave
+    up waiting for its shrink partials, so that call's output was wrong.
+    ``small_reset`` clears the state.
+    """
+    return int(small_sync_buffer(device)[_ERR_WORD].item())
+
+
+def small_pending_count(device: torch.device) -> int:
+    """Sum of the adapters' done counts (synchronises).
+
+    Every completed call leaves them all at 0: the last consumer of an adapter
+    resets its count when it advances the adapter's epoch."""
+    return int(small_sync_buffer(device)[_SYNC_LINE + 1::_SYNC_LINE].sum().item())
+
+
+def small_reset(device: torch.device) -> None:
+    """Zero the small-batch kernel's epoch, error word and partial workspace.
+
+    The epoch restarts at 0, so the workspace must be cleared with it (a stale
+    pair must never carry a tag the next epochs will use)."""
+    small_sync_buffer(device).zero_()
+    ws = _small_workspaces.get(_dev_key(device))
+    if ws is not None:
+        ws.zero_()
 
 
 # ---------------------------------------------------------------------------
@@ -410,25 +493,32 @@ def _xy2(x: torch.Tensor, y: torch.Tensor, packed: PackedAdapters):
 
 def _call_small(x2, y2, packed, eff_ids=None, req=None, pos=None, cu=None, off=None, num_seqs=1):
     T = x2.shape[0]
-    ws = _workspace(x2.device, small_workspace_bytes(packed, T))
+    ws = small_workspace(x2.device, small_workspace_bytes(packed, T))
+    sync = small_sync_buffer(x2.device)
+    # issue every adapter's weight loads before the routing is known when most
+    # adapters are likely to have tokens
+    speculate = int(T >= 2 * packed.num_adapters)
     i64 = lambda v: (ctypes.c_int64 * len(v))(*[int(u) for u in v])
     _lib.call("gs_switched_lora_small", _dtype_code(x2), _lib.ptr(req), _lib.ptr(pos), _lib.ptr(cu), _lib.ptr(off),
               int(num_seqs), _lib.ptr(eff_ids), x2.data_ptr(), x2.stride(0), y2.data_ptr(), y2.stride(0), T,
               packed.hidden, packed.out_total, _i32_array(packed.slice_bounds), packed.num_slices,
               packed.a_pack.data_ptr(), i64(packed.a_off_host), packed.b_pack.data_ptr(), i64(packed.b_off_host),
               _i32_array(packed.ranks_host), packed.num_adapters, packed.max_rank, ws.data_ptr(), ws.numel(),
-              _lib.stream_ptr(x2.device))
+              sync.data_ptr(), sync.numel() * 4, speculate, _lib.stream_ptr(x2.device))
 
 
 def switched_lora_routed_(y: torch.Tensor, x: torch.Tensor, adapter_ids: torch.Tensor, packed: PackedAdapters,
-                          positions=None, cu_seqlens=None, act_offsets=None) -> torch.Tensor:
+                          positions=None, cu_seqlens=None, act_offsets=None, path: str = "auto") -> torch.Tensor:
     """In place: y += switched-LoRA delta of x, routed straight from the per-token ids.
 
     ``adapter_ids`` / ``positions`` / ``cu_seqlens`` / ``act_offsets`` have the
-    meaning of ``build_segments``.  Decode-sized batches (``small_eligible``)
-    run in two launches that gate and group the tokens themselves; larger ones
-    build segments first and run ``switched_lora_``.
+    meaning of ``build_segments``.  ``path="auto"``: decode-sized batches
+    (``small_preferred``) run in one launch that gates and groups the tokens
+    itself; larger ones build segments first and run ``switched_lora_``.
+    ``"small"`` / ``"segments"`` force one of the two.
     """
+    if path not in ("auto", "small", "segments"):
+        raise ValueError(f"unknown path {path!r}")
     x2, y2 = _xy2(x, y, packed)
     dev = x2.device
     ids = _as_i64(adapter_ids.reshape(-1), dev)
@@ -443,22 +533,24 @@ def switched_lora_routed_(y: torch.Tensor, x: torch.Tensor, adapter_ids: torch.T
     num_seqs = 1 if cu is None else cu.numel() - 1
     if off is not None and off.numel() != num_seqs:
         raise ValueError("act_offsets must have one entry per sequence")
-    if small_eligible(packed, T, num_seqs):
+    if path == "small" or (path == "auto" and small_preferred(packed, T, num_seqs)):
+        if not small_eligible(packed, T, num_seqs):
+            raise ValueError("this module / batch is outside the small-batch kernel's limits")
         _call_small(x2, y2, packed, req=ids, pos=pos, cu=cu if off is not None else None, off=off,
                     num_seqs=num_seqs if off is not None else 1)
         return y
     segs = build_segments(ids, packed.num_adapters, pos, cu, off)
-    return switched_lora_(y, x, segs, packed)
+    return switched_lora_(y, x, segs, packed, path="segments")
 
 
 def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed: PackedAdapters,
                    z: torch.Tensor | None = None, path: str = "auto") -> torch.Tensor:
-    """In place: y += switched-LoRA delta of x (two launches).
+    """In place: y += switched-LoRA delta of x.
 
-    ``path="auto"``: decode-sized batches (``small_eligible``) take the
-    small-batch kernels, which group tokens from ``segments.eff_ids``
-    themselves; larger ones the segment kernels.  ``"small"`` / ``"segments"``
-    force one of the two.  On the segment path ``z`` is optional scratch
+    ``path="auto"``: decode-sized batches (``small_preferred``) take the
+    one-launch small-batch kernel, which groups tokens from
+    ``segments.eff_ids`` itself; larger ones the two segment kernels.
+    ``"small"`` / ``"segments"`` force one of the two.  On the segment path ``z`` is optional scratch
     [T, S*max_rank] of y's dtype (allocated when omitted) -- when the shrink
     is split over the hidden dimension the expand reads the fp32 partials from
     the workspace and z is not written.
@@ -470,7 +562,7 @@ def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed:
     if T != segments.num_tokens:
         raise ValueError("x / y shapes do not match the segments")
     _check_segments(segments, packed)
-    if path == "small" or (path == "auto" and T and small_eligible(packed, T)):
+    if path == "small" or (path == "auto" and T and small_preferred(packed, T)):
         _call_small(x2, y2, packed, eff_ids=segments.eff_ids)
         return y
     zw = packed.num_slices * packed.max_rank
@@ -545,7 +637,14 @@ __all__ = [
     "switched_lora_",
     "switched_lora_routed_",
     "small_eligible",
+    "small_preferred",
     "small_workspace_bytes",
+    "small_sync_buffer",
+    "small_workspace",
+    "reserve_small_workspace",
+    "small_status",
+    "small_pending_count",
+    "small_reset",
     "shrink_workspace",
     "reserve_workspace",
     "algorithmic_bytes",

@@ -25,7 +25,7 @@
  *   gs_switched_lora_small the same shrink/expand/add for decode-sized batches,
  *                          with the per-adapter token grouping of
  *                          src/granite_switch/hf/core/lora.py:127-135 done
- *                          inside the two kernels
+ *                          inside the one kernel
  *   gs_compute_bitmasks    torch.ops.granite_switch.compute_per_module_bitmasks
  *                          (src/granite_switch/vllm/core/lora_kernel_meta.py:61-91,
  *                          169-182) plus the remap gather at :294
@@ -153,10 +153,12 @@ int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t
                      const int32_t* perm, void* z, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
- * Small-batch switched-LoRA in two launches, no segment build (decode-sized
+ * Small-batch switched-LoRA in ONE launch, no segment build (decode-sized
  * batches).  Same result as gs_build_segments + gs_switched_lora: every
  * workgroup gates and lists the tokens of its own adapter from the routing
- * input, so no metadata kernel runs first.
+ * input, so no metadata kernel runs first, and the expand workgroups of the
+ * launch wait (bounded) for the shrink partials they read, which carry the
+ * launch's epoch tag.
  *
  * Routing input, one of:
  *   eff_ids [T] int32 -- ids already gated (e.g. gs_build_segments' eff_ids);
@@ -167,21 +169,33 @@ int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t
  * kernel arguments), with the layout described above.
  * Limits (gs_small_eligible): T <= 1024, num_seqs <= 1024,
  * num_adapters <= 64, max_rank <= 64, every slice width a multiple of 128.
- * workspace: gs_small_workspace_bytes(...) bytes, 16-byte aligned, no
- * initialisation; calls sharing it must not overlap in time.
+ * workspace: gs_small_workspace_bytes(...) bytes, 16-byte aligned, ZEROED
+ * before the first call and used by nothing but this entry point (it holds
+ * epoch-tagged partial sums; any size change may reuse the same buffer).
+ * sync: gs_small_sync_bytes() bytes, 8-byte aligned, ZEROED before the first
+ * call: int32 words 0-1 are the 64-bit launch epoch / started count, word 2
+ * an error word whose bit 0 means an expand workgroup gave up waiting (20 ms)
+ * and that call's output is wrong.  Zeroing sync again requires zeroing the
+ * workspace too.  Calls sharing a workspace or sync buffer must not overlap
+ * in time (stream order is enough).
+ * speculate != 0 issues every adapter's weight loads before the routing is
+ * known (saves a memory round trip when most adapters have tokens); 0 reads
+ * only the weights of adapters some token requests.
  * ---------------------------------------------------------------------- */
 int gs_small_eligible(int64_t num_tokens, int32_t num_seqs, int32_t num_slices, const int32_t* slice_bounds,
                       int32_t num_adapters, int32_t max_rank);
 int64_t gs_small_workspace_bytes(int32_t dtype, int64_t num_tokens, int32_t hidden, int32_t num_slices,
                                  int32_t num_adapters, int32_t max_rank, int32_t out_total,
                                  const int32_t* slice_bounds);
+int64_t gs_small_sync_bytes(void);
 int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t* positions,
                            const int32_t* cu_seqlens, const int64_t* act_offsets, int32_t num_seqs,
                            const int32_t* eff_ids, const void* x, int64_t ldx, void* y, int64_t ldy,
                            int64_t num_tokens, int32_t hidden, int32_t out_total, const int32_t* slice_bounds,
                            int32_t num_slices, const void* a_pack, const int64_t* a_off, const void* b_pack,
                            const int64_t* b_off, const int32_t* ranks, int32_t num_adapters, int32_t max_rank,
-                           void* workspace, int64_t workspace_bytes, void* stream);
+                           void* workspace, int64_t workspace_bytes, int32_t* sync, int64_t sync_bytes,
+                           int32_t speculate, void* stream);
 
 /* ------------------------------------------------------------------------
  * Reference op: per-module tile bitmasks and kernel-local ids.

@@ -1,6 +1,6 @@
-"""GPU parity of the two-launch small-batch (decode) path.
+"""GPU parity of the one-launch small-batch (decode) path.
 
-The small path groups tokens inside its kernels, either from pre-gated ids
+The small path groups tokens inside its kernel, either from pre-gated ids
 (``switched_lora_`` with segments) or from the raw routing
 (``switched_lora_routed_``: requested ids + positions + sequence boundaries +
 aLoRA offsets).  Checked against the CPU oracle at the target tolerance
@@ -45,6 +45,16 @@ def _oracle(md, eff, dtype, mode="exact"):
                                      mode)
 
 
+@pytest.fixture(autouse=True)
+def _clean_handoff(dev):
+    """Every test ends with the error word clear and no launch half-counted."""
+    switched.small_reset(dev)
+    yield
+    torch.cuda.synchronize()
+    assert switched.small_status(dev) == 0, f"small-path error word {switched.small_status(dev)}"
+    assert switched.small_pending_count(dev) == 0, "a launch left an adapter's done count behind"
+
+
 def _check(md, y, eff, dtype):
     ref = _oracle(md, eff, dtype)
     _close(_np(y), ref, TOL[dtype], "small path vs oracle")
@@ -63,7 +73,7 @@ def test_small_routed_configs(dev, config):
     y = md.y.clone()
     switched.switched_lora_routed_(y, md.x, torch.tensor(r.req_ids, device=dev), pk,
                                    torch.tensor(r.positions, device=dev), torch.tensor(r.cu_seqlens, device=dev),
-                                   torch.tensor(r.act_offsets, device=dev))
+                                   torch.tensor(r.act_offsets, device=dev), path="small")
     torch.cuda.synchronize()
     eff = omap.alora_effective_ids(r.req_ids, r.positions, r.cu_seqlens, r.act_offsets)
     _check(md, y, eff, wl.dtype)
@@ -110,7 +120,7 @@ def test_small_shapes(dev, dtype, T, NA, ranks, slices, H, seed):
     ids = rng.integers(-1, NA + 2, size=T)           # includes out-of-range ids (-> base)
     _say(f"small shapes dtype={dtype} T={T} NA={NA} ranks={ranks[:6]} slices={slices} H={H}")
     y = md.y.clone()
-    switched.switched_lora_routed_(y, md.x, torch.tensor(ids, device=dev), pk)
+    switched.switched_lora_routed_(y, md.x, torch.tensor(ids, device=dev), pk, path="small")
     torch.cuda.synchronize()
     eff = np.where((ids < 0) | (ids > NA), 0, ids)
     _check(md, y, eff, dtype)
@@ -137,7 +147,7 @@ def test_small_ragged_gating_and_nonapplicable(dev):
         y = md.y.clone()
         switched.switched_lora_routed_(y, md.x, torch.tensor(req, device=dev), pk,
                                        torch.tensor(pos, device=dev) if with_pos else None,
-                                       torch.tensor(cu, device=dev), torch.tensor(offs, device=dev))
+                                       torch.tensor(cu, device=dev), torch.tensor(offs, device=dev), path="small")
         torch.cuda.synchronize()
         eff = omap.alora_effective_ids(req, pos if with_pos else None, cu, offs)
         eff[eff == 3] = 0                             # non-applicable -> base, as the reference remaps it
@@ -150,23 +160,23 @@ def test_small_all_base_and_no_tokens_for_some_adapters(dev):
     md = workloads.make_module(spec, 90, 3, torch.bfloat16, dev, seed=5)
     pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, spec.ranks)
     y = md.y.clone()
-    switched.switched_lora_routed_(y, md.x, torch.zeros(90, dtype=torch.int64, device=dev), pk)
+    switched.switched_lora_routed_(y, md.x, torch.zeros(90, dtype=torch.int64, device=dev), pk, path="small")
     torch.cuda.synchronize()
     assert torch.equal(y, md.y)
     ids = np.where(np.arange(90) % 3 == 0, 2, 0)     # only adapter 2 present
     y = md.y.clone()
-    switched.switched_lora_routed_(y, md.x, torch.tensor(ids, device=dev), pk)
+    switched.switched_lora_routed_(y, md.x, torch.tensor(ids, device=dev), pk, path="small")
     torch.cuda.synchronize()
     _check(md, y, ids, torch.bfloat16)
 
 
 def test_small_graph_replays(dev):
-    """The routed two-launch op captured in a HIP graph; every replay equals eager, bit for bit."""
+    """The routed one-launch op captured in a HIP graph; every replay equals eager, bit for bit."""
     wl = workloads.make_workload(1, dev)
     md, r = wl.modules[0], wl.routing
     pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, md.spec.ranks)
     args = (torch.tensor(r.req_ids, device=dev), pk, torch.tensor(r.positions, device=dev),
-            torch.tensor(r.cu_seqlens, device=dev), torch.tensor(r.act_offsets, device=dev))
+            torch.tensor(r.cu_seqlens, device=dev), torch.tensor(r.act_offsets, device=dev), "small")
     y_eager = md.y.clone()
     switched.switched_lora_routed_(y_eager, md.x, *args)
     torch.cuda.synchronize()
@@ -181,3 +191,40 @@ def test_small_graph_replays(dev):
         torch.cuda.synchronize()
         _say(f"small graph replay {rep}")
         assert torch.equal(y, y_eager), f"replay {rep} differs from eager"
+
+
+@pytest.mark.parametrize("speculate_tokens", [256, 8])
+def test_small_back_to_back_calls(dev, speculate_tokens):
+    """Many calls in a row on one stream (eager and in one graph), with and
+    without speculative weight loads (T >= 2*NA or not): each reuses the
+    counters the previous one left at zero; all outputs match the oracle."""
+    T, NA = speculate_tokens, 12
+    spec = workloads.ModuleSpec("t", 1024, (512, 256, 256), [32] * NA, 32)
+    mods = [workloads.make_module(spec, T, NA, torch.bfloat16, dev, seed=40 + k) for k in range(3)]
+    packs = [switched.PackedAdapters.from_slices(m.lora_A_slices, m.lora_B_slices, spec.ranks) for m in mods]
+    rng = np.random.default_rng(9)
+    ids = rng.integers(0, NA + 1, size=T)
+    ids_d = torch.tensor(ids, device=dev)
+    ys = [m.y.clone() for m in mods]
+    for rep in range(4):
+        for m, pk, y in zip(mods, packs, ys):
+            prev = _np(y)
+            switched.switched_lora_routed_(y, m.x, ids_d, pk, path="small")
+            torch.cuda.synchronize()
+            ref = olora.switched_lora_apply(prev, _np(m.x), ids, [_np(a) for a in m.lora_A_slices],
+                                            [_np(b) for b in m.lora_B_slices], spec.output_slices, spec.ranks, "bf16")
+            _close(_np(y), ref, 2e-2, f"chained small-path call {rep}")
+    _say(f"back-to-back eager T={T}")
+    ys2 = [m.y.clone() for m in mods]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for rep in range(4):
+            for m, pk, y in zip(mods, packs, ys2):
+                switched.switched_lora_routed_(y, m.x, ids_d, pk, path="small")
+    for y, m in zip(ys2, mods):
+        y.copy_(m.y)
+    g.replay()
+    torch.cuda.synchronize()
+    _say(f"back-to-back graph T={T}")
+    for y, y_e in zip(ys2, ys):
+        assert torch.equal(y, y_e), "graph replay of chained calls differs from eager"
