@@ -47,12 +47,13 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
 
-// Round-to-nearest-even float -> bf16 bits (NaN kept quiet).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even float -> bf16 bits: gfx950's v_cvt_pk_bf16_f32 (one
+// instruction for two values; NaN stays NaN).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
@@ -114,7 +115,7 @@ __device__ __forceinline__ u32x4 sel16(bool keep, const u32x4& v) {
 }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 
 // y piece (16 bytes = 8 bf16 / 4 fp32) + delta, rounded once, stored back.
@@ -134,6 +135,25 @@ __device__ __forceinline__ void add_store_y(void* y, int64_t off, const u32x4& i
   } else {
     const f32x4 f = __builtin_bit_cast(f32x4, in);
     *p = __builtin_bit_cast(u32x4, f32x4{f.x + d[0], f.y + d[1], f.z + d[2], f.w + d[3]});
+  }
+}
+
+// y piece (16 bytes = 8 bf16 / 4 fp32) + delta, rounded once; returns the bits.
+template <bool BF16>
+__device__ __forceinline__ u32x4 add_y16(const u32x4& in, const float* d) {
+  if constexpr (BF16) {
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t w = in[e];
+      const float lo = bf16_bits_to_f32(static_cast<uint16_t>(w & 0xffffu)) + d[2 * e];
+      const float hi = bf16_bits_to_f32(static_cast<uint16_t>(w >> 16)) + d[2 * e + 1];
+      o[e] = pack_bf16x2(lo, hi);
+    }
+    return u32x4{o[0], o[1], o[2], o[3]};
+  } else {
+    const f32x4 f = __builtin_bit_cast(f32x4, in);
+    return __builtin_bit_cast(u32x4, f32x4{f.x + d[0], f.y + d[1], f.z + d[2], f.w + d[3]});
   }
 }
 

@@ -12,22 +12,24 @@
 // 16-entry prefix in LDS, giving the list in ascending token order -- the
 // iteration order of the reference HF loop.
 //
-// Hand-off inside the launch: tagged partials.  Each adapter g has an epoch
-// word E_g and a done count in the sync buffer.  Every workgroup of adapter g
-// reads E_g when it starts; a producer stores each partial as one 64-bit pair
-// (tag = E_g + 1, fp32 bits) with agent-coherent stores (sc1: written through
-// past the XCD's L2), and a consumer issues its lora_B and y loads first, then
-// polls its partials with agent-coherent 64-bit loads until every tag equals
-// E_g + 1 (a pair is read in one access, so a value is never taken without its
-// tag).  Once it has its partials, a consumer adds 1 to g's done count; the
-// consumer that completes the count stores E_g + 1 and a zero count for the
-// next launch.  That is safe: every workgroup of g that writes partials is
-// waited for by some consumer of g, so it has read E_g by then, and every
-// consumer of g has read E_g before counting itself done.  No counters on the
-// critical path, no cache writeback or invalidate, no device-scope fence.
-// Adapter g's partials live in a fixed region of the workspace whatever the
-// module's shape, so a stale pair there carries a tag of an earlier epoch of
-// the same g and never the current one (until the 32-bit epoch wraps).
+// Hand-off inside the launch: tagged partials.  Each adapter g has a 64-bit
+// launch counter C_g in the sync buffer whose epoch is E_g = C_g >> 20.
+// Every workgroup of adapter g reads C_g when it starts; a producer stores each
+// partial as one 64-bit pair (tag = E_g + 1, fp32 bits) with agent-coherent
+// stores (sc1: written through past the XCD's L2), and a consumer issues its
+// lora_B and y loads first, then polls its partials with agent-coherent 64-bit
+// loads until every tag equals E_g + 1 (a pair is read in one access, so a
+// value is never taken without its tag).  Once it has its partials, a consumer
+// adds its weight to C_g without waiting for the result; the weights of g's
+// consumers in one launch sum to exactly 2^20, so E_g moves to E_g + 1 only
+// when the last of them has added.  Every workgroup of g in the launch reads
+// E_g: consumers read it before adding, and every producer that writes
+// partials is waited for by some consumer of its slice, which has not added
+// yet.  No counters on the critical path, no cache writeback or invalidate,
+// no device-scope fence.  Adapter g's partials live in a fixed region of the
+// workspace whatever the module's shape, so a stale pair there carries a tag
+// of an earlier epoch of the same g and never the current one (until the
+// 32-bit tag wraps, after 2^32 launches with tokens for g).
 //
 // Forward progress: producers have the lowest workgroup ids and never wait, and
 // workgroups are dispatched in id order, so a waiting consumer never holds a
@@ -41,9 +43,9 @@
 //
 // Workspace: kSmMaxAdapters equal regions, adapter g's holding its tagged
 // partials [KS][cap][zw] uint64; used by nothing else.
-// Sync buffer (int32 words): [2] error word; [32*g] epoch and [32*g + 1] done
-// count of adapter g (one 128-byte line per adapter).  Both buffers are
-// zeroed once before the first call.
+// Sync buffer (int32 words): [2] error word; [32*g .. 32*g + 1] the 64-bit
+// launch counter of adapter g (one 128-byte line per adapter).  Both buffers
+// are zeroed once before the first call.
 #include "gs_common.h"
 
 namespace gs {
@@ -54,11 +56,12 @@ constexpr int kSmT = 256;                    // threads per workgroup (4 waves)
 constexpr int kSmMaxTokens = 1024;           // largest batch of this path
 constexpr int kSmMaxAdapters = 64;           // adapters whose tables ride in the kernel arguments
 constexpr int kSmMaxRank = 64;               // largest (padded) rank of this path
-constexpr int kSmU = kSmMaxTokens / kSmT;    // tokens per thread in the routing pass
+constexpr int kSmMaxU = kSmMaxTokens / kSmT; // tokens per thread in the routing pass (at most)
 constexpr int kKsGrp = 4;                    // split-K partials a consumer polls together
 constexpr int kErrTimeout = 1;               // error word bits
 constexpr int kSyncErrWord = 2;              // int32 index of the error word
-constexpr int kSyncLine = 32;                // int32 words per adapter (epoch, done count)
+constexpr int kSyncLine = 32;                // int32 words per adapter (its 64-bit launch counter)
+constexpr int kEpochShift = 20;              // a launch adds 2^20 to the counter of each adapter with tokens
 
 // Per-adapter weight offsets and ranks, passed by value (load-time constants of
 // the module) so no workgroup waits on a table load before its weight loads.
@@ -81,24 +84,28 @@ struct SmallRoute {
   int NA;
 };
 
+// U = tokens per thread in the routing pass: batches (and sequence counts) of
+// up to U*256 tokens.
+template <int U>
 struct RouteLds {
-  int tok[kSmMaxTokens];
-  int32_t cu[kSmMaxTokens];
-  int64_t off[kSmMaxTokens];
+  int tok[U * kSmT];
+  int32_t cu[U * kSmT];
+  int64_t off[U * kSmT];
   int wreq[4];
-  int wcnt[kSmU * 4];
+  int wcnt[U * 4];
 };
 
 // Routing in three steps so the caller can issue its weight loads between the
 // routing loads and their first use (loads return in order, so a wait for the
 // routing loads does not wait for weight loads issued after them).
+template <int U>
 struct RouteRegs {
-  int64_t rq[kSmU];     // requested ids (req path)
-  int32_t e32[kSmU];    // pre-gated ids (eff path), widened only when used
-  int64_t q[kSmU];
-  int32_t cu[kSmU];
-  int64_t off[kSmU];
-  int id[kSmU];
+  int64_t rq[U];        // requested ids (req path)
+  int32_t e32[U];       // pre-gated ids (eff path), widened only when used
+  int64_t q[U];
+  int32_t cu[U];
+  int64_t off[U];
+  int id[U];
 };
 
 __device__ __forceinline__ bool route_gated(const SmallRoute& r) { return r.eff == nullptr && r.act_off != nullptr; }
@@ -110,43 +117,44 @@ __device__ __forceinline__ int route_nseq(const SmallRoute& r) {
 // checks are uniform and sit outside the loops; inside, every load is issued
 // unconditionally from a clamped in-bounds index (T >= 1, ns >= 1), so the
 // loads stay in flight together.  Entries past T / ns are masked by the users.
-__device__ __forceinline__ void route_issue(const SmallRoute& r, RouteRegs& rr) {
+template <int U>
+__device__ __forceinline__ void route_issue(const SmallRoute& r, RouteRegs<U>& rr) {
   const int tid = threadIdx.x;
   const int tl = r.T - 1;
   if (r.eff != nullptr) {
 #pragma unroll
-    for (int u = 0; u < kSmU; ++u) {
+    for (int u = 0; u < U; ++u) {
       rr.e32[u] = r.eff[min(u * kSmT + tid, tl)];
       rr.rq[u] = 0;
     }
   } else {
 #pragma unroll
-    for (int u = 0; u < kSmU; ++u) {
+    for (int u = 0; u < U; ++u) {
       rr.rq[u] = r.req[min(u * kSmT + tid, tl)];
       rr.e32[u] = 0;
     }
   }
   if (r.eff == nullptr && r.pos != nullptr) {
 #pragma unroll
-    for (int u = 0; u < kSmU; ++u) rr.q[u] = r.pos[min(u * kSmT + tid, tl)];
+    for (int u = 0; u < U; ++u) rr.q[u] = r.pos[min(u * kSmT + tid, tl)];
   } else {
 #pragma unroll
-    for (int u = 0; u < kSmU; ++u) rr.q[u] = 0;
+    for (int u = 0; u < U; ++u) rr.q[u] = 0;
   }
   if (route_gated(r)) {
     const int nl = route_nseq(r) - 1;
 #pragma unroll
-    for (int u = 0; u < kSmU; ++u) rr.off[u] = r.act_off[min(u * kSmT + tid, nl)];
+    for (int u = 0; u < U; ++u) rr.off[u] = r.act_off[min(u * kSmT + tid, nl)];
     if (r.cu != nullptr) {
 #pragma unroll
-      for (int u = 0; u < kSmU; ++u) rr.cu[u] = r.cu[min(u * kSmT + tid, nl)];
+      for (int u = 0; u < U; ++u) rr.cu[u] = r.cu[min(u * kSmT + tid, nl)];
     } else {
 #pragma unroll
-      for (int u = 0; u < kSmU; ++u) rr.cu[u] = 0;
+      for (int u = 0; u < U; ++u) rr.cu[u] = 0;
     }
   } else {
 #pragma unroll
-    for (int u = 0; u < kSmU; ++u) {
+    for (int u = 0; u < U; ++u) {
       rr.off[u] = 0;
       rr.cu[u] = 0;
     }
@@ -156,7 +164,8 @@ __device__ __forceinline__ void route_issue(const SmallRoute& r, RouteRegs& rr) 
 // Step 2: stage sequence boundaries and offsets in LDS, gate every token, and
 // return whether any token REQUESTS adapter g (before gating; exact for
 // pre-gated ids) -- workgroup-uniform.  Ends with a barrier.
-__device__ __forceinline__ bool route_gate(const SmallRoute& r, int g, RouteLds& s, RouteRegs& rr) {
+template <int U>
+__device__ __forceinline__ bool route_gate(const SmallRoute& r, int g, RouteLds<U>& s, RouteRegs<U>& rr) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -164,7 +173,7 @@ __device__ __forceinline__ bool route_gate(const SmallRoute& r, int g, RouteLds&
   const int ns = route_nseq(r);
   if (gate) {
 #pragma unroll
-    for (int u = 0; u < kSmU; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int k = u * kSmT + tid;
       if (k < ns) {
         s.cu[k] = rr.cu[u];
@@ -174,11 +183,11 @@ __device__ __forceinline__ bool route_gate(const SmallRoute& r, int g, RouteLds&
   }
   if (r.eff != nullptr) {
 #pragma unroll
-    for (int u = 0; u < kSmU; ++u) rr.rq[u] = rr.e32[u];
+    for (int u = 0; u < U; ++u) rr.rq[u] = rr.e32[u];
   }
   bool req_g = false;
 #pragma unroll
-  for (int u = 0; u < kSmU; ++u) req_g |= (u * kSmT + tid < r.T) && rr.rq[u] == g;
+  for (int u = 0; u < U; ++u) req_g |= (u * kSmT + tid < r.T) && rr.rq[u] == g;
   const uint64_t any = __ballot(req_g);
   if (lane == 0) s.wreq[wave] = any != 0;
   lds_barrier();
@@ -187,14 +196,14 @@ __device__ __forceinline__ bool route_gate(const SmallRoute& r, int g, RouteLds&
   // is sequence t (a decode batch, one token per sequence), right iff
   // cu[t] <= t < cu[t+1].  Lanes whose guess fails run a fixed-step search
   // (one LDS read per token slot and step; clamped indices stay in bounds).
-  int sq[kSmU];
+  int sq[U];
 #pragma unroll
-  for (int u = 0; u < kSmU; ++u) sq[u] = 0;
+  for (int u = 0; u < U; ++u) sq[u] = 0;
   if (gate) {
-    bool ok[kSmU];
+    bool ok[U];
     bool all_ok = true;
 #pragma unroll
-    for (int u = 0; u < kSmU; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int t = u * kSmT + tid;
       const int gs = min(t, ns - 1);
       const int c0 = s.cu[gs];
@@ -205,20 +214,20 @@ __device__ __forceinline__ bool route_gate(const SmallRoute& r, int g, RouteLds&
     }
     if (!all_ok) {
 #pragma unroll
-      for (int step = kSmMaxTokens / 2; step > 0; step >>= 1) {
+      for (int step = U * kSmT / 2; step > 0; step >>= 1) {
         if (step < ns) {
-          int c[kSmU];
+          int c[U];
 #pragma unroll
-          for (int u = 0; u < kSmU; ++u) c[u] = s.cu[min(sq[u] + step, ns - 1)];
+          for (int u = 0; u < U; ++u) c[u] = s.cu[min(sq[u] + step, ns - 1)];
 #pragma unroll
-          for (int u = 0; u < kSmU; ++u)
+          for (int u = 0; u < U; ++u)
             sq[u] = (!ok[u] && sq[u] + step < ns && c[u] <= u * kSmT + tid) ? sq[u] + step : sq[u];
         }
       }
     }
   }
 #pragma unroll
-  for (int u = 0; u < kSmU; ++u) {
+  for (int u = 0; u < U; ++u) {
     const int t = u * kSmT + tid;
     int64_t v = rr.rq[u];
     if (gate && t < r.T) {
@@ -234,21 +243,22 @@ __device__ __forceinline__ bool route_gate(const SmallRoute& r, int g, RouteLds&
 // Step 3: list adapter g's tokens (ascending) in s.tok and return their count;
 // position = earlier (u, wave) chunks' counts + matches in lower lanes.
 // Ends with a barrier.
-__device__ __forceinline__ int route_list(int g, RouteLds& s, const RouteRegs& rr) {
+template <int U>
+__device__ __forceinline__ int route_list(int g, RouteLds<U>& s, const RouteRegs<U>& rr) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  uint64_t bal[kSmU];
+  uint64_t bal[U];
 #pragma unroll
-  for (int u = 0; u < kSmU; ++u) {
+  for (int u = 0; u < U; ++u) {
     bal[u] = __ballot(rr.id[u] == g);
     if (lane == 0) s.wcnt[u * 4 + wave] = __popcll(bal[u]);
   }
   lds_barrier();
-  int before[kSmU];
+  int before[U];
   int total = 0;
 #pragma unroll
-  for (int u = 0; u < kSmU; ++u) {
+  for (int u = 0; u < U; ++u) {
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       if (w == wave) before[u] = total;
@@ -256,7 +266,7 @@ __device__ __forceinline__ int route_list(int g, RouteLds& s, const RouteRegs& r
     }
   }
 #pragma unroll
-  for (int u = 0; u < kSmU; ++u) {
+  for (int u = 0; u < U; ++u) {
     if (rr.id[u] == g) s.tok[before[u] + __popcll(bal[u] & lanemask_lt())] = u * kSmT + tid;
   }
   lds_barrier();
@@ -325,12 +335,12 @@ __device__ __forceinline__ int tile_slice(const SliceInfo& si, int nt) {
 constexpr int kZld = kSmMaxRank + 8;         // elements per LDS shrink row
 constexpr int kHalf = 128;                   // y columns per delta staging pass
 
-template <bool BF16>
+template <bool BF16, int U>
 struct FusedLds {
-  RouteLds rt;
+  RouteLds<U> rt;
   uint32_t epoch;
   union {
-    float red[3][16][64];                    // producer: cross-wave sums
+    f32x4 red[4][4][64];                     // producer: per-wave sums [wave][rt*2 + c2][lane]
     struct {                                 // consumer
       __attribute__((aligned(16))) char zs[32 * kZld * Elt<BF16>::kSize];
       float dtile[32][kHalf + 4];
@@ -338,10 +348,14 @@ struct FusedLds {
   } u;
 };
 
+__device__ __forceinline__ uint64_t* launch_counter(const FusedParams& p, int g) {
+  return reinterpret_cast<uint64_t*>(p.sync + kSyncLine * g);
+}
+
 // Adapter g's epoch at the start of this launch (thread 0 only).
 __device__ __forceinline__ uint32_t read_epoch(const FusedParams& p, int g) {
   return static_cast<uint32_t>(
-      __hip_atomic_load(p.sync + kSyncLine * g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      __hip_atomic_load(launch_counter(p, g), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> kEpochShift);
 }
 
 // ----------------------------------------------------------------------------
@@ -351,8 +365,8 @@ __device__ __forceinline__ uint32_t read_epoch(const FusedParams& p, int g) {
 // 16-row tiles).  The waves' sums are added in a fixed order in LDS and wave 0
 // stores the tagged partials straight from its registers.
 // ----------------------------------------------------------------------------
-template <bool BF16, int NPW, int NT, bool SPEC>
-__device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16>& L, int bid) {
+template <bool BF16, int NPW, int NT, bool SPEC, int U>
+__device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>& L, int bid) {
   constexpr int P = Elt<BF16>::kPerPiece;
   constexpr int ES = Elt<BF16>::kSize;
   constexpr int KSTEP = 4 * P;      // k per piece over the 4 lane groups
@@ -385,8 +399,8 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16>& L,
   }
 
   if (tid == 0) L.epoch = read_epoch(p, g);
-  RouteRegs rr;
-  route_issue(p.rt, rr);
+  RouteRegs<U> rr;
+  route_issue<U>(p.rt, rr);
   u32x4 av[2][NPW];
   if constexpr (SPEC) {
     // lora_A in the same memory trip as the routing loads: unconditional loads
@@ -401,7 +415,7 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16>& L,
         av[c2][pp] = sel16(ok, ld16(arow[c2] + (ok ? kp : 0) * ES));
       }
   }
-  const bool requested = route_gate(p.rt, g, L.rt, rr);
+  const bool requested = route_gate<U>(p.rt, g, L.rt, rr);
   if constexpr (!SPEC) {
     // only adapters some token asked for read their weights
 #pragma unroll
@@ -413,7 +427,7 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16>& L,
         if (requested && nok[c2] && kp < k_hi) av[c2][pp] = ld16(arow[c2] + kp * ES);
       }
   }
-  const int n_g = route_list(g, L.rt, rr);
+  const int n_g = route_list<U>(g, L.rt, rr);
   if (!active || n_g == 0) return;
   const uint64_t tag = static_cast<uint64_t>(L.epoch + 1u) << 32;
   uint64_t* part = p.part + static_cast<int64_t>(g - 1) * p.region;
@@ -443,21 +457,23 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16>& L,
         for (int pp = 0; pp < NPW; ++pp) acc[rt][c2] = mfma16<BF16>(xv[rt][pp], av[c2][pp], acc[rt][c2]);
       }
 
-    // fixed-order cross-wave sum: ((w0 + w1) + w2) + w3
-    if (wave > 0) {
+    // fixed-order cross-wave sum ((w0 + w1) + w2) + w3; wave w finishes and
+    // stores the 16x16 tile rc = w (row tile rc >> 1, column block rc & 1)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) L.u.red[wave - 1][v][l] = acc[v >> 3][(v >> 2) & 1][v & 3];
-    }
+    for (int rc = 0; rc < 4; ++rc) L.u.red[wave][rc][l] = acc[rc >> 1][rc & 1];
     lds_barrier();
-    if (wave == 0) {
+    {
+      const int rt = wave >> 1;
+      const int nw = cb * 32 + 16 * (wave & 1) + i16;
+      const f32x4 v = ((L.u.red[0][wave][l] + L.u.red[1][wave][l]) + L.u.red[2][wave][l]) + L.u.red[3][wave][l];
+      uint64_t* dst = part + (static_cast<int64_t>(kc) * p.cap + rt0 + 16 * rt + 4 * q4) * p.zw + nw;
+      const int slots = n_g - (rt0 + 16 * rt + 4 * q4);    // rows of this lane's 4 still in the batch
+      if (active && nw < ncols) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int rt = v >> 3, c2 = (v >> 2) & 1, e = v & 3;
-        const int slot = rt0 + 16 * rt + 4 * q4 + e;
-        const float val = ((acc[rt][c2][e] + L.u.red[0][v][l]) + L.u.red[1][v][l]) + L.u.red[2][v][l];
-        if (nok[c2] && slot < n_g)
-          __hip_atomic_store(part + (static_cast<int64_t>(kc) * p.cap + slot) * p.zw + n[c2],
-                             tag | __float_as_uint(val), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int e = 0; e < 4; ++e)
+          if (e < slots)
+            __hip_atomic_store(dst + static_cast<int64_t>(e) * p.zw, tag | __float_as_uint(v[e]), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
       }
     }
     lds_barrier();   // red is reused by the next row chunk
@@ -472,8 +488,8 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16>& L,
 // MFMA deltas go through LDS in 128-column halves, and each thread adds and
 // stores 16-byte pieces of its token rows.
 // ----------------------------------------------------------------------------
-template <bool BF16, int NQ, bool SPEC>
-__device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16>& L, int cid) {
+template <bool BF16, int NQ, bool SPEC, int U>
+__device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>& L, int cid) {
   constexpr int NT = 64 * NQ;
   constexpr int NH = NQ / 2;            // 128-column halves
   constexpr int P = Elt<BF16>::kPerPiece;
@@ -500,8 +516,8 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16>& L,
   const int zc0 = s * r;                 // this slice's columns in the adapter's shrink row
 
   if (tid == 0) L.epoch = read_epoch(p, g);
-  RouteRegs rr;
-  route_issue(p.rt, rr);
+  RouteRegs<U> rr;
+  route_issue<U>(p.rt, rr);
   // lora_B rows of this wave's column blocks (n < out_total always; rank 0
   // reads element 0 of the pack and is masked)
   u32x4 bv[NQ][KG];
@@ -522,7 +538,7 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16>& L,
         bv[q][kg] = sel16(ok, ld16(brow[q] + (ok ? k0 : 0) * ES));
       }
   }
-  const bool requested = route_gate(p.rt, g, L.rt, rr);
+  const bool requested = route_gate<U>(p.rt, g, L.rt, rr);
   if constexpr (!SPEC) {
 #pragma unroll
     for (int q = 0; q < NQ; ++q)
@@ -533,14 +549,13 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16>& L,
         if (requested && k0 < r) bv[q][kg] = ld16(brow[q] + k0 * ES);
       }
   }
-  const int n_g = route_list(g, L.rt, rr);
+  const int n_g = route_list<U>(g, L.rt, rr);
   if (r == 0 || n_g == 0) return;       // no producer wrote partials for it
-  const uint32_t epoch = L.epoch;
-  const uint32_t want = epoch + 1u;
+  const uint32_t want = L.epoch + 1u;
   const uint64_t* part = p.part + static_cast<int64_t>(g - 1) * p.region;
   const int64_t kstride = static_cast<int64_t>(p.cap) * p.zw;
-  int32_t* sync_g = p.sync + kSyncLine * g;
-  int done_before = -1;
+  // this consumer's share of the 2^20 that g's consumers add per launch
+  const uint64_t weight = (uint64_t{1} << kEpochShift) / p.NNT + (nt < (1 << kEpochShift) % p.NNT ? 1 : 0);
   const int cx = (tid % LPR) * EPL;
 
   for (int rt0 = 0; rt0 < n_g; rt0 += 32) {
@@ -548,16 +563,15 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16>& L,
     u32x4 yv[NH][PASSES];
     int64_t yoff[PASSES];
     bool rok[PASSES];
+    // (rows past the adapter's tokens re-read the chunk's first row and are
+    // never stored: unconditional loads keep the wait counts exact)
 #pragma unroll
     for (int ps = 0; ps < PASSES; ++ps) {
       const int row = rt0 + ps * RPP + tid / LPR;
       rok[ps] = row < n_g;
-      yoff[ps] = static_cast<int64_t>(rok[ps] ? L.rt.tok[row] : 0) * p.ldy + n_tile0 + cx;
+      yoff[ps] = static_cast<int64_t>(L.rt.tok[rok[ps] ? row : rt0]) * p.ldy + n_tile0 + cx;
 #pragma unroll
-      for (int hf = 0; hf < NH; ++hf) {
-        yv[hf][ps] = u32x4{0u, 0u, 0u, 0u};
-        if (rok[ps]) yv[hf][ps] = ld16(static_cast<const char*>(p.y) + (yoff[ps] + hf * kHalf) * ES);
-      }
+      for (int hf = 0; hf < NH; ++hf) yv[hf][ps] = ld16(static_cast<const char*>(p.y) + (yoff[ps] + hf * kHalf) * ES);
     }
 
     // shrink rows of the chunk: element m of batch eb of this thread is
@@ -620,10 +634,6 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16>& L,
       }
     }
     lds_barrier();
-    // every thread has its last partials: count this consumer done (the
-    // returned count is only looked at when the workgroup ends)
-    if (tid == 0 && rt0 + 32 >= n_g)
-      done_before = __hip_atomic_fetch_add(sync_g + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
     // D[t][n] = sum_k z[t][k] B[n][k]; acc[rt][q]: token 16*rt + 4*q4 + e of
     // the chunk, column n_tile0 + 16*(q*4 + wave) + i16
@@ -646,6 +656,10 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16>& L,
         }
       }
     }
+    // every y piece is combined with its delta before the first store: on
+    // gfx9 stores count in the same in-order counter as loads, so a wait for a
+    // y load issued after a store would also wait for that store
+    u32x4 yo[NH][PASSES];
 #pragma unroll
     for (int hf = 0; hf < NH; ++hf) {
 #pragma unroll
@@ -660,30 +674,33 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16>& L,
       lds_barrier();
 #pragma unroll
       for (int ps = 0; ps < PASSES; ++ps) {
-        if (rok[ps]) {
-          const int row = ps * RPP + tid / LPR;
-          float d[EPL];
+        const int row = ps * RPP + tid / LPR;
+        float d[EPL];
 #pragma unroll
-          for (int e = 0; e < EPL; ++e) d[e] = L.u.co.dtile[row][cx + e];
-          add_store_y<BF16>(p.y, yoff[ps] + hf * kHalf, yv[hf][ps], d);
-        }
+        for (int e = 0; e < EPL; ++e) d[e] = L.u.co.dtile[row][cx + e];
+        yo[hf][ps] = add_y16<BF16>(yv[hf][ps], d);
       }
       lds_barrier();   // dtile / zs are reused
     }
+#pragma unroll
+    for (int hf = 0; hf < NH; ++hf)
+#pragma unroll
+      for (int ps = 0; ps < PASSES; ++ps)
+        if (rok[ps]) st16(static_cast<char*>(p.y) + (yoff[ps] + hf * kHalf) * ES, yo[hf][ps]);
   }
-  if (done_before == p.NNT - 1) {
-    // the last consumer of g: the next launch uses the next epoch
-    __hip_atomic_store(sync_g + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(sync_g, static_cast<int32_t>(epoch + 1u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  // every thread has had all its partials (barriers since): add this
+  // consumer's weight; issued last and never waited for, since on gfx9 a
+  // wait for any later load would also wait for it
+  if (tid == 0)
+    __hip_atomic_fetch_add(launch_counter(p, g), weight, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <bool BF16, int NPW, int NQ, bool SPEC>
+template <bool BF16, int NPW, int NQ, bool SPEC, int U>
 __global__ __launch_bounds__(kSmT) void small_fused_kernel(FusedParams p) {
-  __shared__ FusedLds<BF16> lds;
+  __shared__ FusedLds<BF16, U> lds;
   const int bid = static_cast<int>(blockIdx.x);
-  if (bid < p.NP) produce<BF16, NPW, 64 * NQ, SPEC>(p, lds, bid);
-  else consume<BF16, NQ, SPEC>(p, lds, bid - p.NP);
+  if (bid < p.NP) produce<BF16, NPW, 64 * NQ, SPEC, U>(p, lds, bid);
+  else consume<BF16, NQ, SPEC, U>(p, lds, bid - p.NP);
 }
 
 // ----------------------------------------------------------------------------
@@ -730,24 +747,31 @@ SmallPlan plan_small(int64_t T, int H, int S, int NA, int max_rank, bool bf16, i
   return pl;
 }
 
-template <bool BF16, int NQ, bool SPEC>
+template <bool BF16, int NQ, bool SPEC, int U>
 void launch_fused_nq(const SmallPlan& pl, const FusedParams& fp, unsigned grid, hipStream_t st) {
   switch (pl.NPW) {
-    case 8: hipLaunchKernelGGL((small_fused_kernel<BF16, 8, NQ, SPEC>), dim3(grid), dim3(kSmT), 0, st, fp); break;
-    default: hipLaunchKernelGGL((small_fused_kernel<BF16, 4, NQ, SPEC>), dim3(grid), dim3(kSmT), 0, st, fp); break;
+    case 8: hipLaunchKernelGGL((small_fused_kernel<BF16, 8, NQ, SPEC, U>), dim3(grid), dim3(kSmT), 0, st, fp); break;
+    default: hipLaunchKernelGGL((small_fused_kernel<BF16, 4, NQ, SPEC, U>), dim3(grid), dim3(kSmT), 0, st, fp); break;
   }
 }
 
-template <bool BF16, bool SPEC>
+template <bool BF16, bool SPEC, int U>
 void launch_fused_spec(const SmallPlan& pl, const FusedParams& fp, unsigned grid, hipStream_t st) {
-  if (pl.NQ == 4) launch_fused_nq<BF16, 4, SPEC>(pl, fp, grid, st);
-  else launch_fused_nq<BF16, 2, SPEC>(pl, fp, grid, st);
+  if (pl.NQ == 4) launch_fused_nq<BF16, 4, SPEC, U>(pl, fp, grid, st);
+  else launch_fused_nq<BF16, 2, SPEC, U>(pl, fp, grid, st);
+}
+
+// U = 1 routes batches of up to 256 tokens and sequences, U = 4 up to 1024.
+template <bool BF16, int U>
+void launch_fused_u(const SmallPlan& pl, const FusedParams& fp, unsigned grid, bool spec, hipStream_t st) {
+  if (spec) launch_fused_spec<BF16, true, U>(pl, fp, grid, st);
+  else launch_fused_spec<BF16, false, U>(pl, fp, grid, st);
 }
 
 template <bool BF16>
 void launch_fused(const SmallPlan& pl, const FusedParams& fp, unsigned grid, bool spec, hipStream_t st) {
-  if (spec) launch_fused_spec<BF16, true>(pl, fp, grid, st);
-  else launch_fused_spec<BF16, false>(pl, fp, grid, st);
+  if (fp.rt.T <= kSmT && fp.rt.num_seqs <= kSmT) launch_fused_u<BF16, 1>(pl, fp, grid, spec, st);
+  else launch_fused_u<BF16, kSmMaxU>(pl, fp, grid, spec, st);
 }
 
 }  // namespace
