@@ -194,6 +194,49 @@ struct TileRef {
   int64_t off;  // offs[g] (the adapter's weight offset), fetched in the same pass
 };
 
+// Number of tiles of TM slots over all applicable adapters (every wave
+// computes the same value).
+template <int TM>
+__device__ __forceinline__ int count_tiles(const int32_t* __restrict__ seg, const int32_t* __restrict__ ranks,
+                                           int num_adapters) {
+  const int l = __lane_id();
+  int total = 0;
+  for (int g0 = 1; g0 <= num_adapters; g0 += 64) {
+    const int g = g0 + l;
+    int ntiles = 0;
+    if (g <= num_adapters && ranks[g] > 0) ntiles = (seg[g] - seg[g - 1] + TM - 1) / TM;
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) ntiles += __shfl_xor(ntiles, d, 64);
+    total += ntiles;
+  }
+  return total;
+}
+
+// Work item `lin` of a 1-D launch over (tile, sub) pairs, sub < nsub.
+// Workgroups are dealt to the 8 XCDs round-robin by id, so XCD x runs ids
+// x, x+8, ...; each XCD gets a contiguous range of the batch's tiles, so the
+// tiles of one adapter -- which read the same weights -- share an XCD's L2.
+// The launch has 8 * ceil(max_tiles / 8) * nsub workgroups; ids past the
+// batch's tiles get tile = -1.
+struct XcdItem {
+  int tile;
+  int sub;
+};
+__device__ __forceinline__ XcdItem xcd_item(int lin, int total_tiles, int nsub) {
+  const int tpx = (total_tiles + 7) >> 3;
+  XcdItem it{-1, 0};
+  if (tpx == 0) return it;
+  const int j = lin >> 3;
+  const int tt = j % tpx;
+  const int sub = j / tpx;
+  const int tile = (lin & 7) * tpx + tt;
+  if (sub < nsub && tile < total_tiles) {
+    it.tile = tile;
+    it.sub = sub;
+  }
+  return it;
+}
+
 template <int TM>
 __device__ __forceinline__ TileRef find_tile(const int32_t* __restrict__ seg, const int32_t* __restrict__ ranks,
                                              const int64_t* __restrict__ offs, int num_adapters, int tile_id) {
@@ -237,6 +280,55 @@ __device__ __forceinline__ TileRef find_tile(const int32_t* __restrict__ seg, co
     }
     carry += total;
   }
+  return ref;
+}
+
+// The tile of work item `lin` of a 1-D launch over (tile, sub) pairs (see
+// xcd_item), in one pass over the adapter table when it fits one wave
+// (<= 64 adapters): the tile count and the tile's lookup share the same
+// loads.  Returns g = 0 when the item has no tile.
+template <int TM>
+__device__ __forceinline__ TileRef locate_tile(const int32_t* __restrict__ seg, const int32_t* __restrict__ ranks,
+                                               const int64_t* __restrict__ offs, int num_adapters, int lin, int nsub,
+                                               int& sub) {
+  TileRef ref{0, 0, 0, 0, 0};
+  if (num_adapters > 64) {
+    const XcdItem it = xcd_item(lin, count_tiles<TM>(seg, ranks, num_adapters), nsub);
+    sub = it.sub;
+    return it.tile < 0 ? ref : find_tile<TM>(seg, ranks, offs, num_adapters, it.tile);
+  }
+  const int l = __lane_id();
+  const int g = 1 + l;
+  int ntiles = 0, lo = 0, hi = 0, rk = 0;
+  int64_t of = 0;
+  if (g <= num_adapters) {
+    lo = seg[g - 1];
+    hi = seg[g];
+    rk = ranks[g];
+    of = offs[g];
+    ntiles = (rk > 0) ? (hi - lo + TM - 1) / TM : 0;
+  }
+  int incl = ntiles;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    int v = __shfl_up(incl, d, 64);
+    if (l >= d) incl += v;
+  }
+  const XcdItem it = xcd_item(lin, __shfl(incl, 63, 64), nsub);
+  sub = it.sub;
+  if (it.tile < 0) return ref;
+  const int excl = incl - ntiles;
+  const uint64_t bal = __ballot(ntiles > 0 && it.tile >= excl && it.tile < incl);
+  if (bal == 0) return ref;
+  const int src = __ffsll(static_cast<long long>(bal)) - 1;
+  const int jj = it.tile - __shfl(excl, src, 64);
+  const int slo = __shfl(lo, src, 64);
+  const int shi = __shfl(hi, src, 64);
+  ref.g = 1 + src;
+  ref.slot0 = slo + jj * TM;
+  ref.nrows = min(TM, shi - ref.slot0);
+  ref.rank = __shfl(rk, src, 64);
+  ref.off = __shfl(of, src, 64);
   return ref;
 }
 

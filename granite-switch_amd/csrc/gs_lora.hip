@@ -22,59 +22,26 @@ __host__ __device__ inline int max_tiles_for(int64_t T, int NA) {
   return static_cast<int>((T + kTM - 1) / kTM + (NA < T ? NA : T));
 }
 
-// Straight-line loads.  Every load below is issued unconditionally from a
-// clamped, in-bounds address and masked afterwards with a select: with no
-// branches around memory instructions the compiler can count the loads in
-// flight, so a prefetch really overlaps the work on the previous batch
-// instead of being drained by a conservative wait.
-
-// The 4 pieces of 16 bytes a lane loads from a row for the batch starting at
-// element kb: piece p covers elements kb + (2p + h)*P .. +P, so the two lane
-// halves of a row read adjacent pieces (32 contiguous bytes per row and
-// access).  Pieces at or past kend (or all, when !valid) read element kclamp
-// instead and become zero.  The MFMA pairs x and A elements by (piece, lane
-// half, element), the same for both operands, so any fixed mapping of k is a
-// correct contraction.
-template <bool BF16>
-__device__ __forceinline__ void load_row4(const char* row, int64_t kb, int h, int64_t kend, int64_t kclamp, bool valid,
-                                          u32x4 out[4]) {
-  constexpr int P = Elt<BF16>::kPerPiece;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int64_t kp = kb + (2 * p + h) * P;
-    const bool ok = valid && kp < kend;
-    out[p] = sel16(ok, ld16(row + (ok ? kp : kclamp) * Elt<BF16>::kSize));
-  }
-}
-
-// acc += (lane's 4 pieces of x) x (lane's 4 pieces of A) over one batch.
-template <bool BF16>
-__device__ __forceinline__ f32x16 mfma_batch(const u32x4 xa[4], const u32x4 wb[4], f32x16 acc) {
-  if constexpr (BF16) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) acc = mfma32_bf16(xa[t], wb[t], acc);
-  } else {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const f32x4 a = __builtin_bit_cast(f32x4, xa[t]);
-      const f32x4 b = __builtin_bit_cast(f32x4, wb[t]);
-      acc = mfma32_f32(a.x, b.x, acc);
-      acc = mfma32_f32(a.y, b.y, acc);
-      acc = mfma32_f32(a.z, b.z, acc);
-      acc = mfma32_f32(a.w, b.w, acc);
-    }
-  }
-  return acc;
-}
+// Loads below are issued unconditionally from clamped, in-bounds addresses and
+// masked afterwards with a select: with no branches around memory
+// instructions the compiler can count the loads in flight, so a prefetch
+// really overlaps the work on the previous batch instead of being drained by
+// a conservative wait.
 
 // ----------------------------------------------------------------------------
-// Shrink.  Grid (max_tiles, n_chunks, KS).  A workgroup computes one tile
-// (32 slots) x NB n-blocks of 32 output columns over the k-chunk
-// [ks*KC, ks*KC+KC); its 4 waves split that chunk in 4, stream it in
-// double-buffered batches, and are reduced through LDS in a fixed order.
-// KS == 1 writes z in the element type; KS > 1 writes the fp32 partial of
-// chunk ks to part[ks][slot][col].
+// Shrink.  1-D grid over (tile, column chunk, k-chunk) items, tiles spread
+// over the XCDs in contiguous ranges (xcd_item).  A workgroup computes one
+// tile of kTMS = 64 slots of one adapter x COLS = 32*NB output columns over
+// the k-chunk [ks*KC, ks*KC + KC).  Each wave owns 16 of the slots and the
+// whole column range, so no cross-wave reduction is needed.  The chunk is
+// streamed in batches of BK k: the workgroup stages the batch's lora_A tile
+// (COLS rows, 512 contiguous bytes per row) in LDS once, each wave keeps its
+// 16 x rows in registers (64 contiguous bytes per row and load), and 16x16
+// MFMAs (x rows x lora_A rows) accumulate.  The next batch's loads are issued
+// before the current batch is computed.  KS == 1 writes z in the element
+// type; KS > 1 writes the fp32 partial of chunk ks to part[ks][slot][col].
 // ----------------------------------------------------------------------------
+constexpr int kTMS = 64;           // slots per shrink tile
 constexpr int kOutPad = 4;
 
 struct ShrinkParams {
@@ -95,148 +62,146 @@ struct ShrinkParams {
   int zw;
   int KS;
   int KC;
+  int n_chunks;
 };
 
+// 16x16 MFMA over one 16-byte piece of each operand (K = 32 bf16, or four
+// K = 4 fp32 steps).  Lane l supplies row l % 16 of each operand and elements
+// of lane group l / 16; both operands pair elements the same way, so any
+// fixed assignment of k to pieces is a correct contraction.  Result: lane l
+// holds D[4*(l/16) + e][l % 16].
 template <bool BF16>
-__device__ __forceinline__ void store_z16(void* z, int64_t ldz, int slot, int col, int ncols, const float* v) {
-  // 16 consecutive columns of one z row; ncols is a multiple of 8.
+__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, f32x4 acc) {
   if constexpr (BF16) {
-    uint16_t* zr = static_cast<uint16_t*>(z) + static_cast<int64_t>(slot) * ldz + col;
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      if (col + half * 8 < ncols) {
-        const float* w = v + half * 8;
-        st16(zr + half * 8, u32x4{pack_bf16x2(w[0], w[1]), pack_bf16x2(w[2], w[3]), pack_bf16x2(w[4], w[5]),
-                                  pack_bf16x2(w[6], w[7])});
-      }
-    }
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc,
+                                                   0, 0, 0);
   } else {
-    float* zr = static_cast<float*>(z) + static_cast<int64_t>(slot) * ldz + col;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (col + q * 4 < ncols) *reinterpret_cast<f32x4*>(zr + q * 4) = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-    }
+    const f32x4 x = __builtin_bit_cast(f32x4, a);
+    const f32x4 w = __builtin_bit_cast(f32x4, b);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, w.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, w.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, w.z, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, w.w, acc, 0, 0, 0);
   }
 }
 
 template <bool BF16, int NB>
 __global__ __launch_bounds__(kThreads) void shrink_kernel(ShrinkParams p) {
+  constexpr int P = Elt<BF16>::kPerPiece;        // elements per 16-byte piece
+  constexpr int ES = Elt<BF16>::kSize;
+  constexpr int KSTEP = 4 * P;                   // k of one piece over the 4 lane groups
+  constexpr int NPB = 8;                         // pieces per batch and lane
+  constexpr int BK = NPB * KSTEP;                // k per batch (256 bf16, 128 fp32)
   constexpr int COLS = 32 * NB;
-  __shared__ float red[2][NB][16][64];                 // cross-wave reduction
-  __shared__ float tile_s[kTM][COLS + kOutPad];        // row-major result
+  constexpr int NC16 = COLS / 16;
+  constexpr int ROWB = BK * ES;                  // bytes of one lora_A row per batch
+  constexpr int ALD = ROWB + 16;                 // LDS row stride (padded against bank conflicts)
+  constexpr int PPR = ROWB / 16;                 // 16-byte pieces per row and batch
+  constexpr int APT = COLS * PPR / kThreads;     // lora_A pieces per thread and batch
+  static_assert(COLS * PPR % kThreads == 0, "lora_A pieces must split evenly over the workgroup");
+  __shared__ __align__(16) char a_s[COLS * ALD];
 
-  const TileRef tr = find_tile<kTM>(p.seg, p.ranks, p.a_off, p.NA, blockIdx.x);
+  int sub = 0;
+  const TileRef tr =
+      locate_tile<kTMS>(p.seg, p.ranks, p.a_off, p.NA, static_cast<int>(blockIdx.x), p.n_chunks * p.KS, sub);
   if (tr.g == 0) return;
-  const int r = tr.rank;
-  const int ncols = p.S * r;
-  const int col0 = blockIdx.y * COLS;
+  const int chunk = sub % p.n_chunks;
+  const int ks = sub / p.n_chunks;
+  const int ncols = p.S * tr.rank;
+  const int col0 = chunk * COLS;
   if (col0 >= ncols) return;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int l = tid & 63;
-  const int i = l & 31;
-  const int h = l >> 5;
-  constexpr int B = Elt<BF16>::kBatch;
-
-  const int64_t k_lo = static_cast<int64_t>(blockIdx.z) * p.KC;
+  const int i16 = l & 15;
+  const int q4 = l >> 4;
+  const int64_t k_lo = static_cast<int64_t>(ks) * p.KC;
   const int64_t k_hi = min(static_cast<int64_t>(p.H), k_lo + p.KC);
-  const int wk = p.KC / 4;
-  const int64_t wk_lo = k_lo + static_cast<int64_t>(wave) * wk;
-  const int64_t wk_hi = min(k_hi, wk_lo + wk);
-  const int nbat = wk_hi > wk_lo ? static_cast<int>((wk_hi - wk_lo + B - 1) / B) : 0;
+  const int nbat = static_cast<int>((k_hi - k_lo + BK - 1) / BK);
 
-  // rows: tokens of the tile (rows past the tile re-read its first token) and
-  // the adapter's A rows for this workgroup's columns (clamped likewise)
-  const bool row_ok = i < tr.nrows;
-  const int token = p.perm[tr.slot0 + (row_ok ? i : 0)];
-  const char* xrow = static_cast<const char*>(p.x) + (static_cast<int64_t>(token) * p.ldx) * Elt<BF16>::kSize;
-  const char* arow[NB];
-  bool n_ok[NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int n = col0 + 32 * nb + i;
-    n_ok[nb] = n < ncols;
-    arow[nb] = static_cast<const char*>(p.a_pack) + (tr.off + static_cast<int64_t>(n_ok[nb] ? n : ncols - 1) * p.H) * Elt<BF16>::kSize;
-  }
+  // this lane's x row (slots past the tile re-read the tile's first token)
+  const int srow = 16 * wave + i16;
+  const bool row_ok = srow < tr.nrows;
+  const int token = p.perm[tr.slot0 + (row_ok ? srow : 0)];
+  // this thread's lora_A pieces: flat piece f = tid + 256*j of the COLS x PPR
+  // batch tile is row tid/PPR + j*(256/PPR), piece tid % PPR of the row, so
+  // PPR consecutive threads read one row's 512 contiguous bytes
+  constexpr int RSTEP = kThreads / PPR;          // rows between a thread's pieces
+  const int ar0 = tid / PPR;
+  const int apc = tid % PPR;
+  const char* abase = static_cast<const char*>(p.a_pack) + (tr.off + static_cast<int64_t>(col0 + ar0) * p.H) * ES;
+  const int64_t astep = static_cast<int64_t>(RSTEP) * p.H * ES;
+  const int arows = ncols - col0 - ar0;          // this thread's pieces j with j*RSTEP < arows are real rows
 
-  f32x16 acc[NB];
+  // Straight-line loads from clamped in-bounds addresses, masked afterwards,
+  // so the compiler counts the loads in flight exactly.
+  auto load_a = [&](int b, u32x4 (&av)[APT]) {
+    const int64_t kp = k_lo + static_cast<int64_t>(b) * BK + apc * P;
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x16{};
-
-  auto load = [&](int b, u32x4 (&xv)[4], u32x4 (&av)[NB][4]) {
-    const int64_t kb = wk_lo + static_cast<int64_t>(b) * B;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) load_row4<BF16>(arow[nb], kb, h, wk_hi, wk_lo, n_ok[nb], av[nb]);
-    load_row4<BF16>(xrow, kb, h, wk_hi, wk_lo, row_ok, xv);
+    for (int j = 0; j < APT; ++j) {
+      const bool ok = j * RSTEP < arows && kp < k_hi;
+      av[j] = sel16(ok, ld16(abase + (ok ? j * astep + kp * ES : k_lo * ES)));
+    }
   };
-  if (nbat > 0) {
-    u32x4 xc[4], ac[NB][4];
-    load(0, xc, ac);
-    for (int b = 0; b + 1 < nbat; ++b) {
-      u32x4 xn[4], an[NB][4];
-      load(b + 1, xn, an);
+  // lora_A of the first batch goes out before the wait for the token index
+  u32x4 xc[NPB], xn[NPB], an[APT];
+  load_a(0, an);
+  const char* xrow = static_cast<const char*>(p.x) + static_cast<int64_t>(token) * p.ldx * ES;
+  auto load_x = [&](int b, u32x4 (&xv)[NPB]) {
+    const int64_t kb = k_lo + static_cast<int64_t>(b) * BK;
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma_batch<BF16>(xc, ac[nb], acc[nb]);
+    for (int pp = 0; pp < NPB; ++pp) {
+      const int64_t kp = kb + pp * KSTEP + q4 * P;
+      const bool ok = row_ok && kp < k_hi;
+      xv[pp] = sel16(ok, ld16(xrow + (ok ? kp : k_lo) * ES));
+    }
+  };
+  auto stage_a = [&](const u32x4 (&av)[APT]) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        xc[q] = xn[q];
+    for (int j = 0; j < APT; ++j) st16(a_s + (ar0 + j * RSTEP) * ALD + apc * 16, av[j]);
+  };
+
+  f32x4 acc[NC16];
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) ac[nb][q] = an[nb][q];
+  for (int c = 0; c < NC16; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  load_x(0, xc);
+  stage_a(an);
+  lds_barrier();
+  for (int b = 0; b < nbat; ++b) {
+    load_x(b + 1, xn);                 // past the chunk every piece is masked
+    load_a(b + 1, an);
+#pragma unroll
+    for (int pp = 0; pp < NPB; ++pp) {
+#pragma unroll
+      for (int c = 0; c < NC16; ++c) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(a_s + (16 * c + i16) * ALD + (pp * KSTEP + q4 * P) * ES);
+        acc[c] = mfma16<BF16>(xc[pp], a, acc[c]);
       }
     }
+    lds_barrier();                     // every wave is done with this batch's tile
+    stage_a(an);
+    lds_barrier();
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma_batch<BF16>(xc, ac[nb], acc[nb]);
+    for (int pp = 0; pp < NPB; ++pp) xc[pp] = xn[pp];
   }
 
-  // Fixed-order cross-wave reduction: (w0 + w2) + (w1 + w3).
-  if (wave >= 2) {
+  // lane (i16, q4) holds slots 16*wave + 4*q4 + e, column col0 + 16*c + i16
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+  for (int c = 0; c < NC16; ++c) {
+    const int col = col0 + 16 * c + i16;
+    if (col >= ncols) continue;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) red[wave - 2][nb][v][l] = acc[nb][v];
-  }
-  lds_barrier();
-  if (wave < 2) {
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[nb][v] += red[wave][nb][v][l];
-  }
-  lds_barrier();
-  if (wave == 1) {
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) red[0][nb][v][l] = acc[nb][v];
-  }
-  lds_barrier();
-  if (wave == 0) {
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) tile_s[mfma32_row(v, l)][32 * nb + i] = acc[nb][v] + red[0][nb][v][l];
-  }
-  lds_barrier();
-
-  // each thread owns 16 consecutive columns of one row
-  constexpr int TPR = COLS / 16;
-  for (int idx = tid; idx < kTM * TPR; idx += kThreads) {
-    const int row = idx / TPR;
-    const int cx = (idx % TPR) * 16;
-    if (row >= tr.nrows) continue;
-    float vals[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) vals[e] = tile_s[row][cx + e];
-    const int slot = tr.slot0 + row;
-    const int col = col0 + cx;
-    if (p.KS == 1) {
-      store_z16<BF16>(p.z, p.ldz, slot, col, ncols, vals);
-    } else {
-      float* dst = p.part + static_cast<int64_t>(blockIdx.z) * p.part_stride + static_cast<int64_t>(slot) * p.zw + col;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (col + 4 * q < ncols) *reinterpret_cast<f32x4*>(dst + 4 * q) = f32x4{vals[4 * q], vals[4 * q + 1], vals[4 * q + 2], vals[4 * q + 3]};
+    for (int e = 0; e < 4; ++e) {
+      const int row = 16 * wave + 4 * q4 + e;
+      if (row >= tr.nrows) continue;
+      const int64_t slot = tr.slot0 + row;
+      if (p.KS == 1) {
+        if constexpr (BF16) static_cast<uint16_t*>(p.z)[slot * p.ldz + col] = f32_to_bf16_bits(acc[c][e]);
+        else static_cast<float*>(p.z)[slot * p.ldz + col] = acc[c][e];
+      } else {
+        p.part[static_cast<int64_t>(ks) * p.part_stride + slot * p.zw + col] = acc[c][e];
+      }
     }
   }
 }
@@ -281,7 +246,8 @@ __global__ __launch_bounds__(kThreads) void reduce_parts_kernel(const float* __r
 }
 
 // ----------------------------------------------------------------------------
-// Expand.  Grid (ceil(n_sub / ni), max_tiles).  A workgroup owns one tile (32
+// Expand.  1-D grid over (tile, group of ni column sub-tiles) items, tiles
+// spread over the XCDs in contiguous ranges (xcd_item).  A workgroup owns one tile (32
 // slots of one adapter) and walks ni consecutive column sub-tiles of NT
 // columns.  The tile's shrink values for every slice (z rows, or the sum of
 // the split-K partials rounded to the element type exactly like a
@@ -392,11 +358,13 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
   __shared__ float dtile[kTM][NT + kOutPad];
   extern __shared__ __align__(16) char zs[];   // [32][S*max_rank + 8] element type
 
-  const TileRef tr = find_tile<kTM>(p.seg, p.ranks, p.b_off, p.NA, blockIdx.y);
+  const int n_sub = (p.out_total + NT - 1) / NT;
+  int sub = 0;
+  const TileRef tr = locate_tile<kTM>(p.seg, p.ranks, p.b_off, p.NA, static_cast<int>(blockIdx.x),
+                                      (n_sub + p.ni - 1) / p.ni, sub);
   if (tr.g == 0) return;
   const int r = tr.rank;
-  const int n_sub = (p.out_total + NT - 1) / NT;
-  const int sub0 = blockIdx.x * p.ni;
+  const int sub0 = sub * p.ni;
   if (sub0 >= n_sub) return;
   const int nsub = min(p.ni, n_sub - sub0);
 
@@ -534,16 +502,17 @@ struct ShrinkPlan {
 
 static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, bool bf16) {
   ShrinkPlan pl{};
-  pl.max_tiles = max_tiles_for(T, NA);
+  pl.max_tiles = static_cast<int>((T + kTMS - 1) / kTMS + (NA < T ? NA : T));
   pl.zw = S * max_rank;
   const int nblk = (pl.zw + 31) / 32;         // 32-column blocks of the widest adapter
   pl.NB = nblk >= 4 ? 4 : nblk;
   pl.n_chunks = (pl.zw + 32 * pl.NB - 1) / (32 * pl.NB);
-  const int unit = 4 * (bf16 ? Elt<true>::kBatch : Elt<false>::kBatch);   // k per workgroup step
+  const int unit = bf16 ? 256 : 128;          // k per batch of the shrink kernel
   const int units = (H + unit - 1) / unit;
-  // aim for ~1024 workgroups; the tile count is an upper bound (T/32 + NA)
+  // split the hidden dimension for about 768 workgroups (the tile count is an
+  // upper bound, T/64 + NA), at most 16 ways (the partial sums' consumers)
   const int64_t wgs = static_cast<int64_t>(pl.max_tiles) * pl.n_chunks;
-  int ks = static_cast<int>((1024 + wgs - 1) / (wgs > 0 ? wgs : 1));
+  int ks = static_cast<int>((768 + wgs - 1) / (wgs > 0 ? wgs : 1));
   if (ks < 1) ks = 1;
   if (ks > 16) ks = 16;
   if (ks > units) ks = units;
@@ -608,6 +577,7 @@ ShrinkParams make_shrink_params(const ShrinkPlan& pl, const void* x, int64_t ldx
   p.zw = pl.zw;
   p.KS = pl.KS;
   p.KC = pl.KC;
+  p.n_chunks = pl.n_chunks;
   return p;
 }
 
@@ -622,7 +592,7 @@ int check_workspace(const ShrinkPlan& pl, const void* workspace, int64_t workspa
 
 template <bool BF16>
 void launch_shrink_t(const ShrinkPlan& pl, const ShrinkParams& p, hipStream_t st) {
-  dim3 grid(pl.max_tiles, pl.n_chunks, pl.KS);
+  dim3 grid(8 * ((pl.max_tiles + 7) / 8) * pl.n_chunks * pl.KS);
   if (pl.NB == 4) hipLaunchKernelGGL((shrink_kernel<BF16, 4>), grid, dim3(kThreads), 0, st, p);
   else if (pl.NB == 3) hipLaunchKernelGGL((shrink_kernel<BF16, 3>), grid, dim3(kThreads), 0, st, p);
   else if (pl.NB == 2) hipLaunchKernelGGL((shrink_kernel<BF16, 2>), grid, dim3(kThreads), 0, st, p);
@@ -695,7 +665,7 @@ void launch_expand(bool bf16, int64_t T, ExpandParams p, hipStream_t st) {
   if (ni < 1) ni = 1;
   if (ni > n_sub) ni = n_sub;
   p.ni = ni;
-  dim3 grid((n_sub + ni - 1) / ni, max_tiles);
+  dim3 grid(8 * ((max_tiles + 7) / 8) * ((n_sub + ni - 1) / ni));
   const size_t lds = expand_lds_bytes(bf16, p.si.S, p.max_rank);
   if (bf16) {
     if (wide) launch_expand_pre<true, 2>(grid, lds, p, st);

@@ -15,20 +15,24 @@ void set_error(const char* fmt, ...) {
 }
 
 // ---------------------------------------------------------------------------
-// Segment builder: one workgroup of 1024 threads (16 waves).
+// Segment builder: one workgroup of 1024 threads (16 waves) per chunk of 1024
+// tokens, with no communication between workgroups.
 //
-// Pass 1 computes every token's effective id (aLoRA gating) and a histogram in
-// LDS.  A wave-0 scan turns the histogram into seg_offsets.  Pass 2 walks the
-// tokens in chunks of 1024, in order; inside a wave, tokens with equal ids are
-// found with one ballot per id bit, so a token's rank among equal ids of lower
-// lanes is a popcount; per-wave counts in LDS give the rank across waves, and a
-// running cursor per adapter carries the order across chunks.  The result is a
-// stable sort (ascending token order within each adapter).
+// Every workgroup gates ALL tokens (aLoRA activation offsets; sequence
+// boundaries staged in LDS) and counts them per adapter: the whole batch's
+// histogram gives seg_offsets (written by workgroup 0), the histogram of the
+// tokens before its own chunk gives the chunk's starting cursor per adapter.
+// Counting is per wave: lanes with equal ids are matched with one ballot per
+// id bit, and the lowest lane of each group adds the group's size to LDS.  Then
+// the workgroup scatters its own chunk: a token's rank among equal ids of lower
+// lanes is a popcount, per-wave counts in LDS give the rank across waves.  The
+// result is a stable sort (ascending token order within each adapter), the
+// iteration order of the reference HF loop.
 // ---------------------------------------------------------------------------
 constexpr int kBuildThreads = 1024;
 constexpr int kBuildWaves = kBuildThreads / 64;
-constexpr int kBuildRegChunks = 8;      // chunks of 1024 tokens whose ids stay in registers
-constexpr int kCuCap = 2048;            // sequences whose boundaries are staged in LDS
+constexpr int kCuCap = 2048;            // sequences whose boundaries and offsets are staged in LDS
+constexpr int kPre = 8;                 // token chunks whose ids and positions are loaded together
 
 // largest s with cu[s] <= t (cu non-decreasing, cu[0] = 0), over n = num_seqs entries
 __device__ __forceinline__ int find_seq(const int32_t* cu, int n, int t) {
@@ -53,68 +57,110 @@ struct BuildArgs {
   int32_t* perm;
 };
 
-__device__ __forceinline__ int effective_id(const BuildArgs& a, const int32_t* cu_lds, int t) {
-  int64_t id = a.req[t];
+// Effective id of token t from its requested id and position (already
+// loaded): base unless the token's position reaches its sequence's activation
+// offset; ids outside [0, NA] are base.  Sequence boundaries and offsets come
+// from LDS when they fit there.
+__device__ __forceinline__ int gate_id(const BuildArgs& a, const int32_t* cu_lds, const int64_t* off_lds, int t,
+                                       int64_t id, int64_t pos) {
   if (a.act_off != nullptr) {
     int s = 0;
     if (a.cu != nullptr) s = cu_lds != nullptr ? find_seq(cu_lds, a.num_seqs, t) : find_seq(a.cu, a.num_seqs, t);
-    const int64_t q = (a.pos != nullptr) ? a.pos[t]
+    const int64_t q = (a.pos != nullptr) ? pos
                                          : static_cast<int64_t>(t - (a.cu != nullptr ? (cu_lds ? cu_lds[s] : a.cu[s]) : 0));
-    if (q < a.act_off[s]) id = 0;
+    if (q < (off_lds != nullptr ? off_lds[s] : a.act_off[s])) id = 0;
   }
   if (id < 0 || id > a.NA) id = 0;
   return static_cast<int>(id);
 }
 
+// Lanes of the wave whose id equals this lane's (one ballot per id bit).
+__device__ __forceinline__ uint64_t match_id(int id, bool active, int nbits) {
+  uint64_t match = __ballot(active);
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = (id >> b) & 1;
+    const uint64_t bal = __ballot(bit);
+    match &= bit ? bal : ~bal;
+  }
+  return match;
+}
+
 __global__ __launch_bounds__(kBuildThreads) void build_segments_kernel(BuildArgs a) {
-  __shared__ int hist[GS_MAX_ADAPTERS + 1];
-  __shared__ int cursor[GS_MAX_ADAPTERS + 1];
+  __shared__ int total[GS_MAX_ADAPTERS + 1];
+  __shared__ int cursor[GS_MAX_ADAPTERS + 1];     // counts before this chunk, then the chunk's cursors
   __shared__ int wcnt[kBuildWaves][GS_MAX_ADAPTERS + 1];
   __shared__ int32_t cu_s[kCuCap];
+  __shared__ int64_t off_s[kCuCap];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int NA = a.NA;
   const int T = a.T;
+  const int c0 = static_cast<int>(blockIdx.x) * kBuildThreads;   // this workgroup's chunk
 
   for (int i = tid; i <= NA; i += kBuildThreads) {
-    hist[i] = 0;
-    for (int w = 0; w < kBuildWaves; ++w) wcnt[w][i] = 0;
+    total[i] = 0;
+    cursor[i] = 0;
   }
-  const bool cu_in_lds = a.cu != nullptr && a.act_off != nullptr && a.num_seqs <= kCuCap;
-  if (cu_in_lds)
-    for (int i = tid; i < a.num_seqs; i += kBuildThreads) cu_s[i] = a.cu[i];
-  lds_barrier();
-  const int32_t* cu_lds = cu_in_lds ? cu_s : nullptr;
-
-  // Pass 1: effective ids + histogram; the first chunks keep their ids in registers.
-  int ereg[kBuildRegChunks];
-#pragma unroll
-  for (int c = 0; c < kBuildRegChunks; ++c) {
-    const int t = c * kBuildThreads + tid;
-    ereg[c] = 0;
-    if (t < T) {
-      const int id = effective_id(a, cu_lds, t);
-      ereg[c] = id;
-      a.eff[t] = id;
-      if (id > 0) atomicAdd(&hist[id], 1);
+  for (int i = tid; i < kBuildWaves * (GS_MAX_ADAPTERS + 1); i += kBuildThreads) (&wcnt[0][0])[i] = 0;
+  const int nseq = a.cu != nullptr ? a.num_seqs : 1;
+  const bool seq_in_lds = a.act_off != nullptr && nseq <= kCuCap;
+  if (seq_in_lds) {
+    for (int i = tid; i < nseq; i += kBuildThreads) {
+      cu_s[i] = a.cu != nullptr ? a.cu[i] : 0;
+      off_s[i] = a.act_off[i];
     }
   }
-  for (int t = kBuildRegChunks * kBuildThreads + tid; t < T; t += kBuildThreads) {
-    const int id = effective_id(a, cu_lds, t);
-    a.eff[t] = id;
-    if (id > 0) atomicAdd(&hist[id], 1);
+  lds_barrier();
+  const int32_t* cu_lds = seq_in_lds && a.cu != nullptr ? cu_s : nullptr;
+  const int64_t* off_lds = seq_in_lds ? off_s : nullptr;
+  int nbits = 0;
+  while ((1 << nbits) <= NA) ++nbits;
+
+  // Pass 1: gate every token of the batch and count per adapter.  The ids and
+  // positions of kPre chunks are loaded together (clamped, in bounds) before
+  // any is used.
+  int mine = 0;                                   // this thread's token of the own chunk
+  const int nchunks = (T + kBuildThreads - 1) / kBuildThreads;
+  for (int k0 = 0; k0 < nchunks; k0 += kPre) {
+    int64_t rq[kPre], ps[kPre];
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) {
+      const int tc = min((k0 + u) * kBuildThreads + tid, T - 1);
+      rq[u] = a.req[tc];
+      ps[u] = a.pos != nullptr ? a.pos[tc] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) {
+      const int b0 = (k0 + u) * kBuildThreads;
+      if (b0 < T) {
+        const int t = b0 + tid;
+        const int id = t < T ? gate_id(a, cu_lds, off_lds, t, rq[u], ps[u]) : 0;
+        if (b0 == c0) {
+          mine = id;
+          if (t < T) a.eff[t] = id;
+        }
+        const bool active = id > 0;
+        const uint64_t match = match_id(id, active, nbits);
+        if (active && (match & lanemask_lt()) == 0) {
+          const int n = __popcll(match);
+          atomicAdd(&total[id], n);
+          if (b0 < c0) atomicAdd(&cursor[id], n);
+        }
+      }
+    }
   }
   lds_barrier();
 
-  // Exclusive scan of hist[1..NA] by wave 0 -> cursor, seg.
+  // Exclusive scan of total[1..NA] by wave 0: segment starts; the chunk's
+  // cursor = segment start + tokens of the adapter before the chunk.
   if (wave == 0) {
     const int lane = tid & 63;
     int carry = 0;
-    if (lane == 0) a.seg[0] = 0;
+    if (lane == 0 && blockIdx.x == 0) a.seg[0] = 0;
     for (int g0 = 1; g0 <= NA; g0 += 64) {
       const int g = g0 + lane;
-      const int v = (g <= NA) ? hist[g] : 0;
+      const int v = (g <= NA) ? total[g] : 0;
       int incl = v;
 #pragma unroll
       for (int d = 1; d < 64; d <<= 1) {
@@ -122,54 +168,25 @@ __global__ __launch_bounds__(kBuildThreads) void build_segments_kernel(BuildArgs
         if (lane >= d) incl += u;
       }
       if (g <= NA) {
-        cursor[g] = carry + incl - v;
-        a.seg[g] = carry + incl;
+        cursor[g] += carry + incl - v;
+        if (blockIdx.x == 0) a.seg[g] = carry + incl;
       }
       carry += __shfl(incl, 63, 64);
     }
   }
   lds_barrier();
 
-  int nbits = 0;
-  while ((1 << nbits) <= NA) ++nbits;
-
-  // Pass 2: stable scatter, chunk by chunk in token order.
-  const int nchunks = (T + kBuildThreads - 1) / kBuildThreads;
-  for (int c = 0; c < nchunks; ++c) {
-    const int t = c * kBuildThreads + tid;
-    int id = 0;
-    if (c < kBuildRegChunks) {
-#pragma unroll
-      for (int u = 0; u < kBuildRegChunks; ++u)
-        if (u == c) id = ereg[u];
-    } else if (t < T) {
-      id = a.eff[t];    // written by this same thread in pass 1
-    }
-    const bool active = id > 0;
-    uint64_t match = __ballot(active);
-    for (int b = 0; b < nbits; ++b) {
-      const bool bit = (id >> b) & 1;
-      const uint64_t bal = __ballot(bit);
-      match &= bit ? bal : ~bal;
-    }
-    const uint64_t below = match & lanemask_lt();
-    if (active && below == 0) wcnt[wave][id] = __popcll(match);
-    lds_barrier();
-    if (active) {
-      int pp = cursor[id] + __popcll(below);
-      for (int w = 0; w < wave; ++w) pp += wcnt[w][id];
-      a.perm[pp] = t;
-    }
-    lds_barrier();
-    for (int g = tid + 1; g <= NA; g += kBuildThreads) {
-      int add = 0;
-      for (int w = 0; w < kBuildWaves; ++w) {
-        add += wcnt[w][g];
-        wcnt[w][g] = 0;
-      }
-      cursor[g] += add;
-    }
-    lds_barrier();
+  // Pass 2: stable scatter of this chunk.
+  const int t = c0 + tid;
+  const bool active = t < T && mine > 0;
+  const uint64_t match = match_id(mine, active, nbits);
+  const uint64_t below = match & lanemask_lt();
+  if (active && below == 0) wcnt[wave][mine] = __popcll(match);
+  lds_barrier();
+  if (active) {
+    int pp = cursor[mine] + __popcll(below);
+    for (int w = 0; w < wave; ++w) pp += wcnt[w][mine];   // zero where wave w has none of this id
+    a.perm[pp] = t;
   }
 }
 
@@ -318,7 +335,8 @@ int gs_build_segments(const int64_t* req_ids, const int64_t* positions, const in
                "gs_build_segments: num_seqs=%d with cu_seqlens", num_seqs);
   BuildArgs a{req_ids, positions, cu_seqlens, act_offsets, static_cast<int>(num_tokens), cu_seqlens ? num_seqs : 1,
               num_adapters, eff_ids, seg_offsets, perm};
-  hipLaunchKernelGGL(build_segments_kernel, dim3(1), dim3(kBuildThreads), 0, static_cast<hipStream_t>(stream), a);
+  const unsigned chunks = num_tokens > 0 ? static_cast<unsigned>((num_tokens + kBuildThreads - 1) / kBuildThreads) : 1u;
+  hipLaunchKernelGGL(build_segments_kernel, dim3(chunks), dim3(kBuildThreads), 0, static_cast<hipStream_t>(stream), a);
   GS_CHECK_LAUNCH("gs_build_segments");
   return GS_OK;
 }

@@ -371,10 +371,15 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
   constexpr int ES = Elt<BF16>::kSize;
   constexpr int KSTEP = 4 * P;      // k per piece over the 4 lane groups
   constexpr int KW = NPW * KSTEP;   // k per wave
-  const int cb = bid % p.NCB;
-  const int rem = bid / p.NCB;
-  const int kc = rem % p.KS;
-  const int g = rem / p.KS + 1;
+  // Workgroups are dealt to the 8 XCDs round-robin by id, so the NCB
+  // column-block siblings of one (k-chunk, adapter) -- which read the same x
+  // rows -- get ids 8 apart and share an XCD's L2.  Ids past the last
+  // (k-chunk, adapter) pair have no work.
+  const int cb = (bid >> 3) % p.NCB;
+  const int q = ((bid >> 3) / p.NCB) * 8 + (bid & 7);
+  if (q >= p.KS * p.rt.NA) return;
+  const int kc = q % p.KS;
+  const int g = q / p.KS + 1;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int l = tid & 63;
@@ -866,7 +871,7 @@ int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t*
   fp.S = num_slices;
   fp.KS = pl.KS;
   fp.NCB = pl.NCB;
-  fp.NP = pl.NCB * pl.KS * num_adapters;
+  fp.NP = 8 * pl.NCB * ((pl.KS * num_adapters + 7) / 8);
   fp.part = static_cast<uint64_t*>(workspace);
   fp.region = region_bytes / 8;
   fp.cap = pl.cap;
