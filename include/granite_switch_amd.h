@@ -173,11 +173,13 @@ int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t
  * before the first call and used by nothing but this entry point (it holds
  * epoch-tagged partial sums; any size change may reuse the same buffer).
  * sync: gs_small_sync_bytes() bytes, 8-byte aligned, ZEROED before the first
- * call: int32 words 0-1 are the 64-bit launch epoch / started count, word 2
- * an error word whose bit 0 means an expand workgroup gave up waiting (20 ms)
- * and that call's output is wrong.  Zeroing sync again requires zeroing the
- * workspace too.  Calls sharing a workspace or sync buffer must not overlap
- * in time (stream order is enough).
+ * call: int32 word 2 is an error word whose bit 0 means an expand workgroup
+ * gave up waiting (20 ms) and that call's output is wrong; int32 words
+ * [32*g, 32*g + 1] hold adapter g's 64-bit launch counter (each launch with
+ * tokens for g adds 2^20; bits 20 and up are g's epoch, the tag of its
+ * partials).  Zeroing sync again requires zeroing the workspace too.  Calls
+ * sharing a workspace or sync buffer must not overlap in time (stream order
+ * is enough).
  * speculate != 0 issues every adapter's weight loads before the routing is
  * known (saves a memory round trip when most adapters have tokens); 0 reads
  * only the weights of adapters some token requests.
