@@ -14,6 +14,9 @@ K launches of that kernel alone, rotating buffers).  The CPU baseline is the
 reference's HF loop restated on torch-CPU, timed on the host cores.
 
   python bench.py [--steps K] [--warmup W] [--config {0..4}] [--no-cpu]
+  python bench.py --copy-probe MIB   # a plain device copy of MIB MiB, the
+                                     # reference for scaling rocprofv3's
+                                     # FETCH_SIZE / WRITE_SIZE counters
 """
 
 from __future__ import annotations
@@ -34,10 +37,51 @@ HBM_PEAK_GBS = 8000.0
 MFMA_PEAK = {"bf16": 2.5e15, "fp32": 157.3e12}
 MALL_BYTES = 256 << 20
 DEFAULT_STEPS = {0: 200, 1: 200, 2: 40, 3: 100, 4: 8}
+# workload names used by the rocprofv3 summaries under profiles/
+WORKLOAD_KEY = {0: "fp32_single_op_2048x2048_T512", 1: "decode_qkv_4096x6144_T256",
+                2: "prefill_gate_up_4096x25600_T8192", 3: "multiswitch_down_12800x4096_T4096",
+                4: "decoder_step_32_layers_T4144"}
+TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
+
+
+def measured_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` on `workload` from the rocprofv3 PMC summary, or None."""
+    try:
+        lines = open(TRAFFIC_TABLE).read().splitlines()
+    except OSError:
+        return None
+    for line in lines:
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 6 and cells[0] == workload and cells[1] == kernel:
+            try:
+                return int(cells[5])
+            except ValueError:
+                return None
+    return None
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def copy_probe(mib: int) -> None:
+    """Five copies of `mib` MiB between fresh device buffers (torch's copy kernel)."""
+    import torch
+
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty(n, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(5):
+        dst.copy_(src)
+    end.record()
+    end.synchronize()
+    ms = start.elapsed_time(end) / 5
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "us_per_copy": ms * 1e3,
+                      "gbs_read_plus_write": 2 * n / (ms * 1e-3) / 1e9}), flush=True)
 
 
 def main():
@@ -48,7 +92,12 @@ def main():
     ap.add_argument("--config", type=int, default=1, choices=[0, 1, 2, 3, 4])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--sets", type=int, default=None, help="buffer sets to rotate (default: > 2x MALL)")
+    ap.add_argument("--copy-probe", type=int, default=None, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB five times (counter calibration)")
     args = ap.parse_args()
+    if args.copy_probe is not None:
+        copy_probe(args.copy_probe)
+        return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -278,7 +327,7 @@ def main():
                    "projections": [f"{s.name} {s.hidden}->{sum(s.output_slices)}" for s in specs],
                    "layers": layers, "buffer_sets": nsets},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": dom_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": dom_gbs / HBM_PEAK_GBS, "traffic": None,
+                     "frac": dom_gbs / HBM_PEAK_GBS, "traffic": measured_traffic(WORKLOAD_KEY[cfg], dom),
                      "algorithmic_bytes": per_kernel_bytes[dom], "avg_us": kern_us[dom]},
         "cpu_baseline": cpu,
         "us_per_op": us_op,
