@@ -60,6 +60,7 @@ SIGNATURES = {
     "gs_switch_lora_expand_swiglu": (c_i32, [c_void_p, c_i64, c_i64, c_void_p, c_i64, c_i64, c_i64, c_void_p, c_i32,
                                              c_void_p, c_i64, c_void_p, c_void_p, c_void_p, c_i32, c_i32, c_i32, c_i32,
                                              c_void_p]),
+    "gs_gemm_bf16_tn": (c_i32, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i64, c_i64, c_void_p]),
 }
 
 

@@ -18,7 +18,7 @@ REPO_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libgranite_switch_amd.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ("gs_meta.hip", "gs_lora.hip", "gs_small.hip", "gs_xext.hip")
+SOURCES = ("gs_meta.hip", "gs_lora.hip", "gs_small.hip", "gs_xext.hip", "gs_gemm.hip")
 ARCH = os.environ.get("GS_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

@@ -593,6 +593,31 @@ def _i32_array(vals):
     return (ctypes.c_int32 * len(vals))(*[int(v) for v in vals])
 
 
+def linear_bf16(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[M, N] = x[M, K] . w[N, K]^T in bf16 with fp32 accumulation (``gs_gemm_bf16_tn``).
+
+    The vLLM layer's one GEMM, ``x_ext = x . w_ext^T``
+    (src/granite_switch/vllm/core/lora.py:544).  ``x`` and ``w`` need
+    unit-stride rows; ``out`` (allocated when omitted) may have a row stride.
+    """
+    _require_cuda(x, w)
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise ValueError("linear_bf16 takes bf16 operands")
+    if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
+        raise ValueError(f"shapes {tuple(x.shape)} and {tuple(w.shape)} do not contract")
+    if x.stride(1) != 1 or w.stride(1) != 1:
+        raise ValueError("x and w need unit-stride rows")
+    M, K = x.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or (M and out.stride(1) != 1):
+        raise ValueError("out must be a bf16 [M, N] tensor with unit-stride rows")
+    _lib.call("gs_gemm_bf16_tn", x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(),
+              out.stride(0) if M else N, M, N, K, _lib.stream_ptr(x.device))
+    return out
+
+
 def algorithmic_bytes(segments_host_ids, packed: PackedAdapters, true_ranks=None, elem_bytes: int = 2) -> int:
     """Bytes the op must move at minimum, for the roofline.
 

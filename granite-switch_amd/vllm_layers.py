@@ -7,6 +7,9 @@ as arguments so the class works without vLLM:
 
   forward(x) -> (out, output_bias):
     x_ext = x . w_ext^T           one GEMM: base output + every adapter's shrink
+                                  (gs_gemm_bf16_tn, this library's MFMA GEMM, for
+                                  bf16; torch.mm when ``native_gemm`` is False
+                                  or for fp32)
     expand, in place into x_ext[:, :N_total]
     [row-parallel all-reduce] [bias]
 
@@ -28,6 +31,7 @@ from torch import nn
 
 from . import _lib, ops
 from .kernels import BLOCK_M, BLOCK_N, SUPPORTED_RANKS, build_w_ext, promote_rank
+from . import switched
 from .switched import _dtype_code, _i32_array
 
 logger = logging.getLogger(__name__)
@@ -37,6 +41,8 @@ class SwitchedLoRALinear(nn.Module):
     """Fused switched-LoRA linear layer (reference: vllm/core/lora.py:40-130 for the layout)."""
 
     _lora_ctx = None
+    # x . w_ext^T through gs_gemm_bf16_tn (True) or torch.mm (False)
+    native_gemm = True
 
     def __init__(self, base_layer: nn.Module, num_adapters: int, max_lora_rank: int, num_slices: int = 1,
                  output_slices: tuple | None = None, fuse_swiglu: bool = False, *, tp_size: int = 1,
@@ -263,7 +269,7 @@ class SwitchedLoRALinear(nn.Module):
     # -- forward -------------------------------------------------------------
     def forward(self, x: torch.Tensor):
         assert self._finalized, "finalize_weights() must be called before forward()"
-        x_ext = torch.mm(x, self.w_ext.T)
+        x_ext = self._gemm(x)
         if self.fuse_swiglu:
             return self._forward_swiglu(x, x_ext)
         base_out = x_ext[:, :self._N_total]
@@ -285,6 +291,13 @@ class SwitchedLoRALinear(nn.Module):
         if self._fused_bias is not None:
             base_out = base_out + self._fused_bias
         return base_out, self._output_bias
+
+    def _gemm(self, x: torch.Tensor) -> torch.Tensor:
+        """x_ext = x . w_ext^T (src/granite_switch/vllm/core/lora.py:544)."""
+        if (self.native_gemm and x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(-1) == 1
+                and x.shape[1] % 8 == 0 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0):
+            return switched.linear_bf16(x, self.w_ext)
+        return torch.mm(x, self.w_ext.T)
 
     def _forward_swiglu(self, x: torch.Tensor, x_ext: torch.Tensor):
         M = x.shape[0]

@@ -35,6 +35,10 @@
  *   gs_switch_lora_expand_swiglu
  *                          torch.ops.granite_switch.switch_lora_expand_swiglu
  *                          (lora_ops.py:82-113,204-214; switch_lora_kernel.py:809-857)
+ *   gs_gemm_bf16_tn        the layer's one GEMM x_ext = x . w_ext^T over the base
+ *                          weight stacked with every adapter's lora_A rows
+ *                          (src/granite_switch/vllm/core/lora.py:544;
+ *                          w_ext from src/granite_switch/kernels/switch_lora_kernel.py:134-163)
  */
 #ifndef GRANITE_SWITCH_AMD_H_
 #define GRANITE_SWITCH_AMD_H_
@@ -234,6 +238,16 @@ int gs_switch_lora_expand_swiglu(void* out, int64_t stride_om, int64_t stride_on
                                  int32_t idx_bytes, const int64_t* bitmask, int64_t stride_bm,
                                  const void* lb_packed, const int32_t* slice_col_r, const int32_t* na, int32_t S,
                                  int32_t block_n, int32_t H, int32_t N, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Dense bf16 GEMM C[M,N] = A[M,K] . B[N,K]^T with fp32 accumulation and one
+ * bf16 rounding per element (round-to-nearest-even).  A, B, C row-major with
+ * row strides lda, ldb, ldc in elements; A and B rows K-contiguous (the
+ * layer's x and w_ext).  K a positive multiple of 8, lda and ldb multiples
+ * of 8, A and B 16-byte aligned.  No size limit on M and N.
+ * ---------------------------------------------------------------------- */
+int gs_gemm_bf16_tn(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc, int64_t M,
+                    int64_t N, int64_t K, void* stream);
 
 #ifdef __cplusplus
 }

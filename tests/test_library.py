@@ -66,6 +66,12 @@ def test_validation_errors_without_launch():
     with pytest.raises(_lib.GraniteSwitchError) as e:
         _lib.call("gs_compute_bitmasks", None, 2, 4, None, 2, 1, 32, None, None, None)
     assert "idx_bytes" in str(e.value)
+    with pytest.raises(_lib.GraniteSwitchError) as e:
+        _lib.call("gs_gemm_bf16_tn", None, 12, None, 12, None, 8, 4, 8, 12, None)
+    assert "multiple of 8" in str(e.value)
+    with pytest.raises(_lib.GraniteSwitchError) as e:
+        _lib.call("gs_gemm_bf16_tn", None, 8, None, 16, None, 4, 4, 8, 16, None)
+    assert "lda" in str(e.value)
 
 
 def test_workspace_plan_is_consistent():
