@@ -14,6 +14,9 @@ K launches of that kernel alone, rotating buffers).  The CPU baseline is the
 reference's HF loop restated on torch-CPU, timed on the host cores.
 
   python bench.py [--steps K] [--warmup W] [--config {0..4}] [--no-cpu]
+  python bench.py --config N --layer-gemm   # the vLLM layer's x . w_ext^T GEMM at
+                                            # the workload's shapes, this library's
+                                            # MFMA kernel and torch.mm, in TFLOP/s
   python bench.py --copy-probe MIB   # a plain device copy of MIB MiB, the
                                      # reference for scaling rocprofv3's
                                      # FETCH_SIZE / WRITE_SIZE counters
@@ -84,6 +87,60 @@ def copy_probe(mib: int) -> None:
                       "gbs_read_plus_write": 2 * n / (ms * 1e-3) / 1e9}), flush=True)
 
 
+def layer_gemm(cfg: int, n: int) -> None:
+    """x . w_ext^T of every projection of the workload: w_ext stacks the base
+    weight [O, H] with every adapter's lora_A rows at the reference's promoted
+    tier ranks (src/granite_switch/vllm/core/lora.py:544, kernels/switch_lora_kernel.py:134-163)."""
+    import torch
+
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    from granite_switch_amd import switched, workloads
+    from granite_switch_amd.kernels import promote_rank
+
+    dev = torch.device("cuda:0")
+    T = workloads.routing_for(cfg).num_tokens
+    NA = workloads.num_adapters_for(cfg)
+    rows = []
+    for spec in workloads.module_specs(cfg):
+        S, H, O = len(spec.output_slices), spec.hidden, sum(spec.output_slices)
+        n_ext = O + S * sum(promote_rank(r) for r in spec.ranks[:NA])
+        g = torch.Generator(device=dev).manual_seed(17)
+        x = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
+        w = (torch.randn(n_ext, H, generator=g, device=dev) / H ** 0.5).to(torch.bfloat16)
+        out = torch.empty(T, n_ext, dtype=torch.bfloat16, device=dev)
+        flops = 2.0 * T * n_ext * H
+
+        def timed(fn):
+            fn()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(n):
+                    fn()
+            graph.replay()
+            torch.cuda.synchronize()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            graph.replay()
+            end.record()
+            end.synchronize()
+            return start.elapsed_time(end) * 1e3 / n
+
+        t_native = timed(lambda: switched.linear_bf16(x, w, out))
+        t_lib = timed(lambda: torch.mm(x, w.T, out=out))
+        rows.append({"projection": spec.name, "M": T, "N": n_ext, "K": H,
+                     "native_us": t_native, "native_tflops": flops / t_native / 1e6,
+                     "native_mfma_frac": flops / t_native / 1e6 / (MFMA_PEAK["bf16"] / 1e12),
+                     "torch_mm_us": t_lib, "torch_mm_tflops": flops / t_lib / 1e6,
+                     "torch_mm_mfma_frac": flops / t_lib / 1e6 / (MFMA_PEAK["bf16"] / 1e12)})
+        del x, w, out
+    print(json.dumps({"workload": WORKLOAD_KEY[cfg], "gemm": "x . w_ext^T (bf16, fp32 accumulate)",
+                      "peak_tflops": MFMA_PEAK["bf16"] / 1e12, "projections": rows}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -94,9 +151,14 @@ def main():
     ap.add_argument("--sets", type=int, default=None, help="buffer sets to rotate (default: > 2x MALL)")
     ap.add_argument("--copy-probe", type=int, default=None, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB five times (counter calibration)")
+    ap.add_argument("--layer-gemm", action="store_true",
+                    help="only time the vLLM layer's x . w_ext^T GEMM at the workload's shapes")
     args = ap.parse_args()
     if args.copy_probe is not None:
         copy_probe(args.copy_probe)
+        return
+    if args.layer_gemm:
+        layer_gemm(args.config, args.steps or 10)
         return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))

@@ -7,9 +7,9 @@ as arguments so the class works without vLLM:
 
   forward(x) -> (out, output_bias):
     x_ext = x . w_ext^T           one GEMM: base output + every adapter's shrink
-                                  (gs_gemm_bf16_tn, this library's MFMA GEMM, for
-                                  bf16; torch.mm when ``native_gemm`` is False
-                                  or for fp32)
+                                  (torch.mm, i.e. hipBLASLt; this library's own
+                                  MFMA GEMM gs_gemm_bf16_tn with
+                                  ``native_gemm = True``, bf16 only)
     expand, in place into x_ext[:, :N_total]
     [row-parallel all-reduce] [bias]
 
@@ -41,8 +41,9 @@ class SwitchedLoRALinear(nn.Module):
     """Fused switched-LoRA linear layer (reference: vllm/core/lora.py:40-130 for the layout)."""
 
     _lora_ctx = None
-    # x . w_ext^T through gs_gemm_bf16_tn (True) or torch.mm (False)
-    native_gemm = True
+    # x . w_ext^T through gs_gemm_bf16_tn (True) or torch.mm (False); the
+    # library GEMM is faster at every measured workload shape
+    native_gemm = False
 
     def __init__(self, base_layer: nn.Module, num_adapters: int, max_lora_rank: int, num_slices: int = 1,
                  output_slices: tuple | None = None, fuse_swiglu: bool = False, *, tp_size: int = 1,

@@ -93,6 +93,7 @@ def test_vllm_layer_native_and_library_gemm_agree(dev):
                 layer.lora_A_slices[s].data[a, 0, :r] = (torch.randn(r, K, generator=g, device=dev) / K ** 0.5).to(torch.bfloat16)
     layer.finalize_weights(ranks)
     x = torch.randn(T, K, generator=g, device=dev).to(torch.bfloat16)
+    layer.native_gemm = True
     native = layer._gemm(x)
     layer.native_gemm = False
     library = layer._gemm(x)

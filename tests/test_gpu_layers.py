@@ -66,12 +66,14 @@ def _ctx_for(dev, layer, ids):
     return ctx
 
 
+@pytest.mark.parametrize("native_gemm", [False, True])
 @pytest.mark.parametrize("slices,ranks", [((4096, 1024, 1024), [32] * 12), ((2048,), [8, 16, 32, 64, 128, 16]),
                                           ((512, 256), [16, 512, 8])])
-def test_vllm_layer_segment_and_op_paths(dev, slices, ranks):
+def test_vllm_layer_segment_and_op_paths(dev, slices, ranks, native_gemm):
     K, T = 1024, 300
-    _say(f"vllm layer slices={slices} ranks={ranks}")
+    _say(f"vllm layer slices={slices} ranks={ranks} native_gemm={native_gemm}")
     layer, W, A, B = _make_vllm_layer(dev, K, slices, ranks, seed=5, zero=(1,))
+    layer.native_gemm = native_gemm
     g = torch.Generator(device=dev).manual_seed(8)
     x = torch.randn(T, K, generator=g, device=dev).to(torch.bfloat16)
     ids = torch.randint(0, len(ranks) + 1, (T,), generator=g, device=dev)
