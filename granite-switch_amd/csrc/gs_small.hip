@@ -100,8 +100,7 @@ struct RouteLds {
 // routing loads does not wait for weight loads issued after them).
 template <int U>
 struct RouteRegs {
-  int64_t rq[U];        // requested ids (req path)
-  int32_t e32[U];       // pre-gated ids (eff path), widened only when used
+  int64_t rq[U];        // requested ids (req path) or pre-gated ids (eff path)
   int64_t q[U];
   int32_t cu[U];
   int64_t off[U];
@@ -122,17 +121,13 @@ __device__ __forceinline__ void route_issue(const SmallRoute& r, RouteRegs<U>& r
   const int tid = threadIdx.x;
   const int tl = r.T - 1;
   if (r.eff != nullptr) {
+    // zero-extended: a negative id becomes a large one, base either way, and
+    // no instruction depends on the load before the routing wait
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      rr.e32[u] = r.eff[min(u * kSmT + tid, tl)];
-      rr.rq[u] = 0;
-    }
+    for (int u = 0; u < U; ++u) rr.rq[u] = static_cast<uint32_t>(r.eff[min(u * kSmT + tid, tl)]);
   } else {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      rr.rq[u] = r.req[min(u * kSmT + tid, tl)];
-      rr.e32[u] = 0;
-    }
+    for (int u = 0; u < U; ++u) rr.rq[u] = r.req[min(u * kSmT + tid, tl)];
   }
   if (r.eff == nullptr && r.pos != nullptr) {
 #pragma unroll
@@ -180,10 +175,6 @@ __device__ __forceinline__ bool route_gate(const SmallRoute& r, int g, RouteLds<
         s.off[k] = rr.off[u];
       }
     }
-  }
-  if (r.eff != nullptr) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) rr.rq[u] = rr.e32[u];
   }
   bool req_g = false;
 #pragma unroll
@@ -353,9 +344,11 @@ __device__ __forceinline__ uint64_t* launch_counter(const FusedParams& p, int g)
 }
 
 // Adapter g's epoch at the start of this launch (thread 0 only).
-__device__ __forceinline__ uint32_t read_epoch(const FusedParams& p, int g) {
-  return static_cast<uint32_t>(
-      __hip_atomic_load(launch_counter(p, g), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> kEpochShift);
+// Adapter g's launch counter; its epoch is the value >> kEpochShift.  Issued
+// with the workgroup's first loads and consumed after the routing wait, so
+// the read adds no memory round trip of its own.
+__device__ __forceinline__ uint64_t read_counter(const FusedParams& p, int g) {
+  return __hip_atomic_load(launch_counter(p, g), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ----------------------------------------------------------------------------
@@ -403,7 +396,7 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
                (p.tab.a_off[g] + static_cast<int64_t>(nok[c2] ? n[c2] : 0) * p.H) * ES;
   }
 
-  if (tid == 0) L.epoch = read_epoch(p, g);
+  const uint64_t counter = read_counter(p, g);   // one 8-byte request per wave
   RouteRegs<U> rr;
   route_issue<U>(p.rt, rr);
   u32x4 av[2][NPW];
@@ -421,6 +414,7 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
       }
   }
   const bool requested = route_gate<U>(p.rt, g, L.rt, rr);
+  if (tid == 0) L.epoch = static_cast<uint32_t>(counter >> kEpochShift);   // visible after route_list's barriers
   if constexpr (!SPEC) {
     // only adapters some token asked for read their weights
 #pragma unroll
@@ -520,7 +514,7 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
   const int s = tile_slice<NT>(p.si, nt);
   const int zc0 = s * r;                 // this slice's columns in the adapter's shrink row
 
-  if (tid == 0) L.epoch = read_epoch(p, g);
+  const uint64_t counter = read_counter(p, g);   // one 8-byte request per wave
   RouteRegs<U> rr;
   route_issue<U>(p.rt, rr);
   // lora_B rows of this wave's column blocks (n < out_total always; rank 0
@@ -544,6 +538,7 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
       }
   }
   const bool requested = route_gate<U>(p.rt, g, L.rt, rr);
+  if (tid == 0) L.epoch = static_cast<uint32_t>(counter >> kEpochShift);   // visible after route_list's barriers
   if constexpr (!SPEC) {
 #pragma unroll
     for (int q = 0; q < NQ; ++q)
