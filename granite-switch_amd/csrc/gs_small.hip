@@ -399,40 +399,21 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
   const uint64_t counter = read_counter(p, g);   // one 8-byte request per wave
   RouteRegs<U> rr;
   route_issue<U>(p.rt, rr);
-  u32x4 av[2][NPW];
-  if constexpr (SPEC) {
-    // lora_A in the same memory trip as the routing loads: unconditional loads
-    // from clamped addresses, so the wait for the routing loads below does not
-    // also wait for these
-#pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2)
-#pragma unroll
-      for (int pp = 0; pp < NPW; ++pp) {
-        const int64_t kp = k_lo + pp * KSTEP + q4 * P;
-        const bool ok = nok[c2] && kp < k_hi;
-        av[c2][pp] = sel16(ok, ld16(arow[c2] + (ok ? kp : 0) * ES));
-      }
-  }
-  const bool requested = route_gate<U>(p.rt, g, L.rt, rr);
+  // Order of the memory trips: the routing loads go out alone (with the
+  // consumers' lora_B); once the token list is known, the x rows of the first
+  // row chunk, then lora_A.  Loads complete in order, so x issued first is
+  // not stuck behind this producer's lora_A, and the x and lora_A streams of
+  // all producers share the bandwidth instead of x starting after lora_A.  A
+  // producer with no tokens reads no weights.
+  route_gate<U>(p.rt, g, L.rt, rr);
   if (tid == 0) L.epoch = static_cast<uint32_t>(counter >> kEpochShift);   // visible after route_list's barriers
-  if constexpr (!SPEC) {
-    // only adapters some token asked for read their weights
-#pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2)
-#pragma unroll
-      for (int pp = 0; pp < NPW; ++pp) {
-        const int64_t kp = k_lo + pp * KSTEP + q4 * P;
-        av[c2][pp] = u32x4{0u, 0u, 0u, 0u};
-        if (requested && nok[c2] && kp < k_hi) av[c2][pp] = ld16(arow[c2] + kp * ES);
-      }
-  }
   const int n_g = route_list<U>(g, L.rt, rr);
   if (!active || n_g == 0) return;
   const uint64_t tag = static_cast<uint64_t>(L.epoch + 1u) << 32;
   uint64_t* part = p.part + static_cast<int64_t>(g - 1) * p.region;
 
-  for (int rt0 = 0; rt0 < n_g; rt0 += 32) {
-    u32x4 xv[2][NPW];
+  u32x4 xv[2][NPW];
+  auto load_x = [&](int rt0) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       const int slot = rt0 + 16 * rt + i16;
@@ -445,6 +426,24 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
         if (rok && kp < k_hi) xv[rt][pp] = ld16(xrow + kp * ES);
       }
     }
+  };
+  load_x(0);
+  // lora_A: a piece outside the adapter's columns or past the k-chunk reads
+  // row 0 at k 0 (finite weights) and is not masked -- past the chunk its x
+  // piece is zero, and outside the columns the result is never stored -- so
+  // no instruction waits on these loads before the MFMAs
+  u32x4 av[2][NPW];
+#pragma unroll
+  for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+    for (int pp = 0; pp < NPW; ++pp) {
+      const int64_t kp = k_lo + pp * KSTEP + q4 * P;
+      const bool ok = nok[c2] && kp < k_hi;
+      av[c2][pp] = ld16(arow[c2] + (ok ? kp : 0) * ES);
+    }
+
+  for (int rt0 = 0; rt0 < n_g; rt0 += 32) {
+    if (rt0 > 0) load_x(rt0);
     // acc[rt][c2]: token slots rt0 + 16*rt + 4*q4 + e, column n[c2]
     f32x4 acc[2][2];
 #pragma unroll
@@ -527,7 +526,8 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
     brow[q] = static_cast<const char*>(p.b_pack) + (p.tab.b_off[g] + static_cast<int64_t>(n) * r) * ES;
   }
   if constexpr (SPEC) {
-    // unconditional loads from clamped addresses (see the producer)
+    // lora_B in the first memory trip, while the producers wait for their
+    // token lists: unconditional loads from clamped addresses
 #pragma unroll
     for (int q = 0; q < NQ; ++q)
 #pragma unroll
