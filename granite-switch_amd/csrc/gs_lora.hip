@@ -509,14 +509,19 @@ static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, boo
   pl.n_chunks = (pl.zw + 32 * pl.NB - 1) / (32 * pl.NB);
   const int unit = bf16 ? 256 : 128;          // k per batch of the shrink kernel
   const int units = (H + unit - 1) / unit;
-  // split the hidden dimension for about 768 workgroups (the tile count is an
-  // upper bound, T/64 + NA), at most 16 ways (the partial sums' consumers)
+  // split the hidden dimension for about 640 workgroups (the tile count is an
+  // upper bound, T/64 + NA), at most 16 ways (the partial sums' consumers).
+  // Where the grid stays at 512 workgroups or more, a workgroup takes at
+  // least 3 batches, so its start (tile lookup, token rows, first batch) is
+  // spread over enough streaming; measured on the prefill and decoder-step
+  // shapes
   const int64_t wgs = static_cast<int64_t>(pl.max_tiles) * pl.n_chunks;
-  int ks = static_cast<int>((768 + wgs - 1) / (wgs > 0 ? wgs : 1));
+  int ks = static_cast<int>((640 + wgs / 2) / (wgs > 0 ? wgs : 1));
   if (ks < 1) ks = 1;
   if (ks > 16) ks = 16;
   if (ks > units) ks = units;
-  const int per = (units + ks - 1) / ks;
+  int per = (units + ks - 1) / ks;
+  if (per < 3 && units >= 3 && wgs * ((units + 2) / 3) >= 512) per = 3;
   pl.KC = per * unit;
   pl.KS = (H + pl.KC - 1) / pl.KC;
   if (pl.KS < 1) pl.KS = 1;
