@@ -286,14 +286,16 @@ __device__ __forceinline__ TileRef find_tile(const int32_t* __restrict__ seg, co
 // The tile of work item `lin` of a 1-D launch over (tile, sub) pairs (see
 // xcd_item), in one pass over the adapter table when it fits one wave
 // (<= 64 adapters): the tile count and the tile's lookup share the same
-// loads.  Returns g = 0 when the item has no tile.
-template <int TM>
-__device__ __forceinline__ TileRef locate_tile(const int32_t* __restrict__ seg, const int32_t* __restrict__ ranks,
-                                               const int64_t* __restrict__ offs, int num_adapters, int lin, int nsub,
-                                               int& sub) {
+// loads.  nsub_of(total tiles) gives the number of subs per tile (every wave
+// computes the same value).  Returns g = 0 when the item has no tile.
+template <int TM, typename NsubOf>
+__device__ __forceinline__ TileRef locate_tile_by(const int32_t* __restrict__ seg, const int32_t* __restrict__ ranks,
+                                                  const int64_t* __restrict__ offs, int num_adapters, int lin,
+                                                  NsubOf nsub_of, int& sub) {
   TileRef ref{0, 0, 0, 0, 0};
   if (num_adapters > 64) {
-    const XcdItem it = xcd_item(lin, count_tiles<TM>(seg, ranks, num_adapters), nsub);
+    const int total = count_tiles<TM>(seg, ranks, num_adapters);
+    const XcdItem it = xcd_item(lin, total, nsub_of(total));
     sub = it.sub;
     return it.tile < 0 ? ref : find_tile<TM>(seg, ranks, offs, num_adapters, it.tile);
   }
@@ -314,7 +316,8 @@ __device__ __forceinline__ TileRef locate_tile(const int32_t* __restrict__ seg, 
     int v = __shfl_up(incl, d, 64);
     if (l >= d) incl += v;
   }
-  const XcdItem it = xcd_item(lin, __shfl(incl, 63, 64), nsub);
+  const int total = __shfl(incl, 63, 64);
+  const XcdItem it = xcd_item(lin, total, nsub_of(total));
   sub = it.sub;
   if (it.tile < 0) return ref;
   const int excl = incl - ntiles;
@@ -330,6 +333,14 @@ __device__ __forceinline__ TileRef locate_tile(const int32_t* __restrict__ seg, 
   ref.rank = __shfl(rk, src, 64);
   ref.off = __shfl(of, src, 64);
   return ref;
+}
+
+// As locate_tile_by with a fixed number of subs per tile.
+template <int TM>
+__device__ __forceinline__ TileRef locate_tile(const int32_t* __restrict__ seg, const int32_t* __restrict__ ranks,
+                                               const int64_t* __restrict__ offs, int num_adapters, int lin, int nsub,
+                                               int& sub) {
+  return locate_tile_by<TM>(seg, ranks, offs, num_adapters, lin, [nsub](int) { return nsub; }, sub);
 }
 
 }  // namespace gs

@@ -246,10 +246,14 @@ __global__ __launch_bounds__(kThreads) void reduce_parts_kernel(const float* __r
 }
 
 // ----------------------------------------------------------------------------
-// Expand.  1-D grid over (tile, group of ni column sub-tiles) items, tiles
-// spread over the XCDs in contiguous ranges (xcd_item).  A workgroup owns one tile (32
-// slots of one adapter) and walks ni consecutive column sub-tiles of NT
-// columns.  The tile's shrink values for every slice (z rows, or the sum of
+// Expand.  1-D grid over (tile, group of column sub-tiles) items, tiles
+// spread over the XCDs in contiguous ranges (xcd_item).  A workgroup owns one
+// tile (32 slots of one adapter) and walks its group's consecutive column
+// sub-tiles of NT columns.  The number of groups per tile is chosen on the
+// device from the batch's tile count so that the items about fill the GPU
+// once (wt workgroups): each workgroup's start -- the tile lookup and the
+// staging of its shrink values -- is paid once per group, and a group long
+// enough to hide it beats a second round of workgroups.  The tile's shrink values for every slice (z rows, or the sum of
 // the split-K partials rounded to the element type exactly like a
 // materialised z) are staged in LDS once.  Per sub-tile each wave computes NBW
 // 32x32 delta blocks with MFMA over the adapter's rank (all KSTEP k-groups of
@@ -276,7 +280,7 @@ struct ExpandParams {
   const int32_t* ranks;
   int NA;
   int max_rank;
-  int ni;                 // column sub-tiles per workgroup
+  int wt;                 // workgroups that fill the GPU once
   const int32_t* seg;
   const int32_t* perm;
 };
@@ -343,6 +347,16 @@ __device__ __forceinline__ void z_stage(const ExpandParams& p, const TileRef& tr
   }
 }
 
+// Column groups per tile: as many as keep 8*ceil(tiles/8) * groups within wt
+// (the launch holds max(wt, 8*ceil(max_tiles/8)) workgroups), 1..n_sub.
+__host__ __device__ inline int expand_groups(int tiles, int n_sub, int wt) {
+  const int t8 = 8 * ((tiles + 7) / 8);
+  int g = t8 > 0 ? wt / t8 : n_sub;
+  if (g > n_sub) g = n_sub;
+  if (g < 1) g = 1;
+  return g;
+}
+
 template <bool BF16, int NBW, int PRE>
 __global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
   constexpr int NT = 4 * NBW * 32;           // columns per sub-tile
@@ -359,14 +373,18 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
   extern __shared__ __align__(16) char zs[];   // [32][S*max_rank + 8] element type
 
   const int n_sub = (p.out_total + NT - 1) / NT;
-  int sub = 0;
-  const TileRef tr = locate_tile<kTM>(p.seg, p.ranks, p.b_off, p.NA, static_cast<int>(blockIdx.x),
-                                      (n_sub + p.ni - 1) / p.ni, sub);
+  int sub = 0, groups = 1;
+  const TileRef tr = locate_tile_by<kTM>(p.seg, p.ranks, p.b_off, p.NA, static_cast<int>(blockIdx.x),
+                                         [&](int total) {
+                                           groups = expand_groups(total, n_sub, p.wt);
+                                           return groups;
+                                         }, sub);
   if (tr.g == 0) return;
   const int r = tr.rank;
-  const int sub0 = sub * p.ni;
-  if (sub0 >= n_sub) return;
-  const int nsub = min(p.ni, n_sub - sub0);
+  // group sub of `groups` covers sub-tiles [sub*n_sub/groups, (sub+1)*n_sub/groups)
+  const int sub0 = (sub * n_sub) / groups;
+  const int nsub = ((sub + 1) * n_sub) / groups - sub0;
+  if (nsub <= 0) return;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -640,44 +658,58 @@ int prepare_expand(ExpandParams& p, const char* who, int32_t dtype, void* y, int
   return GS_OK;
 }
 
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 template <bool BF16, int NBW, int PRE>
-void launch_expand_t(dim3 grid, size_t lds, const ExpandParams& p, hipStream_t st) {
+void launch_expand_t(int max_tiles, size_t lds, ExpandParams p, hipStream_t st) {
   auto kern = expand_kernel<BF16, NBW, PRE>;
   if (lds > 64 * 1024) (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-  hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, st, p);
+  // workgroups resident per CU for this LDS size (queried once per size)
+  static size_t q_lds = ~size_t(0);
+  static int q_per_cu = 1;
+  if (q_lds != lds) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kern), kThreads, lds) != hipSuccess || n < 1) n = 1;
+    q_per_cu = n;
+    q_lds = lds;
+  }
+  p.wt = q_per_cu * device_cus();
+  const int t8 = 8 * ((max_tiles + 7) / 8);
+  const int grid = (std::max(p.wt, t8) + 7) / 8 * 8;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, st, p);
 }
 
 template <bool BF16, int NBW>
-void launch_expand_pre(dim3 grid, size_t lds, const ExpandParams& p, hipStream_t st) {
+void launch_expand_pre(int max_tiles, size_t lds, const ExpandParams& p, hipStream_t st) {
   constexpr int KSTEP = BF16 ? 16 : 8;
   const int need = (p.max_rank + KSTEP - 1) / KSTEP;
-  if (need <= 2) launch_expand_t<BF16, NBW, 2>(grid, lds, p, st);
-  else if (need <= 4) launch_expand_t<BF16, NBW, 4>(grid, lds, p, st);
-  else launch_expand_t<BF16, NBW, 8>(grid, lds, p, st);
+  if (need <= 2) launch_expand_t<BF16, NBW, 2>(max_tiles, lds, p, st);
+  else if (need <= 4) launch_expand_t<BF16, NBW, 4>(max_tiles, lds, p, st);
+  else launch_expand_t<BF16, NBW, 8>(max_tiles, lds, p, st);
 }
 
 void launch_expand(bool bf16, int64_t T, ExpandParams p, hipStream_t st) {
   const int max_tiles = max_tiles_for(T, p.NA);
   // wider column tiles halve the z / partial reads per output byte
   const bool wide = T >= 2048 || p.nparts > 1;
-  const int NT = wide ? 256 : 128;
-  const int n_sub = (p.out_total + NT - 1) / NT;
-  // enough sub-tiles per workgroup that ~4096 workgroups cover the grid, and
-  // at least 2 (so the prefetch has something to overlap) once that still
-  // leaves over 1024 workgroups
-  int ni = static_cast<int>((static_cast<int64_t>(n_sub) * max_tiles + 4095) / 4096);
-  if (ni < 2 && static_cast<int64_t>(n_sub) * max_tiles >= 2 * 1024) ni = 2;
-  if (ni < 1) ni = 1;
-  if (ni > n_sub) ni = n_sub;
-  p.ni = ni;
-  dim3 grid(8 * ((max_tiles + 7) / 8) * ((n_sub + ni - 1) / ni));
   const size_t lds = expand_lds_bytes(bf16, p.si.S, p.max_rank);
   if (bf16) {
-    if (wide) launch_expand_pre<true, 2>(grid, lds, p, st);
-    else launch_expand_pre<true, 1>(grid, lds, p, st);
+    if (wide) launch_expand_pre<true, 2>(max_tiles, lds, p, st);
+    else launch_expand_pre<true, 1>(max_tiles, lds, p, st);
   } else {
-    if (wide) launch_expand_pre<false, 2>(grid, lds, p, st);
-    else launch_expand_pre<false, 1>(grid, lds, p, st);
+    if (wide) launch_expand_pre<false, 2>(max_tiles, lds, p, st);
+    else launch_expand_pre<false, 1>(max_tiles, lds, p, st);
   }
 }
 
