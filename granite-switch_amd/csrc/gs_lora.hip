@@ -285,21 +285,22 @@ struct ExpandParams {
   const int32_t* perm;
 };
 
-// Shrink values of the tile for all slices, 4 elements per item: item it
-// covers row it / (zwa/4) and columns c4 .. c4+3 of the row's S*r values
-// (slice c4 / r).  Split-K partials are loaded kPartGroup at a time and
-// summed in ks order; values are rounded to the element type when stored to
-// LDS, exactly as a materialised z would have been.
+// Shrink values of the tile for slices s_lo..s_hi (the ones the workgroup's
+// output columns lie in), 4 elements per item: item it covers row
+// it / (width/4) and columns c4 .. c4+3 of the row's S*r values (slice c4 / r).
+// Split-K partials are loaded kPartGroup at a time and summed in ks order;
+// values are rounded to the element type when stored to LDS, exactly as a
+// materialised z would have been.
 constexpr int kPartGroup = 8;
 
 template <bool BF16>
-__device__ __forceinline__ void z_stage(const ExpandParams& p, const TileRef& tr, int r, int zo, char* zs, int zs_ld) {
-  const int zwa = p.si.S * r;                 // this adapter's shrink width
-  const int per_row = zwa >> 2;
+__device__ __forceinline__ void z_stage(const ExpandParams& p, const TileRef& tr, int r, int zo, char* zs, int zs_ld,
+                                        int s_lo, int s_hi) {
+  const int per_row = ((s_hi - s_lo + 1) * r) >> 2;
   const int items = kTM * per_row;
   for (int it = threadIdx.x; it < items; it += kThreads) {
     const int row = it / per_row;
-    const int c4 = (it - row * per_row) * 4;
+    const int c4 = s_lo * r + (it - row * per_row) * 4;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (row < tr.nrows) {
       const int slot = tr.slot0 + row;
@@ -431,7 +432,16 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
   u32x4 yc[PASSES], bc[NBW][PRE];
   load_b(sub0, 0, bc);
   load_y(sub0, yc);
-  z_stage<BF16>(p, tr, r, zo, zs, zs_ld);
+  // the slices of the group's first and last output column
+  int s_lo = 0, s_hi = 0;
+  {
+    const int c_first = sub0 * NT;
+    const int c_last = min((sub0 + nsub) * NT, p.out_total) - 1;
+    while (s_lo + 1 < p.si.S && c_first >= p.si.bounds[s_lo + 1]) ++s_lo;
+    s_hi = s_lo;
+    while (s_hi + 1 < p.si.S && c_last >= p.si.bounds[s_hi + 1]) ++s_hi;
+  }
+  z_stage<BF16>(p, tr, r, zo, zs, zs_ld, s_lo, s_hi);
   lds_barrier();
 
   auto compute = [&](int sub, u32x4 (&bcur)[NBW][PRE], u32x4 (&ycur)[PASSES]) {
