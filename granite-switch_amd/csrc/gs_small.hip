@@ -396,15 +396,28 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
                (p.tab.a_off[g] + static_cast<int64_t>(nok[c2] ? n[c2] : 0) * p.H) * ES;
   }
 
+  // lora_A: a piece outside the adapter's columns or past the k-chunk reads
+  // row 0 at k 0 (finite weights) and is not masked -- past the chunk its x
+  // piece is zero, and outside the columns the result is never stored -- so
+  // no instruction waits on these loads before the MFMAs
+  u32x4 av[2][NPW];
+
   const uint64_t counter = read_counter(p, g);   // one 8-byte request per wave
   RouteRegs<U> rr;
   route_issue<U>(p.rt, rr);
-  // Order of the memory trips: the routing loads go out alone (with the
-  // consumers' lora_B); once the token list is known, the x rows of the first
-  // row chunk, then lora_A.  Loads complete in order, so x issued first is
-  // not stuck behind this producer's lora_A, and the x and lora_A streams of
-  // all producers share the bandwidth instead of x starting after lora_A.  A
-  // producer with no tokens reads no weights.
+  // Order of the memory trips: the routing loads go out first, then the first
+  // 16-row block of lora_A, so HBM streams weights while the routing is
+  // waited for (loads complete in order: the routing wait does not wait for
+  // them).  Once the token list is known, the x rows of the first row chunk,
+  // then the second lora_A block.  Issuing all of lora_A before the wait
+  // measured the same but delays the routing under load; issuing none of it
+  // leaves HBM idle during the routing (3.5 % slower).
+#pragma unroll
+  for (int pp = 0; pp < NPW; ++pp) {
+    const int64_t kp = k_lo + pp * KSTEP + q4 * P;
+    const bool ok = nok[0] && kp < k_hi;
+    av[0][pp] = ld16(arow[0] + (ok ? kp : 0) * ES);
+  }
   route_gate<U>(p.rt, g, L.rt, rr);
   if (tid == 0) L.epoch = static_cast<uint32_t>(counter >> kEpochShift);   // visible after route_list's barriers
   const int n_g = route_list<U>(g, L.rt, rr);
@@ -428,19 +441,12 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
     }
   };
   load_x(0);
-  // lora_A: a piece outside the adapter's columns or past the k-chunk reads
-  // row 0 at k 0 (finite weights) and is not masked -- past the chunk its x
-  // piece is zero, and outside the columns the result is never stored -- so
-  // no instruction waits on these loads before the MFMAs
-  u32x4 av[2][NPW];
 #pragma unroll
-  for (int c2 = 0; c2 < 2; ++c2)
-#pragma unroll
-    for (int pp = 0; pp < NPW; ++pp) {
-      const int64_t kp = k_lo + pp * KSTEP + q4 * P;
-      const bool ok = nok[c2] && kp < k_hi;
-      av[c2][pp] = ld16(arow[c2] + (ok ? kp : 0) * ES);
-    }
+  for (int pp = 0; pp < NPW; ++pp) {
+    const int64_t kp = k_lo + pp * KSTEP + q4 * P;
+    const bool ok = nok[1] && kp < k_hi;
+    av[1][pp] = ld16(arow[1] + (ok ? kp : 0) * ES);
+  }
 
   for (int rt0 = 0; rt0 < n_g; rt0 += 32) {
     if (rt0 > 0) load_x(rt0);
