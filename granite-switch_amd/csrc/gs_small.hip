@@ -425,18 +425,23 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
   const uint64_t tag = static_cast<uint64_t>(L.epoch + 1u) << 32;
   uint64_t* part = p.part + static_cast<int64_t>(g - 1) * p.region;
 
+  // x rows of one 32-token chunk.  Rows past the adapter's tokens re-read its
+  // first token (their sums are never stored) and pieces past the k-chunk
+  // read the row's first piece and are zeroed where they are multiplied, so
+  // the loads are unconditional and go out back to back with lora_A's second
+  // block: no wait for x sits between them.
   u32x4 xv[2][NPW];
+  bool xk[NPW];
   auto load_x = [&](int rt0) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       const int slot = rt0 + 16 * rt + i16;
-      const bool rok = slot < n_g;
-      const char* xrow = static_cast<const char*>(p.x) + static_cast<int64_t>(L.rt.tok[rok ? slot : rt0]) * p.ldx * ES;
+      const char* xrow = static_cast<const char*>(p.x) + static_cast<int64_t>(L.rt.tok[slot < n_g ? slot : rt0]) * p.ldx * ES;
 #pragma unroll
       for (int pp = 0; pp < NPW; ++pp) {
         const int64_t kp = k_lo + pp * KSTEP + q4 * P;
-        xv[rt][pp] = u32x4{0u, 0u, 0u, 0u};
-        if (rok && kp < k_hi) xv[rt][pp] = ld16(xrow + kp * ES);
+        xk[pp] = kp < k_hi;
+        xv[rt][pp] = ld16(xrow + (xk[pp] ? kp : 0) * ES);
       }
     }
   };
@@ -447,6 +452,7 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
     const bool ok = nok[1] && kp < k_hi;
     av[1][pp] = ld16(arow[1] + (ok ? kp : 0) * ES);
   }
+  __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the MFMAs wait
 
   for (int rt0 = 0; rt0 < n_g; rt0 += 32) {
     if (rt0 > 0) load_x(rt0);
@@ -458,7 +464,7 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
       for (int c2 = 0; c2 < 2; ++c2) {
         acc[rt][c2] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int pp = 0; pp < NPW; ++pp) acc[rt][c2] = mfma16<BF16>(xv[rt][pp], av[c2][pp], acc[rt][c2]);
+        for (int pp = 0; pp < NPW; ++pp) acc[rt][c2] = mfma16<BF16>(sel16(xk[pp], xv[rt][pp]), av[c2][pp], acc[rt][c2]);
       }
 
     // fixed-order cross-wave sum ((w0 + w1) + w2) + w3; wave w finishes and
