@@ -539,14 +539,16 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
   }
   if constexpr (SPEC) {
     // lora_B in the first memory trip, while the producers wait for their
-    // token lists: unconditional loads from clamped addresses
+    // token lists: unconditional loads from clamped addresses.  Pieces past
+    // the rank read the row's first piece and are not masked: the MFMAs
+    // multiply them by shrink values that are zeroed there, so no
+    // instruction waits on these loads before the y loads go out.
 #pragma unroll
     for (int q = 0; q < NQ; ++q)
 #pragma unroll
       for (int kg = 0; kg < KG; ++kg) {
         const int k0 = kg * KSTEP + q4 * P;
-        const bool ok = k0 < r;
-        bv[q][kg] = sel16(ok, ld16(brow[q] + (ok ? k0 : 0) * ES));
+        bv[q][kg] = ld16(brow[q] + (k0 < r ? k0 : 0) * ES);
       }
   }
   const bool requested = route_gate<U>(p.rt, g, L.rt, rr);
