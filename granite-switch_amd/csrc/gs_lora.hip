@@ -11,6 +11,9 @@
 // writes fp32 partial sums; the consumer -- the expand kernel, or a small
 // reduce kernel when z itself is asked for -- adds the partials in a fixed
 // order, so results are deterministic and need no cross-XCD fences.
+#include <algorithm>
+#include <atomic>
+
 #include "gs_common.h"
 
 namespace gs {
@@ -668,35 +671,43 @@ int prepare_expand(ExpandParams& p, const char* who, int32_t dtype, void* y, int
   return GS_OK;
 }
 
-// Compute units of the current device (cached per device).
+// Compute units of the current device (cached per device; concurrent first
+// calls store the same value).
 int device_cus() {
-  static int cache[64] = {0};
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 
 template <bool BF16, int NBW, int PRE>
 void launch_expand_t(int max_tiles, size_t lds, ExpandParams p, hipStream_t st) {
   auto kern = expand_kernel<BF16, NBW, PRE>;
   if (lds > 64 * 1024) (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-  // workgroups resident per CU for this LDS size (queried once per size)
-  static size_t q_lds = ~size_t(0);
-  static int q_per_cu = 1;
-  if (q_lds != lds) {
+  // workgroups resident per CU for this LDS size, queried once per size and
+  // kept as one word (lds << 16 | count) so concurrent callers read a
+  // consistent pair
+  static std::atomic<uint64_t> occ{0};
+  uint64_t o = occ.load(std::memory_order_relaxed);
+  if (o == 0 || (o >> 16) != lds) {
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kern), kThreads, lds) != hipSuccess || n < 1) n = 1;
-    q_per_cu = n;
-    q_lds = lds;
+    o = (static_cast<uint64_t>(lds) << 16) | static_cast<uint64_t>(std::min(n, 0xffff));
+    occ.store(o, std::memory_order_relaxed);
   }
-  p.wt = q_per_cu * device_cus();
+  p.wt = static_cast<int>(o & 0xffff) * device_cus();
+  // the items never exceed wt (or one per tile slot when the tiles alone
+  // exceed it) nor one per (tile slot, sub-tile)
   const int t8 = 8 * ((max_tiles + 7) / 8);
-  const int grid = (std::max(p.wt, t8) + 7) / 8 * 8;
+  constexpr int NT = 4 * NBW * 32;
+  const int64_t n_sub = (p.out_total + NT - 1) / NT;
+  const int64_t items = std::min<int64_t>(std::max(p.wt, t8), static_cast<int64_t>(t8) * n_sub);
+  const int grid = static_cast<int>((items + 7) / 8 * 8);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, st, p);
 }
 
