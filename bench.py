@@ -17,6 +17,10 @@ reference's HF loop restated on torch-CPU, timed on the host cores.
   python bench.py --config N --layer-gemm   # the vLLM layer's x . w_ext^T GEMM at
                                             # the workload's shapes, this library's
                                             # MFMA kernel and torch.mm, in TFLOP/s
+  python bench.py --config N --xext   # the reference-semantics ops over x_ext
+                                      # (switch_lora_expand, and the fused
+                                      # SwiGLU expand for gate_up) at the
+                                      # workload's shapes, in HBM GB/s
   python bench.py --copy-probe MIB   # a plain device copy of MIB MiB, the
                                      # reference for scaling rocprofv3's
                                      # FETCH_SIZE / WRITE_SIZE counters
@@ -141,6 +145,110 @@ def layer_gemm(cfg: int, n: int) -> None:
                       "peak_tflops": MFMA_PEAK["bf16"] / 1e12, "projections": rows}), flush=True)
 
 
+def xext_ops(cfg: int, n: int) -> None:
+    """The reference's own ops over x_ext = x . w_ext^T, as its vLLM layer calls
+    them (src/granite_switch/vllm/core/lora.py:596-686): switch_lora_expand in
+    place on x_ext[:, :N] (src/granite_switch/kernels/switch_lora_kernel.py:171-458)
+    and, for gate_up, switch_lora_expand_swiglu into a [T, H] output (:668-857).
+    x_ext is computed once per buffer set outside the timed region.  Algorithmic
+    bytes: per adapted row its N output values read and written and its S*r
+    shrink values read, each used adapter's lora_B tiers once, the ids; the
+    SwiGLU form reads both halves of every row and writes every output row."""
+    import torch
+
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    from granite_switch_amd import meta, ops, switched, vllm_layers, workloads
+    from granite_switch_amd.kernels import promote_rank
+
+    dev = torch.device("cuda:0")
+    routing = workloads.routing_for(cfg)
+    NA = workloads.num_adapters_for(cfg)
+    T = routing.num_tokens
+    ids = torch.tensor(routing.req_ids, device=dev)
+    segs = switched.build_segments(ids, NA, torch.tensor(routing.positions, device=dev),
+                                   torch.tensor(routing.cu_seqlens, device=dev),
+                                   torch.tensor(routing.act_offsets, device=dev) if routing.act_offsets is not None else None)
+    eff = segs.eff_ids.to(torch.int64)              # 0 = base, a + 1 = adapter a (the reference's ids)
+    eff_np = eff.cpu().numpy()
+    rows = []
+    for spec in workloads.module_specs(cfg):
+        S, H = len(spec.output_slices), spec.hidden
+        N = sum(spec.output_slices)
+        fuse = spec.name == "gate_up_proj"
+        ranks = list(spec.ranks[:NA])
+        g = torch.Generator(device=dev).manual_seed(23)
+        base = torch.nn.Linear(H, N, bias=False).to(device=dev, dtype=torch.bfloat16)
+        with torch.no_grad():
+            base.weight.copy_(torch.randn(N, H, generator=g, device=dev) / H ** 0.5)
+        layer = vllm_layers.SwitchedLoRALinear(base, NA, max(ranks), num_slices=S,
+                                               output_slices=tuple(spec.output_slices) if S > 1 else None,
+                                               fuse_swiglu=fuse)
+        A_sl = [layer.lora_A] if S == 1 else list(layer.lora_A_slices)
+        B_sl = [layer.lora_B] if S == 1 else list(layer.lora_B_slices)
+        with torch.no_grad():
+            for s_ in range(S):
+                for a, r in enumerate(ranks):
+                    A_sl[s_].data[a, 0, :r] = (torch.randn(r, H, generator=g, device=dev) / H ** 0.5).to(torch.bfloat16)
+                    B_sl[s_].data[a, 0, :, :r] = (torch.randn(spec.output_slices[s_], r, generator=g, device=dev)
+                                                  * 0.02).to(torch.bfloat16)
+        layer.finalize_weights(ranks)
+        fm = meta.FusedLoRAKernelMeta(dev)
+        fm.register_remap_tables(layer.remap_table.unsqueeze(0), [(H, layer._N_total, layer._num_applicable)])
+        ctx = meta.LoRAContext()
+        fm.prepare_and_store(eff, ctx)
+        nsets = 2
+        x_exts = []
+        for _ in range(nsets):
+            x = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
+            x_exts.append(torch.mm(x, layer.w_ext.T))
+            del x
+        out = torch.empty(T, N // 2 if fuse else 1, dtype=torch.bfloat16, device=dev)
+        loc, bm = ctx.remapped_indices[0], ctx.per_module_bitmasks[0]
+        if fuse:
+            def call(i):
+                ops.op("switch_lora_expand_swiglu")(out, x_exts[i % nsets], loc, bm, layer._lb_packed,
+                                                     layer.slice_col_r, *layer._na, 2, layer._block_n, N // 2, N)
+        else:
+            def call(i):
+                ops.op("switch_lora_expand")(x_exts[i % nsets], loc, bm, layer._lb_packed, layer.tile_to_slice,
+                                              layer.slice_col_r, *layer._na, S, layer._block_n, N)
+        call(0)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(n):
+                call(i)
+        graph.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        end.record()
+        end.synchronize()
+        us = start.elapsed_time(end) * 1e3 / n
+        # adapted rows: an applicable adapter (a token of a non-applicable one stays base)
+        rp = [promote_rank(r) for r in ranks]
+        adapted = [a for a in range(NA) if ranks[a] > 0]
+        act = np.isin(eff_np, [a + 1 for a in adapted])
+        t_act = int(act.sum())
+        used = sorted(set(int(v) - 1 for v in eff_np[act]))
+        b_bytes = sum(N * rp[a] * 2 for a in used)
+        shrink_bytes = sum(int((eff_np == a + 1).sum()) * S * rp[a] * 2 for a in used)
+        if fuse:
+            alg = T * N * 2 + T * (N // 2) * 2 + shrink_bytes + b_bytes + T * 8
+        else:
+            alg = 2 * t_act * N * 2 + shrink_bytes + b_bytes + T * 8
+        rows.append({"projection": spec.name, "op": "switch_lora_expand_swiglu" if fuse else "switch_lora_expand",
+                     "tokens": T, "adapted_tokens": t_act, "N": N, "us": us, "algorithmic_bytes": alg,
+                     "hbm_gbs": alg / us / 1e3, "hbm_frac": alg / us / 1e3 / HBM_PEAK_GBS})
+        del x_exts, out, layer, base
+    print(json.dumps({"workload": WORKLOAD_KEY[cfg], "ops": "reference-semantics expand over x_ext (bf16)",
+                      "peak_gbs": HBM_PEAK_GBS, "projections": rows}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -153,12 +261,17 @@ def main():
                     help="only run a plain device-to-device copy of MIB MiB five times (counter calibration)")
     ap.add_argument("--layer-gemm", action="store_true",
                     help="only time the vLLM layer's x . w_ext^T GEMM at the workload's shapes")
+    ap.add_argument("--xext", action="store_true",
+                    help="only time the reference-semantics expand ops over x_ext at the workload's shapes")
     args = ap.parse_args()
     if args.copy_probe is not None:
         copy_probe(args.copy_probe)
         return
     if args.layer_gemm:
         layer_gemm(args.config, args.steps or 10)
+        return
+    if args.xext:
+        xext_ops(args.config, args.steps or 20)
         return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))

@@ -37,7 +37,9 @@ __device__ __forceinline__ int load_id(const void* p, int bytes, int64_t i) {
 
 // Delta of one 32x32 block: rows m0..m0+31, columns n0..n0+31 (lane i owns
 // row m0+i for the A operand and column n0+i for the B operand), slice s.
-__device__ f32x16 xext_block_delta(const XextArgs& a, int64_t m0, int n0, int s, int id, bool row_ok, uint64_t bm) {
+// scr is the slice_col_r table staged in LDS.
+__device__ f32x16 xext_block_delta(const XextArgs& a, const int* scr, int64_t m0, int n0, int s, int id, bool row_ok,
+                                   uint64_t bm) {
   const int l = __lane_id();
   const int i = l & 31;
   const int h = l >> 5;
@@ -49,7 +51,7 @@ __device__ f32x16 xext_block_delta(const XextArgs& a, int64_t m0, int n0, int s,
   uint64_t todo = mine & bm;
   const uint16_t* xrow = static_cast<const uint16_t*>(a.x_ext) + (m0 + i) * a.stride_m;
   while (todo) {
-    const int b = __ffsll(static_cast<long long>(todo)) - 1;
+    const int b = __builtin_amdgcn_readfirstlane(__ffsll(static_cast<long long>(todo)) - 1);   // uniform
     todo &= todo - 1;
     const int kid = b + 1;   // kernel-local id
     // tier lookup: ids are numbered 1.. across tiers in ascending-rank order
@@ -57,13 +59,13 @@ __device__ f32x16 xext_block_delta(const XextArgs& a, int64_t m0, int n0, int s,
     int64_t lb_off = 0;
     while (t < 6 && kid >= first + a.na[t]) {
       first += a.na[t];
-      lb_off += static_cast<int64_t>(a.na[t]) * a.N * kRanks[t];
+      lb_off += static_cast<int64_t>(a.na[t]) * a.N * (16 << t);   // tier t holds rank 16 << t
       ++t;
     }
     if (t >= 6) break;   // cannot happen: the loop runs only over bits <= total count
-    const int r = kRanks[t];
+    const int r = 16 << t;
     const int idx = kid - first;
-    const int64_t c0 = static_cast<int64_t>(a.slice_col_r[s * 6 + t]) + static_cast<int64_t>(idx) * a.S * r;
+    const int64_t c0 = static_cast<int64_t>(scr[s * 6 + t]) + static_cast<int64_t>(idx) * a.S * r;
     const uint16_t* brow = a.lb + lb_off + static_cast<int64_t>(idx) * a.N * r + static_cast<int64_t>(n0 + i) * r;
     const bool sel = row_ok && id == kid;
     for (int kb = 0; kb < r; kb += 16) {
@@ -86,9 +88,12 @@ __device__ __forceinline__ uint64_t valid_bits(const int na[6]) {
 __global__ __launch_bounds__(256) void xext_expand_kernel(XextArgs a, uint16_t* x_out, const int32_t* __restrict__ tile_slice,
                                                           int block_n) {
   __shared__ float dtile[32][128 + 4];
+  __shared__ int scr[GS_MAX_SLICES * 6];
   const int64_t pm = blockIdx.y;
   const uint64_t bm = static_cast<uint64_t>(a.bitmask[pm * a.stride_bm]) & valid_bits(a.na);
   if (a.bitmask[pm * a.stride_bm] == 0) return;
+  // the slice column table, staged once (the adapter loop reads it per adapter)
+  if (threadIdx.x < a.S * 6) scr[threadIdx.x] = a.slice_col_r[threadIdx.x];
   const int n_tile0 = blockIdx.x * 128;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -99,11 +104,10 @@ __global__ __launch_bounds__(256) void xext_expand_kernel(XextArgs a, uint16_t* 
   const int id = row_ok ? load_id(a.ids, a.idx_bytes, m0 + i) : 0;
 
   const int n0 = n_tile0 + 32 * wave;
+  const int s = tile_slice[(n0 < a.N ? n0 : n_tile0) / block_n];
+  lds_barrier();
   f32x16 acc = f32x16{};
-  if (n0 < a.N) {
-    const int s = tile_slice[n0 / block_n];
-    acc = xext_block_delta(a, m0, n0, s, id, row_ok, bm);
-  }
+  if (n0 < a.N) acc = xext_block_delta(a, scr, m0, n0, s, id, row_ok, bm);
 #pragma unroll
   for (int v = 0; v < 16; ++v) dtile[mfma32_row(v, l)][32 * wave + i] = acc[v];
   lds_barrier();
@@ -131,6 +135,7 @@ __global__ __launch_bounds__(256) void xext_expand_kernel(XextArgs a, uint16_t* 
 __global__ __launch_bounds__(256) void xext_swiglu_kernel(XextArgs a, uint16_t* out, int64_t stride_om, int H) {
   __shared__ float dg[32][128 + 4];
   __shared__ float du[32][128 + 4];
+  __shared__ int scr[GS_MAX_SLICES * 6];
   const int64_t pm = blockIdx.y;
   const int64_t bm_raw = a.bitmask[pm * a.stride_bm];
   const uint64_t bm = static_cast<uint64_t>(bm_raw) & valid_bits(a.na);
@@ -141,14 +146,30 @@ __global__ __launch_bounds__(256) void xext_swiglu_kernel(XextArgs a, uint16_t* 
   const int i = l & 31;
   const int64_t m0 = pm * 32;
   const bool row_ok = (m0 + i) < a.M;
+  // this thread's gate and up pieces (row tid / 8, 16 columns) do not depend
+  // on the delta: they go out first, from a clamped in-bounds address
+  const int row = tid >> 3;
+  const int cx = (tid & 7) * 16;
+  const int64_t m = m0 + row;
+  const bool out_ok = m < a.M && h_tile0 + cx < H;
+  const uint16_t* xr = static_cast<const uint16_t*>(a.x_ext) + (out_ok ? m : m0) * a.stride_m +
+                       (out_ok ? h_tile0 + cx : h_tile0);
+  u32x4 gi[2], ui[2];
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    gi[half] = *reinterpret_cast<const u32x4*>(xr + half * 8);
+    ui[half] = *reinterpret_cast<const u32x4*>(xr + H + half * 8);
+  }
 
   if (bm_raw != 0) {
+    if (tid < a.S * 6) scr[tid] = a.slice_col_r[tid];
     const int id = row_ok ? load_id(a.ids, a.idx_bytes, m0 + i) : 0;
+    lds_barrier();
     const int h0 = h_tile0 + 32 * wave;
     f32x16 ag = f32x16{}, au = f32x16{};
     if (h0 < H) {
-      ag = xext_block_delta(a, m0, h0, 0, id, row_ok, bm);
-      au = xext_block_delta(a, m0, H + h0, 1, id, row_ok, bm);
+      ag = xext_block_delta(a, scr, m0, h0, 0, id, row_ok, bm);
+      au = xext_block_delta(a, scr, m0, H + h0, 1, id, row_ok, bm);
     }
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -158,16 +179,10 @@ __global__ __launch_bounds__(256) void xext_swiglu_kernel(XextArgs a, uint16_t* 
   }
   lds_barrier();
 
-  const int row = tid >> 3;
-  const int cx = (tid & 7) * 16;
-  const int64_t m = m0 + row;
-  if (m >= a.M || h_tile0 + cx >= H) return;
-  const uint16_t* xr = static_cast<const uint16_t*>(a.x_ext) + m * a.stride_m + h_tile0 + cx;
+  if (!out_ok) return;
   uint16_t* orow = out + m * stride_om + h_tile0 + cx;
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
-    const u32x4 gi = *reinterpret_cast<const u32x4*>(xr + half * 8);
-    const u32x4 ui = *reinterpret_cast<const u32x4*>(xr + H + half * 8);
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -175,8 +190,8 @@ __global__ __launch_bounds__(256) void xext_swiglu_kernel(XextArgs a, uint16_t* 
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int c = half * 8 + 2 * e + j;
-        float g = bf16_bits_to_f32(static_cast<uint16_t>((gi[e] >> (16 * j)) & 0xffffu));
-        float u = bf16_bits_to_f32(static_cast<uint16_t>((ui[e] >> (16 * j)) & 0xffffu));
+        float g = bf16_bits_to_f32(static_cast<uint16_t>((gi[half][e] >> (16 * j)) & 0xffffu));
+        float u = bf16_bits_to_f32(static_cast<uint16_t>((ui[half][e] >> (16 * j)) & 0xffffu));
         if (bm_raw != 0) {
           g += dg[row][cx + c];
           u += du[row][cx + c];
