@@ -249,6 +249,92 @@ def xext_ops(cfg: int, n: int) -> None:
                       "peak_gbs": HBM_PEAK_GBS, "projections": rows}), flush=True)
 
 
+def path_choice() -> None:
+    """Both y-given paths on the same batches: the one-launch decode kernel
+    (path="small") and build + shrink + expand (path="segments"), over
+    projection shapes of 2048- to 12800-wide layers with 2-48 adapters at
+    T = 64..1024 (ids uniform per token, 20 % of tokens on the base model),
+    plus the 4-sequence aLoRA batch of the 2048-wide CPU-sized workload, whose
+    sequences each hold one adapter.  Each timing is one graph replay over
+    rotating buffer sets (~250 MB, so weights come from HBM), divided by the
+    calls.  "auto" is the path that switched.small_preferred picks."""
+    import numpy as np
+    import torch
+
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    from granite_switch_amd import switched, workloads
+
+    dev = torch.device("cuda:0")
+    mixed = [8, 16, 32, 64] * 12
+    shapes = (("proj2048", 2048, (2048,), 16, (2, 4, 8)), ("qkv", 4096, (4096, 1024, 1024), 16, (2, 4, 8, 12)),
+              ("down", 12800, (4096,), 16, (2, 4, 8)), ("o_r64", 4096, (4096,), 64, (2, 4, 8)),
+              ("qkv_r64", 4096, (4096, 1024, 1024), 64, (12,)), ("o", 4096, (4096,), 32, (24,)),
+              ("down", 12800, (4096,), 32, (24,)), ("gate_up", 4096, (12800, 12800), 32, (24,)),
+              ("down_mixed_rank", 12800, (4096,), None, (48,)))
+    cases = []
+    for name, H, sl, r, nas in shapes:
+        for NA in nas:
+            ranks = [r] * NA if r else mixed[:NA]
+            spec = workloads.ModuleSpec(name=name, hidden=H, output_slices=sl, ranks=ranks, max_rank=max(ranks))
+            for T in (64, 128, 256, 512, 1024):
+                if T // NA <= 256 and (NA <= 8 or T >= 128):
+                    g = torch.Generator(device="cpu").manual_seed(T)
+                    ids = torch.randint(1, NA + 1, (T,), generator=g)
+                    ids[torch.rand(T, generator=g) < 0.2] = 0
+                    cases.append((spec, NA, T, ids, None, None, None))
+    r0 = workloads.routing_for(0)
+    spec0 = workloads.module_specs(0)[0]
+    cases.append((spec0, workloads.num_adapters_for(0), r0.num_tokens, torch.tensor(r0.req_ids),
+                   torch.tensor(r0.positions), torch.tensor(r0.cu_seqlens),
+                   None if r0.act_offsets is None else torch.tensor(r0.act_offsets)))
+    rows = []
+    for spec, NA, T, ids, pos, cu, off in cases:
+        H, sl = spec.hidden, spec.output_slices
+        per_call = NA * spec.max_rank * (len(sl) * H + sum(sl)) * 2
+        nsets = max(4, min(28, int(2.5e8 // (T * (H + sum(sl)) * 2 + per_call))))
+        sets = []
+        for i in range(nsets):
+            md = workloads.make_module(spec, T, NA, torch.bfloat16, dev, seed=50 + i)
+            pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, spec.ranks)
+            md.lora_A_slices = md.lora_B_slices = None
+            sets.append((md, pk))
+        ids_d = ids.to(dev)
+        pos_d, cu_d, off_d = (None if t is None else t.to(dev) for t in (pos, cu, off))
+        res = {}
+        for path in ("small", "segments"):
+            def call(i):
+                md, pk = sets[i % nsets]
+                switched.switched_lora_routed_(md.y, md.x, ids_d, pk, pos_d, cu_d, off_d, path=path)
+            call(0)
+            torch.cuda.synchronize()
+            n = nsets * 2
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for i in range(n):
+                    call(i)
+            graph.replay()
+            torch.cuda.synchronize()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            graph.replay()
+            end.record()
+            end.synchronize()
+            res[path] = start.elapsed_time(end) * 1e3 / n
+        nseq = None if cu is None else cu.numel() - 1
+        largest = int(np.bincount(ids.numpy(), minlength=NA + 1)[1:].max())
+        auto = "small" if switched.small_preferred(sets[0][1], T, nseq) else "segments"
+        rows.append({"projection": spec.name, "hidden": H, "output_slices": list(sl), "adapters": NA,
+                     "ranks": sorted(set(spec.ranks)), "tokens": T, "sequences": nseq, "largest_group": largest,
+                     "small_us": res["small"], "segments_us": res["segments"], "auto": auto})
+        log(f"{spec.name} H={H} NA={NA} T={T} seqs={nseq} largest={largest}: small {res['small']:.2f} us, "
+            f"segments {res['segments']:.2f} us, auto {auto}")
+        del sets
+    print(json.dumps({"comparison": "one-launch decode kernel vs segment kernels (bf16)", "rows": rows}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -263,6 +349,8 @@ def main():
                     help="only time the vLLM layer's x . w_ext^T GEMM at the workload's shapes")
     ap.add_argument("--xext", action="store_true",
                     help="only time the reference-semantics expand ops over x_ext at the workload's shapes")
+    ap.add_argument("--path-choice", action="store_true",
+                    help="only time the one-launch decode kernel against the segment kernels over T = 128..1024")
     args = ap.parse_args()
     if args.copy_probe is not None:
         copy_probe(args.copy_probe)
@@ -272,6 +360,9 @@ def main():
         return
     if args.xext:
         xext_ops(args.config, args.steps or 20)
+        return
+    if args.path_choice:
+        path_choice()
         return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))

@@ -821,6 +821,16 @@ int64_t gs_small_workspace_bytes(int32_t dtype, int64_t num_tokens, int32_t hidd
 
 int64_t gs_small_sync_bytes(void) { return kSyncBytes; }
 
+int64_t gs_small_workgroups(int32_t dtype, int64_t num_tokens, int32_t hidden, int32_t num_slices,
+                            int32_t num_adapters, int32_t max_rank, int32_t out_total,
+                            const int32_t* slice_bounds) {
+  if (num_tokens <= 0 || hidden <= 0 || slice_bounds == nullptr || num_adapters < 1) return 0;
+  const SmallPlan pl = plan_small(num_tokens, hidden, num_slices, num_adapters, max_rank, dtype == GS_DTYPE_BF16,
+                                  out_total, slice_bounds);
+  const int64_t np = 8 * static_cast<int64_t>(pl.NCB) * ((static_cast<int64_t>(pl.KS) * num_adapters + 7) / 8);
+  return np + static_cast<int64_t>(pl.NNT) * num_adapters;
+}
+
 int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t* positions,
                            const int32_t* cu_seqlens, const int64_t* act_offsets, int32_t num_seqs,
                            const int32_t* eff_ids, const void* x, int64_t ldx, void* y, int64_t ldy,

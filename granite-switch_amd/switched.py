@@ -334,12 +334,50 @@ def small_eligible(packed: "PackedAdapters", num_tokens: int, num_seqs: int = 1)
                                               packed.max_rank))
 
 
-def small_preferred(packed: "PackedAdapters", num_tokens: int, num_seqs: int = 1) -> bool:
-    """The ``auto`` path choice: the small-batch kernel when it is eligible and
-    the batch averages at most one 32-token row tile per adapter (decode); the
-    segment kernels otherwise, which spread longer per-adapter runs over more
-    workgroups."""
-    return small_eligible(packed, num_tokens, num_seqs) and num_tokens <= max(64, 32 * packed.num_adapters)
+_cu_counts: dict = {}
+
+
+def _device_cus(device: torch.device) -> int:
+    key = _dev_key(device)
+    n = _cu_counts.get(key)
+    if n is None:
+        n = int(torch.cuda.get_device_properties(device).multi_processor_count)
+        _cu_counts[key] = n
+    return n
+
+
+def small_preferred(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None = None) -> bool:
+    """The ``auto`` path choice between the one-launch small-batch kernel and
+    the segment kernels (build + shrink + expand).
+
+    Each workgroup of the one-launch kernel walks all the tokens of its adapter,
+    so its time grows with the largest adapter group, while the segment kernels
+    spread an adapter's tokens over row tiles.  The host cannot see the groups
+    without a synchronisation, so it estimates the largest one as
+    ``T / min(adapters, sequences)``: a sequence's tokens mostly share an
+    adapter.  ``num_seqs`` is the number of sequences when the caller knows
+    them (``cu_seqlens``); ``None`` estimates ``T / adapters``.  The one-launch
+    kernel is taken when it is eligible, the estimate is at most 96 tokens,
+    and its grid (producers + consumers) fits the GPU about once: at most 4
+    workgroups per CU, or 8 for batches of up to 256 tokens.
+
+    Measured on one MI355X (H = 2048..12800, 2..48 adapters, T = 64..1024):
+    the one-launch kernel wins up to ~64-110 tokens in the largest group
+    (4096 -> 6144 with 12 adapters at T = 512: 15.6 against 23.5 us) and loses
+    beyond it (4 sequences of 128 tokens on 4 adapters, one adapter holding
+    two of them: 29.9 against 19.5 us), and on grids past the GPU's size
+    (gate_up 4096 -> 25600 with 24 adapters: 2592 workgroups).
+    """
+    if not small_eligible(packed, num_tokens, num_seqs or 1):
+        return False
+    spread = packed.num_adapters if not num_seqs else min(packed.num_adapters, num_seqs)
+    if (num_tokens + spread - 1) // spread > 96:
+        return False
+    wgs = int(_lib.load().gs_small_workgroups(_DTYPES[packed.dtype], int(num_tokens), packed.hidden,
+                                              packed.num_slices, packed.num_adapters, packed.max_rank,
+                                              packed.out_total, _i32_array(packed.slice_bounds)))
+    cus = _device_cus(packed.a_pack.device)
+    return wgs <= 4 * cus or (num_tokens <= 256 and wgs <= 8 * cus)
 
 
 def reserve_workspace(device: torch.device, nbytes: int) -> None:
@@ -533,7 +571,7 @@ def switched_lora_routed_(y: torch.Tensor, x: torch.Tensor, adapter_ids: torch.T
     num_seqs = 1 if cu is None else cu.numel() - 1
     if off is not None and off.numel() != num_seqs:
         raise ValueError("act_offsets must have one entry per sequence")
-    if path == "small" or (path == "auto" and small_preferred(packed, T, num_seqs)):
+    if path == "small" or (path == "auto" and small_preferred(packed, T, num_seqs if cu is not None else None)):
         if not small_eligible(packed, T, num_seqs):
             raise ValueError("this module / batch is outside the small-batch kernel's limits")
         _call_small(x2, y2, packed, req=ids, pos=pos, cu=cu if off is not None else None, off=off,

@@ -194,6 +194,13 @@ int64_t gs_small_workspace_bytes(int32_t dtype, int64_t num_tokens, int32_t hidd
                                  int32_t num_adapters, int32_t max_rank, int32_t out_total,
                                  const int32_t* slice_bounds);
 int64_t gs_small_sync_bytes(void);
+/* Workgroups of one gs_switched_lora_small launch for this shape (producers +
+ * consumers).  No counterpart in the reference: this library's path choice
+ * uses it -- the one-launch kernel wins while its grid fits the GPU about
+ * once, the segment kernels beyond (measured on decode-sized batches). */
+int64_t gs_small_workgroups(int32_t dtype, int64_t num_tokens, int32_t hidden, int32_t num_slices,
+                            int32_t num_adapters, int32_t max_rank, int32_t out_total,
+                            const int32_t* slice_bounds);
 int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t* positions,
                            const int32_t* cu_seqlens, const int64_t* act_offsets, int32_t num_seqs,
                            const int32_t* eff_ids, const void* x, int64_t ldx, void* y, int64_t ldy,
