@@ -254,10 +254,12 @@ def path_choice() -> None:
     (path="small") and build + shrink + expand (path="segments"), over
     projection shapes of 2048- to 12800-wide layers with 2-48 adapters at
     T = 64..1024 (ids uniform per token, 20 % of tokens on the base model),
-    plus the 4-sequence aLoRA batch of the 2048-wide CPU-sized workload, whose
-    sequences each hold one adapter.  Each timing is one graph replay over
-    rotating buffer sets (~250 MB, so weights come from HBM), divided by the
-    calls.  "auto" is the path that switched.small_preferred picks."""
+    then batches of 4-8 sequences of 128-256 tokens that each hold one adapter
+    (chunked-prefill mixes), and the 4-sequence aLoRA batch of the 2048-wide
+    CPU-sized workload.  Each timing is one graph replay over rotating buffer
+    sets (~250 MB, so weights come from HBM), divided by the calls.  "auto" is
+    the path that switched.small_preferred picks; the one-launch kernel runs
+    with the row split switched.small_row_split picks."""
     import numpy as np
     import torch
 
@@ -284,6 +286,18 @@ def path_choice() -> None:
                     ids = torch.randint(1, NA + 1, (T,), generator=g)
                     ids[torch.rand(T, generator=g) < 0.2] = 0
                     cases.append((spec, NA, T, ids, None, None, None))
+    for name, H, sl, r, NA, T, L in (("qkv", 4096, (4096, 1024, 1024), 16, 4, 512, 128),
+                                     ("qkv", 4096, (4096, 1024, 1024), 16, 12, 512, 128),
+                                     ("qkv", 4096, (4096, 1024, 1024), 16, 12, 1024, 128),
+                                     ("qkv", 4096, (4096, 1024, 1024), 16, 24, 1024, 256),
+                                     ("down", 12800, (4096,), 16, 4, 512, 128),
+                                     ("down", 12800, (4096,), 16, 12, 512, 128),
+                                     ("gate_up", 4096, (12800, 12800), 32, 4, 512, 128),
+                                     ("gate_up", 4096, (12800, 12800), 32, 12, 1024, 128)):
+        spec = workloads.ModuleSpec(name=name, hidden=H, output_slices=sl, ranks=[r] * NA, max_rank=r)
+        g = np.random.default_rng(T + L + NA)
+        ids = torch.tensor(np.repeat(g.integers(1, NA + 1, T // L), L))
+        cases.append((spec, NA, T, ids, None, torch.arange(0, T + 1, L, dtype=torch.int32), None))
     r0 = workloads.routing_for(0)
     spec0 = workloads.module_specs(0)[0]
     cases.append((spec0, workloads.num_adapters_for(0), r0.num_tokens, torch.tensor(r0.req_ids),
@@ -326,10 +340,11 @@ def path_choice() -> None:
         nseq = None if cu is None else cu.numel() - 1
         largest = int(np.bincount(ids.numpy(), minlength=NA + 1)[1:].max())
         auto = "small" if switched.small_preferred(sets[0][1], T, nseq) else "segments"
+        rs = switched.small_row_split(sets[0][1], T, nseq)
         rows.append({"projection": spec.name, "hidden": H, "output_slices": list(sl), "adapters": NA,
                      "ranks": sorted(set(spec.ranks)), "tokens": T, "sequences": nseq, "largest_group": largest,
-                     "small_us": res["small"], "segments_us": res["segments"], "auto": auto})
-        log(f"{spec.name} H={H} NA={NA} T={T} seqs={nseq} largest={largest}: small {res['small']:.2f} us, "
+                     "row_split": rs, "small_us": res["small"], "segments_us": res["segments"], "auto": auto})
+        log(f"{spec.name} H={H} NA={NA} T={T} seqs={nseq} largest={largest} rs={rs}: small {res['small']:.2f} us, "
             f"segments {res['segments']:.2f} us, auto {auto}")
         del sets
     print(json.dumps({"comparison": "one-launch decode kernel vs segment kernels (bf16)", "rows": rows}), flush=True)

@@ -49,11 +49,11 @@ SIGNATURES = {
     "gs_small_eligible": (c_i32, [c_i64, c_i32, c_i32, c_void_p, c_i32, c_i32]),
     "gs_small_workspace_bytes": (c_i64, [c_i32, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_void_p]),
     "gs_small_sync_bytes": (c_i64, []),
-    "gs_small_workgroups": (c_i64, [c_i32, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_void_p]),
+    "gs_small_workgroups": (c_i64, [c_i32, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_void_p, c_i32]),
     "gs_switched_lora_small": (c_i32, [c_i32, c_void_p, c_void_p, c_void_p, c_void_p, c_i32, c_void_p, c_void_p,
                                        c_i64, c_void_p, c_i64, c_i64, c_i32, c_i32, c_void_p, c_i32, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_i32, c_i32, c_void_p, c_i64,
-                                       c_void_p, c_i64, c_i32, c_void_p]),
+                                       c_void_p, c_i64, c_i32, c_i32, c_void_p]),
     "gs_compute_bitmasks": (c_i32, [c_void_p, c_i32, c_i64, c_void_p, c_i32, c_i32, c_i32, c_void_p, c_void_p,
                                     c_void_p]),
     "gs_switch_lora_expand": (c_i32, [c_void_p, c_i64, c_i64, c_i64, c_void_p, c_i32, c_void_p, c_i64, c_void_p,

@@ -2,10 +2,13 @@
 // launch, with no separate segment build.
 //
 // The grid is 1-D: NP producer workgroups, then NC consumer workgroups.
-//   producer (cb, kc, g): the shrink of adapter g's 32-column block cb over the
-//     k-chunk kc, written as fp32 partial sums;
-//   consumer (nt, g): the expand of adapter g into the NT-column tile nt of y
-//     (inside one slice), which adds the partials of its slice in ks order.
+//   producer (cb, kc, g, rs): the shrink of adapter g's 32-column block cb over
+//     the k-chunk kc, written as fp32 partial sums;
+//   consumer (nt, g, rs): the expand of adapter g into the NT-column tile nt of
+//     y (inside one slice), which adds the partials of its slice in ks order.
+// An adapter's token list is cut into 32-token row chunks; row split rs of RS
+// takes chunks rs, rs + RS, rs + 2 RS, ..., so an adapter with many tokens is
+// spread over RS times the workgroups.
 // Every workgroup gates and lists the tokens of its own adapter from the
 // routing input (ids outside [0, NA] are base; aLoRA: a token before its
 // sequence's activation offset is base), with one ballot per token chunk and a
@@ -21,8 +24,9 @@
 // loads until every tag equals E_g + 1 (a pair is read in one access, so a
 // value is never taken without its tag).  Once it has its partials, a consumer
 // adds its weight to C_g without waiting for the result; the weights of g's
-// consumers in one launch sum to exactly 2^20, so E_g moves to E_g + 1 only
-// when the last of them has added.  Every workgroup of g in the launch reads
+// NNT * RS consumers in one launch sum to exactly 2^20, so E_g moves to E_g + 1
+// only when the last of them has added (a consumer whose row split holds no
+// chunk adds its weight without waiting).  Every workgroup of g in the launch reads
 // E_g: consumers read it before adding, and every producer that writes
 // partials is waited for by some consumer of its slice, which has not added
 // yet.  No counters on the critical path, no cache writeback or invalidate,
@@ -62,6 +66,7 @@ constexpr int kErrTimeout = 1;               // error word bits
 constexpr int kSyncErrWord = 2;              // int32 index of the error word
 constexpr int kSyncLine = 32;                // int32 words per adapter (its 64-bit launch counter)
 constexpr int kEpochShift = 20;              // a launch adds 2^20 to the counter of each adapter with tokens
+constexpr int kSmMaxRowSplit = 32;           // row splits: at most one 32-token chunk each at 1024 tokens
 
 // Per-adapter weight offsets and ranks, passed by value (load-time constants of
 // the module) so no workgroup waits on a table load before its weight loads.
@@ -294,6 +299,7 @@ struct FusedParams {
   int S;
   int KS;
   int NCB;
+  int RS;                 // row splits: split rs takes row chunks rs, rs + RS, ...
   int NP;                 // producer workgroups (the first NP ids)
   uint64_t* part;         // tagged partials: region (g-1) at part + (g-1)*region, [KS][cap][zw]
   int64_t region;
@@ -364,12 +370,14 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
   constexpr int ES = Elt<BF16>::kSize;
   constexpr int KSTEP = 4 * P;      // k per piece over the 4 lane groups
   constexpr int KW = NPW * KSTEP;   // k per wave
-  // Workgroups are dealt to the 8 XCDs round-robin by id, so the NCB
-  // column-block siblings of one (k-chunk, adapter) -- which read the same x
-  // rows -- get ids 8 apart and share an XCD's L2.  Ids past the last
-  // (k-chunk, adapter) pair have no work.
-  const int cb = (bid >> 3) % p.NCB;
-  const int q = ((bid >> 3) / p.NCB) * 8 + (bid & 7);
+  // Workgroups are dealt to the 8 XCDs round-robin by id, so the NCB * RS
+  // column-block and row-split siblings of one (k-chunk, adapter) -- which
+  // read the same x rows or the same lora_A rows -- get ids 8 apart and share
+  // an XCD's L2.  Ids past the last (k-chunk, adapter) pair have no work.
+  const int inner = (bid >> 3) % (p.NCB * p.RS);
+  const int cb = inner % p.NCB;
+  const int rs = inner / p.NCB;
+  const int q = ((bid >> 3) / (p.NCB * p.RS)) * 8 + (bid & 7);
   if (q >= p.KS * p.rt.NA) return;
   const int kc = q % p.KS;
   const int g = q / p.KS + 1;
@@ -421,7 +429,8 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
   route_gate<U>(p.rt, g, L.rt, rr);
   if (tid == 0) L.epoch = static_cast<uint32_t>(counter >> kEpochShift);   // visible after route_list's barriers
   const int n_g = route_list<U>(g, L.rt, rr);
-  if (!active || n_g == 0) return;
+  const int first = 32 * rs;             // this row split's first chunk
+  if (!active || n_g <= first) return;
   const uint64_t tag = static_cast<uint64_t>(L.epoch + 1u) << 32;
   uint64_t* part = p.part + static_cast<int64_t>(g - 1) * p.region;
 
@@ -445,7 +454,7 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
       }
     }
   };
-  load_x(0);
+  load_x(first);
 #pragma unroll
   for (int pp = 0; pp < NPW; ++pp) {
     const int64_t kp = k_lo + pp * KSTEP + q4 * P;
@@ -454,8 +463,8 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
   }
   __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the MFMAs wait
 
-  for (int rt0 = 0; rt0 < n_g; rt0 += 32) {
-    if (rt0 > 0) load_x(rt0);
+  for (int rt0 = first; rt0 < n_g; rt0 += 32 * p.RS) {
+    if (rt0 > first) load_x(rt0);
     // acc[rt][c2]: token slots rt0 + 16*rt + 4*q4 + e, column n[c2]
     f32x4 acc[2][2];
 #pragma unroll
@@ -513,8 +522,14 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
   constexpr int EPT = 4;                // shrink elements per thread and batch
   constexpr int NEB = 32 * kSmMaxRank / (kSmT * EPT);   // batches (rank <= 64)
 
-  const int nt = cid % p.NNT;
-  const int g = cid / p.NNT + 1;
+  // (tile, adapter) items are dealt to the XCDs by the low 3 id bits; the RS
+  // row-split siblings of an item, which read the same lora_B rows, get ids 8
+  // apart and share an XCD's L2.  Ids past the last item have no work.
+  const int item = ((cid >> 3) / p.RS) * 8 + (cid & 7);
+  const int rs = (cid >> 3) % p.RS;
+  if (item >= p.NNT * p.rt.NA) return;
+  const int nt = item % p.NNT;
+  const int g = item / p.NNT + 1;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int l = tid & 63;
@@ -568,11 +583,13 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
   const uint32_t want = L.epoch + 1u;
   const uint64_t* part = p.part + static_cast<int64_t>(g - 1) * p.region;
   const int64_t kstride = static_cast<int64_t>(p.cap) * p.zw;
-  // this consumer's share of the 2^20 that g's consumers add per launch
-  const uint64_t weight = (uint64_t{1} << kEpochShift) / p.NNT + (nt < (1 << kEpochShift) % p.NNT ? 1 : 0);
+  // this consumer's share of the 2^20 that g's NNT * RS consumers add per launch
+  const int ncons = p.NNT * p.RS;
+  const int cidx = rs * p.NNT + nt;
+  const uint64_t weight = (uint64_t{1} << kEpochShift) / ncons + (cidx < (1 << kEpochShift) % ncons ? 1 : 0);
   const int cx = (tid % LPR) * EPL;
 
-  for (int rt0 = 0; rt0 < n_g; rt0 += 32) {
+  for (int rt0 = 32 * rs; rt0 < n_g; rt0 += 32 * p.RS) {
     // y pieces of this row chunk (issued before the wait)
     u32x4 yv[NH][PASSES];
     int64_t yoff[PASSES];
@@ -734,8 +751,11 @@ constexpr int kSmTargetShrinkWgs = GS_SMALL_TARGET_PRODUCERS;
 constexpr int64_t kDefaultTimeoutTicks = 2000000;   // 20 ms of the 100 MHz wall clock
 constexpr int64_t kSyncBytes = 4 * kSyncLine * (kSmMaxAdapters + 1);
 
+// The row split RS multiplies the producers like the k-split does, so it
+// counts towards the target: a larger RS never gives a larger KS (and so
+// never a larger workspace than RS = 1).
 SmallPlan plan_small(int64_t T, int H, int S, int NA, int max_rank, bool bf16, int out_total,
-                     const int32_t* slice_bounds) {
+                     const int32_t* slice_bounds, int RS = 1) {
   SmallPlan pl{};
   pl.zw = S * max_rank;
   pl.NCB = (pl.zw + 31) / 32;
@@ -746,7 +766,7 @@ SmallPlan plan_small(int64_t T, int H, int S, int NA, int max_rank, bool bf16, i
   int ks = 1;
   for (;;) {
     ks = (H + 4 * npw * kstep - 1) / (4 * npw * kstep);
-    if (static_cast<int64_t>(NA) * pl.NCB * ks >= kSmTargetShrinkWgs || npw == 4) break;
+    if (static_cast<int64_t>(NA) * pl.NCB * ks * RS >= kSmTargetShrinkWgs || npw == 4) break;
     npw >>= 1;
   }
   pl.NPW = npw;
@@ -759,6 +779,15 @@ SmallPlan plan_small(int64_t T, int H, int S, int NA, int max_rank, bool bf16, i
   pl.NNT = out_total / (64 * pl.NQ);
   pl.region_bytes = static_cast<int64_t>(pl.KS) * pl.cap * pl.zw * 8;
   return pl;
+}
+
+// Producers: NCB * RS siblings for each group of 8 (k-chunk, adapter) pairs.
+// Consumers: RS siblings for each group of 8 (tile, adapter) items.
+int64_t producer_wgs(const SmallPlan& pl, int NA, int RS) {
+  return 8 * static_cast<int64_t>(pl.NCB) * RS * ((static_cast<int64_t>(pl.KS) * NA + 7) / 8);
+}
+int64_t consumer_wgs(const SmallPlan& pl, int NA, int RS) {
+  return 8 * static_cast<int64_t>(RS) * ((static_cast<int64_t>(pl.NNT) * NA + 7) / 8);
 }
 
 template <bool BF16, int NQ, bool SPEC, int U>
@@ -823,12 +852,12 @@ int64_t gs_small_sync_bytes(void) { return kSyncBytes; }
 
 int64_t gs_small_workgroups(int32_t dtype, int64_t num_tokens, int32_t hidden, int32_t num_slices,
                             int32_t num_adapters, int32_t max_rank, int32_t out_total,
-                            const int32_t* slice_bounds) {
+                            const int32_t* slice_bounds, int32_t row_split) {
   if (num_tokens <= 0 || hidden <= 0 || slice_bounds == nullptr || num_adapters < 1) return 0;
+  if (row_split < 1 || row_split > kSmMaxRowSplit) return 0;
   const SmallPlan pl = plan_small(num_tokens, hidden, num_slices, num_adapters, max_rank, dtype == GS_DTYPE_BF16,
-                                  out_total, slice_bounds);
-  const int64_t np = 8 * static_cast<int64_t>(pl.NCB) * ((static_cast<int64_t>(pl.KS) * num_adapters + 7) / 8);
-  return np + static_cast<int64_t>(pl.NNT) * num_adapters;
+                                  out_total, slice_bounds, row_split);
+  return producer_wgs(pl, num_adapters, row_split) + consumer_wgs(pl, num_adapters, row_split);
 }
 
 int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t* positions,
@@ -838,7 +867,7 @@ int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t*
                            int32_t num_slices, const void* a_pack, const int64_t* a_off, const void* b_pack,
                            const int64_t* b_off, const int32_t* ranks, int32_t num_adapters, int32_t max_rank,
                            void* workspace, int64_t workspace_bytes, int32_t* sync, int64_t sync_bytes,
-                           int32_t speculate, void* stream) {
+                           int32_t row_split, int32_t speculate, void* stream) {
   const char* who = "gs_switched_lora_small";
   GS_CHECK_ARG(dtype == GS_DTYPE_BF16 || dtype == GS_DTYPE_FP32, "%s: dtype=%d", who, dtype);
   const int nseq = (cu_seqlens != nullptr) ? num_seqs : 1;
@@ -846,6 +875,8 @@ int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t*
                "%s: shape outside the small-batch path (T <= %d, <= %d adapters, max_rank <= %d, slice widths "
                "multiples of 128)", who, kSmMaxTokens, kSmMaxAdapters, kSmMaxRank);
   GS_CHECK_ARG(nseq >= 1, "%s: num_seqs=%d", who, num_seqs);
+  GS_CHECK_ARG(row_split >= 1 && row_split <= kSmMaxRowSplit, "%s: row_split=%d outside [1, %d]", who, row_split,
+               kSmMaxRowSplit);
   GS_CHECK_ARG(eff_ids != nullptr || req_ids != nullptr || num_tokens == 0, "%s: no routing input", who);
   GS_CHECK_ARG(slice_bounds[num_slices] == out_total, "%s: slice_bounds must end at out_total", who);
   GS_CHECK_ARG(hidden > 0 && hidden % 8 == 0, "%s: hidden=%d must be a positive multiple of 8", who, hidden);
@@ -867,7 +898,7 @@ int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t*
   if (num_tokens == 0) return GS_OK;
   const bool bf16 = dtype == GS_DTYPE_BF16;
   const SmallPlan pl = plan_small(num_tokens, hidden, num_slices, num_adapters, max_rank, bf16, out_total,
-                                  slice_bounds);
+                                  slice_bounds, row_split);
   // adapter regions are a fixed fraction of the workspace, whatever the shape
   const int64_t region_bytes = (workspace_bytes / kSmMaxAdapters) & ~int64_t(15);
   if (region_bytes < pl.region_bytes) {
@@ -890,7 +921,8 @@ int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t*
   fp.S = num_slices;
   fp.KS = pl.KS;
   fp.NCB = pl.NCB;
-  fp.NP = 8 * pl.NCB * ((pl.KS * num_adapters + 7) / 8);
+  fp.RS = row_split;
+  fp.NP = static_cast<int>(producer_wgs(pl, num_adapters, row_split));
   fp.part = static_cast<uint64_t*>(workspace);
   fp.region = region_bytes / 8;
   fp.cap = pl.cap;
@@ -905,7 +937,7 @@ int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t*
   fp.sync = sync;
   fp.timeout_ticks = kDefaultTimeoutTicks;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const unsigned grid = static_cast<unsigned>(fp.NP + pl.NNT * num_adapters);
+  const unsigned grid = static_cast<unsigned>(fp.NP + consumer_wgs(pl, num_adapters, row_split));
   if (bf16) launch_fused<true>(pl, fp, grid, speculate != 0, st);
   else launch_fused<false>(pl, fp, grid, speculate != 0, st);
   GS_CHECK_LAUNCH(who);

@@ -346,38 +346,73 @@ def _device_cus(device: torch.device) -> int:
     return n
 
 
+def small_workgroups(packed: "PackedAdapters", num_tokens: int, row_split: int = 1) -> int:
+    """Workgroups of one small-batch launch (producers + consumers)."""
+    return int(_lib.load().gs_small_workgroups(_DTYPES[packed.dtype], int(num_tokens), packed.hidden,
+                                               packed.num_slices, packed.num_adapters, packed.max_rank,
+                                               packed.out_total, _i32_array(packed.slice_bounds), int(row_split)))
+
+
+def _small_plan(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None) -> tuple[bool, int]:
+    """(prefer the small-batch kernel, its row split) for this module and batch."""
+    T = int(num_tokens)
+    key = (_dev_key(packed.a_pack.device), packed.dtype, packed.hidden, packed.num_slices, packed.num_adapters,
+           packed.max_rank, packed.out_total, tuple(packed.slice_bounds), T, num_seqs)
+    plan = _small_plans.get(key)
+    if plan is not None:
+        return plan
+    if not small_eligible(packed, T, num_seqs or 1):
+        plan = (False, 1)
+    else:
+        spread = packed.num_adapters if not num_seqs else min(packed.num_adapters, num_seqs)
+        largest = (T + spread - 1) // spread
+        chunks = (largest + 31) // 32                   # 32-token chunks in the estimated largest group
+        cus = _device_cus(packed.a_pack.device)
+        rs = 1
+        while rs < chunks and rs * 2 <= 32 and small_workgroups(packed, T, rs * 2) <= 3 * cus:
+            rs *= 2
+        per_wg = -(-chunks // rs)
+        fits = small_workgroups(packed, T, rs) <= (8 if T <= 256 else 4) * cus
+        plan = (fits and (per_wg <= 2 or (rs == 1 and chunks <= 3)), rs)
+    _small_plans[key] = plan
+    return plan
+
+
+_small_plans: dict = {}
+
+
+def small_row_split(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None = None) -> int:
+    """Row split of the small-batch kernel for this batch (see ``small_preferred``)."""
+    return _small_plan(packed, num_tokens, num_seqs)[1]
+
+
 def small_preferred(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None = None) -> bool:
     """The ``auto`` path choice between the one-launch small-batch kernel and
-    the segment kernels (build + shrink + expand).
+    the segment kernels (build + shrink + expand), and with it the kernel's
+    row split.
 
-    Each workgroup of the one-launch kernel walks all the tokens of its adapter,
-    so its time grows with the largest adapter group, while the segment kernels
-    spread an adapter's tokens over row tiles.  The host cannot see the groups
-    without a synchronisation, so it estimates the largest one as
-    ``T / min(adapters, sequences)``: a sequence's tokens mostly share an
-    adapter.  ``num_seqs`` is the number of sequences when the caller knows
-    them (``cu_seqlens``); ``None`` estimates ``T / adapters``.  The one-launch
-    kernel is taken when it is eligible, the estimate is at most 96 tokens,
-    and its grid (producers + consumers) fits the GPU about once: at most 4
-    workgroups per CU, or 8 for batches of up to 256 tokens.
+    A workgroup set of the one-launch kernel walks the 32-token chunks of its
+    adapter's tokens one after another; a row split of RS gives chunks rs,
+    rs + RS, ... to RS sets, multiplying the grid by about RS.  The host cannot
+    see the groups without a synchronisation, so it estimates the largest one
+    as ``T / min(adapters, sequences)`` (a sequence's tokens mostly share an
+    adapter; ``num_seqs`` is the number of sequences when the caller knows
+    them, ``None`` estimates ``T / adapters``).  The row split doubles while
+    it is below the estimate's chunk count and the grid stays within 3
+    workgroups per CU (the kernel holds 2 per CU at a time); the one-launch
+    kernel is taken when it is eligible, its grid is within 4 workgroups per
+    CU (8 for batches of up to 256 tokens), and each workgroup is left with at
+    most 2 chunks (3 without a split).
 
     Measured on one MI355X (H = 2048..12800, 2..48 adapters, T = 64..1024):
-    the one-launch kernel wins up to ~64-110 tokens in the largest group
-    (4096 -> 6144 with 12 adapters at T = 512: 15.6 against 23.5 us) and loses
-    beyond it (4 sequences of 128 tokens on 4 adapters, one adapter holding
-    two of them: 29.9 against 19.5 us), and on grids past the GPU's size
-    (gate_up 4096 -> 25600 with 24 adapters: 2592 workgroups).
+    past these grids a second round of workgroups costs more than it saves
+    (gate_up 4096 -> 25600 with 24 adapters: 2592 workgroups), and past two
+    chunks per workgroup the segment kernels, which spread an adapter's tokens
+    over row tiles, are faster.  Row splits took the 2048-wide 4-sequence
+    aLoRA batch from 34.6 us (no split) to 14.3 us, against 17.8 us for the
+    segment kernels.
     """
-    if not small_eligible(packed, num_tokens, num_seqs or 1):
-        return False
-    spread = packed.num_adapters if not num_seqs else min(packed.num_adapters, num_seqs)
-    if (num_tokens + spread - 1) // spread > 96:
-        return False
-    wgs = int(_lib.load().gs_small_workgroups(_DTYPES[packed.dtype], int(num_tokens), packed.hidden,
-                                              packed.num_slices, packed.num_adapters, packed.max_rank,
-                                              packed.out_total, _i32_array(packed.slice_bounds)))
-    cus = _device_cus(packed.a_pack.device)
-    return wgs <= 4 * cus or (num_tokens <= 256 and wgs <= 8 * cus)
+    return _small_plan(packed, num_tokens, num_seqs)[0]
 
 
 def reserve_workspace(device: torch.device, nbytes: int) -> None:
@@ -529,7 +564,7 @@ def _xy2(x: torch.Tensor, y: torch.Tensor, packed: PackedAdapters):
     return x2, y2
 
 
-def _call_small(x2, y2, packed, eff_ids=None, req=None, pos=None, cu=None, off=None, num_seqs=1):
+def _call_small(x2, y2, packed, eff_ids=None, req=None, pos=None, cu=None, off=None, num_seqs=1, row_split=1):
     T = x2.shape[0]
     ws = small_workspace(x2.device, small_workspace_bytes(packed, T))
     sync = small_sync_buffer(x2.device)
@@ -542,7 +577,7 @@ def _call_small(x2, y2, packed, eff_ids=None, req=None, pos=None, cu=None, off=N
               packed.hidden, packed.out_total, _i32_array(packed.slice_bounds), packed.num_slices,
               packed.a_pack.data_ptr(), i64(packed.a_off_host), packed.b_pack.data_ptr(), i64(packed.b_off_host),
               _i32_array(packed.ranks_host), packed.num_adapters, packed.max_rank, ws.data_ptr(), ws.numel(),
-              sync.data_ptr(), sync.numel() * 4, speculate, _lib.stream_ptr(x2.device))
+              sync.data_ptr(), sync.numel() * 4, int(row_split), speculate, _lib.stream_ptr(x2.device))
 
 
 def switched_lora_routed_(y: torch.Tensor, x: torch.Tensor, adapter_ids: torch.Tensor, packed: PackedAdapters,
@@ -575,7 +610,8 @@ def switched_lora_routed_(y: torch.Tensor, x: torch.Tensor, adapter_ids: torch.T
         if not small_eligible(packed, T, num_seqs):
             raise ValueError("this module / batch is outside the small-batch kernel's limits")
         _call_small(x2, y2, packed, req=ids, pos=pos, cu=cu if off is not None else None, off=off,
-                    num_seqs=num_seqs if off is not None else 1)
+                    num_seqs=num_seqs if off is not None else 1,
+                    row_split=small_row_split(packed, T, num_seqs if cu is not None else None))
         return y
     segs = build_segments(ids, packed.num_adapters, pos, cu, off)
     return switched_lora_(y, x, segs, packed, path="segments")
@@ -601,7 +637,7 @@ def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed:
         raise ValueError("x / y shapes do not match the segments")
     _check_segments(segments, packed)
     if path == "small" or (path == "auto" and T and small_preferred(packed, T)):
-        _call_small(x2, y2, packed, eff_ids=segments.eff_ids)
+        _call_small(x2, y2, packed, eff_ids=segments.eff_ids, row_split=small_row_split(packed, T))
         return y
     zw = packed.num_slices * packed.max_rank
     if z is None:

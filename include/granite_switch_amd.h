@@ -184,6 +184,11 @@ int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t
  * partials).  Zeroing sync again requires zeroing the workspace too.  Calls
  * sharing a workspace or sync buffer must not overlap in time (stream order
  * is enough).
+ * row_split (1..32) cuts each adapter's token list into 32-token chunks and
+ * gives chunks rs, rs + row_split, ... to a workgroup set of their own, so an
+ * adapter with many tokens runs on row_split times the workgroups; the result
+ * does not depend on it.  1 suits decode (a few tokens per adapter); about
+ * (largest adapter group) / 64 suits larger batches.
  * speculate != 0 issues every adapter's weight loads before the routing is
  * known (saves a memory round trip when most adapters have tokens); 0 reads
  * only the weights of adapters some token requests.
@@ -194,13 +199,14 @@ int64_t gs_small_workspace_bytes(int32_t dtype, int64_t num_tokens, int32_t hidd
                                  int32_t num_adapters, int32_t max_rank, int32_t out_total,
                                  const int32_t* slice_bounds);
 int64_t gs_small_sync_bytes(void);
-/* Workgroups of one gs_switched_lora_small launch for this shape (producers +
- * consumers).  No counterpart in the reference: this library's path choice
- * uses it -- the one-launch kernel wins while its grid fits the GPU about
- * once, the segment kernels beyond (measured on decode-sized batches). */
+/* Workgroups of one gs_switched_lora_small launch for this shape and row split
+ * (producers + consumers; 0 for arguments outside the limits).  No
+ * counterpart in the reference: this library's path choice uses it -- the
+ * one-launch kernel wins while its grid fits the GPU about once, the segment
+ * kernels beyond. */
 int64_t gs_small_workgroups(int32_t dtype, int64_t num_tokens, int32_t hidden, int32_t num_slices,
                             int32_t num_adapters, int32_t max_rank, int32_t out_total,
-                            const int32_t* slice_bounds);
+                            const int32_t* slice_bounds, int32_t row_split);
 int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t* positions,
                            const int32_t* cu_seqlens, const int64_t* act_offsets, int32_t num_seqs,
                            const int32_t* eff_ids, const void* x, int64_t ldx, void* y, int64_t ldy,
@@ -208,7 +214,7 @@ int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t*
                            int32_t num_slices, const void* a_pack, const int64_t* a_off, const void* b_pack,
                            const int64_t* b_off, const int32_t* ranks, int32_t num_adapters, int32_t max_rank,
                            void* workspace, int64_t workspace_bytes, int32_t* sync, int64_t sync_bytes,
-                           int32_t speculate, void* stream);
+                           int32_t row_split, int32_t speculate, void* stream);
 
 /* ------------------------------------------------------------------------
  * Reference op: per-module tile bitmasks and kernel-local ids.

@@ -228,3 +228,89 @@ def test_small_back_to_back_calls(dev, speculate_tokens):
     _say(f"back-to-back graph T={T}")
     for y, y_e in zip(ys2, ys):
         assert torch.equal(y, y_e), "graph replay of chained calls differs from eager"
+
+
+def _small_call(y, md, pk, ids, row_split):
+    switched._call_small(md.x, y, pk, req=ids, row_split=row_split)
+
+
+@pytest.mark.parametrize("dtype,T,NA,ranks,slices,H,splits,seed", [
+    (torch.bfloat16, 1000, 3, [16, 64, 8], (256, 128), 1024, (2, 3, 8, 32), 61),   # ~330 tokens per adapter
+    (torch.float32, 512, 4, [8, 8, 8, 8], (2048,), 2048, (4, 16), 62),             # one adapter with 256 tokens
+    (torch.bfloat16, 1024, 64, [32] * 64, (256,), 512, (2, 32), 63),               # every limit at once
+])
+def test_small_row_split(dev, dtype, T, NA, ranks, slices, H, splits, seed):
+    """Row splits spread an adapter's 32-token chunks over more workgroups.
+    Every split matches the oracle, and row_split = 1 within one output ulp
+    (a larger split may use fewer k-chunks, so the fp32 partials are added in
+    another grouping)."""
+    spec = workloads.ModuleSpec("t", H, slices, ranks, max(ranks))
+    md = workloads.make_module(spec, T, NA, dtype, dev, seed=seed)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, ranks)
+    rng = np.random.default_rng(seed)
+    # long runs of one adapter, as sequences give them, plus base tokens
+    cuts = np.sort(rng.choice(np.arange(1, T), size=max(1, NA // 2), replace=False))
+    runs = np.split(np.arange(T), cuts)
+    ids = np.zeros(T, np.int64)
+    for run in runs:
+        ids[run] = rng.integers(1, NA + 1)
+    ids[rng.random(T) < 0.1] = 0
+    ids_d = torch.tensor(ids, device=dev)
+    y1 = md.y.clone()
+    _small_call(y1, md, pk, ids_d, 1)
+    torch.cuda.synchronize()
+    _check(md, y1, ids, dtype)
+    for rs in splits:
+        _say(f"row split {rs}: dtype={dtype} T={T} NA={NA} largest group {int(np.bincount(ids)[1:].max())}")
+        y = md.y.clone()
+        _small_call(y, md, pk, ids_d, rs)
+        torch.cuda.synchronize()
+        _check(md, y, ids, dtype)
+        d = (y.float() - y1.float()).abs()
+        ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -20
+        assert bool((d <= ulp * y1.float().abs().clamp_min(1.0)).all()), f"row_split={rs} vs row_split=1"
+
+
+def test_small_row_split_changes_between_calls(dev):
+    """Calls in a row on one stream with a different row split each (so a
+    different number of consumers shares each adapter's epoch weight), eager
+    and in one graph: every output matches the oracle."""
+    T, NA = 640, 5
+    spec = workloads.ModuleSpec("t", 1024, (256, 256), [16, 32, 8, 64, 24], 64)
+    md = workloads.make_module(spec, T, NA, torch.bfloat16, dev, seed=64)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, spec.ranks)
+    rng = np.random.default_rng(64)
+    ids = np.repeat(rng.integers(0, NA + 1, size=T // 64), 64)
+    ids_d = torch.tensor(ids, device=dev)
+    order = (1, 4, 2, 20, 3, 1, 8)
+    y = md.y.clone()
+    for rs in order:
+        prev = _np(y)
+        _small_call(y, md, pk, ids_d, rs)
+        torch.cuda.synchronize()
+        ref = olora.switched_lora_apply(prev, _np(md.x), ids, [_np(a) for a in md.lora_A_slices],
+                                        [_np(b) for b in md.lora_B_slices], spec.output_slices, spec.ranks, "bf16")
+        _close(_np(y), ref, 2e-2, f"chained call with row_split={rs}")
+    _say("row split chain eager")
+    y2 = md.y.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for rs in order:
+            _small_call(y2, md, pk, ids_d, rs)
+    y2.copy_(md.y)
+    g.replay()
+    torch.cuda.synchronize()
+    _say("row split chain graph")
+    assert torch.equal(y2, y), "graph replay of the chain differs from eager"
+
+
+def test_small_row_split_rejected_outside_limits(dev):
+    spec = workloads.ModuleSpec("t", 512, (256,), [16, 16], 16)
+    md = workloads.make_module(spec, 64, 2, torch.bfloat16, dev, seed=65)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, spec.ranks)
+    ids_d = torch.ones(64, dtype=torch.int64, device=dev)
+    for bad in (0, 33):
+        with pytest.raises(Exception, match="row_split"):
+            _small_call(md.y.clone(), md, pk, ids_d, bad)
+    assert switched.small_workgroups(pk, 64, 0) == 0
+    assert switched.small_workgroups(pk, 64, 2) > switched.small_workgroups(pk, 64, 1)
