@@ -45,6 +45,10 @@ __host__ __device__ inline int max_tiles_for(int64_t T, int NA) {
 // type; KS > 1 writes the fp32 partial of chunk ks to part[ks][slot][col].
 // ----------------------------------------------------------------------------
 constexpr int kTMS = 64;           // slots per shrink tile
+#ifndef GS_SHRINK_TARGET_WGS
+#define GS_SHRINK_TARGET_WGS 640
+#endif
+constexpr int kShrinkTargetWgs = GS_SHRINK_TARGET_WGS;   // workgroups the k-split aims for
 constexpr int kOutPad = 4;
 
 struct ShrinkParams {
@@ -88,8 +92,11 @@ __device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, f32x4 ac
   }
 }
 
+// NB <= 2 fits 3 workgroups per CU (<= 168 registers, no spills), so a grid
+// of ~640 runs in one round on 256 CUs; wider tiles would spill.
 template <bool BF16, int NB>
-__global__ __launch_bounds__(kThreads) void shrink_kernel(ShrinkParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NB <= 2 ? 3 : 1))) void shrink_kernel(
+    ShrinkParams p) {
   constexpr int P = Elt<BF16>::kPerPiece;        // elements per 16-byte piece
   constexpr int ES = Elt<BF16>::kSize;
   constexpr int KSTEP = 4 * P;                   // k of one piece over the 4 lane groups
@@ -547,7 +554,7 @@ static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, boo
   // spread over enough streaming; measured on the prefill and decoder-step
   // shapes
   const int64_t wgs = static_cast<int64_t>(pl.max_tiles) * pl.n_chunks;
-  int ks = static_cast<int>((640 + wgs / 2) / (wgs > 0 ? wgs : 1));
+  int ks = static_cast<int>((kShrinkTargetWgs + wgs / 2) / (wgs > 0 ? wgs : 1));
   if (ks < 1) ks = 1;
   if (ks > 16) ks = 16;
   if (ks > units) ks = units;

@@ -119,16 +119,19 @@ __global__ __launch_bounds__(kBuildThreads) void build_segments_kernel(BuildArgs
 
   // Pass 1: gate every token of the batch and count per adapter.  The ids and
   // positions of kPre chunks are loaded together (clamped, in bounds) before
-  // any is used.
+  // any is used.  Every workgroup reads the whole batch, at the rate one CU
+  // fetches from beyond its L2, so positions are read only when gating uses
+  // them.
   int mine = 0;                                   // this thread's token of the own chunk
   const int nchunks = (T + kBuildThreads - 1) / kBuildThreads;
+  const bool need_pos = a.pos != nullptr && a.act_off != nullptr;
   for (int k0 = 0; k0 < nchunks; k0 += kPre) {
     int64_t rq[kPre], ps[kPre];
 #pragma unroll
     for (int u = 0; u < kPre; ++u) {
       const int tc = min((k0 + u) * kBuildThreads + tid, T - 1);
       rq[u] = a.req[tc];
-      ps[u] = a.pos != nullptr ? a.pos[tc] : 0;
+      ps[u] = need_pos ? a.pos[tc] : 0;
     }
 #pragma unroll
     for (int u = 0; u < kPre; ++u) {
