@@ -67,8 +67,8 @@ def switched_lora_apply(y, x, ids, lora_A_slices, lora_B_slices, output_slices,
         idx = np.nonzero(ids == a)[0]
         xa = x[idx]
         for s in range(len(output_slices)):
-            A = np.asarray(lora_A_slices[s], dtype=np.float64)[a - 1, 0]
-            B = np.asarray(lora_B_slices[s], dtype=np.float64)[a - 1, 0]
+            A = np.asarray(lora_A_slices[s][a - 1, 0], dtype=np.float64)
+            B = np.asarray(lora_B_slices[s][a - 1, 0], dtype=np.float64)
             if ranks is not None:
                 r = int(ranks[a - 1])
                 A = A[:r]
