@@ -61,7 +61,10 @@ constexpr int kSmMaxTokens = 1024;           // largest batch of this path
 constexpr int kSmMaxAdapters = 64;           // adapters whose tables ride in the kernel arguments
 constexpr int kSmMaxRank = 64;               // largest (padded) rank of this path
 constexpr int kSmMaxU = kSmMaxTokens / kSmT; // tokens per thread in the routing pass (at most)
-constexpr int kKsGrp = 4;                    // split-K partials a consumer polls together
+#ifndef GS_SMALL_KS_GROUP
+#define GS_SMALL_KS_GROUP 4
+#endif
+constexpr int kKsGrp = GS_SMALL_KS_GROUP;     // split-K partials a consumer polls together
 constexpr int kErrTimeout = 1;               // error word bits
 constexpr int kSyncErrWord = 2;              // int32 index of the error word
 constexpr int kSyncLine = 32;                // int32 words per adapter (its 64-bit launch counter)
