@@ -356,6 +356,8 @@ def small_workgroups(packed: "PackedAdapters", num_tokens: int, row_split: int =
 def _small_plan(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None) -> tuple[bool, int]:
     """(prefer the small-batch kernel, its row split) for this module and batch."""
     T = int(num_tokens)
+    if packed.a_off_host is None or packed.b_off_host is None or not packed.ranks_host:
+        return (False, 1)                             # no host tables: the small kernel cannot run
     key = (_dev_key(packed.a_pack.device), packed.dtype, packed.hidden, packed.num_slices, packed.num_adapters,
            packed.max_rank, packed.out_total, tuple(packed.slice_bounds), T, num_seqs)
     plan = _small_plans.get(key)
@@ -374,11 +376,14 @@ def _small_plan(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None)
         per_wg = -(-chunks // rs)
         fits = small_workgroups(packed, T, rs) <= (8 if T <= 256 else 4) * cus
         plan = (fits and (per_wg <= 2 or (rs == 1 and chunks <= 3)), rs)
+    if len(_small_plans) >= _SMALL_PLAN_CAP:     # batch sizes vary per step: keep the cache bounded
+        _small_plans.clear()
     _small_plans[key] = plan
     return plan
 
 
 _small_plans: dict = {}
+_SMALL_PLAN_CAP = 4096
 
 
 def small_row_split(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None = None) -> int:

@@ -211,3 +211,40 @@ def test_workload_module_on_cpu():
     assert torch.all(md.lora_A_slices[0][0, 0, 8:] == 0) and torch.all(md.lora_B_slices[1][0, 0, :, 8:] == 0)
     # B is pre-scaled by alpha/r: std ~ 0.02 * 16/r
     assert md.lora_B_slices[0][1, 0].std().item() < 0.05
+
+
+def _packed_stub(H, slices, NA, max_rank, dtype=torch.bfloat16):
+    """The attributes the small-path plan reads, without device memory."""
+    from types import SimpleNamespace
+
+    bounds = [0]
+    for w in slices:
+        bounds.append(bounds[-1] + w)
+    return SimpleNamespace(dtype=dtype, hidden=H, num_slices=len(slices), num_adapters=NA, max_rank=max_rank,
+                           out_total=bounds[-1], slice_bounds=bounds, a_pack=SimpleNamespace(device=torch.device("cuda", 0)),
+                           a_off_host=[0] * (NA + 1), b_off_host=[0] * (NA + 1), ranks_host=[0] + [max_rank] * NA)
+
+
+@pytest.mark.parametrize("H,slices,NA,r,T,seqs,small,rs", [
+    (4096, (4096, 1024, 1024), 12, 32, 256, 256, True, 1),     # decode QKV: one chunk per adapter
+    (2048, (2048,), 4, 8, 512, 4, True, 4),                     # 4 sequences of 128 on 4 adapters
+    (4096, (4096,), 2, 64, 512, None, True, 8),                 # ~256 tokens per adapter
+    (4096, (12800, 12800), 24, 32, 128, None, False, 1),        # gate_up: grid past the GPU
+    (12800, (4096,), 12, 16, 1024, 8, True, 2),                 # 128-token groups: split 2 fits 3 WG/CU
+    (12800, (4096,), 12, 16, 1024, 4, False, 1),                # 256-token groups: 4 chunks per WG, segments
+    (4096, (4096,), 4, 128, 64, None, False, 1),                # rank past the small kernel's limit
+])
+def test_small_path_plan(monkeypatch, H, slices, NA, r, T, seqs, small, rs):
+    """The host's path choice and row split on a 256-CU part (the decisions
+    measured on the GPU for these shapes)."""
+    from granite_switch_amd import switched
+
+    monkeypatch.setattr(switched, "_device_cus", lambda device: 256)
+    monkeypatch.setattr(switched, "_small_plans", {})
+    pk = _packed_stub(H, slices, NA, r)
+    assert switched.small_preferred(pk, T, seqs) is small
+    if small:
+        assert switched.small_row_split(pk, T, seqs) == rs
+        assert switched.small_workgroups(pk, T, rs) <= 4 * 256
+    pk.a_off_host = None                                        # without host tables: never the small kernel
+    assert switched.small_preferred(pk, T, seqs) is False
