@@ -6,6 +6,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+
 #include "../../include/granite_switch_amd.h"
 
 namespace gs {
@@ -32,6 +34,21 @@ void set_error(const char* fmt, ...);
       return GS_ERR_HIP;                                                        \
     }                                                                           \
   } while (0)
+
+// Compute units of the current device, cached per device (one cache for the
+// whole library; concurrent first calls store the same value); 256 when no
+// device answers.
+inline int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

@@ -678,20 +678,6 @@ int prepare_expand(ExpandParams& p, const char* who, int32_t dtype, void* y, int
   return GS_OK;
 }
 
-// Compute units of the current device (cached per device; concurrent first
-// calls store the same value).
-int device_cus() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int n = cache[dev].load(std::memory_order_relaxed);
-  if (n == 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
-
 template <bool BF16, int NBW, int PRE>
 void launch_expand_t(int max_tiles, size_t lds, ExpandParams p, hipStream_t st) {
   auto kern = expand_kernel<BF16, NBW, PRE>;

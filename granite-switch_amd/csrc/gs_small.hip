@@ -315,6 +315,8 @@ struct FusedParams {
   SliceInfo si;
   const void* b_pack;
   int NNT;                // column tiles per adapter
+  int TG;                 // tiles per consumer (consecutive, inside one slice)
+  int NG;                 // consumer tile groups per adapter (NNT / TG)
   // hand-off
   int32_t* sync;
   int64_t timeout_ticks;
@@ -510,90 +512,92 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
 // MFMA deltas go through LDS in 128-column halves, and each thread adds and
 // stores 16-byte pieces of its token rows.
 // ----------------------------------------------------------------------------
-template <bool BF16, int NQ, bool SPEC, int U>
+// RMAX: the module's largest rank rounded up to 32 or 64 (lora_B pieces held
+// per column block); tile groups (TG > 1) are compiled for bf16 at RMAX = 32
+// only, where the next tile's lora_B and y fit beside the current tile's.
+template <bool BF16, int NQ, bool SPEC, int U, int RMAX>
 __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>& L, int cid) {
   constexpr int NT = 64 * NQ;
   constexpr int NH = NQ / 2;            // 128-column halves
   constexpr int P = Elt<BF16>::kPerPiece;
   constexpr int ES = Elt<BF16>::kSize;
   constexpr int KSTEP = 4 * P;          // rank per MFMA (over the 4 lane groups)
-  constexpr int KG = kSmMaxRank / KSTEP;
+  constexpr int KG = RMAX / KSTEP;
   constexpr int EPL = 16 / ES;          // y elements per 16-byte piece
   constexpr int LPR = kHalf / EPL;      // lanes per y row in a half
   constexpr int RPP = kSmT / LPR;       // y rows per workgroup-wide access
   constexpr int PASSES = 32 / RPP;
   constexpr int EPT = 4;                // shrink elements per thread and batch
   constexpr int NEB = 32 * kSmMaxRank / (kSmT * EPT);   // batches (rank <= 64)
+  constexpr bool kTileGroups = BF16 && RMAX == 32;       // the next tile's lora_B and y fit beside the current's
 
-  // (tile, adapter) items are dealt to the XCDs by the low 3 id bits; the RS
-  // row-split siblings of an item, which read the same lora_B rows, get ids 8
-  // apart and share an XCD's L2.  Ids past the last item have no work.
+  // (tile group, adapter) items are dealt to the XCDs by the low 3 id bits;
+  // the RS row-split siblings of an item, which read the same lora_B rows, get
+  // ids 8 apart and share an XCD's L2.  Ids past the last item have no work.
   const int item = ((cid >> 3) / p.RS) * 8 + (cid & 7);
   const int rs = (cid >> 3) % p.RS;
-  if (item >= p.NNT * p.rt.NA) return;
-  const int nt = item % p.NNT;
-  const int g = item / p.NNT + 1;
+  if (item >= p.NG * p.rt.NA) return;
+  const int grp = item % p.NG;
+  const int g = item / p.NG + 1;
+  const int nt0 = grp * p.TG;            // the group's first tile (all of its tiles lie in one slice)
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int l = tid & 63;
   const int i16 = l & 15;
   const int q4 = l >> 4;
   const int r = p.tab.rank[g];
-  const int n_tile0 = nt * NT;
-  const int s = tile_slice<NT>(p.si, nt);
+  const int s = tile_slice<NT>(p.si, nt0);
   const int zc0 = s * r;                 // this slice's columns in the adapter's shrink row
 
   const uint64_t counter = read_counter(p, g);   // one 8-byte request per wave
   RouteRegs<U> rr;
   route_issue<U>(p.rt, rr);
-  // lora_B rows of this wave's column blocks (n < out_total always; rank 0
-  // reads element 0 of the pack and is masked)
-  u32x4 bv[NQ][KG];
-  const char* brow[NQ];
+  // lora_B rows of this wave's column blocks of tile nt (n < out_total always;
+  // rank 0 reads element 0 of the pack and is masked).  Pieces past the rank
+  // read the row's first piece and are not masked: the MFMAs multiply them by
+  // shrink values that are zeroed there, so no instruction waits on these
+  // loads before later loads go out.
+  auto load_b = [&](int nt, u32x4 (&bv)[NQ][KG]) {
 #pragma unroll
-  for (int q = 0; q < NQ; ++q) {
-    const int n = n_tile0 + 16 * (q * 4 + wave) + i16;
-    brow[q] = static_cast<const char*>(p.b_pack) + (p.tab.b_off[g] + static_cast<int64_t>(n) * r) * ES;
-  }
-  if constexpr (SPEC) {
-    // lora_B in the first memory trip, while the producers wait for their
-    // token lists: unconditional loads from clamped addresses.  Pieces past
-    // the rank read the row's first piece and are not masked: the MFMAs
-    // multiply them by shrink values that are zeroed there, so no
-    // instruction waits on these loads before the y loads go out.
-#pragma unroll
-    for (int q = 0; q < NQ; ++q)
+    for (int q = 0; q < NQ; ++q) {
+      const int n = nt * NT + 16 * (q * 4 + wave) + i16;
+      const char* brow = static_cast<const char*>(p.b_pack) + (p.tab.b_off[g] + static_cast<int64_t>(n) * r) * ES;
 #pragma unroll
       for (int kg = 0; kg < KG; ++kg) {
         const int k0 = kg * KSTEP + q4 * P;
-        bv[q][kg] = ld16(brow[q] + (k0 < r ? k0 : 0) * ES);
+        bv[q][kg] = ld16(brow + (k0 < r ? k0 : 0) * ES);
       }
-  }
+    }
+  };
+  u32x4 bv[NQ][KG];
+  // SPEC: tile nt0's lora_B in the first memory trip, while the producers
+  // wait for their token lists
+  if constexpr (SPEC) load_b(nt0, bv);
   const bool requested = route_gate<U>(p.rt, g, L.rt, rr);
   if (tid == 0) L.epoch = static_cast<uint32_t>(counter >> kEpochShift);   // visible after route_list's barriers
   if constexpr (!SPEC) {
 #pragma unroll
     for (int q = 0; q < NQ; ++q)
 #pragma unroll
-      for (int kg = 0; kg < KG; ++kg) {
-        const int k0 = kg * KSTEP + q4 * P;
-        bv[q][kg] = u32x4{0u, 0u, 0u, 0u};
-        if (requested && k0 < r) bv[q][kg] = ld16(brow[q] + k0 * ES);
-      }
+      for (int kg = 0; kg < KG; ++kg) bv[q][kg] = u32x4{0u, 0u, 0u, 0u};
+    if (requested) load_b(nt0, bv);
   }
   const int n_g = route_list<U>(g, L.rt, rr);
   if (r == 0 || n_g == 0) return;       // no producer wrote partials for it
   const uint32_t want = L.epoch + 1u;
   const uint64_t* part = p.part + static_cast<int64_t>(g - 1) * p.region;
   const int64_t kstride = static_cast<int64_t>(p.cap) * p.zw;
-  // this consumer's share of the 2^20 that g's NNT * RS consumers add per launch
-  const int ncons = p.NNT * p.RS;
-  const int cidx = rs * p.NNT + nt;
+  // this consumer's share of the 2^20 that g's NG * RS consumers add per launch
+  const int ncons = p.NG * p.RS;
+  const int cidx = rs * p.NG + grp;
   const uint64_t weight = (uint64_t{1} << kEpochShift) / ncons + (cidx < (1 << kEpochShift) % ncons ? 1 : 0);
   const int cx = (tid % LPR) * EPL;
 
   for (int rt0 = 32 * rs; rt0 < n_g; rt0 += 32 * p.RS) {
-    // y pieces of this row chunk (issued before the wait)
+    // tile nt0's lora_B again for a later row chunk when other tiles of the
+    // group have used the registers since
+    if (p.TG > 1 && rt0 != 32 * rs) load_b(nt0, bv);
+    // y pieces of tile nt0 for this row chunk (issued before the wait)
     u32x4 yv[NH][PASSES];
     int64_t yoff[PASSES];
     bool rok[PASSES];
@@ -603,7 +607,7 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
     for (int ps = 0; ps < PASSES; ++ps) {
       const int row = rt0 + ps * RPP + tid / LPR;
       rok[ps] = row < n_g;
-      yoff[ps] = static_cast<int64_t>(L.rt.tok[rok[ps] ? row : rt0]) * p.ldy + n_tile0 + cx;
+      yoff[ps] = static_cast<int64_t>(L.rt.tok[rok[ps] ? row : rt0]) * p.ldy + nt0 * NT + cx;
 #pragma unroll
       for (int hf = 0; hf < NH; ++hf) yv[hf][ps] = ld16(static_cast<const char*>(p.y) + (yoff[ps] + hf * kHalf) * ES);
     }
@@ -669,58 +673,92 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
     }
     lds_barrier();
 
-    // D[t][n] = sum_k z[t][k] B[n][k]; acc[rt][q]: token 16*rt + 4*q4 + e of
-    // the chunk, column n_tile0 + 16*(q*4 + wave) + i16
-    f32x4 acc[2][NQ];
+    // One tile of the group: D[t][n] = sum_k z[t][k] B[n][k] (acc[rt][q]: token
+    // 16*rt + 4*q4 + e of the chunk, column 16*(q*4 + wave) + i16 of the tile),
+    // through LDS in 128-column halves, added to the tile's y pieces and stored.
+    // Every y piece is combined with its delta before the tile's first store:
+    // on gfx9 stores count in the same in-order counter as loads.
+    auto tile_out = [&](const u32x4 (&b)[NQ][KG], const u32x4 (&yin)[NH][PASSES], int col) {
+      f32x4 acc[2][NQ];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+      for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) acc[rt][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < NQ; ++q) acc[rt][q] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kg = 0; kg < KG; ++kg) {
-      if (kg * KSTEP < r) {
-        const int k0 = kg * KSTEP + q4 * P;
+      for (int kg = 0; kg < KG; ++kg) {
+        if (kg * KSTEP < r) {
+          const int k0 = kg * KSTEP + q4 * P;
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-          const bool kin = k0 < r;
-          const u32x4 za =
-              sel16(kin, *reinterpret_cast<const u32x4*>(L.u.co.zs + ((16 * rt + i16) * kZld + (kin ? k0 : 0)) * ES));
+          for (int rt = 0; rt < 2; ++rt) {
+            const bool kin = k0 < r;
+            const u32x4 za =
+                sel16(kin, *reinterpret_cast<const u32x4*>(L.u.co.zs + ((16 * rt + i16) * kZld + (kin ? k0 : 0)) * ES));
 #pragma unroll
-          for (int q = 0; q < NQ; ++q) acc[rt][q] = mfma16<BF16>(za, bv[q][kg], acc[rt][q]);
+            for (int q = 0; q < NQ; ++q) acc[rt][q] = mfma16<BF16>(za, b[q][kg], acc[rt][q]);
+          }
         }
       }
-    }
-    // every y piece is combined with its delta before the first store: on
-    // gfx9 stores count in the same in-order counter as loads, so a wait for a
-    // y load issued after a store would also wait for that store
-    u32x4 yo[NH][PASSES];
+      u32x4 yo[NH][PASSES];
 #pragma unroll
-    for (int hf = 0; hf < NH; ++hf) {
+      for (int hf = 0; hf < NH; ++hf) {
 #pragma unroll
-      for (int qq = 0; qq < 2; ++qq) {
-        const int q = 2 * hf + qq;
-        const int col = 16 * (qq * 4 + wave) + i16;      // within the half
+        for (int qq = 0; qq < 2; ++qq) {
+          const int q = 2 * hf + qq;
+          const int cc = 16 * (qq * 4 + wave) + i16;      // within the half
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
+          for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) L.u.co.dtile[16 * rt + 4 * q4 + e][col] = acc[rt][q][e];
+            for (int e = 0; e < 4; ++e) L.u.co.dtile[16 * rt + 4 * q4 + e][cc] = acc[rt][q][e];
+        }
+        lds_barrier();
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+          const int row = ps * RPP + tid / LPR;
+          float d[EPL];
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) d[e] = L.u.co.dtile[row][cx + e];
+          yo[hf][ps] = add_y16<BF16>(yin[hf][ps], d);
+        }
+        lds_barrier();   // dtile is reused
       }
-      lds_barrier();
 #pragma unroll
-      for (int ps = 0; ps < PASSES; ++ps) {
-        const int row = ps * RPP + tid / LPR;
-        float d[EPL];
+      for (int hf = 0; hf < NH; ++hf)
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) d[e] = L.u.co.dtile[row][cx + e];
-        yo[hf][ps] = add_y16<BF16>(yv[hf][ps], d);
+        for (int ps = 0; ps < PASSES; ++ps)
+          if (rok[ps]) st16(static_cast<char*>(p.y) + (yoff[ps] + col + hf * kHalf) * ES, yo[hf][ps]);
+    };
+
+    if (!kTileGroups || p.TG == 1) {
+      tile_out(bv, yv, 0);
+    } else if constexpr (kTileGroups) {
+      // tiles 1.. of the group: the next tile's lora_B and y go out before the
+      // current tile is computed
+      u32x4 bn[NQ][KG], yn[NH][PASSES];
+      auto load_y = [&](int t, u32x4 (&yt)[NH][PASSES]) {
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps)
+#pragma unroll
+          for (int hf = 0; hf < NH; ++hf)
+            yt[hf][ps] = ld16(static_cast<const char*>(p.y) + (yoff[ps] + t * NT + hf * kHalf) * ES);
+      };
+      load_b(nt0 + 1, bn);
+      load_y(1, yn);
+      tile_out(bv, yv, 0);
+      for (int t = 1; t < p.TG; ++t) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+#pragma unroll
+          for (int kg = 0; kg < KG; ++kg) bv[q][kg] = bn[q][kg];
+#pragma unroll
+        for (int hf = 0; hf < NH; ++hf)
+#pragma unroll
+          for (int ps = 0; ps < PASSES; ++ps) yv[hf][ps] = yn[hf][ps];
+        const int tn = t + 1 < p.TG ? t + 1 : t;      // the last tile re-reads itself (no extra line)
+        load_b(nt0 + tn, bn);
+        load_y(tn, yn);
+        tile_out(bv, yv, t * NT);
       }
-      lds_barrier();   // dtile / zs are reused
     }
-#pragma unroll
-    for (int hf = 0; hf < NH; ++hf)
-#pragma unroll
-      for (int ps = 0; ps < PASSES; ++ps)
-        if (rok[ps]) st16(static_cast<char*>(p.y) + (yoff[ps] + hf * kHalf) * ES, yo[hf][ps]);
   }
   // every thread has had all its partials (barriers since): add this
   // consumer's weight; issued last and never waited for, since on gfx9 a
@@ -729,19 +767,19 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
     __hip_atomic_fetch_add(launch_counter(p, g), weight, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <bool BF16, int NPW, int NQ, bool SPEC, int U>
+template <bool BF16, int NPW, int NQ, bool SPEC, int U, int RMAX>
 __global__ __launch_bounds__(kSmT) void small_fused_kernel(FusedParams p) {
   __shared__ FusedLds<BF16, U> lds;
   const int bid = static_cast<int>(blockIdx.x);
   if (bid < p.NP) produce<BF16, NPW, 64 * NQ, SPEC, U>(p, lds, bid);
-  else consume<BF16, NQ, SPEC, U>(p, lds, bid - p.NP);
+  else consume<BF16, NQ, SPEC, U, RMAX>(p, lds, bid - p.NP);
 }
 
 // ----------------------------------------------------------------------------
 // Host-side plan.
 // ----------------------------------------------------------------------------
 struct SmallPlan {
-  int NPW, KS, NCB, cap, zw, NQ, NNT;
+  int NPW, KS, NCB, cap, zw, NQ, NNT, TG;
   int64_t region_bytes;       // one adapter's tagged partials
 };
 
@@ -751,6 +789,10 @@ struct SmallPlan {
 #define GS_SMALL_TARGET_PRODUCERS 128
 #endif
 constexpr int kSmTargetShrinkWgs = GS_SMALL_TARGET_PRODUCERS;
+#ifndef GS_SMALL_TILE_GROUP
+#define GS_SMALL_TILE_GROUP 8
+#endif
+constexpr int kSmTileGroup = GS_SMALL_TILE_GROUP;      // most column tiles one consumer walks
 constexpr int64_t kDefaultTimeoutTicks = 2000000;   // 20 ms of the 100 MHz wall clock
 constexpr int64_t kSyncBytes = 4 * kSyncLine * (kSmMaxAdapters + 1);
 
@@ -780,6 +822,23 @@ SmallPlan plan_small(int64_t T, int H, int S, int NA, int max_rank, bool bf16, i
     if ((slice_bounds[s + 1] - slice_bounds[s]) % 256 != 0) all256 = false;
   pl.NQ = all256 ? 4 : 2;
   pl.NNT = out_total / (64 * pl.NQ);
+  // Tiles per consumer: the smallest group (a divisor of every slice's tile
+  // count, so it never straddles a slice) that brings the consumers within 2
+  // per CU, else the largest allowed.  Each consumer polls its partials once
+  // and walks its tiles, so long groups serialise: measured on decode batches
+  // (gate_up 4096 -> 25600, 24 adapters, T = 128: no groups 30.6 us, groups
+  // of 5 18.1, of 10 20.3; groups of 16 on a 4096-wide down projection were
+  // 1.5x slower than none).
+  const int64_t limit = 2 * static_cast<int64_t>(device_cus());
+  pl.TG = 1;
+  for (int d = 1; d <= (bf16 && max_rank <= 32 ? kSmTileGroup : 1); ++d) {
+    bool ok = true;
+    for (int s = 0; s < S; ++s)
+      if (((slice_bounds[s + 1] - slice_bounds[s]) / (64 * pl.NQ)) % d != 0) ok = false;
+    if (!ok) continue;
+    pl.TG = d;
+    if (8 * static_cast<int64_t>(RS) * ((static_cast<int64_t>(pl.NNT / d) * NA + 7) / 8) <= limit) break;
+  }
   pl.region_bytes = static_cast<int64_t>(pl.KS) * pl.cap * pl.zw * 8;
   return pl;
 }
@@ -790,15 +849,21 @@ int64_t producer_wgs(const SmallPlan& pl, int NA, int RS) {
   return 8 * static_cast<int64_t>(pl.NCB) * RS * ((static_cast<int64_t>(pl.KS) * NA + 7) / 8);
 }
 int64_t consumer_wgs(const SmallPlan& pl, int NA, int RS) {
-  return 8 * static_cast<int64_t>(RS) * ((static_cast<int64_t>(pl.NNT) * NA + 7) / 8);
+  return 8 * static_cast<int64_t>(RS) * ((static_cast<int64_t>(pl.NNT / pl.TG) * NA + 7) / 8);
+}
+
+template <bool BF16, int NQ, bool SPEC, int U, int RMAX>
+void launch_fused_r(const SmallPlan& pl, const FusedParams& fp, unsigned grid, hipStream_t st) {
+  switch (pl.NPW) {
+    case 8: hipLaunchKernelGGL((small_fused_kernel<BF16, 8, NQ, SPEC, U, RMAX>), dim3(grid), dim3(kSmT), 0, st, fp); break;
+    default: hipLaunchKernelGGL((small_fused_kernel<BF16, 4, NQ, SPEC, U, RMAX>), dim3(grid), dim3(kSmT), 0, st, fp); break;
+  }
 }
 
 template <bool BF16, int NQ, bool SPEC, int U>
 void launch_fused_nq(const SmallPlan& pl, const FusedParams& fp, unsigned grid, hipStream_t st) {
-  switch (pl.NPW) {
-    case 8: hipLaunchKernelGGL((small_fused_kernel<BF16, 8, NQ, SPEC, U>), dim3(grid), dim3(kSmT), 0, st, fp); break;
-    default: hipLaunchKernelGGL((small_fused_kernel<BF16, 4, NQ, SPEC, U>), dim3(grid), dim3(kSmT), 0, st, fp); break;
-  }
+  if (pl.zw <= 32 * fp.S) launch_fused_r<BF16, NQ, SPEC, U, 32>(pl, fp, grid, st);
+  else launch_fused_r<BF16, NQ, SPEC, U, 64>(pl, fp, grid, st);
 }
 
 template <bool BF16, bool SPEC, int U>
@@ -937,6 +1002,8 @@ int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t*
   for (int s = 0; s <= num_slices; ++s) fp.si.bounds[s] = slice_bounds[s];
   fp.b_pack = b_pack;
   fp.NNT = pl.NNT;
+  fp.TG = pl.TG;
+  fp.NG = pl.NNT / pl.TG;
   fp.sync = sync;
   fp.timeout_ticks = kDefaultTimeoutTicks;
   hipStream_t st = static_cast<hipStream_t>(stream);

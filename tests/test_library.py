@@ -229,7 +229,8 @@ def _packed_stub(H, slices, NA, max_rank, dtype=torch.bfloat16):
     (4096, (4096, 1024, 1024), 12, 32, 256, 256, True, 1),     # decode QKV: one chunk per adapter
     (2048, (2048,), 4, 8, 512, 4, True, 4),                     # 4 sequences of 128 on 4 adapters
     (4096, (4096,), 2, 64, 512, None, True, 8),                 # ~256 tokens per adapter
-    (4096, (12800, 12800), 24, 32, 128, None, False, 1),        # gate_up: grid past the GPU
+    (4096, (12800, 12800), 24, 32, 128, None, True, 1),         # gate_up: tile groups of 5 bring the grid to 672
+    (4096, (12800, 12800), 24, 64, 512, None, False, 1),        # rank 64 (no tile groups): grid past the GPU
     (12800, (4096,), 12, 16, 1024, 8, True, 2),                 # 128-token groups: split 2 fits 3 WG/CU
     (12800, (4096,), 12, 16, 1024, 4, False, 1),                # 256-token groups: 4 chunks per WG, segments
     (4096, (4096,), 4, 128, 64, None, False, 1),                # rank past the small kernel's limit
