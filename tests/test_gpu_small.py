@@ -314,3 +314,29 @@ def test_small_row_split_rejected_outside_limits(dev):
             _small_call(md.y.clone(), md, pk, ids_d, bad)
     assert switched.small_workgroups(pk, 64, 0) == 0
     assert switched.small_workgroups(pk, 64, 2) > switched.small_workgroups(pk, 64, 1)
+
+
+@pytest.mark.parametrize("row_split", [1, 2, 4])
+def test_small_tile_groups(dev, row_split):
+    """Consumers that walk several column tiles (64 adapters x 20 tiles puts
+    them past 2 per CU, so the library groups 5 tiles each), with long runs of
+    one adapter (several 32-token chunks per consumer, so the first tile's
+    lora_B is reloaded) and row splits: oracle and the segment path agree."""
+    T, NA = 1024, 64
+    spec = workloads.ModuleSpec("t", 1024, (2560, 2560), [32] * NA, 32)
+    md = workloads.make_module(spec, T, NA, torch.bfloat16, dev, seed=70 + row_split)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, spec.ranks)
+    rng = np.random.default_rng(70)
+    ids = np.repeat(rng.integers(0, NA + 1, size=T // 128), 128)   # 8 runs of 128 tokens
+    ids[rng.random(T) < 0.05] = 0
+    ids_d = torch.tensor(ids, device=dev)
+    assert switched.small_workgroups(pk, T, row_split) < 8 * row_split * ((20 * NA + 7) // 8), "tile groups in use"
+    _say(f"tile groups: row split {row_split}, grid {switched.small_workgroups(pk, T, row_split)}")
+    y = md.y.clone()
+    switched._call_small(md.x, y, pk, req=ids_d, row_split=row_split)
+    y_seg = md.y.clone()
+    switched.switched_lora_routed_(y_seg, md.x, ids_d, pk, path="segments")
+    torch.cuda.synchronize()
+    _check(md, y, ids, torch.bfloat16)
+    d = (y.float() - y_seg.float()).abs()
+    assert bool((d <= 2.0 ** -7 * y_seg.float().abs().clamp_min(1.0)).all()), "small path vs segment path"
