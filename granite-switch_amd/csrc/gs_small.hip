@@ -1004,6 +1004,9 @@ int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t*
   fp.NNT = pl.NNT;
   fp.TG = pl.TG;
   fp.NG = pl.NNT / pl.TG;
+  // tile groups exist only in the bf16, rank <= 32 instantiation (kTileGroups)
+  GS_CHECK_ARG(pl.TG == 1 || (bf16 && max_rank <= 32 && pl.NNT % pl.TG == 0), "%s: tile group %d for this module",
+               who, pl.TG);
   fp.sync = sync;
   fp.timeout_ticks = kDefaultTimeoutTicks;
   hipStream_t st = static_cast<hipStream_t>(stream);
