@@ -255,3 +255,30 @@ def test_graph_capture_replays(dev):
         torch.cuda.synchronize()
         _say(f"graph replay {rep}")
         assert torch.equal(y, y_eager), f"replay {rep} differs from eager"
+
+
+@pytest.mark.parametrize("path", ["small", "segments"])
+def test_slice_independence(dev, path):
+    """LoRA weights on slice 0 only (reference tests/hf/test_lora.py:133-168):
+    slice 0 changes, slices 1+ come back bit-identical, on both kernel paths."""
+    T, NA = 96, 3
+    spec = workloads.ModuleSpec("t", 512, (256, 128, 128), [16, 32, 8], 32)
+    md = workloads.make_module(spec, T, NA, torch.bfloat16, dev, seed=81)
+    for s in (1, 2):
+        md.lora_A_slices[s].zero_()
+        md.lora_B_slices[s].zero_()
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, spec.ranks)
+    ids = torch.ones(T, dtype=torch.int64, device=dev)
+    ids[::3] = 2
+    y = md.y.clone()
+    switched.switched_lora_routed_(y, md.x, ids, pk, path=path)
+    torch.cuda.synchronize()
+    print(f"slice independence path={path}", flush=True)
+    assert not torch.equal(y[:, :256], md.y[:, :256]), "slice 0 should carry the delta"
+    assert torch.equal(y[:, 256:], md.y[:, 256:]), "slices 1+ must stay bit-identical"
+    ref = olora.switched_lora_apply(md.y.float().cpu().numpy(), md.x.float().cpu().numpy(), ids.cpu().numpy(),
+                                    [a.float().cpu().numpy() for a in md.lora_A_slices],
+                                    [b.float().cpu().numpy() for b in md.lora_B_slices], spec.output_slices,
+                                    spec.ranks, "bf16")
+    got = y.float().cpu().numpy()
+    assert np.all(np.abs(got - ref) <= 2e-2 + 2e-2 * np.abs(ref))
