@@ -258,8 +258,9 @@ def path_choice() -> None:
     (chunked-prefill mixes), and the 4-sequence aLoRA batch of the 2048-wide
     CPU-sized workload.  Each timing is one graph replay over rotating buffer
     sets (~250 MB, so weights come from HBM), divided by the calls.  "auto" is
-    the path that switched.small_preferred picks; the one-launch kernel runs
-    with the row split switched.small_row_split picks."""
+    the path that switched.small_preferred picks (also with the batch's
+    largest adapter group passed as a hint); the one-launch kernel runs with
+    the row split switched.small_row_split picks."""
     import numpy as np
     import torch
 
@@ -340,10 +341,12 @@ def path_choice() -> None:
         nseq = None if cu is None else cu.numel() - 1
         largest = int(np.bincount(ids.numpy(), minlength=NA + 1)[1:].max())
         auto = "small" if switched.small_preferred(sets[0][1], T, nseq) else "segments"
+        auto_hint = "small" if switched.small_preferred(sets[0][1], T, nseq, largest) else "segments"
         rs = switched.small_row_split(sets[0][1], T, nseq)
         rows.append({"projection": spec.name, "hidden": H, "output_slices": list(sl), "adapters": NA,
                      "ranks": sorted(set(spec.ranks)), "tokens": T, "sequences": nseq, "largest_group": largest,
-                     "row_split": rs, "small_us": res["small"], "segments_us": res["segments"], "auto": auto})
+                     "row_split": rs, "small_us": res["small"], "segments_us": res["segments"], "auto": auto,
+                     "auto_with_largest_group": auto_hint})
         log(f"{spec.name} H={H} NA={NA} T={T} seqs={nseq} largest={largest} rs={rs}: small {res['small']:.2f} us, "
             f"segments {res['segments']:.2f} us, auto {auto}")
         del sets

@@ -353,13 +353,14 @@ def small_workgroups(packed: "PackedAdapters", num_tokens: int, row_split: int =
                                                packed.out_total, _i32_array(packed.slice_bounds), int(row_split)))
 
 
-def _small_plan(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None) -> tuple[bool, int]:
+def _small_plan(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None,
+                largest_group: int | None = None) -> tuple[bool, int]:
     """(prefer the small-batch kernel, its row split) for this module and batch."""
     T = int(num_tokens)
     if packed.a_off_host is None or packed.b_off_host is None or not packed.ranks_host:
         return (False, 1)                             # no host tables: the small kernel cannot run
     key = (_dev_key(packed.a_pack.device), packed.dtype, packed.hidden, packed.num_slices, packed.num_adapters,
-           packed.max_rank, packed.out_total, tuple(packed.slice_bounds), T, num_seqs)
+           packed.max_rank, packed.out_total, tuple(packed.slice_bounds), T, num_seqs, largest_group)
     plan = _small_plans.get(key)
     if plan is not None:
         return plan
@@ -367,7 +368,7 @@ def _small_plan(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None)
         plan = (False, 1)
     else:
         spread = packed.num_adapters if not num_seqs else min(packed.num_adapters, num_seqs)
-        largest = (T + spread - 1) // spread
+        largest = (T + spread - 1) // spread if largest_group is None else max(1, min(int(largest_group), T))
         chunks = (largest + 31) // 32                   # 32-token chunks in the estimated largest group
         cus = _device_cus(packed.a_pack.device)
         rs = 1
@@ -386,12 +387,14 @@ _small_plans: dict = {}
 _SMALL_PLAN_CAP = 4096
 
 
-def small_row_split(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None = None) -> int:
+def small_row_split(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None = None,
+                    largest_group: int | None = None) -> int:
     """Row split of the small-batch kernel for this batch (see ``small_preferred``)."""
-    return _small_plan(packed, num_tokens, num_seqs)[1]
+    return _small_plan(packed, num_tokens, num_seqs, largest_group)[1]
 
 
-def small_preferred(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None = None) -> bool:
+def small_preferred(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None = None,
+                    largest_group: int | None = None) -> bool:
     """The ``auto`` path choice between the one-launch small-batch kernel and
     the segment kernels (build + shrink + expand), and with it the kernel's
     row split.
@@ -402,7 +405,10 @@ def small_preferred(packed: "PackedAdapters", num_tokens: int, num_seqs: int | N
     see the groups without a synchronisation, so it estimates the largest one
     as ``T / min(adapters, sequences)`` (a sequence's tokens mostly share an
     adapter; ``num_seqs`` is the number of sequences when the caller knows
-    them, ``None`` estimates ``T / adapters``).  The row split doubles while
+    them, ``None`` estimates ``T / adapters``).  A caller that knows the
+    largest group (a serving scheduler assigns adapters per request on the
+    host) passes it as ``largest_group`` and the estimate is not used.  The
+    row split doubles while
     it is below the estimate's chunk count and the grid stays within 3
     workgroups per CU (the kernel holds 2 per CU at a time); the one-launch
     kernel is taken when it is eligible, its grid is within 4 workgroups per
@@ -417,7 +423,7 @@ def small_preferred(packed: "PackedAdapters", num_tokens: int, num_seqs: int | N
     aLoRA batch from 34.6 us (no split) to 14.3 us, against 17.8 us for the
     segment kernels.
     """
-    return _small_plan(packed, num_tokens, num_seqs)[0]
+    return _small_plan(packed, num_tokens, num_seqs, largest_group)[0]
 
 
 def reserve_workspace(device: torch.device, nbytes: int) -> None:
@@ -586,14 +592,17 @@ def _call_small(x2, y2, packed, eff_ids=None, req=None, pos=None, cu=None, off=N
 
 
 def switched_lora_routed_(y: torch.Tensor, x: torch.Tensor, adapter_ids: torch.Tensor, packed: PackedAdapters,
-                          positions=None, cu_seqlens=None, act_offsets=None, path: str = "auto") -> torch.Tensor:
+                          positions=None, cu_seqlens=None, act_offsets=None, path: str = "auto",
+                          largest_group: int | None = None) -> torch.Tensor:
     """In place: y += switched-LoRA delta of x, routed straight from the per-token ids.
 
     ``adapter_ids`` / ``positions`` / ``cu_seqlens`` / ``act_offsets`` have the
     meaning of ``build_segments``.  ``path="auto"``: decode-sized batches
     (``small_preferred``) run in one launch that gates and groups the tokens
     itself; larger ones build segments first and run ``switched_lora_``.
-    ``"small"`` / ``"segments"`` force one of the two.
+    ``"small"`` / ``"segments"`` force one of the two.  ``largest_group``
+    (optional): the most tokens any one adapter has in the batch, when the
+    caller knows it on the host; it replaces the path choice's estimate.
     """
     if path not in ("auto", "small", "segments"):
         raise ValueError(f"unknown path {path!r}")
@@ -611,19 +620,20 @@ def switched_lora_routed_(y: torch.Tensor, x: torch.Tensor, adapter_ids: torch.T
     num_seqs = 1 if cu is None else cu.numel() - 1
     if off is not None and off.numel() != num_seqs:
         raise ValueError("act_offsets must have one entry per sequence")
-    if path == "small" or (path == "auto" and small_preferred(packed, T, num_seqs if cu is not None else None)):
+    nseq_hint = num_seqs if cu is not None else None
+    if path == "small" or (path == "auto" and small_preferred(packed, T, nseq_hint, largest_group)):
         if not small_eligible(packed, T, num_seqs):
             raise ValueError("this module / batch is outside the small-batch kernel's limits")
         _call_small(x2, y2, packed, req=ids, pos=pos, cu=cu if off is not None else None, off=off,
                     num_seqs=num_seqs if off is not None else 1,
-                    row_split=small_row_split(packed, T, num_seqs if cu is not None else None))
+                    row_split=small_row_split(packed, T, nseq_hint, largest_group))
         return y
     segs = build_segments(ids, packed.num_adapters, pos, cu, off)
     return switched_lora_(y, x, segs, packed, path="segments")
 
 
 def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed: PackedAdapters,
-                   z: torch.Tensor | None = None, path: str = "auto") -> torch.Tensor:
+                   z: torch.Tensor | None = None, path: str = "auto", largest_group: int | None = None) -> torch.Tensor:
     """In place: y += switched-LoRA delta of x.
 
     ``path="auto"``: decode-sized batches (``small_preferred``) take the
@@ -632,7 +642,8 @@ def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed:
     ``"small"`` / ``"segments"`` force one of the two.  On the segment path ``z`` is optional scratch
     [T, S*max_rank] of y's dtype (allocated when omitted) -- when the shrink
     is split over the hidden dimension the expand reads the fp32 partials from
-    the workspace and z is not written.
+    the workspace and z is not written.  ``largest_group`` as for
+    ``switched_lora_routed_``.
     """
     if path not in ("auto", "small", "segments"):
         raise ValueError(f"unknown path {path!r}")
@@ -641,8 +652,8 @@ def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed:
     if T != segments.num_tokens:
         raise ValueError("x / y shapes do not match the segments")
     _check_segments(segments, packed)
-    if path == "small" or (path == "auto" and T and small_preferred(packed, T)):
-        _call_small(x2, y2, packed, eff_ids=segments.eff_ids, row_split=small_row_split(packed, T))
+    if path == "small" or (path == "auto" and T and small_preferred(packed, T, None, largest_group)):
+        _call_small(x2, y2, packed, eff_ids=segments.eff_ids, row_split=small_row_split(packed, T, None, largest_group))
         return y
     zw = packed.num_slices * packed.max_rank
     if z is None:

@@ -249,3 +249,20 @@ def test_small_path_plan(monkeypatch, H, slices, NA, r, T, seqs, small, rs):
         assert switched.small_workgroups(pk, T, rs) <= 4 * 256
     pk.a_off_host = None                                        # without host tables: never the small kernel
     assert switched.small_preferred(pk, T, seqs) is False
+
+
+def test_small_path_plan_largest_group_hint(monkeypatch):
+    """A known largest group replaces the estimate: 4 sequences of 128 tokens
+    on 4 adapters with 3 of them on one adapter (384 tokens) go to the segment
+    kernels, which measured faster there (gate_up 4096 -> 25600: 28.7 against
+    34.5 us); without the hint the estimate (128) picks the one-launch kernel."""
+    from granite_switch_amd import switched
+
+    monkeypatch.setattr(switched, "_device_cus", lambda device: 256)
+    monkeypatch.setattr(switched, "_small_plans", {})
+    pk = _packed_stub(4096, (12800, 12800), 4, 32)
+    assert switched.small_preferred(pk, 512, 4) is True
+    assert switched.small_preferred(pk, 512, 4, largest_group=384) is False
+    assert switched.small_preferred(pk, 512, 4, largest_group=128) is True
+    # a hint larger than the batch is clamped to it
+    assert switched.small_row_split(pk, 512, 4, largest_group=10 ** 6) == switched.small_row_split(pk, 512, 4, 512)
