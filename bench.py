@@ -14,6 +14,12 @@ K launches of that kernel alone, rotating buffers).  The CPU baseline is the
 reference's HF loop restated on torch-CPU, timed on the host cores.
 
   python bench.py [--steps K] [--warmup W] [--config {0..4}] [--no-cpu]
+                                   # default: the 32-layer decoder step (config 4)
+  python bench.py --config N --kernel-only KIND:PROJ
+                                   # only one kernel's timing graph (e.g.
+                                   # expand:gate_up_proj), so a rocprofv3
+                                   # --stats summary of the run shows that
+                                   # kernel's average alone
   python bench.py --config N --layer-gemm   # the vLLM layer's x . w_ext^T GEMM at
                                             # the workload's shapes, this library's
                                             # MFMA kernel and torch.mm, in TFLOP/s
@@ -358,7 +364,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=1, choices=[0, 1, 2, 3, 4])
+    ap.add_argument("--config", type=int, default=4, choices=[0, 1, 2, 3, 4])
+    ap.add_argument("--kernel-only", default=None, metavar="KIND:PROJ",
+                    help="time only this kernel (build_segments, shrink:P, expand:P, switched_lora:P, "
+                         "small_fused:P); no step, no CPU baseline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--sets", type=int, default=None, help="buffer sets to rotate (default: > 2x MALL)")
     ap.add_argument("--copy-probe", type=int, default=None, metavar="MIB",
@@ -468,8 +477,15 @@ def main():
         else:
             switched.switched_lora_(md.y, md.x, segs, pk, zbuf[k], path="segments")
 
+    ks_split = {}
+    for k, spec in enumerate(specs):
+        ks_split[spec.name] = int(_lib.load().gs_shrink_workspace_bytes(T, spec.hidden, len(spec.output_slices), NA,
+                                                                          sets[0][k][1].max_rank)) > 256
+
     def shrink(k, md, pk):
-        switched.shrink(md.x, segs, pk, zbuf[k])
+        # split hidden dimension: the shrink kernel alone (fp32 partials, what
+        # switched_lora's expand reads); otherwise the kernel writing z
+        switched.shrink(md.x, segs, pk, zbuf[k], partials_only=ks_split[specs[k].name])
 
     def expand(k, md, pk):
         switched.expand_add_(md.y, zbuf[k], segs, pk)
@@ -481,8 +497,12 @@ def main():
             pair(j % len(specs), md, pk)
 
     # -- warm-up, capture, timed replay ---------------------------------------
-    for i in range(W):
-        step(i)
+    only = args.kernel_only
+    if only is None:
+        for i in range(W):
+            step(i)
+    else:
+        build()
     torch.cuda.synchronize()
 
     def capture(fn):
@@ -503,9 +523,12 @@ def main():
         end.synchronize()
         return start.elapsed_time(end) / n       # ms per unit
 
-    g_steps = capture(lambda: [step(i) for i in range(K)])
-    ms_per_step = timed(g_steps, K)
-    log(f"step: {ms_per_step * 1e3:.2f} us over {K} graph-captured steps")
+    ms_per_step = None
+    if only is None:
+        g_steps = capture(lambda: [step(i) for i in range(K)])
+        ms_per_step = timed(g_steps, K)
+        del g_steps
+        log(f"step: {ms_per_step * 1e3:.2f} us over {K} graph-captured steps")
 
     # -- host-side accounting --------------------------------------------------
     from granite_switch_amd.switched import algorithmic_bytes, algorithmic_flops
@@ -537,8 +560,8 @@ def main():
     # hidden dimension is split; expand alone reads a materialised z.
     kern_us = {}
     kern_launches = {}
-    ks_split = {}
-    if not small:
+    wanted = (lambda name: only is None or name == only)
+    if not small and wanted("build_segments"):
         kern_launches["build_segments"] = 1
         g_b = capture(lambda: [build() for _ in range(K)])
         kern_us["build_segments"] = timed(g_b, K) * 1e3
@@ -547,32 +570,38 @@ def main():
         n = max(K, len(mods)) if cfg != 4 else len(mods)
         kinds = (("small_fused", pair),) if small else (("switched_lora", pair), ("shrink", shrink), ("expand", expand))
         for kind, fn in kinds:
+            name = f"{kind}:{spec.name}"
+            if not wanted(name):
+                continue
+            if kind == "expand":          # the expand alone reads a materialised z
+                switched.shrink(mods[0][0].x, segs, mods[0][1], zbuf[k])
             g_k = capture(lambda: [fn(k, *mods[j % len(mods)]) for j in range(n)])
-            kern_us[f"{kind}:{spec.name}"] = timed(g_k, n) * 1e3
-            kern_launches[f"{kind}:{spec.name}"] = layers
+            kern_us[name] = timed(g_k, n) * 1e3
+            kern_launches[name] = layers
             del g_k
         pk0 = sets[0][k][1]
-        ks_split[spec.name] = int(_lib.load().gs_shrink_workspace_bytes(T, spec.hidden, len(spec.output_slices), NA,
-                                                                          pk0.max_rank)) > 256
         per_kernel_bytes[f"switched_lora:{spec.name}"] = (per_kernel_bytes[f"shrink:{spec.name}"]
                                                           + per_kernel_bytes[f"expand:{spec.name}"])
         per_kernel_bytes[f"small_fused:{spec.name}"] = algorithmic_bytes(eff, pk0, spec.ranks, e)
+    if only is not None and not kern_us:
+        raise SystemExit(f"--kernel-only {only}: no such kernel on this workload")
     if small:
-        if switched.small_status(dev) != 0:
-            raise RuntimeError(f"small-batch kernel reported error word {switched.small_status(dev)}")
+        switched.check(dev)
     for name, us in kern_us.items():
         log(f"kernel {name}: {us:.2f} us/launch, {per_kernel_bytes[name] / us / 1e3:.0f} GB/s algorithmic")
-    singles = [n for n in kern_us if n.startswith("expand:") or n == "build_segments" or n.startswith("small_fused:")
-               or (n.startswith("shrink:") and not ks_split[n.split(":", 1)[1]])]
+    # every single kernel competes (the pair is two kernels): the split
+    # shrinks are timed as the shrink kernel alone
+    singles = [n for n in kern_us if not n.startswith("switched_lora:")]
     dom = max(singles, key=lambda n: kern_us[n] * kern_launches[n])
     dom_gbs = per_kernel_bytes[dom] / (kern_us[dom] * 1e-6) / 1e9
 
     # -- CPU baseline -----------------------------------------------------------
     cpu = None
-    if not args.no_cpu and cpu_sample:
+    if not args.no_cpu and cpu_sample and only is None:
         from oracle import baseline
 
         ids_cpu = torch.tensor(eff.astype(np.int64))
+        host = baseline.host_cpu()
         med, runs, threads = baseline.time_modules(cpu_sample, ids_cpu, budget_s=12.0, min_runs=3)
         step_cpu = med * layers
         cpu = {
@@ -582,13 +611,16 @@ def main():
             "kind": "port",
             "sample": (f"reference HF per-adapter loop (torch-CPU, {dname}) over "
                        f"{'one layer (4 projections), scaled x32' if cfg == 4 else 'the full op'}; "
-                       f"median of {runs} runs; {baseline.cpu_model()}"),
+                       f"median of {runs} runs on {threads} threads; host {host['model']}, "
+                       f"{host.get('physical_cores')} physical cores / {host['logical_cpus']} threads "
+                       f"({host['sockets']} sockets), {host['affinity']} CPUs in this process's affinity, "
+                       f"cgroup quota {host['quota'] if host['quota'] is not None else 'none'}"),
         }
         log(f"cpu baseline: {med * 1e3:.2f} ms per sample pass on {threads} threads")
 
-    us_op = ms_per_step * 1e3
-    value = T / (ms_per_step * 1e-3)
-    op_gbs = op_bytes / (ms_per_step * 1e-3) / 1e9
+    us_op = None if ms_per_step is None else ms_per_step * 1e3
+    value = None if ms_per_step is None else T / (ms_per_step * 1e-3)
+    op_gbs = None if ms_per_step is None else op_bytes / (ms_per_step * 1e-3) / 1e9
     wl_name = {0: "switched-LoRA single op fp32 2048->2048 T=512 (4x128) 4 adapters r8 aLoRA",
                1: "switched-LoRA decode QKV 4096->6144 T=256 12 adapters r32 (20% not yet activated)",
                2: "switched-LoRA chunked prefill gate_up 4096->25600 T=8192 (16 seqs) 12 adapters r32",
@@ -617,10 +649,12 @@ def main():
         "us_per_op": us_op,
         "op_algorithmic_bytes": op_bytes,
         "op_hbm_gbs": op_gbs,
-        "op_hbm_frac": op_gbs / HBM_PEAK_GBS,
-        "op_mfma_frac": op_flops / (ms_per_step * 1e-3) / MFMA_PEAK[dname],
+        "op_hbm_frac": None if op_gbs is None else op_gbs / HBM_PEAK_GBS,
+        "op_mfma_frac": None if ms_per_step is None else op_flops / (ms_per_step * 1e-3) / MFMA_PEAK[dname],
         "kernels_us": kern_us,
     }
+    if only is not None:
+        out["mode"] = f"kernel-only {only}: no step timed"
     print(json.dumps(out), flush=True)
 
 

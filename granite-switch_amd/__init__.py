@@ -9,6 +9,7 @@ driven from Python on PyTorch-ROCm:
   meta         ``LoRAContext`` / ``FusedLoRAKernelMeta``
   vllm_layers  vLLM-form ``SwitchedLoRALinear`` (fused w_ext GEMM + expand)
   hf_layers    HF-form ``SwitchedLoRALinear`` / ``MergedSwitchedLoRALinear``
+  probe_routing  drop-in for ``granite_switch.probe_routing`` (probe-slot split)
   workloads    seeded synthetic benchmark shapes
 
 The directory name carries a dash, so the package is imported under the name

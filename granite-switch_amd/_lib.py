@@ -49,6 +49,7 @@ SIGNATURES = {
     "gs_small_eligible": (c_i32, [c_i64, c_i32, c_i32, c_void_p, c_i32, c_i32]),
     "gs_small_workspace_bytes": (c_i64, [c_i32, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_void_p]),
     "gs_small_sync_bytes": (c_i64, []),
+    "gs_small_set_wait_limit": (c_i64, [c_i64]),
     "gs_small_workgroups": (c_i64, [c_i32, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_void_p, c_i32]),
     "gs_switched_lora_small": (c_i32, [c_i32, c_void_p, c_void_p, c_void_p, c_void_p, c_i32, c_void_p, c_void_p,
                                        c_i64, c_void_p, c_i64, c_i64, c_i32, c_i32, c_void_p, c_i32, c_void_p,
@@ -61,6 +62,10 @@ SIGNATURES = {
     "gs_switch_lora_expand_swiglu": (c_i32, [c_void_p, c_i64, c_i64, c_void_p, c_i64, c_i64, c_i64, c_void_p, c_i32,
                                              c_void_p, c_i64, c_void_p, c_void_p, c_void_p, c_i32, c_i32, c_i32, c_i32,
                                              c_void_p]),
+    "gs_split_adapter_indices": (c_i32, [c_void_p, c_i32, c_void_p, c_i32, c_i64, c_void_p, c_void_p, c_void_p]),
+    "gs_switch_lora_shrink_expand": (c_i32, [c_void_p, c_i32, c_i64, c_i64, c_void_p, c_i64, c_i64, c_i64, c_void_p,
+                                             c_i32, c_void_p, c_i64, c_void_p, c_void_p, c_void_p, c_void_p, c_i32,
+                                             c_i32, c_i32, c_void_p]),
     "gs_gemm_bf16_tn": (c_i32, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i64, c_i64, c_void_p]),
 }
 

@@ -749,10 +749,12 @@ int gs_shrink(int32_t dtype, const void* x, int64_t ldx, int64_t num_tokens, int
   rc = check_shrink(dtype, x, ldx, hidden, a_pack);
   if (rc != GS_OK) return rc;
   const bool bf16 = dtype == GS_DTYPE_BF16;
-  GS_CHECK_ARG(ldz >= int64_t(num_slices) * max_rank && ldz % 8 == 0 && aligned16(z), "gs_shrink: ldz=%lld / z alignment",
-               (long long)ldz);
+  GS_CHECK_ARG(z == nullptr || (ldz >= int64_t(num_slices) * max_rank && ldz % 8 == 0 && aligned16(z)),
+               "gs_shrink: ldz=%lld / z alignment", (long long)ldz);
   if (num_tokens == 0) return GS_OK;
   const ShrinkPlan pl = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, bf16);
+  GS_CHECK_ARG(z != nullptr || pl.KS > 1, "gs_shrink: z may be NULL only when the hidden dimension is split "
+               "(gs_shrink_workspace_bytes > 256)");
   rc = check_workspace(pl, workspace, workspace_bytes);
   if (rc != GS_OK) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -760,7 +762,7 @@ int gs_shrink(int32_t dtype, const void* x, int64_t ldx, int64_t num_tokens, int
                                             seg_offsets, perm, z, ldz, workspace, num_tokens);
   launch_shrink(bf16, pl, p, st);
   GS_CHECK_LAUNCH("gs_shrink");
-  if (pl.KS > 1) {
+  if (pl.KS > 1 && z != nullptr) {
     const int64_t n8 = (num_tokens * pl.zw) / 8;
     const unsigned blocks = static_cast<unsigned>((n8 + kThreads - 1) / kThreads);
     if (bf16) hipLaunchKernelGGL(reduce_parts_kernel<true>, dim3(blocks), dim3(kThreads), 0, st, p.part, p.part_stride,

@@ -315,6 +315,27 @@ __global__ __launch_bounds__(256) void bitmask_kernel(const void* __restrict__ i
   }
 }
 
+// Probe-slot split: one thread per token.  The kind table (<= 257 bytes) is
+// staged in LDS; an index outside the table is not a probe.
+__global__ __launch_bounds__(256) void split_indices_kernel(const uint8_t* __restrict__ kind_lut, int lut_len,
+                                                            const void* __restrict__ ids, int idx_bytes, int64_t n,
+                                                            void* lora_out, void* probe_out) {
+  __shared__ uint8_t lut[GS_MAX_ADAPTERS + 1];
+  for (int k = threadIdx.x; k < lut_len; k += blockDim.x) lut[k] = kind_lut[k];
+  __syncthreads();
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  const int64_t v = load_idx(ids, idx_bytes, t);
+  const bool probe = v >= 0 && v < lut_len && lut[v] != 0;
+  if (idx_bytes == 8) {
+    if (lora_out) static_cast<int64_t*>(lora_out)[t] = probe ? 0 : v;
+    if (probe_out) static_cast<int64_t*>(probe_out)[t] = probe ? v : 0;
+  } else {
+    if (lora_out) static_cast<int32_t*>(lora_out)[t] = probe ? 0 : static_cast<int32_t>(v);
+    if (probe_out) static_cast<int32_t*>(probe_out)[t] = probe ? static_cast<int32_t>(v) : 0;
+  }
+}
+
 }  // namespace gs
 
 using namespace gs;
@@ -322,6 +343,23 @@ using namespace gs;
 extern "C" {
 
 int gs_version(void) { return 100; }
+
+int gs_split_adapter_indices(const uint8_t* kind_lut, int32_t lut_len, const void* adapter_indices,
+                             int32_t idx_bytes, int64_t num_tokens, void* lora_indices, void* probe_indices,
+                             void* stream) {
+  const char* who = "gs_split_adapter_indices";
+  GS_CHECK_ARG(idx_bytes == 4 || idx_bytes == 8, "%s: idx_bytes=%d", who, idx_bytes);
+  GS_CHECK_ARG(lut_len >= 1 && lut_len <= GS_MAX_ADAPTERS + 1 && kind_lut != nullptr,
+               "%s: kind table of %d entries (1..%d)", who, lut_len, GS_MAX_ADAPTERS + 1);
+  GS_CHECK_ARG(num_tokens >= 0 && num_tokens < (int64_t(1) << 31), "%s: num_tokens out of range", who);
+  GS_CHECK_ARG(num_tokens == 0 || adapter_indices != nullptr, "%s: NULL adapter_indices", who);
+  if (num_tokens == 0 || (lora_indices == nullptr && probe_indices == nullptr)) return GS_OK;
+  hipLaunchKernelGGL(split_indices_kernel, dim3(static_cast<unsigned>((num_tokens + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), kind_lut, lut_len, adapter_indices, idx_bytes, num_tokens,
+                     lora_indices, probe_indices);
+  GS_CHECK_LAUNCH(who);
+  return GS_OK;
+}
 
 const char* gs_last_error(void) { return g_err; }
 

@@ -38,8 +38,9 @@
 // Forward progress: producers have the lowest workgroup ids and never wait, and
 // workgroups are dispatched in id order, so a waiting consumer never holds a
 // slot a producer still needs.  The wait is nevertheless bounded: after
-// timeout_ticks of the 100 MHz wall clock a consumer sets bit 0 of the error
-// word and goes on, so every wave of the grid always ends.
+// max_polls looks at a group of partials a consumer sets bit 0 of the error
+// word and goes on, so every wave of the grid always ends.  The bound counts
+// looks, not time, so a queue preempted mid-wait does not use it up.
 //
 // MFMA shapes: 16x16x32 bf16 (16x16x4 fp32) throughout, so each global load
 // instruction reads 64 contiguous bytes of 16 rows (4 lanes per row) instead
@@ -319,7 +320,7 @@ struct FusedParams {
   int NG;                 // consumer tile groups per adapter (NNT / TG)
   // hand-off
   int32_t* sync;
-  int64_t timeout_ticks;
+  int64_t max_polls;      // looks at a partial group before giving up (sets the error word)
   SmallTab tab;
 };
 
@@ -631,8 +632,17 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
       }
       for (int ks0 = 0; ks0 < p.KS; ks0 += kKsGrp) {
         uint64_t pv[EPT][kKsGrp];
-        const int64_t t_start = wall_clock64();
-        for (;;) {
+#pragma unroll
+        for (int m = 0; m < EPT; ++m)
+#pragma unroll
+          for (int u = 0; u < kKsGrp; ++u) pv[m][u] = static_cast<uint64_t>(want) << 32;
+        // At most max_polls looks: counting looks instead of time keeps the
+        // bound from expiring while the queue is preempted
+        for (int64_t polls = 0;; ++polls) {
+          if (polls >= p.max_polls) {
+            __hip_atomic_fetch_or(p.sync + kSyncErrWord, kErrTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
           bool ready = true;
 #pragma unroll
           for (int m = 0; m < EPT; ++m)
@@ -647,10 +657,6 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
 #pragma unroll
             for (int u = 0; u < kKsGrp; ++u) ready = ready && static_cast<uint32_t>(pv[m][u] >> 32) == want;
           if (ready) break;
-          if (wall_clock64() - t_start > p.timeout_ticks) {
-            __hip_atomic_fetch_or(p.sync + kSyncErrWord, kErrTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-          }
           __builtin_amdgcn_s_sleep(1);
         }
 #pragma unroll
@@ -793,7 +799,12 @@ constexpr int kSmTargetShrinkWgs = GS_SMALL_TARGET_PRODUCERS;
 #define GS_SMALL_TILE_GROUP 8
 #endif
 constexpr int kSmTileGroup = GS_SMALL_TILE_GROUP;      // most column tiles one consumer walks
-constexpr int64_t kDefaultTimeoutTicks = 2000000;   // 20 ms of the 100 MHz wall clock
+// Looks a consumer takes at one group of partials before it gives up.  One
+// look is a coherent load round trip (>= ~0.3 us) plus a short sleep, so the
+// default bounds the wait at tens to hundreds of milliseconds; a completed
+// hand-off takes a few microseconds.
+constexpr int64_t kDefaultWaitPolls = 200000;
+std::atomic<int64_t> g_wait_polls{kDefaultWaitPolls};
 constexpr int64_t kSyncBytes = 4 * kSyncLine * (kSmMaxAdapters + 1);
 
 // The row split RS multiplies the producers like the k-split does, so it
@@ -918,6 +929,11 @@ int64_t gs_small_workspace_bytes(int32_t dtype, int64_t num_tokens, int32_t hidd
 
 int64_t gs_small_sync_bytes(void) { return kSyncBytes; }
 
+int64_t gs_small_set_wait_limit(int64_t polls) {
+  const int64_t v = polls < 0 ? kDefaultWaitPolls : polls;
+  return g_wait_polls.exchange(v, std::memory_order_relaxed);
+}
+
 int64_t gs_small_workgroups(int32_t dtype, int64_t num_tokens, int32_t hidden, int32_t num_slices,
                             int32_t num_adapters, int32_t max_rank, int32_t out_total,
                             const int32_t* slice_bounds, int32_t row_split) {
@@ -1008,7 +1024,7 @@ int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t*
   GS_CHECK_ARG(pl.TG == 1 || (bf16 && max_rank <= 32 && pl.NNT % pl.TG == 0), "%s: tile group %d for this module",
                who, pl.TG);
   fp.sync = sync;
-  fp.timeout_ticks = kDefaultTimeoutTicks;
+  fp.max_polls = g_wait_polls.load(std::memory_order_relaxed);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned grid = static_cast<unsigned>(fp.NP + consumer_wgs(pl, num_adapters, row_split));
   if (bf16) launch_fused<true>(pl, fp, grid, speculate != 0, st);

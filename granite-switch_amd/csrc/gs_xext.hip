@@ -1,6 +1,7 @@
-// The reference's in-place expand ops over x_ext = x . w_ext^T, with the
-// reference's argument list and semantics (bitmask skip, tier layout of the
-// packed lora_B, kernel-local ids), on gfx950 bf16 MFMA.
+// The reference's expand ops over x_ext = x . w_ext^T, with the reference's
+// argument lists and semantics (bitmask skip, tier layout of the packed
+// lora_B, kernel-local ids), on gfx950 bf16 MFMA: the in-place expand, the
+// fused gate/up expand + SwiGLU, and the W-less expand into a fresh output.
 //
 // A workgroup owns 32 rows x 128 columns (4 waves x one 32-column block).  Each
 // wave loops over the adapters that are both set in the tile bitmask and
@@ -132,6 +133,67 @@ __global__ __launch_bounds__(256) void xext_expand_kernel(XextArgs a, uint16_t* 
   }
 }
 
+// W-less expand (the reference's switch_lora_shrink_expand): x_ext holds only
+// shrink columns, and out[M, N] receives the delta itself.  The reference
+// zeroes out and then stores the delta of every tile with a nonzero bitmask;
+// here every workgroup stores its whole 32 x 128 tile -- the delta, exactly
+// zero for base rows (they select no adapter), and zeros for a tile whose
+// bitmask is 0 -- so out is written once and no zeroing pass is needed.
+template <bool F32OUT>
+__global__ __launch_bounds__(256) void xext_shrink_expand_kernel(XextArgs a, void* out, int64_t stride_om,
+                                                                 const int32_t* __restrict__ tile_slice,
+                                                                 int block_n) {
+  __shared__ float dtile[32][128 + 4];
+  __shared__ int scr[GS_MAX_SLICES * 6];
+  const int64_t pm = blockIdx.y;
+  const int64_t bm_raw = a.bitmask[pm * a.stride_bm];
+  const uint64_t bm = static_cast<uint64_t>(bm_raw) & valid_bits(a.na);
+  const int n_tile0 = blockIdx.x * 128;
+  const int tid = threadIdx.x;
+  const int64_t m0 = pm * 32;
+  if (bm_raw != 0) {   // uniform over the workgroup
+    const int wave = tid >> 6;
+    const int l = tid & 63;
+    const int i = l & 31;
+    if (tid < a.S * 6) scr[tid] = a.slice_col_r[tid];
+    const bool row_ok = (m0 + i) < a.M;
+    const int id = row_ok ? load_id(a.ids, a.idx_bytes, m0 + i) : 0;
+    const int n0 = n_tile0 + 32 * wave;
+    const int s = tile_slice[(n0 < a.N ? n0 : n_tile0) / block_n];
+    lds_barrier();
+    f32x16 acc = f32x16{};
+    if (n0 < a.N) acc = xext_block_delta(a, scr, m0, n0, s, id, row_ok, bm);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) dtile[mfma32_row(v, l)][32 * wave + i] = acc[v];
+    lds_barrier();
+  }
+  const int row = tid >> 3;
+  const int cx = (tid & 7) * 16;
+  const int64_t m = m0 + row;
+  if (m >= a.M || n_tile0 + cx >= a.N) return;
+  float d[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) d[c] = bm_raw != 0 ? dtile[row][cx + c] : 0.f;
+  if constexpr (F32OUT) {
+    float* p = static_cast<float*>(out) + m * stride_om + n_tile0 + cx;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<u32x4*>(p + 4 * q) = u32x4{__float_as_uint(d[4 * q]), __float_as_uint(d[4 * q + 1]),
+                                                   __float_as_uint(d[4 * q + 2]), __float_as_uint(d[4 * q + 3])};
+  } else {
+    uint16_t* p = static_cast<uint16_t*>(out) + m * stride_om + n_tile0 + cx;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = static_cast<uint32_t>(f32_to_bf16_bits(d[half * 8 + 2 * e])) |
+               (static_cast<uint32_t>(f32_to_bf16_bits(d[half * 8 + 2 * e + 1])) << 16);
+      *reinterpret_cast<u32x4*>(p + half * 8) = u32x4{o[0], o[1], o[2], o[3]};
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void xext_swiglu_kernel(XextArgs a, uint16_t* out, int64_t stride_om, int H) {
   __shared__ float dg[32][128 + 4];
   __shared__ float du[32][128 + 4];
@@ -254,6 +316,43 @@ int gs_switch_lora_expand(void* x_ext, int64_t stride_m, int64_t stride_n, int64
   hipLaunchKernelGGL(xext_expand_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a,
                      static_cast<uint16_t*>(x_ext), tile_slice, block_n);
   GS_CHECK_LAUNCH("gs_switch_lora_expand");
+  return GS_OK;
+}
+
+int gs_switch_lora_shrink_expand(void* out, int32_t out_dtype, int64_t stride_om, int64_t stride_on,
+                                 const void* x_ext, int64_t stride_m, int64_t stride_n, int64_t M,
+                                 const void* adapter_indices, int32_t idx_bytes, const int64_t* bitmask,
+                                 int64_t stride_bm, const void* lb_packed, const int32_t* tile_slice,
+                                 const int32_t* slice_col_r, const int32_t* na, int32_t S, int32_t block_n, int32_t N,
+                                 void* stream) {
+  const char* who = "gs_switch_lora_shrink_expand";
+  int rc = check_xext(who, x_ext, stride_n, stride_m, M, idx_bytes, na, S, block_n, N, lb_packed);
+  if (rc != GS_OK) return rc;
+  GS_CHECK_ARG(out_dtype == GS_DTYPE_BF16 || out_dtype == GS_DTYPE_FP32, "%s: out_dtype=%d", who, out_dtype);
+  const int vec = out_dtype == GS_DTYPE_BF16 ? 8 : 4;
+  GS_CHECK_ARG(stride_on == 1 && stride_om >= N && stride_om % vec == 0 && aligned16(out),
+               "%s: out must be row-contiguous [M, >= N] with 16-byte aligned rows", who);
+  if (M == 0) return GS_OK;
+  XextArgs a{};
+  a.x_ext = x_ext;
+  a.stride_m = stride_m;
+  a.M = M;
+  a.ids = adapter_indices;
+  a.idx_bytes = idx_bytes;
+  a.bitmask = bitmask;
+  a.stride_bm = stride_bm;
+  a.lb = static_cast<const uint16_t*>(lb_packed);
+  a.slice_col_r = slice_col_r;
+  for (int t = 0; t < 6; ++t) a.na[t] = na[t];
+  a.S = S;
+  a.N = N;
+  dim3 grid((N + 127) / 128, static_cast<unsigned>((M + 31) / 32));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (out_dtype == GS_DTYPE_FP32)
+    hipLaunchKernelGGL(xext_shrink_expand_kernel<true>, grid, dim3(256), 0, st, a, out, stride_om, tile_slice, block_n);
+  else
+    hipLaunchKernelGGL(xext_shrink_expand_kernel<false>, grid, dim3(256), 0, st, a, out, stride_om, tile_slice, block_n);
+  GS_CHECK_LAUNCH(who);
   return GS_OK;
 }
 

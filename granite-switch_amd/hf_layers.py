@@ -7,7 +7,9 @@ lora_B pre-scaled), ``weight``/``bias`` properties, context-passing
 src/granite_switch/hf/core/lora.py:23-348.  The per-adapter Python loop with
 its host syncs (``torch.any``, ``unique``) is replaced by the three device
 steps of ``switched`` (segments, shrink, expand-add), so forward never syncs
-once the adapters are packed (``freeze``).
+once the adapters are packed: ``freeze()`` packs them once; without it the
+pack is cached and rebuilt only when a LoRA parameter changes.  The kernels
+compute no gradients, so a forward that autograd would track raises.
 """
 
 from __future__ import annotations
@@ -23,35 +25,65 @@ class _SwitchedBase(nn.Module):
         raise NotImplementedError
 
     def freeze(self, adapter_ranks=None) -> None:
-        """Pack the current adapter weights once; forward then reuses the pack.
+        """Pack the current adapter weights once and stop tracking them.
 
         ``adapter_ranks`` (true rank per adapter) limits the bytes read to the
         true-rank rows; the default reads all max_lora_rank rows (zero rows of
-        a smaller adapter contribute nothing, so the result is the same).
-        Call ``unfreeze()`` (or ``freeze()`` again) after changing weights.
+        a smaller adapter contribute nothing, so the result is the same).  The
+        LoRA parameters stop requiring grad.  ``unfreeze()`` goes back to
+        packing on demand.
         """
         A_sl, B_sl = self._slices()
+        for p in (*A_sl, *B_sl):
+            p.requires_grad_(False)
         with torch.no_grad():
             self._packed = switched.PackedAdapters.from_slices([a.detach() for a in A_sl], [b.detach() for b in B_sl],
                                                                adapter_ranks)
 
     def unfreeze(self) -> None:
         self._packed = None
+        self._auto_pack = None
+        self._auto_key = None
+        self._auto_pack = None
 
-    def _apply_lora(self, output: torch.Tensor, x: torch.Tensor, adapter_indices: torch.Tensor) -> torch.Tensor:
-        packed = self._packed
-        if packed is None:
+    def _weights_key(self):
+        A_sl, B_sl = self._slices()
+        return tuple((p.data_ptr(), p._version) for p in (*A_sl, *B_sl))
+
+    def _current_pack(self) -> "switched.PackedAdapters":
+        """The frozen pack, else a pack cached until the weights change.
+
+        A change is seen through each parameter's storage address and version
+        counter: in-place updates under ``no_grad`` or through ``detach()``,
+        optimizer steps and reassignment all move them.  Writes through
+        ``.data`` bypass the version counter; call ``unfreeze()`` after those.
+        """
+        if self._packed is not None:
+            return self._packed
+        key = self._weights_key()
+        if getattr(self, "_auto_pack", None) is None or self._auto_key != key:
             A_sl, B_sl = self._slices()
             with torch.no_grad():
-                packed = switched.PackedAdapters.from_slices([a.detach() for a in A_sl], [b.detach() for b in B_sl])
+                self._auto_pack = switched.PackedAdapters.from_slices([a.detach() for a in A_sl],
+                                                                      [b.detach() for b in B_sl])
+            self._auto_key = key
+        return self._auto_pack
+
+    def _apply_lora(self, output: torch.Tensor, x: torch.Tensor, adapter_indices: torch.Tensor) -> torch.Tensor:
+        if torch.is_grad_enabled():
+            A_sl, B_sl = self._slices()
+            if x.requires_grad or any(p.requires_grad for p in (*A_sl, *B_sl)):
+                raise RuntimeError(
+                    "the MI355X switched-LoRA kernels compute no gradients: run the forward under torch.no_grad() / "
+                    "torch.inference_mode(), or freeze() the layer and pass inputs that do not require grad")
+        packed = self._current_pack()
         x_flat = x.reshape(-1, self.in_features)
         out_flat = output.view(-1, output.shape[-1])
         ids = adapter_indices.reshape(-1)
         if ids.numel() != x_flat.shape[0]:
             raise ValueError("adapter_indices must have one entry per token")
         segs = switched.build_segments(ids, self.num_adapters)
-        with torch.no_grad():
-            switched.switched_lora_(out_flat, x_flat.to(packed.dtype), segs, packed)
+        switched.switched_lora_(out_flat, x_flat.to(packed.dtype), segs, packed)
         return output
 
     @property
@@ -79,6 +111,8 @@ class SwitchedLoRALinear(_SwitchedBase):
         nn.init.zeros_(self.lora_B)
         self._adapter_indices: torch.Tensor | None = None
         self._packed = None
+        self._auto_pack = None
+        self._auto_key = None
 
     def _slices(self):
         return [self.lora_A], [self.lora_B]
@@ -114,6 +148,8 @@ class MergedSwitchedLoRALinear(_SwitchedBase):
             nn.init.zeros_(B)
         self._adapter_indices: torch.Tensor | None = None
         self._packed = None
+        self._auto_pack = None
+        self._auto_key = None
 
     def _slices(self):
         return list(self.lora_A_slices), list(self.lora_B_slices)

@@ -171,12 +171,51 @@ def compute_per_module_bitmasks(adapter_indices: torch.Tensor, remap_tables_t: t
     return out
 
 
-def switch_lora_shrink_expand(*args, **kwargs):
-    """Shrink-only (W-less) expand of the Shadow-Residual cross-stream shunt.
+def switch_lora_shrink_expand(out: torch.Tensor, x_ext: torch.Tensor, adapter_indices: torch.Tensor,
+                              bitmask: torch.Tensor, lb_packed: torch.Tensor, tile_slice: torch.Tensor,
+                              slice_col_r: torch.Tensor, na: tuple, S: int, block_n: int, N: int) -> None:
+    """W-less expand of the Shadow-Residual cross-stream shunt into ``out[M, N]``.
 
-    Not provided: that decoder variant is outside this library's path.
+    Signature and semantics of src/granite_switch/kernels/switch_lora_kernel.py:
+    1094-1146 (kernel :883-1091): ``x_ext`` holds only shrink columns (the
+    cross weight has no base rows, so ``slice_col_r`` bases start at 0); a row
+    of an adapter gets ``shrink[:, :r] . lb^T`` in ``out``'s dtype, a base row
+    and every row of a skipped tile read back exactly zero.  The kernel writes
+    all of ``out[:M, :N]``; a larger ``out`` is zeroed first, as the
+    reference's launcher zeroes all of it.
     """
-    raise NotImplementedError("switch_lora_shrink_expand (Shadow-Residual W_cross) is not part of this library")
+    if x_ext.dtype != torch.bfloat16 or lb_packed.dtype != torch.bfloat16:
+        raise TypeError("switch_lora_shrink_expand: x_ext and lb_packed must be bfloat16")
+    if out.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"switch_lora_shrink_expand: out must be bfloat16 or float32, got {out.dtype}")
+    if tile_slice.dtype != torch.int32 or slice_col_r.dtype != torch.int32 or bitmask.dtype != torch.int64:
+        raise TypeError("switch_lora_shrink_expand: tile_slice/slice_col_r int32, bitmask int64 expected")
+    M = x_ext.shape[0]
+    if out.dim() != 2 or out.shape[0] < M or out.shape[1] < int(N):
+        raise ValueError(f"switch_lora_shrink_expand: out {tuple(out.shape)} is smaller than [M, N] = [{M}, {N}]")
+    if adapter_indices.numel() < M or bitmask.numel() < (M + BLOCK_M - 1) // BLOCK_M:
+        raise ValueError("switch_lora_shrink_expand: adapter_indices / bitmask shorter than x_ext's rows")
+    if len(na) != 6:
+        raise ValueError("switch_lora_shrink_expand: na must have 6 tier counts")
+    shrink_cols = sum(int(n) * int(S) * r for n, r in zip(na, SUPPORTED_RANKS))
+    if x_ext.dim() != 2 or x_ext.shape[1] < shrink_cols:
+        raise ValueError(f"switch_lora_shrink_expand: x_ext has {x_ext.shape[-1]} columns, the tiers need "
+                         f"{shrink_cols}")
+    lb_need = sum(int(n) * int(N) * r for n, r in zip(na, SUPPORTED_RANKS))
+    if lb_packed.numel() < lb_need:
+        raise ValueError(f"switch_lora_shrink_expand: lb_packed holds {lb_packed.numel()} elements, needs {lb_need}")
+    if slice_col_r.numel() < int(S) * 6:
+        raise ValueError("switch_lora_shrink_expand: slice_col_r must be [S, 6]")
+    if tile_slice.numel() < (int(N) + int(block_n) - 1) // int(block_n):
+        raise ValueError("switch_lora_shrink_expand: tile_slice has fewer than ceil(N / block_n) entries")
+    if tuple(out.shape) != (M, int(N)):
+        out.zero_()
+    ids = adapter_indices if adapter_indices.stride(-1) == 1 else adapter_indices.contiguous()
+    code = _lib.GS_DTYPE_BF16 if out.dtype == torch.bfloat16 else _lib.GS_DTYPE_FP32
+    _lib.call("gs_switch_lora_shrink_expand", out.data_ptr(), code, out.stride(0), out.stride(1), x_ext.data_ptr(),
+              x_ext.stride(0), x_ext.stride(1), M, ids.data_ptr(), _idx_bytes(ids), bitmask.data_ptr(),
+              bitmask.stride(0), lb_packed.data_ptr(), tile_slice.data_ptr(), slice_col_r.data_ptr(),
+              _na_array(na), int(S), int(block_n), int(N), _lib.stream_ptr(x_ext.device))
 
 
 __all__ = [

@@ -6,8 +6,9 @@ opaque (src/granite_switch/vllm/core/lora_ops.py:25-27,192-226;
 src/granite_switch/vllm/core/lora_kernel_meta.py:166-182).  This module
 registers the same op names with the same argument lists, ``mutates_args`` and
 fake implementations, so callers such as ``SwitchedLoRALinear._run_expand``
-(src/granite_switch/vllm/core/lora.py:659-686) run unchanged on MI355X, plus
-three new ops for the y-given switched-LoRA path.
+(src/granite_switch/vllm/core/lora.py:659-686) and ``WCrossShunt.forward``
+(src/granite_switch/vllm/decoder/shadow_residual/wcross_shunt.py:198-242) run
+unchanged on MI355X, plus three new ops for the y-given switched-LoRA path.
 
 Only one provider of the ``granite_switch`` ops can be loaded in a process.
 """
@@ -61,6 +62,22 @@ if not _registered("switch_lora_expand_swiglu"):
     @switch_lora_expand_swiglu.register_fake
     def _(out, x_ext, adapter_indices, bitmask, lb_packed, slice_col_r, NA_16, NA_32, NA_64, NA_128, NA_256, NA_512,
           S, block_n, H, N):
+        return None
+
+
+if not _registered("switch_lora_shrink_expand"):
+
+    @torch.library.custom_op(f"{_NS}::switch_lora_shrink_expand", mutates_args=("out",))
+    def switch_lora_shrink_expand(out: torch.Tensor, x_ext: torch.Tensor, adapter_indices: torch.Tensor,
+                                  bitmask: torch.Tensor, lb_packed: torch.Tensor, tile_slice: torch.Tensor,
+                                  slice_col_r: torch.Tensor, NA_16: int, NA_32: int, NA_64: int, NA_128: int,
+                                  NA_256: int, NA_512: int, S: int, block_n: int, N: int) -> None:
+        kernels.switch_lora_shrink_expand(out, x_ext, adapter_indices, bitmask, lb_packed, tile_slice, slice_col_r,
+                                          (NA_16, NA_32, NA_64, NA_128, NA_256, NA_512), S, block_n, N)
+
+    @switch_lora_shrink_expand.register_fake
+    def _(out, x_ext, adapter_indices, bitmask, lb_packed, tile_slice, slice_col_r, NA_16, NA_32, NA_64, NA_128,
+          NA_256, NA_512, S, block_n, N):
         return None
 
 

@@ -21,6 +21,7 @@ library must be built.
 from __future__ import annotations
 
 import ctypes
+import os
 from dataclasses import dataclass
 
 import torch
@@ -287,18 +288,28 @@ class PackedAdapters:
 # Workspace (split-K partial sums), cached per device
 # ---------------------------------------------------------------------------
 _workspaces: dict = {}
+# Buffers replaced by a larger one.  They are never freed: a HIP graph captured
+# while one was current still holds its address, and its replays keep using it
+# (freed memory would go back to torch's allocator and could be handed to
+# another tensor while a replay writes into it).
+_retired: list = []
+
+
+def _grow(table: dict, key, need: int, what: str, zero: bool = True) -> torch.Tensor:
+    buf = table.get(key)
+    if buf is None or buf.numel() < need:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f"switched-LoRA {what} must be allocated before graph capture "
+                               "(call reserve_workspace / reserve_small_workspace, or run once eagerly)")
+        new = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=torch.device(key[0], key[1]))
+        if buf is not None:
+            _retired.append(buf)
+        table[key] = buf = new
+    return buf
 
 
 def _workspace(device: torch.device, need: int) -> torch.Tensor:
-    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
-    ws = _workspaces.get(key)
-    if ws is None or ws.numel() < need:
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("switched-LoRA workspace must be allocated before graph capture "
-                               "(call reserve_workspace)")
-        ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=device)
-        _workspaces[key] = ws
-    return ws
+    return _grow(_workspaces, _dev_key(device), need, "workspace")
 
 
 def shrink_workspace(num_tokens: int, hidden: int, num_slices: int, num_adapters: int, max_rank: int,
@@ -428,10 +439,7 @@ def small_preferred(packed: "PackedAdapters", num_tokens: int, num_seqs: int | N
 
 def reserve_workspace(device: torch.device, nbytes: int) -> None:
     """Pre-allocate the per-device shrink workspace (before graph capture)."""
-    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
-    ws = _workspaces.get(key)
-    if ws is None or ws.numel() < nbytes:
-        _workspaces[key] = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+    _workspace(device, nbytes)
 
 
 # The small-batch kernel's state, one set per device: its sync buffer (the
@@ -462,16 +470,14 @@ def small_sync_buffer(device: torch.device) -> torch.Tensor:
 
 
 def small_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """The per-device workspace of the small-batch kernel (at least ``nbytes``)."""
-    key = _dev_key(device)
-    ws = _small_workspaces.get(key)
-    if ws is None or ws.numel() < nbytes:
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("switched-LoRA small-batch workspace must be allocated before graph capture "
-                               "(call reserve_small_workspace or run once eagerly)")
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _small_workspaces[key] = ws
-    return ws
+    """The per-device workspace of the small-batch kernel (at least ``nbytes``).
+
+    A larger request replaces the buffer with a new zeroed one and retires the
+    old one (never freed, see ``_retired``).  A graph captured earlier keeps
+    the old buffer: its partials carry tags of the same per-adapter epochs as
+    the new buffer's, and epochs only grow, so neither buffer ever holds a
+    pair tagged with an epoch that has not started."""
+    return _grow(_small_workspaces, _dev_key(device), nbytes, "small-batch workspace")
 
 
 def reserve_small_workspace(device: torch.device, nbytes: int) -> None:
@@ -487,15 +493,72 @@ def small_status(device: torch.device) -> int:
     up waiting for its shrink partials, so that call's output was wrong.
     ``small_reset`` clears the state.
     """
+    if _dev_key(device) not in _sync_buffers:
+        return 0                       # no small-batch call has run on this device
     return int(small_sync_buffer(device)[_ERR_WORD].item())
 
 
-def small_pending_count(device: torch.device) -> int:
-    """Sum of the adapters' done counts (synchronises).
+class SmallPathError(_lib.GraniteSwitchError):
+    """A one-launch decode call gave up waiting for its shrink partials: the
+    output of that call (and of any call since the last check) is wrong."""
 
-    Every completed call leaves them all at 0: the last consumer of an adapter
-    resets its count when it advances the adapter's epoch."""
-    return int(small_sync_buffer(device)[_SYNC_LINE + 1::_SYNC_LINE].sum().item())
+
+def check(device: torch.device | None = None) -> None:
+    """Raise ``SmallPathError`` if a one-launch decode call on ``device`` has
+    reported a failed hand-off since the last ``small_reset`` (synchronises).
+
+    The kernel never stops the stream: a consumer whose wait runs out sets the
+    error word and finishes, so the launch and every later one complete.  Call
+    this at a point that synchronises anyway (end of a step, before returning
+    results), or set ``GS_CHECK_EACH_CALL=1`` to check after every eager call.
+    """
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    word = small_status(dev)
+    if word:
+        raise SmallPathError("gs_switched_lora_small", word,
+                             f"error word {word:#x}: an expand workgroup gave up waiting for its shrink partials; "
+                             "the affected outputs are wrong (small_reset() clears the state)")
+
+
+def set_small_wait_limit(polls: int | None) -> int:
+    """Bound the decode kernel's hand-off wait to ``polls`` looks (None restores
+    the default); returns the previous bound.  0 makes every consumer give up
+    at once and report it -- a test hook that still lets every launch end."""
+    return int(_lib.load().gs_small_set_wait_limit(-1 if polls is None else int(polls)))
+
+
+_CHECK_EACH_CALL = os.environ.get("GS_CHECK_EACH_CALL", "0") not in ("", "0")
+
+
+_EPOCH_SHIFT = 20
+
+
+def pending_from_counters(counters: torch.Tensor) -> int:
+    """Weight of unfinished launches in the adapters' 64-bit launch counters.
+
+    Every consumer of adapter g adds its share of 2^20 to g's counter, and the
+    shares of one launch sum to exactly 2^20, so after complete launches the
+    low 20 bits of every counter are 0 (the bits above count the epochs).
+    Returns the sum of the low 20 bits: 0 iff no launch was half counted.
+    """
+    low = counters.to(torch.int64) & ((1 << _EPOCH_SHIFT) - 1)
+    return int(low.sum().item())
+
+
+def small_pending_count(device: torch.device) -> int:
+    """Weight of unfinished small-batch launches on ``device`` (synchronises).
+
+    Reads adapter g's launch counter, int32 words [32 g, 32 g + 1] of the
+    sync buffer (one 128-byte line per adapter, g = 1..64), and returns
+    ``pending_from_counters`` of them: 0 after every completed call."""
+    return pending_from_sync(small_sync_buffer(device))
+
+
+def pending_from_sync(sync: torch.Tensor) -> int:
+    """``pending_from_counters`` of the counters held in a sync buffer
+    (int32 words; adapter g's counter is the int64 at int32 word 32 g)."""
+    words = sync.view(torch.int64)
+    return pending_from_counters(words[_SYNC_LINE // 2::_SYNC_LINE // 2])
 
 
 def small_reset(device: torch.device) -> None:
@@ -512,8 +575,14 @@ def small_reset(device: torch.device) -> None:
 # ---------------------------------------------------------------------------
 # Shrink / expand / fused apply
 # ---------------------------------------------------------------------------
-def shrink(x: torch.Tensor, segments: Segments, packed: PackedAdapters, z: torch.Tensor | None = None) -> torch.Tensor:
-    """z[slot, s*r_g + j] = x[perm[slot]] . A_{g,s}[j] (compact, slot-major)."""
+def shrink(x: torch.Tensor, segments: Segments, packed: PackedAdapters, z: torch.Tensor | None = None,
+           partials_only: bool = False) -> torch.Tensor | None:
+    """z[slot, s*r_g + j] = x[perm[slot]] . A_{g,s}[j] (compact, slot-major).
+
+    ``partials_only``: when the hidden dimension is split, write only the fp32
+    split-K partials to the per-device workspace (the shrink half of
+    ``switched_lora_``) and return None; raises if this shape is not split.
+    """
     _require_cuda(x)
     x2 = x.reshape(-1, x.shape[-1])
     if x2.stride(-1) != 1:
@@ -525,15 +594,17 @@ def shrink(x: torch.Tensor, segments: Segments, packed: PackedAdapters, z: torch
         raise ValueError("x shape does not match the segments / adapters")
     _check_segments(segments, packed)
     zw = packed.num_slices * packed.max_rank
-    if z is None:
+    if partials_only:
+        z = None
+    elif z is None:
         z = torch.empty(max(T, 1), zw, dtype=x2.dtype, device=x2.device)
     elif z.dtype != x2.dtype or z.stride(-1) != 1 or z.dim() != 2 or z.shape[0] < T or z.shape[1] < zw:
         raise ValueError("z must be a [T, >= S*max_rank] buffer of x's dtype with unit column stride")
     ws = shrink_workspace(T, H, packed.num_slices, packed.num_adapters, packed.max_rank, x2.device)
     _lib.call("gs_shrink", _dtype_code(x2), x2.data_ptr(), x2.stride(0), T, H, packed.a_pack.data_ptr(),
               packed.a_off.data_ptr(), packed.ranks.data_ptr(), packed.num_slices, packed.num_adapters,
-              packed.max_rank, segments.seg_offsets.data_ptr(), segments.perm.data_ptr(), z.data_ptr(), z.stride(0),
-              ws.data_ptr(), ws.numel(), _lib.stream_ptr(x2.device))
+              packed.max_rank, segments.seg_offsets.data_ptr(), segments.perm.data_ptr(), _lib.ptr(z),
+              zw if z is None else z.stride(0), ws.data_ptr(), ws.numel(), _lib.stream_ptr(x2.device))
     return z
 
 
@@ -589,6 +660,8 @@ def _call_small(x2, y2, packed, eff_ids=None, req=None, pos=None, cu=None, off=N
               packed.a_pack.data_ptr(), i64(packed.a_off_host), packed.b_pack.data_ptr(), i64(packed.b_off_host),
               _i32_array(packed.ranks_host), packed.num_adapters, packed.max_rank, ws.data_ptr(), ws.numel(),
               sync.data_ptr(), sync.numel() * 4, int(row_split), speculate, _lib.stream_ptr(x2.device))
+    if _CHECK_EACH_CALL and not torch.cuda.is_current_stream_capturing():
+        check(x2.device)
 
 
 def switched_lora_routed_(y: torch.Tensor, x: torch.Tensor, adapter_ids: torch.Tensor, packed: PackedAdapters,
@@ -758,6 +831,11 @@ __all__ = [
     "small_workspace",
     "reserve_small_workspace",
     "small_status",
+    "SmallPathError",
+    "check",
+    "set_small_wait_limit",
+    "pending_from_counters",
+    "pending_from_sync",
     "small_pending_count",
     "small_reset",
     "shrink_workspace",

@@ -24,8 +24,8 @@ expand+SwiGLU op.
 from __future__ import annotations
 
 import logging
-from collections import OrderedDict
 
+import numpy as np
 import torch
 from torch import nn
 
@@ -37,12 +37,98 @@ from .switched import _dtype_code, _i32_array
 logger = logging.getLogger(__name__)
 
 
+class _FusionPlan:
+    """Host-side tables of the fused layer, derived from the checkpoint.
+
+    Definitions (src/granite_switch/vllm/core/lora.py:353-492 and :637-657
+    compute the same tables):
+
+    * adapter ``a`` (0-based) is *applicable* iff some value in the first
+      ``rank[a]`` rows of its lora_A is nonzero in some slice;
+    * its *tier* is ``promote_rank(rank[a])``;
+    * kernel-local numbering: tiers in ascending order, and inside a tier the
+      applicable adapters in ascending index -- ``order`` lists (a, tier) in
+      that numbering, ``remap[a + 1]`` is a's kernel-local id (0 = none);
+    * ``na[t]`` counts the adapters of tier ``SUPPORTED_RANKS[t]``;
+    * shrink columns of x_ext follow the N base columns tier by tier, each
+      adapter taking S * tier columns (slice-major), so slice s of tier t
+      starts at ``slice_col_r[s][t] = N + sum_{t' < t} na[t'] S r_t' + s r_t``;
+    * ``tile_slice[j]`` is the slice holding output column ``j * block_n``.
+    """
+
+    def __init__(self, A_slices, ranks, output_slices, block_n):
+        NA, _, stored, _ = A_slices[0].shape
+        dev = A_slices[0].device
+        rk = torch.as_tensor([int(r) for r in ranks], device=dev)
+        live = torch.zeros(NA, stored, dtype=torch.bool, device=dev)
+        for A in A_slices:
+            live |= A[:, 0].ne(0).any(dim=-1)
+        within = torch.arange(stored, device=dev).unsqueeze(0) < rk.unsqueeze(1)
+        applicable = (live & within).any(dim=1).tolist()          # the one host sync
+        self.tier = [promote_rank(int(r)) for r in ranks]
+        self.order = [(a, r) for r in SUPPORTED_RANKS for a in range(NA) if applicable[a] and self.tier[a] == r]
+        self.remap = [0] * (NA + 1)
+        for local, (a, _) in enumerate(self.order, start=1):
+            self.remap[a + 1] = local
+        self.na = tuple(sum(1 for _, r in self.order if r == t) for t in SUPPORTED_RANKS)
+        self.S = len(output_slices)
+        self.bounds = [0] + list(np.cumsum(output_slices, dtype=np.int64).tolist())
+        self.n_total = int(self.bounds[-1])
+        self.tier_base = (self.n_total + np.concatenate(
+            [[0], np.cumsum([n * self.S * r for n, r in zip(self.na, SUPPORTED_RANKS)])[:-1]])).astype(np.int64)
+        self.slice_col_r = (self.tier_base[None, :]
+                            + np.arange(self.S)[:, None] * np.asarray(SUPPORTED_RANKS)[None, :]).tolist()
+        starts = np.arange(-(-self.n_total // block_n)) * block_n
+        self.tile_slice = (np.searchsorted(np.asarray(self.bounds), starts, side="right") - 1).tolist()
+
+    @staticmethod
+    def _rows(mat, r):
+        """The first r rows of ``mat``, zero rows appended past its end."""
+        if mat.shape[0] >= r:
+            return mat[:r]
+        return torch.cat([mat, mat.new_zeros(r - mat.shape[0], *mat.shape[1:])])
+
+    def lora_A_by_tier(self, A_slices) -> dict:
+        """{tier: [n_t, S, tier, K]} in kernel-local order (build_w_ext's input)."""
+        out = {}
+        for r in SUPPORTED_RANKS:
+            members = [a for a, t in self.order if t == r]
+            if members:
+                out[r] = torch.stack([torch.stack([self._rows(A[a, 0], r) for A in A_slices]) for a in members])
+        return out
+
+    def lb_packed(self, B_slices) -> torch.Tensor:
+        """Every kernel-local adapter's [N, tier] lora_B (slices stacked along N,
+        rank contiguous), concatenated in kernel-local order."""
+        parts = [torch.cat([self._rows(B[a, 0].t(), r).t() for B in B_slices]).reshape(-1) for a, r in self.order]
+        if not parts:
+            return B_slices[0].new_zeros(8)
+        return torch.cat(parts).contiguous()
+
+    def segment_tables(self, NA):
+        """Per global adapter id g: its tier rank, the element offset of its
+        lora_B block in lb_packed, and its first shrink column in x_ext (all 0
+        when g is not applicable)."""
+        rank, boff, zoff = [0] * (NA + 1), [0] * (NA + 1), [0] * (NA + 1)
+        b = 0
+        seen = [0] * len(SUPPORTED_RANKS)
+        for a, r in self.order:
+            t = SUPPORTED_RANKS.index(r)
+            rank[a + 1] = r
+            boff[a + 1] = b
+            zoff[a + 1] = int(self.tier_base[t]) + seen[t] * self.S * r
+            seen[t] += 1
+            b += self.n_total * r
+        return rank, boff, zoff
+
+
 class SwitchedLoRALinear(nn.Module):
     """Fused switched-LoRA linear layer (reference: vllm/core/lora.py:40-130 for the layout)."""
 
     _lora_ctx = None
-    # x . w_ext^T through gs_gemm_bf16_tn (True) or torch.mm (False); the
-    # library GEMM is faster at every measured workload shape
+    # x . w_ext^T through this library's MFMA GEMM gs_gemm_bf16_tn (True) or
+    # torch.mm, i.e. hipBLASLt (False, the default: measured faster at every
+    # workload shape)
     native_gemm = False
 
     def __init__(self, base_layer: nn.Module, num_adapters: int, max_lora_rank: int, num_slices: int = 1,
@@ -55,10 +141,17 @@ class SwitchedLoRALinear(nn.Module):
         self.max_lora_rank = max_lora_rank
         self.num_slices = num_slices
         self.fuse_swiglu = fuse_swiglu
-        if not hasattr(base_layer, "weight"):
+        if hasattr(base_layer, "weight"):
+            out_features, in_features = base_layer.weight.shape
+            device, dtype = base_layer.weight.device, base_layer.weight.dtype
+        elif hasattr(base_layer, "qweight"):
+            # a quantized base layer: sizes from the layer, fp16 adapters, as
+            # src/granite_switch/vllm/core/lora.py:157-161; finalize_weights
+            # needs the dense weight and says so
+            in_features, out_features = base_layer.input_size, base_layer.output_size
+            device, dtype = base_layer.qweight.device, torch.float16
+        else:
             raise ValueError(f"Unsupported base layer type: {type(base_layer)}")
-        out_features, in_features = base_layer.weight.shape
-        device, dtype = base_layer.weight.device, base_layer.weight.dtype
         self.in_features = in_features
         self.out_features = out_features
         self._device = device
@@ -129,143 +222,84 @@ class SwitchedLoRALinear(nn.Module):
         return weight_loader
 
     # -- load time -----------------------------------------------------------
-    def finalize_weights(self, adapter_ranks: list, block_n: int | None = None):
-        """Checkpoint layout -> fused layout (vllm/core/lora.py:299-538).
+    def _checkpoint_slices(self):
+        if self.num_slices == 1:
+            return [self.lora_A.data], [self.lora_B.data]
+        return [p.data for p in self.lora_A_slices], [p.data for p in self.lora_B_slices]
 
-        Applicability scan (one host sync), rank promotion with zero padding,
-        stable ascending-rank order -> ``remap_table``, ``w_ext``, packed lora_B,
-        ``tile_to_slice``, ``slice_col_r``; plus the per-global-adapter tables
-        the segment expand reads (rank, lora_B offset, shrink column in x_ext).
+    def finalize_weights(self, adapter_ranks: list, block_n: int | None = None):
+        """Checkpoint layout -> the fused layout the expand ops read.
+
+        Produces the tables of src/granite_switch/vllm/core/lora.py:299-538
+        (see ``_FusionPlan`` for their definitions): ``remap_table``,
+        ``w_ext`` (base rows, then every kernel-local adapter's lora_A rows),
+        ``_lb_packed``, ``tile_to_slice``, ``slice_col_r``, ``_na``; plus the
+        per-global-adapter tables of the segment expand (rank, lora_B offset,
+        first shrink column in x_ext).  One host sync (the applicability scan).
+        The checkpoint parameters are emptied afterwards.
         """
         if self._finalized:
             return
-        if block_n is None:
-            block_n = BLOCK_N
-        device, dtype = self._device, self._dtype
-        NA, S = self.num_adapters, self.num_slices
-        if S == 1:
-            lora_A_all = [self.lora_A.data]
-            lora_B_all = [self.lora_B.data]
-        else:
-            lora_A_all = [p.data for p in self.lora_A_slices]
-            lora_B_all = [p.data for p in self.lora_B_slices]
-        max_rank = lora_A_all[0].shape[2]
-        ranks_t = torch.tensor(adapter_ranks, device=device)
-        rank_mask = torch.arange(max_rank, device=device)[None, :] < ranks_t[:, None]
-        applicable_t = torch.zeros(NA, dtype=torch.bool, device=device)
-        for s in range(S):
-            nz = lora_A_all[s][:, 0, :, :].ne(0).any(dim=-1)
-            applicable_t |= (nz & rank_mask).any(dim=1)
-        applicable = applicable_t.tolist()
-        applicable_adapters = [i for i in range(NA) if applicable[i]]
+        if not hasattr(self.base_layer, "weight"):
+            raise NotImplementedError(
+                f"{type(self.base_layer).__name__} is quantized (qweight): the fused layout stacks lora_A under a "
+                "dense base weight (w_ext = [W; A...]), so dequantize the base layer to bf16 first")
+        bn = BLOCK_N if block_n is None else int(block_n)
+        if any(w % bn for w in self.output_slices):
+            raise AssertionError(f"block_n={bn} must divide the width of every output slice, got {self.output_slices}")
+        A_ck, B_ck = self._checkpoint_slices()
+        plan = _FusionPlan(A_ck, adapter_ranks, self.output_slices, bn)
+        dev = self._device
 
-        eff_ranks = [promote_rank(int(r)) for r in adapter_ranks]
-        pad_to = max((eff_ranks[i] for i in applicable_adapters), default=0)
-        if pad_to > max_rank:
-            pad = pad_to - max_rank
-            lora_A_all = [torch.nn.functional.pad(a, (0, 0, 0, pad)) for a in lora_A_all]
-            lora_B_all = [torch.nn.functional.pad(b, (0, pad)) for b in lora_B_all]
-        adapter_ranks = eff_ranks
+        self.register_buffer("remap_table", torch.tensor(plan.remap, dtype=torch.long, device=dev), persistent=False)
+        W = self.base_layer.weight.data
+        self.register_buffer("w_ext", build_w_ext(W, plan.lora_A_by_tier(A_ck)), persistent=False)
+        self._N_total = plan.n_total
+        self.base_layer.weight.data = self.w_ext[:plan.n_total]          # the base rows are a view of w_ext
+        self.register_buffer("_lb_packed", plan.lb_packed(B_ck), persistent=False)
+        self.register_buffer("tile_to_slice", torch.tensor(plan.tile_slice, dtype=torch.int32, device=dev),
+                             persistent=False)
+        self.register_buffer("slice_col_r", torch.tensor(plan.slice_col_r, dtype=torch.int32, device=dev),
+                             persistent=False)
+        self._na = plan.na
+        self._S = self.num_slices
+        self._block_n = bn
+        self._num_applicable = len(plan.order)
+        self._block_cfg_key = (self.in_features, plan.n_total, self._num_applicable)
 
-        rank_order = sorted(applicable_adapters, key=lambda i: adapter_ranks[i])
-        remap = torch.zeros(NA + 1, dtype=torch.long, device=device)
-        for k, orig in enumerate(rank_order):
-            remap[orig + 1] = k + 1
-        self.register_buffer("remap_table", remap, persistent=False)
-
-        tiers = OrderedDict()
-        for orig in rank_order:
-            tiers.setdefault(adapter_ranks[orig], []).append(orig)
-
-        lora_A_by_rank = {}
-        for rank, idxs in tiers.items():
-            lora_A_by_rank[rank] = torch.stack(
-                [torch.stack([lora_A_all[s][oi, 0, :rank, :] for s in range(S)], dim=0) for oi in idxs], dim=0)
-        W_base = self.base_layer.weight.data
-        w_ext = build_w_ext(W_base, lora_A_by_rank)
-        self.register_buffer("w_ext", w_ext, persistent=False)
-        N_total = W_base.shape[0]
-        self._N_total = N_total
-        self.base_layer.weight.data = self.w_ext[:N_total]
-        del W_base
-
-        tier_info, lora_B_merged = {}, {}
-        for rank, idxs in tiers.items():
-            lora_B_merged[rank] = torch.stack(
-                [torch.cat([lora_B_all[s][oi, 0, :, :rank] for s in range(S)], dim=0) for oi in idxs], dim=0)
-            tier_info[rank] = len(idxs)
-        self._num_applicable = sum(tier_info.values())
-        self._block_cfg_key = (self.in_features, N_total, self._num_applicable)
-
-        self._block_n = block_n
-        assert all(n_s % block_n == 0 for n_s in self.output_slices), (
-            f"block_n={block_n} must divide every output slice: {self.output_slices}")
-        num_tiles_n = (N_total + block_n - 1) // block_n
-        cum = [0]
-        for n_s in self.output_slices:
-            cum.append(cum[-1] + n_s)
-        tile_slice = torch.zeros(num_tiles_n, dtype=torch.int32)
-        for t in range(num_tiles_n):
-            c = t * block_n
-            for s in range(S):
-                if cum[s] <= c < cum[s + 1]:
-                    tile_slice[t] = s
-                    break
-        self.register_buffer("tile_to_slice", tile_slice.to(device), persistent=False)
-
-        tier_col_bases, off = [], N_total
-        for r in SUPPORTED_RANKS:
-            tier_col_bases.append(off)
-            off += tier_info.get(r, 0) * S * r
-        self.register_buffer("slice_col_r", torch.tensor(
-            [[tier_col_bases[t] + s * SUPPORTED_RANKS[t] for t in range(6)] for s in range(S)],
-            dtype=torch.int32, device=device), persistent=False)
-
-        self._na = tuple(tier_info.get(r, 0) for r in SUPPORTED_RANKS)
-        self._S = S
-        parts = [lora_B_merged[r].reshape(-1) for r in SUPPORTED_RANKS if r in lora_B_merged]
-        lb = torch.cat(parts) if parts else torch.zeros(8, device=device, dtype=dtype)
-        self.register_buffer("_lb_packed", lb.contiguous(), persistent=False)
-
-        # per-GLOBAL-adapter tables for the segment expand (0 = not applicable)
-        g_rank = [0] * (NA + 1)
-        g_boff = [0] * (NA + 1)
-        g_zoff = [0] * (NA + 1)
-        lb_off = 0
-        for t, r in enumerate(SUPPORTED_RANKS):
-            for idx, orig in enumerate(tiers.get(r, [])):
-                g = orig + 1
-                g_rank[g] = r
-                g_boff[g] = lb_off + idx * N_total * r
-                g_zoff[g] = tier_col_bases[t] + idx * S * r
-            lb_off += tier_info.get(r, 0) * N_total * r
-        self.register_buffer("_seg_ranks", torch.tensor(g_rank, dtype=torch.int32, device=device), persistent=False)
-        self._seg_boff = torch.tensor(g_boff, dtype=torch.int64, device=device)
-        self._seg_zoff = torch.tensor(g_zoff, dtype=torch.int32, device=device)
-        self._seg_max_rank = max([16] + g_rank)
-        self._slice_bounds = _i32_array(cum)
+        seg_rank, seg_boff, seg_zoff = plan.segment_tables(self.num_adapters)
+        self.register_buffer("_seg_ranks", torch.tensor(seg_rank, dtype=torch.int32, device=dev), persistent=False)
+        self._seg_boff = torch.tensor(seg_boff, dtype=torch.int64, device=dev)
+        self._seg_zoff = torch.tensor(seg_zoff, dtype=torch.int32, device=dev)
+        self._seg_max_rank = max([16] + seg_rank)
+        self._slice_bounds = _i32_array(plan.bounds)
 
         if self.fuse_swiglu:
-            assert S == 2 and self.output_slices[0] == self.output_slices[1], (
-                "fuse_swiglu requires the merged 2-slice (gate, up) layout with "
-                f"equal widths; got S={S}, output_slices={self.output_slices}")
-            assert getattr(self.base_layer, "bias", None) is None, (
-                "fuse_swiglu does not support a biased gate/up projection")
-            self._H = N_total // 2
+            gate, up = (self.output_slices + (None, None))[:2]
+            if self.num_slices != 2 or gate != up:
+                raise AssertionError(f"fuse_swiglu needs two equal (gate, up) slices, got {self.output_slices}")
+            if getattr(self.base_layer, "bias", None) is not None:
+                raise AssertionError("fuse_swiglu: the gate/up projection must have no bias")
+            self._H = plan.n_total // 2
 
+        bias = getattr(self.base_layer, "bias", None)
         self._fused_bias = None
         self._output_bias = None
-        if getattr(self.base_layer, "bias", None) is not None:
-            if not getattr(self.base_layer, "skip_bias_add", False):
-                self._fused_bias = self.base_layer.bias.data
+        if bias is not None:
+            if getattr(self.base_layer, "skip_bias_add", False):
+                self._output_bias = bias          # the caller adds it (vLLM's skip_bias_add contract)
             else:
-                self._output_bias = self.base_layer.bias
+                self._fused_bias = bias.data
 
-        ckpt = [self.lora_A, self.lora_B] if S == 1 else [*self.lora_A_slices, *self.lora_B_slices]
-        for p in ckpt:
+        for p in self._checkpoint_params():
             p.requires_grad_(False)
             p.data = p.data.new_empty(0)
         self._finalized = True
+
+    def _checkpoint_params(self):
+        if self.num_slices == 1:
+            return [self.lora_A, self.lora_B]
+        return [*self.lora_A_slices, *self.lora_B_slices]
 
     # -- forward -------------------------------------------------------------
     def forward(self, x: torch.Tensor):

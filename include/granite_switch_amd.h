@@ -35,6 +35,13 @@
  *   gs_switch_lora_expand_swiglu
  *                          torch.ops.granite_switch.switch_lora_expand_swiglu
  *                          (lora_ops.py:82-113,204-214; switch_lora_kernel.py:809-857)
+ *   gs_switch_lora_shrink_expand
+ *                          torch.ops.granite_switch.switch_lora_shrink_expand, the
+ *                          Shadow-Residual W_cross shunt's W-less expand
+ *                          (lora_ops.py:137-226; switch_lora_kernel.py:883-1146)
+ *   gs_split_adapter_indices
+ *                          granite_switch.probe_routing.split_adapter_indices
+ *                          (src/granite_switch/probe_routing.py:36-58)
  *   gs_gemm_bf16_tn        the layer's one GEMM x_ext = x . w_ext^T over the base
  *                          weight stacked with every adapter's lora_A rows
  *                          (src/granite_switch/vllm/core/lora.py:544;
@@ -90,6 +97,21 @@ int gs_build_segments(const int64_t* req_ids, const int64_t* positions, const in
                       int32_t* eff_ids, int32_t* seg_offsets, int32_t* perm, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Probe-slot split of the per-token index stream (reference ids, 0 = base).
+ *
+ * kind_lut [lut_len] bytes (torch.bool): entry i != 0 marks adapter index i as
+ * an activation-probe slot (build_adapter_kind_lut; entry 0, base, is 0).
+ * lora_indices[t] = 0 where adapter_indices[t] is a probe, else the index;
+ * probe_indices[t] = the index where it is a probe, else 0.  Either output may
+ * be NULL.  Indices outside [0, lut_len) are not probes (the reference's
+ * table lookup would reject them).  adapter_indices and both outputs have
+ * element size idx_bytes (4 or 8).  Limits: 1 <= lut_len <= GS_MAX_ADAPTERS+1.
+ * ---------------------------------------------------------------------- */
+int gs_split_adapter_indices(const uint8_t* kind_lut, int32_t lut_len, const void* adapter_indices,
+                             int32_t idx_bytes, int64_t num_tokens, void* lora_indices, void* probe_indices,
+                             void* stream);
+
+/* ------------------------------------------------------------------------
  * Latest-wins routing from control tokens (per sequence, across chunks).
  *
  * out_ids[t] = the adapter fired by the most recent control token at or before
@@ -129,7 +151,10 @@ int64_t gs_shrink_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t nu
 
 /* z[slot, s*r_g + j] = sum_k x[perm[slot], k] * lora_A_{g,s}[j, k] for every
  * active slot (slot < seg_offsets[num_adapters]) whose adapter is applicable.
- * x [T, hidden] (ld ldx); z [T, ldz] with ldz >= S*max_rank; same dtype. */
+ * x [T, hidden] (ld ldx); z [T, ldz] with ldz >= S*max_rank; same dtype.
+ * When the hidden dimension is split (gs_shrink_workspace_bytes > 256), z
+ * may be NULL: only the fp32 partials [KS][T][S*max_rank] are written to the
+ * workspace, the shrink half of gs_switched_lora. */
 int gs_shrink(int32_t dtype, const void* x, int64_t ldx, int64_t num_tokens, int32_t hidden, const void* a_pack,
               const int64_t* a_off, const int32_t* ranks, int32_t num_slices, int32_t num_adapters,
               int32_t max_rank, const int32_t* seg_offsets, const int32_t* perm, void* z, int64_t ldz,
@@ -178,7 +203,9 @@ int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t
  * epoch-tagged partial sums; any size change may reuse the same buffer).
  * sync: gs_small_sync_bytes() bytes, 8-byte aligned, ZEROED before the first
  * call: int32 word 2 is an error word whose bit 0 means an expand workgroup
- * gave up waiting (20 ms) and that call's output is wrong; int32 words
+ * gave up waiting for its shrink partials (gs_small_set_wait_limit) and that
+ * call's output is wrong -- callers read it at a point that already
+ * synchronises and treat a nonzero word as a failed call; int32 words
  * [32*g, 32*g + 1] hold adapter g's 64-bit launch counter (each launch with
  * tokens for g adds 2^20; bits 20 and up are g's epoch, the tag of its
  * partials).  Zeroing sync again requires zeroing the workspace too.  Calls
@@ -199,6 +226,16 @@ int64_t gs_small_workspace_bytes(int32_t dtype, int64_t num_tokens, int32_t hidd
                                  int32_t num_adapters, int32_t max_rank, int32_t out_total,
                                  const int32_t* slice_bounds);
 int64_t gs_small_sync_bytes(void);
+/* Process-wide bound on the expand workgroups' wait: each gives up after
+ * `polls` looks at a group of its shrink partials (a look is one coherent
+ * load round trip plus a short sleep), sets bit 0 of the error word and
+ * finishes, so every launch ends.  The bound counts looks, not time, so a
+ * preempted queue does not use it up.  polls < 0 restores the default
+ * (200000, tens to hundreds of milliseconds); 0 never looks and always
+ * reports the error (a test hook: the launch still completes normally).
+ * Returns the previous value.  Applies to launches made after the call.
+ * No counterpart in the reference (its kernels never wait on each other). */
+int64_t gs_small_set_wait_limit(int64_t polls);
 /* Workgroups of one gs_switched_lora_small launch for this shape and row split
  * (producers + consumers; 0 for arguments outside the limits).  No
  * counterpart in the reference: this library's path choice uses it -- the
@@ -251,6 +288,22 @@ int gs_switch_lora_expand_swiglu(void* out, int64_t stride_om, int64_t stride_on
                                  int32_t idx_bytes, const int64_t* bitmask, int64_t stride_bm,
                                  const void* lb_packed, const int32_t* slice_col_r, const int32_t* na, int32_t S,
                                  int32_t block_n, int32_t H, int32_t N, void* stream);
+
+/* Reference op: the W-less expand of the Shadow-Residual cross-stream shunt.
+ * out[m, n] = sum over the tier adapters present in m's 32-row tile of
+ * shrink[m, :r] . lb[n, :r] for a row whose kernel-local id selects that
+ * adapter, 0 for base rows and for every row of a tile whose bitmask is 0;
+ * out[:M, :N] is written in full (the reference zeroes out first and stores
+ * the delta of the tiles it does not skip).  x_ext [M, >= shrink cols] holds
+ * only shrink columns (slice_col_r bases start at 0); other arguments as for
+ * gs_switch_lora_expand.  out_dtype GS_DTYPE_BF16 or GS_DTYPE_FP32, row
+ * stride stride_om >= N (elements), stride_on == 1, rows 16-byte aligned. */
+int gs_switch_lora_shrink_expand(void* out, int32_t out_dtype, int64_t stride_om, int64_t stride_on,
+                                 const void* x_ext, int64_t stride_m, int64_t stride_n, int64_t M,
+                                 const void* adapter_indices, int32_t idx_bytes, const int64_t* bitmask,
+                                 int64_t stride_bm, const void* lb_packed, const int32_t* tile_slice,
+                                 const int32_t* slice_col_r, const int32_t* na, int32_t S, int32_t block_n, int32_t N,
+                                 void* stream);
 
 /* ------------------------------------------------------------------------
  * Dense bf16 GEMM C[M,N] = A[M,K] . B[N,K]^T with fp32 accumulation and one

@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import os
 import statistics
+import subprocess
 import time
 
 import torch
@@ -39,23 +40,59 @@ def hf_loop(out: torch.Tensor, x: torch.Tensor, ids: torch.Tensor, lora_A_slices
     return out
 
 
-def cpu_threads() -> int:
+def _cgroup_cpu_quota() -> float | None:
+    """CPUs granted by the cgroup v2 quota (``cpu.max``), or None when unlimited."""
     try:
-        n = len(os.sched_getaffinity(0))
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota == "max":
+            return None
+        return float(quota) / float(period)
+    except (OSError, ValueError):
+        return None
+
+
+def host_cpu() -> dict:
+    """The host's CPU as lscpu reports it, plus what this process may use.
+
+    ``affinity``: CPUs in this process's affinity mask; ``quota``: CPUs its
+    cgroup grants (None = no limit); ``threads``: the threads the baseline runs
+    on -- every CPU it may run on, capped by the quota (more threads than the
+    quota only queue for it).
+    """
+    info = {"model": "unknown", "sockets": None, "cores_per_socket": None, "threads_per_core": None,
+            "logical_cpus": os.cpu_count()}
+    try:
+        out = subprocess.run(["lscpu"], stdout=subprocess.PIPE, stderr=subprocess.DEVNULL, text=True,
+                             timeout=10).stdout
+        keys = {"Model name": "model", "Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket",
+                "Thread(s) per core": "threads_per_core", "CPU(s)": "logical_cpus"}
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k in keys:
+                v = v.strip()
+                info[keys[k]] = v if keys[k] == "model" else int(v) if v.isdigit() else v
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+        affinity = os.cpu_count() or 1
+    quota = _cgroup_cpu_quota()
+    threads = affinity if quota is None else max(1, min(affinity, int(quota)))
+    info.update(affinity=affinity, quota=quota, threads=threads)
+    if isinstance(info["sockets"], int) and isinstance(info["cores_per_socket"], int):
+        info["physical_cores"] = info["sockets"] * info["cores_per_socket"]
+    return info
+
+
+def cpu_threads() -> int:
+    return host_cpu()["threads"]
 
 
 def cpu_model() -> str:
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
+    return str(host_cpu()["model"])
 
 
 def time_modules(modules, ids: torch.Tensor, budget_s: float = 12.0, min_runs: int = 5):

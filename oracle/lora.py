@@ -195,6 +195,35 @@ def switch_lora_expand_xext(x_ext, adapter_indices, bitmask, lb_packed, tile_sli
     return xe
 
 
+def shrink_expand_xext(x_ext, adapter_indices, bitmask, lb_packed, tile_slice, slice_col_r, na, S, block_n, N,
+                       block_m=32, dtype="bf16"):
+    """W-less expand: a fresh ``out[M, N]`` holding only the LoRA delta.
+
+    Restates src/granite_switch/kernels/switch_lora_kernel.py:883-1146: the
+    launcher zeroes ``out`` (:1117); tiles whose bitmask is 0 are skipped and
+    stay zero; every other tile gets the same per-adapter delta as the in-place
+    expand (shrink columns at ``slice_col_r[s][tier] + a*S*r``, which start at
+    0 because the cross weight has no base rows) and STORES it, rounded to the
+    output dtype, on every row of the tile -- a base row (id 0) selects no
+    adapter, so it stores an exact zero.
+    """
+    xe = np.asarray(x_ext, dtype=np.float64)
+    ids = np.asarray(adapter_indices, dtype=np.int64)
+    M = xe.shape[0]
+    bms = np.asarray(bitmask, dtype=np.int64).reshape(-1)
+    out = np.zeros((M, N), dtype=np.float64)
+    for pm in range((M + block_m - 1) // block_m):
+        if bms[pm] == 0:
+            continue
+        rows = np.arange(pm * block_m, min(M, (pm + 1) * block_m))
+        for pn in range((N + block_n - 1) // block_n):
+            cols = np.arange(pn * block_n, min(N, (pn + 1) * block_n))
+            s = int(tile_slice[pn])
+            d = _xext_tile_delta(xe, ids[rows], rows, bms[pm], lb_packed, slice_col_r[s], na, S, N, cols)
+            out[np.ix_(rows, cols)] = round_to(d, dtype)
+    return out
+
+
 def expand_swiglu_xext(x_ext, adapter_indices, bitmask, lb_packed, slice_col_r, na, S, H, N,
                        block_m=32, dtype="bf16"):
     """``out[M, H] = silu(gate + dgate) * (up + dup)``, always written.

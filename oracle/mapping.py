@@ -79,16 +79,43 @@ def alora_effective_ids(req_ids, positions, cu_seqlens, act_offsets) -> np.ndarr
     return out
 
 
-def split_adapter_indices(ids, probe_slots=()) -> np.ndarray:
-    """Zero the probe-slot ids out of the LoRA stream.
+def build_adapter_kind_lut(adapter_kinds):
+    """Bool table over adapter indices marking the probe slots, or None.
 
-    Restates src/granite_switch/probe_routing.py:36-58 (a no-op when no slot is
-    a probe).
+    Restates src/granite_switch/probe_routing.py:17-33: entry ``i`` is True
+    when adapter index ``i`` (slot ``i - 1``) is a probe; index 0 (base) is
+    always False; None when no slot is a probe (or no kinds are given).
     """
-    ids = np.asarray(ids, dtype=np.int64).copy()
-    for p in probe_slots:
-        ids[ids == p] = 0
-    return ids
+    if adapter_kinds is None or not any(k == "probe" for k in adapter_kinds):
+        return None
+    lut = np.zeros(len(adapter_kinds) + 1, dtype=bool)
+    for slot, kind in enumerate(adapter_kinds):
+        if kind == "probe":
+            lut[slot + 1] = True
+    return lut
+
+
+def split_adapter_indices(kind_lut, ids):
+    """Split one per-token index stream into (LoRA stream, probe stream).
+
+    Restates src/granite_switch/probe_routing.py:36-58: where the LUT marks an
+    index as a probe, the LoRA stream holds 0 and the probe stream the index;
+    elsewhere the LoRA stream holds the index and the probe stream 0.  With no
+    LUT the LoRA stream is the input and the probe stream all zeros.  Shapes
+    are preserved.
+    """
+    ids = np.asarray(ids, dtype=np.int64)
+    if kind_lut is None:
+        return ids.copy(), np.zeros_like(ids)
+    lut = np.asarray(kind_lut, dtype=bool)
+    lora = np.empty_like(ids)
+    probe = np.empty_like(ids)
+    for pos in np.ndindex(ids.shape):
+        v = int(ids[pos])
+        is_probe = bool(lut[v])            # the reference indexes the LUT directly
+        lora[pos] = 0 if is_probe else v
+        probe[pos] = v if is_probe else 0
+    return lora, probe
 
 
 def build_remap(applicable, adapter_ranks) -> tuple[np.ndarray, list[int], list[int]]:

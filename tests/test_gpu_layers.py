@@ -197,22 +197,43 @@ def test_hf_layers_match_hf_loop(dev, merged):
             B.copy_(torch.randn_like(B) * 0.1)
     x = torch.randn(3, 40, K, device=dev)
     ids = torch.randint(0, NA + 1, (3, 40), device=dev)
-    out = layer(x, ids)
-    base = layer.base_layer(x)
+    # the kernels compute no gradients: a forward autograd would track raises
+    with pytest.raises(RuntimeError, match="no gradients"):
+        layer(x, ids)
+    with torch.no_grad():
+        out = layer(x, ids)
+        base = layer.base_layer(x)
     torch.cuda.synchronize()
-    ref = olora.switched_lora_apply(_np(base).reshape(-1, sum(slices)), _np(x).reshape(-1, K),
-                                    ids.cpu().numpy().reshape(-1), [_np(a) for a in A_sl], [_np(b) for b in B_sl],
-                                    slices, None, "fp32")
-    _close(_np(out).reshape(-1, sum(slices)), ref, 1e-4, "hf layer")
+
+    def ref_of(b_slices):
+        return olora.switched_lora_apply(_np(base).reshape(-1, sum(slices)), _np(x).reshape(-1, K),
+                                         ids.cpu().numpy().reshape(-1), [_np(a) for a in A_sl],
+                                         [_np(b) for b in b_slices], slices, None, "fp32")
+
+    _close(_np(out).reshape(-1, sum(slices)), ref_of(B_sl), 1e-4, "hf layer")
+    # without freeze() the pack is cached until a weight changes
+    pack = layer._auto_pack
+    with torch.no_grad():
+        layer(x, ids)
+        assert layer._auto_pack is pack
+        B_sl[0].mul_(2.0)                       # an in-place update moves the version counter
+        out_b = layer(x, ids)
+    assert layer._auto_pack is not pack
+    torch.cuda.synchronize()
+    _close(_np(out_b).reshape(-1, sum(slices)), ref_of(B_sl), 1e-4, "hf layer after a weight update")
+    with torch.no_grad():
+        B_sl[0].mul_(0.5)
     # frozen pack gives the same answer; context-passing indices too
     layer.freeze()
     layer._adapter_indices = ids
-    out2 = layer(x)
+    with torch.no_grad():
+        out2 = layer(x)
     torch.cuda.synchronize()
     assert torch.allclose(out2, out, atol=1e-6, rtol=1e-6)
     # all-base == base layer exactly
-    out3 = layer(x, torch.zeros_like(ids))
-    assert torch.equal(out3, layer.base_layer(x))
+    with torch.no_grad():
+        out3 = layer(x, torch.zeros_like(ids))
+        assert torch.equal(out3, layer.base_layer(x))
 
 
 def test_custom_ops_under_torch_compile(dev):

@@ -78,7 +78,7 @@ def test_switched_lora_full_config(dev, config):
 
 
 def test_switched_lora_prefill_config2(dev):
-    """Config 2 at full size; the oracle checks 768 sampled rows plus every base row's bits."""
+    """Config 2 at full size: every row against the oracle, base rows' bits, B-linearity."""
     wl = workloads.make_workload(2, dev)
     md = wl.modules[0]
     r = wl.routing
@@ -92,6 +92,14 @@ def test_switched_lora_prefill_config2(dev):
     _check_module(md, y, eff, rows, wl.dtype, hf_too=False)
     base = torch.tensor(eff == 0, device=dev)
     assert torch.equal(y[base], md.y[base]), "base rows were modified"
+    # every row against the oracle, in 1024-row blocks
+    A = [_np(a) for a in md.lora_A_slices]
+    B = [_np(b) for b in md.lora_B_slices]
+    for r0 in range(0, r.num_tokens, 1024):
+        blk = np.arange(r0, min(r.num_tokens, r0 + 1024))
+        ref = olora.switched_lora_apply(_np(md.y[r0:r0 + 1024]), _np(md.x[r0:r0 + 1024]), eff[blk], A, B,
+                                        md.spec.output_slices, md.spec.ranks, "bf16")
+        _close(_np(y[r0:r0 + 1024]), ref, TOL[wl.dtype], f"config 2 rows {r0}..")
     # size-independent property: the delta is linear in B -> doubling B doubles y - y0 (to rounding)
     d1 = (y.float() - md.y.float())[torch.tensor(act[:256], device=dev)]
     packed2 = switched.PackedAdapters.from_slices(md.lora_A_slices, [2 * b for b in md.lora_B_slices], md.spec.ranks)
@@ -101,7 +109,9 @@ def test_switched_lora_prefill_config2(dev):
     assert torch.allclose(d2, 2 * d1, atol=0.05, rtol=0.05)
 
 
-def test_switched_lora_config4_two_layers(dev):
+def test_switched_lora_config4_one_layer_eager(dev):
+    """One layer of the decoder step, eagerly, every projection on the shared
+    segments (the full 32-layer graph-captured step: test_gpu_step.py)."""
     wl = workloads.make_workload(4, dev, layers=1)
     r = wl.routing
     eff = omap.alora_effective_ids(r.req_ids, r.positions, r.cu_seqlens, r.act_offsets)

@@ -1,0 +1,139 @@
+"""GPU parity of the probe-slot split and the W-less (Shadow-Residual) expand.
+
+* ``probe_routing.split_adapter_indices`` through ``gs_split_adapter_indices``
+  against the reference's known answers (tests/unit/test_probe_routing.py)
+  and the oracle on random streams, bit-exact;
+* ``torch.ops.granite_switch.switch_lora_shrink_expand`` through
+  ``gs_switch_lora_shrink_expand`` against the oracle's restatement of the
+  reference kernel, on the reference test's cases
+  (tests/unit/test_wcross_shrink_kernel.py:151-214) with metadata packed by
+  hand the way that test packs it: bf16 |got - ref| <= 2e-2 + 2e-2 |ref|,
+  fp32 1e-5 + 1e-5 |ref|; base rows and skipped tiles exactly zero.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from granite_switch_amd import kernels, ops, probe_routing
+from oracle import lora as olora
+from oracle import mapping as omap
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+# -- probe-slot split ------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.int64, torch.int32])
+def test_split_adapter_indices_reference_kats(dev, kats, dtype):
+    for case in kats["probe_routing"]["split_cases"]:
+        _say(f"split {case['adapter_kinds']} {case['ids']} {dtype}")
+        lut = probe_routing.build_adapter_kind_lut(case["adapter_kinds"])
+        ids = torch.tensor(case["ids"], dtype=dtype, device=dev)
+        lora, probe = probe_routing.split_adapter_indices(lut, ids)
+        torch.cuda.synchronize()
+        assert lora.shape == ids.shape and probe.shape == ids.shape
+        assert lora.dtype == dtype and probe.dtype == dtype
+        assert lora.cpu().tolist() == case["lora"]
+        assert probe.cpu().tolist() == case["probe"]
+        if lut is None:
+            assert lora is ids                     # passes through untouched
+
+
+def test_kind_lut_reference_kats(kats):
+    for case in kats["probe_routing"]["lut_cases"]:
+        lut = probe_routing.build_adapter_kind_lut(case["adapter_kinds"])
+        assert (lut is None) if case["lut"] is None else lut.tolist() == case["lut"]
+
+
+@pytest.mark.parametrize("T,slots,seed", [(1, 3, 0), (4144, 24, 1), (70001, 256, 2)])
+def test_split_adapter_indices_random_matches_oracle(dev, T, slots, seed):
+    rng = np.random.default_rng(seed)
+    kinds = ["probe" if rng.random() < 0.3 else "lora" for _ in range(slots)]
+    kinds[0] = "probe"
+    lut = probe_routing.build_adapter_kind_lut(kinds)
+    ids_h = rng.integers(0, slots + 1, size=T)
+    _say(f"split random T={T} slots={slots}")
+    lora, probe = probe_routing.split_adapter_indices(lut, torch.tensor(ids_h, device=dev))
+    torch.cuda.synchronize()
+    lora_ref, probe_ref = omap.split_adapter_indices(omap.build_adapter_kind_lut(kinds), ids_h)
+    assert np.array_equal(lora.cpu().numpy(), lora_ref)
+    assert np.array_equal(probe.cpu().numpy(), probe_ref)
+
+
+# -- W-less expand -----------------------------------------------------------------
+def _wless_inputs(dev, ranks, ids, K, N, seed, scale=0.05):
+    """Adapters in ascending rank order (kernel-local ids 1.. in that order),
+    packed by hand as the reference test does; x_ext = x . w_ext_cross^T in bf16."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    A = [(torch.randn(r, K, generator=g, device=dev) * scale).to(torch.bfloat16) for r in ranks]
+    B = [(torch.randn(N, r, generator=g, device=dev) * scale).to(torch.bfloat16) for r in ranks]
+    w_ext = torch.cat(A, dim=0)                                   # no base rows
+    na = tuple(sum(1 for r in ranks if r == R) for R in omap.SUPPORTED_RANKS)
+    col = np.zeros((1, 6), dtype=np.int32)
+    run = 0
+    for k, R in enumerate(omap.SUPPORTED_RANKS):
+        col[0, k] = run
+        run += na[k] * R
+    lb = torch.cat([torch.stack([B[i] for i, r in enumerate(ranks) if r == R]).reshape(-1)
+                    for R in omap.SUPPORTED_RANKS if R in ranks]).contiguous()
+    ids_h = np.asarray(ids, dtype=np.int64)
+    M = ids_h.shape[0]
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    x_ext = torch.mm(x, w_ext.T).contiguous()
+    bm = np.zeros((M + 31) // 32, dtype=np.int64)
+    for m, a in enumerate(ids_h):
+        if a > 0:
+            bm[m // 32] |= np.int64(1) << np.int64(a - 1)
+    return dict(x_ext=x_ext, ids=torch.tensor(ids_h, device=dev), ids_h=ids_h, bm=torch.tensor(bm, device=dev),
+                bm_h=bm, lb=lb, tile_slice=torch.zeros(N // 32, dtype=torch.int32, device=dev),
+                scr=torch.tensor(col, device=dev), scr_h=col, na=na, M=M, N=N)
+
+
+CASES = [
+    ("single tier, mixed rows", (16,), [0, 1] * 20, 256, 64),
+    ("all-base tile", (16,), [0] * 32, 256, 64),
+    ("two tiers", (16, 32), [0, 1, 2, 2, 0, 1] * 8, 512, 128),
+    ("two adapters of one tier", (16, 16), [1, 2, 0, 1, 2, 0] * 8, 256, 64),
+    ("three tiers, ragged", (16, 32, 64, 128), [3] * 5 + [0] * 40 + [1, 2, 4] * 11, 384, 4096),
+]
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("name,ranks,ids,K,N", CASES)
+def test_shrink_expand_matches_oracle(dev, name, ranks, ids, K, N, out_dtype):
+    _say(f"W-less expand: {name}, out {out_dtype}")
+    d = _wless_inputs(dev, ranks, ids, K, N, seed=len(ids) + K)
+    out = torch.full((d["M"], N), 7.0, dtype=out_dtype, device=dev)     # stale contents must not survive
+    ops.op("switch_lora_shrink_expand")(out, d["x_ext"], d["ids"], d["bm"], d["lb"], d["tile_slice"], d["scr"],
+                                        *d["na"], 1, 32, N)
+    torch.cuda.synchronize()
+    dt = "bf16" if out_dtype == torch.bfloat16 else "fp32"
+    ref = olora.shrink_expand_xext(d["x_ext"].float().cpu().numpy(), d["ids_h"], d["bm_h"], d["lb"].float().cpu().numpy(),
+                                   np.zeros(N // 32, np.int32), d["scr_h"], d["na"], 1, 32, N, dtype=dt)
+    got = out.double().cpu().numpy()
+    tol = 2e-2 if out_dtype == torch.bfloat16 else 1e-5
+    err = np.abs(got - ref)
+    assert np.all(err <= tol + tol * np.abs(ref)), f"max abs err {err.max():.3e}"
+    base = d["ids_h"] == 0
+    assert np.all(got[base] == 0), "base rows must read back exactly zero"
+
+
+def test_shrink_expand_zeroes_a_larger_output_and_skips_zero_tiles(dev):
+    ranks, K, N = (32,), 256, 128
+    ids = [1] * 64
+    d = _wless_inputs(dev, ranks, ids, K, N, seed=3)
+    bm = d["bm"].clone()
+    bm[1] = 0                                   # second row tile marked empty: skipped, reads zero
+    out = torch.full((80, 160), -3.0, dtype=torch.bfloat16, device=dev)
+    kernels.switch_lora_shrink_expand(out, d["x_ext"], d["ids"], bm, d["lb"], d["tile_slice"], d["scr"], d["na"], 1,
+                                      32, N)
+    torch.cuda.synchronize()
+    o = out.float().cpu()
+    assert torch.count_nonzero(o[32:]) == 0 and torch.count_nonzero(o[:, N:]) == 0
+    assert torch.count_nonzero(o[:32, :N]) > 0

@@ -52,7 +52,7 @@ def _clean_handoff(dev):
     yield
     torch.cuda.synchronize()
     assert switched.small_status(dev) == 0, f"small-path error word {switched.small_status(dev)}"
-    assert switched.small_pending_count(dev) == 0, "a launch left an adapter's done count behind"
+    assert switched.small_pending_count(dev) == 0, "a launch was left half counted in an adapter's launch counter"
 
 
 def _check(md, y, eff, dtype):
@@ -340,3 +340,35 @@ def test_small_tile_groups(dev, row_split):
     _check(md, y, ids, torch.bfloat16)
     d = (y.float() - y_seg.float()).abs()
     assert bool((d <= 2.0 ** -7 * y_seg.float().abs().clamp_min(1.0)).all()), "small path vs segment path"
+
+
+def test_small_wait_limit_zero_reports_and_next_call_is_correct(dev):
+    """With the wait bound at 0 looks every consumer gives up at once: the
+    launch still ends, the error word is set and ``check`` raises.  After
+    ``small_reset`` (and the default bound) the next call is correct."""
+    wl = workloads.make_workload(1, dev)
+    md, r = wl.modules[0], wl.routing
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, md.spec.ranks)
+    args = (torch.tensor(r.req_ids, device=dev), pk, torch.tensor(r.positions, device=dev),
+            torch.tensor(r.cu_seqlens, device=dev), torch.tensor(r.act_offsets, device=dev))
+    _say("small path: wait bound 0 (forced give-up from the host)")
+    prev = switched.set_small_wait_limit(0)
+    try:
+        y = md.y.clone()
+        switched.switched_lora_routed_(y, md.x, *args, path="small")
+        torch.cuda.synchronize()
+    finally:
+        switched.set_small_wait_limit(prev)
+    assert switched.small_status(dev) & 1
+    with pytest.raises(switched.SmallPathError):
+        switched.check(dev)
+    assert switched.small_pending_count(dev) == 0          # consumers still add their shares
+    switched.small_reset(dev)
+    switched.check(dev)
+    _say("small path: default wait bound after reset")
+    y = md.y.clone()
+    switched.switched_lora_routed_(y, md.x, *args, path="small")
+    torch.cuda.synchronize()
+    switched.check(dev)
+    eff = omap.alora_effective_ids(r.req_ids, r.positions, r.cu_seqlens, r.act_offsets)
+    _check(md, y, eff, wl.dtype)

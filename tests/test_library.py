@@ -147,6 +147,44 @@ def test_vllm_finalize_tables_match_oracle():
     assert all(p.numel() == 0 for p in layer.lora_A_slices)
 
 
+def test_vllm_finalize_pads_ranks_promoted_past_storage():
+    """Stored rank 8 promotes to tier 16: the tier rows past the stored ones are zero."""
+    slices = (32,)
+    ranks = [8, 4, 8]
+    base = torch.nn.Linear(24, 32, bias=False)
+    layer = vllm_layers.SwitchedLoRALinear(base, 3, 8)
+    A, B = _fill(layer, ranks, seed=3, zero=(1,))
+    W = base.weight.data.clone().numpy()
+    layer.finalize_weights(ranks)
+    remap, order, eff = omap.build_remap(omap.applicability(A, ranks), ranks)
+    na, tile_slice, scr, tiers = omap.finalize_tables(slices, order, eff, 32)
+    assert layer.remap_table.tolist() == remap.tolist() == [0, 1, 0, 2]
+    assert layer._na == na == (2, 0, 0, 0, 0, 0)
+    np.testing.assert_array_equal(layer.w_ext.numpy(), omap.build_w_ext(W, A, tiers))
+    np.testing.assert_array_equal(layer._lb_packed.numpy(), omap.build_lb_packed(B, tiers))
+    assert layer.w_ext.shape == (32 + 2 * 16, 24)
+    assert layer._seg_ranks.tolist() == [0, 16, 0, 16]
+    assert layer._seg_zoff.tolist() == [0, 32, 0, 48]
+    assert layer._seg_boff.tolist() == [0, 0, 0, 32 * 16]
+
+
+def test_vllm_quantized_base_layer_is_refused_at_finalize():
+    class QLinear(torch.nn.Module):
+        input_size, output_size = 64, 32
+
+        def __init__(self):
+            super().__init__()
+            self.qweight = torch.zeros(8, 32, dtype=torch.int32)
+
+    layer = vllm_layers.SwitchedLoRALinear(QLinear(), 2, 16)
+    assert (layer.in_features, layer.out_features) == (64, 32)
+    assert layer.lora_A.dtype == torch.float16 and tuple(layer.lora_A.shape) == (2, 1, 16, 64)
+    with pytest.raises(NotImplementedError, match="dequantize"):
+        layer.finalize_weights([16, 16])
+    with pytest.raises(ValueError, match="Unsupported base layer"):
+        vllm_layers.SwitchedLoRALinear(torch.nn.ReLU(), 2, 16)
+
+
 def test_vllm_block_n_alignment_assert():
     base = torch.nn.Linear(16, 96 + 65, bias=False)
     layer = vllm_layers.SwitchedLoRALinear(base, 1, 16, num_slices=2, output_slices=(96, 65))
@@ -266,3 +304,29 @@ def test_small_path_plan_largest_group_hint(monkeypatch):
     assert switched.small_preferred(pk, 512, 4, largest_group=128) is True
     # a hint larger than the batch is clamped to it
     assert switched.small_row_split(pk, 512, 4, largest_group=10 ** 6) == switched.small_row_split(pk, 512, 4, 512)
+
+
+def test_pending_from_sync_reads_each_adapters_counter_low_bits():
+    """Adapter g's 64-bit launch counter sits at int32 words [32 g, 32 g + 1]
+    (low half first); an unfinished launch shows in its low 20 bits."""
+    sync = torch.zeros(int(_lib.load().gs_small_sync_bytes()) // 4, dtype=torch.int32)
+    counters = {1: 3 << 20,                       # three complete launches
+                5: (7 << 32) | (1 << 20) | 17,    # a high epoch, one launch half counted (17)
+                64: (2 << 20) | 5}                # last adapter line: 5 pending
+    for g, c in counters.items():
+        sync[32 * g] = np.int64(c & 0xFFFFFFFF).astype(np.uint32).view(np.int32)
+        sync[32 * g + 1] = np.int32(c >> 32)
+    sync[2] = 1                                   # the error word is not a counter
+    sync[0] = 123                                 # nor is line 0
+    assert switched.pending_from_sync(sync) == 17 + 5
+    assert switched.pending_from_counters(torch.tensor([0, 1 << 20, (9 << 20) + 3])) == 3
+
+
+def test_wait_limit_setter_round_trips():
+    prev = switched.set_small_wait_limit(7)
+    try:
+        assert switched.set_small_wait_limit(0) == 7
+        assert switched.set_small_wait_limit(None) == 0
+        assert switched.set_small_wait_limit(None) == prev        # None restores the default
+    finally:
+        switched.set_small_wait_limit(prev)

@@ -276,3 +276,211 @@ def test_planted_mistake_is_caught(monkeypatch):
     monkeypatch.setattr(olora, "switched_lora_apply", wrong)
     with pytest.raises(AssertionError):
         test_identity_closed_form({"lora_identity": {"in_features": 32, "out_features": 16, "rank": 8}})
+
+
+# -- applicability -------------------------------------------------------------
+def test_applicability_hand_cases():
+    """src/granite_switch/vllm/core/lora.py:353-362: any nonzero value in the
+    first r rows of lora_A, in any slice, makes an adapter applicable."""
+    NA, maxr, H = 5, 8, 6
+    A0 = np.zeros((NA, 1, maxr, H))
+    A1 = np.zeros((NA, 1, maxr, H))
+    A0[0, 0, 3, 2] = 1.0          # adapter 0: nonzero inside its rank (4) in slice 0
+    A0[1, 0, 5, 0] = 2.0          # adapter 1: nonzero only in row 5, past its rank (4)
+    A1[2, 0, 0, 5] = -1.0         # adapter 2: zero in slice 0, nonzero in slice 1
+    A0[3, 0, 0, 0] = 1.0          # adapter 3: rank 0 never applies
+    ranks = [4, 4, 4, 0, 8]       # adapter 4: all zero
+    assert omap.applicability([A0, A1], ranks) == [True, False, True, False, False]
+    # rank past the nonzero row: adapter 1 at rank 6 applies
+    assert omap.applicability([A0, A1], [4, 6, 4, 0, 8])[1] is True
+
+
+# -- probe routing -------------------------------------------------------------
+def test_probe_kind_lut_kats(kats):
+    for case in kats["probe_routing"]["lut_cases"]:
+        lut = omap.build_adapter_kind_lut(case["adapter_kinds"])
+        if case["lut"] is None:
+            assert lut is None
+        else:
+            assert lut.tolist() == case["lut"]
+
+
+def test_split_adapter_indices_kats(kats):
+    for case in kats["probe_routing"]["split_cases"]:
+        lut = omap.build_adapter_kind_lut(case["adapter_kinds"])
+        lora, probe = omap.split_adapter_indices(lut, case["ids"])
+        assert lora.tolist() == case["lora"], case
+        assert probe.tolist() == case["probe"], case
+
+
+def test_split_adapter_indices_partition():
+    """Every index lands in exactly one stream; probe streams hold only probe slots."""
+    rng = np.random.default_rng(9)
+    lut = omap.build_adapter_kind_lut(["lora", "probe", "lora", "probe", "probe"])
+    ids = rng.integers(0, 6, size=(7, 33))
+    lora, probe = omap.split_adapter_indices(lut, ids)
+    assert np.array_equal(lora + probe, ids)
+    assert np.all((lora == 0) | (probe == 0))
+    assert set(np.unique(probe).tolist()) <= {0, 2, 4, 5}
+    assert set(np.unique(lora).tolist()) <= {0, 1, 3}
+
+
+# -- shrink rows ---------------------------------------------------------------
+def test_shrink_rows_identity_closed_form():
+    """With A_a = eye(r, H) * 0.1 (a+1) (tests/shared/lora_cases.py:355-426),
+    slot k of adapter a holds 0.1 (a+1) x[perm[k], :r] in every slice."""
+    rng = np.random.default_rng(4)
+    NA, H, maxr, S = 4, 20, 8, 3
+    ranks = [8, 4, 0, 6]
+    A = []
+    for s in range(S):
+        a_s = np.zeros((NA, 1, maxr, H))
+        for a in range(NA):
+            a_s[a, 0, :ranks[a]] = np.eye(ranks[a], H) * 0.1 * (a + 1)
+        A.append(a_s)
+    T = 30
+    x = rng.standard_normal((T, H))
+    ids = rng.integers(0, NA + 1, size=T)
+    seg, perm = omap.build_segments(ids, NA)
+    z = olora.shrink_rows(x, perm, seg, A, ranks, S * maxr)
+    for g in range(1, NA + 1):
+        r = ranks[g - 1]
+        for k in range(seg[g - 1], seg[g]):
+            t = perm[k]
+            for s in range(S):
+                exp = 0.1 * g * x[t, :r]
+                np.testing.assert_allclose(z[k, s * r:(s + 1) * r], exp, rtol=1e-12, atol=1e-12)
+            assert np.all(z[k, S * r:] == 0)
+
+
+def test_per_token_reference_identity_closed_form(kats):
+    k = kats["lora_identity"]
+    IN, OUT, R, NA = k["in_features"], k["out_features"], k["rank"], 4
+    A = np.zeros((NA, 1, R, IN))
+    B = np.zeros((NA, 1, OUT, R))
+    for a in range(NA):
+        A[a, 0] = np.eye(R, IN) * 0.1 * (a + 1)
+        B[a, 0] = np.eye(OUT, R) * 0.2 * (a + 1)
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((9, IN))
+    y = rng.standard_normal((9, OUT))
+    ids = np.array([4, 0, 1, 2, 3, 3, 0, 1, 4])
+    got = olora.per_token_reference(y, x, ids, [A], [B], (OUT,), [R] * NA)
+    exp = y.copy()
+    for t, a in enumerate(ids):
+        if a:
+            exp[t, :R] += x[t, :R] * 0.02 * a * a
+    np.testing.assert_allclose(got, exp, rtol=1e-12, atol=1e-12)
+
+
+# -- the CPU baseline loop -----------------------------------------------------
+def _hf_case(dtype, seed):
+    import torch
+
+    rng = np.random.default_rng(seed)
+    NA, H, slices, maxr = 5, 48, (32, 16, 16), 16
+    ranks = [16, 8, 0, 12, 16]
+    A = [rng.standard_normal((NA, 1, maxr, H)) / np.sqrt(H) for _ in slices]
+    B = [rng.standard_normal((NA, 1, o, maxr)) * 0.5 for o in slices]
+    for s in range(len(slices)):
+        for a in range(NA):
+            A[s][a, 0, ranks[a]:] = 0
+            B[s][a, 0, :, ranks[a]:] = 0
+    x = rng.standard_normal((40, H))
+    y = rng.standard_normal((40, sum(slices)))
+    ids = rng.integers(0, NA + 1, size=40)
+    ids[:3] = 0
+    to = lambda a: torch.tensor(a, dtype=dtype)
+    if dtype != torch.float64:
+        # inputs representable in the dtype, so both sides start from the same values
+        x, y = to(x).double().numpy(), to(y).double().numpy()
+        A = [to(a).double().numpy() for a in A]
+        B = [to(b).double().numpy() for b in B]
+    return dict(x=x, y=y, ids=ids, A=A, B=B, slices=slices, ranks=ranks, to=to)
+
+
+def test_hf_loop_matches_oracle_f64():
+    """The baseline loop and the oracle agree exactly in float64."""
+    import torch
+
+    from oracle import baseline
+
+    c = _hf_case(torch.float64, 11)
+    out = c["to"](c["y"])
+    baseline.hf_loop(out, c["to"](c["x"]), torch.tensor(c["ids"]), [c["to"](a) for a in c["A"]],
+                     [c["to"](b) for b in c["B"]], c["slices"])
+    exp = olora.switched_lora_apply(c["y"], c["x"], c["ids"], c["A"], c["B"], c["slices"], c["ranks"], dtype="f64")
+    np.testing.assert_allclose(out.numpy(), exp, rtol=1e-12, atol=1e-12)
+    assert np.array_equal(out.numpy()[c["ids"] == 0], c["y"][c["ids"] == 0])
+
+
+@pytest.mark.parametrize("name,tol", [("bfloat16", 2e-2), ("float32", 1e-5)])
+def test_hf_loop_matches_oracle_rounding_mode(name, tol):
+    """In bf16 / fp32 the loop follows the oracle's "hf" rounding sequence
+    (shrink rounded, expand rounded, then the add rounded)."""
+    import torch
+
+    from oracle import baseline
+
+    dt = getattr(torch, name)
+    c = _hf_case(dt, 12)
+    out = c["to"](c["y"])
+    baseline.hf_loop(out, c["to"](c["x"]), torch.tensor(c["ids"]), [c["to"](a) for a in c["A"]],
+                     [c["to"](b) for b in c["B"]], c["slices"])
+    dname = "bf16" if dt == torch.bfloat16 else "fp32"
+    exp = olora.switched_lora_apply(c["y"], c["x"], c["ids"], c["A"], c["B"], c["slices"], c["ranks"], dtype=dname,
+                                    mode="hf")
+    got = out.double().numpy()
+    assert np.all(np.abs(got - exp) <= tol + tol * np.abs(exp))
+    assert np.array_equal(got[c["ids"] == 0], c["y"][c["ids"] == 0])
+
+
+# -- W-less shrink-expand ------------------------------------------------------
+def _wless_case(adapters_spec, ids, K, N, seed):
+    """Packed metadata built by hand, as tests/unit/test_wcross_shrink_kernel.py:41-101
+    does it, independently of finalize_tables: adapters in ascending rank
+    order, kernel-local ids 1.. in that order, no base rows in the cross
+    weight, so shrink columns start at 0."""
+    rng = np.random.default_rng(seed)
+    adapters = [(r, rng.standard_normal((r, K)) * 0.05, rng.standard_normal((N, r)) * 0.05) for r in adapters_spec]
+    w_ext = np.concatenate([A for _, A, _ in adapters], axis=0)
+    na = tuple(sum(1 for r, _, _ in adapters if r == R) for R in omap.SUPPORTED_RANKS)
+    slice_col = np.zeros((1, 6), dtype=np.int32)
+    running = 0
+    for k_, R in enumerate(omap.SUPPORTED_RANKS):
+        slice_col[0, k_] = running
+        running += na[k_] * R
+    lb = np.concatenate([np.stack([B for r, _, B in adapters if r == R]).reshape(-1)
+                         for R in omap.SUPPORTED_RANKS if any(r == R for r, _, _ in adapters)])
+    col_of = np.cumsum([0] + [r for r, _, _ in adapters])[:-1]
+    ids = np.asarray(ids)
+    M = ids.shape[0]
+    x = rng.standard_normal((M, K))
+    x_ext = x @ w_ext.T
+    bm = np.zeros((M + 31) // 32, dtype=np.int64)
+    for m, a in enumerate(ids):
+        if a > 0:
+            bm[m // 32] |= np.int64(1) << np.int64(a - 1)
+    ref = np.zeros((M, N))
+    for m, a in enumerate(ids):
+        if a > 0:
+            r, _, B = adapters[a - 1]
+            ref[m] = x_ext[m, col_of[a - 1]:col_of[a - 1] + r] @ B.T
+    return dict(x_ext=x_ext, ids=ids, bm=bm, lb=lb, tile_slice=np.zeros(N // 32, np.int32), scr=slice_col, na=na,
+                ref=ref)
+
+
+@pytest.mark.parametrize("spec,ids,K,N", [
+    ((16,), [0, 1] * 20, 256, 64),                      # single tier, mixed rows, two row tiles
+    ((16,), [0] * 32, 256, 64),                         # one all-base tile
+    ((16, 32), [0, 1, 2, 2, 0, 1] * 8, 512, 128),       # two tiers
+    ((16, 16), [1, 2, 0, 1, 2, 0] * 8, 256, 64),        # two adapters of one tier
+    ((16, 32, 64), [3] * 5 + [0] * 40 + [1, 2] * 10, 128, 96),
+])
+def test_shrink_expand_xext_matches_per_token_loop(spec, ids, K, N):
+    d = _wless_case(spec, ids, K, N, seed=len(ids) + K)
+    got = olora.shrink_expand_xext(d["x_ext"], d["ids"], d["bm"], d["lb"], d["tile_slice"], d["scr"], d["na"], 1, 32,
+                                   N, dtype="f64")
+    np.testing.assert_allclose(got, d["ref"], rtol=1e-10, atol=1e-12)
+    base = d["ids"] == 0
+    assert np.all(got[base] == 0)                      # base rows exactly zero
