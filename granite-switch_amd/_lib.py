@@ -29,6 +29,7 @@ GS_DTYPE_FP32 = 1
 GS_MAX_ADAPTERS = 256
 GS_MAX_SLICES = 8
 GS_MAX_RANK = 512
+GS_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 # name -> (restype, argtypes); mirrors include/granite_switch_amd.h
 SIGNATURES = {
@@ -46,6 +47,9 @@ SIGNATURES = {
     "gs_switched_lora": (c_i32, [c_i32, c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i32, c_i32, c_void_p, c_i32,
                                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_i32, c_i32, c_void_p, c_void_p,
                                  c_void_p, c_void_p, c_i64, c_void_p]),
+    "gs_switched_lora_noalloc": (c_i32, [c_i32, c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i32, c_i32, c_void_p,
+                                         c_i32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_i32, c_i32,
+                                         c_void_p, c_void_p, c_void_p]),
     "gs_small_eligible": (c_i32, [c_i64, c_i32, c_i32, c_void_p, c_i32, c_i32]),
     "gs_small_workspace_bytes": (c_i64, [c_i32, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_void_p]),
     "gs_small_sync_bytes": (c_i64, []),

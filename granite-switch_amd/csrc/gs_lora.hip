@@ -13,6 +13,7 @@
 // order, so results are deterministic and need no cross-XCD fences.
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 
 #include "gs_common.h"
 
@@ -729,6 +730,94 @@ void launch_expand(bool bf16, int64_t T, ExpandParams p, hipStream_t st) {
 
 }  // namespace
 
+// ----------------------------------------------------------------------------
+// The allocation-free variant's scratch: one static device array per GPU (each
+// device holds its own copy at its own address), used for the split-K
+// partials and z.  Host code never passes the array's name to a kernel -- on
+// the host that name is only a stand-in -- but the device address that
+// hipGetSymbolAddress returns for the current device, looked up once per
+// device and kept.  Nothing in it needs to start at zero: every call writes
+// the partials (or z) before its expand reads them.  Calls that overlap in
+// time on one GPU share the array and race.
+// ----------------------------------------------------------------------------
+namespace {
+
+constexpr int64_t kNoallocScratchBytes = GS_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[kNoallocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<char*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int noalloc_scratch(const char* who, char** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("%s: no current HIP device (got %d)", who, dev);
+    return GS_ERR_HIP;
+  }
+  char* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      void* addr = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || addr == nullptr) {
+        set_error("%s: hipGetSymbolAddress of the static scratch failed on device %d: %s", who, dev,
+                  hipGetErrorString(e));
+        return GS_ERR_HIP;
+      }
+      p = static_cast<char*>(addr);
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return GS_OK;
+}
+
+// Shrink, then the expand reading its output (shared by gs_switched_lora and
+// gs_switched_lora_noalloc, which differ only in where z and the partials live).
+int switched_lora_impl(const char* who, int32_t dtype, const void* x, int64_t ldx, void* y, int64_t ldy,
+                       int64_t num_tokens, int32_t hidden, int32_t out_total, const int32_t* slice_bounds,
+                       int32_t num_slices, const void* a_pack, const int64_t* a_off, const void* b_pack,
+                       const int64_t* b_off, const int32_t* ranks, int32_t num_adapters, int32_t max_rank,
+                       const int32_t* seg_offsets, const int32_t* perm, void* z, void* workspace,
+                       int64_t workspace_bytes, void* stream) {
+  int rc = check_common(who, dtype, num_tokens, num_slices, num_adapters, max_rank);
+  if (rc != GS_OK) return rc;
+  rc = check_shrink(dtype, x, ldx, hidden, a_pack);
+  if (rc != GS_OK) return rc;
+  ExpandParams ep{};
+  rc = prepare_expand(ep, who, dtype, y, ldy, num_tokens, out_total, slice_bounds, num_slices, b_pack, b_off, ranks,
+                      num_adapters, max_rank, seg_offsets, perm);
+  if (rc != GS_OK) return rc;
+  GS_CHECK_ARG(aligned16(z), "%s: z must be 16-byte aligned", who);
+  if (num_tokens == 0) return GS_OK;
+  const bool bf16 = dtype == GS_DTYPE_BF16;
+  const ShrinkPlan pl = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, bf16);
+  rc = check_workspace(pl, workspace, workspace_bytes);
+  if (rc != GS_OK) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t ldz = static_cast<int64_t>(num_slices) * max_rank;
+  const ShrinkParams sp = make_shrink_params(pl, x, ldx, hidden, a_pack, a_off, ranks, num_slices, num_adapters,
+                                             seg_offsets, perm, z, ldz, workspace, num_tokens);
+  launch_shrink(bf16, pl, sp, st);
+  GS_CHECK_LAUNCH(who);
+  ep.z = z;
+  ep.ldz = ldz;
+  ep.z_by_token = 0;
+  ep.z_off = nullptr;
+  ep.part = sp.part;
+  ep.part_stride = sp.part_stride;
+  ep.zw = sp.zw;
+  ep.nparts = pl.KS > 1 ? pl.KS : 0;
+  launch_expand(bf16, num_tokens, ep, st);
+  GS_CHECK_LAUNCH(who);
+  return GS_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int64_t gs_shrink_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t num_slices, int32_t num_adapters,
@@ -802,37 +891,37 @@ int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t
                      const void* a_pack, const int64_t* a_off, const void* b_pack, const int64_t* b_off,
                      const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* seg_offsets,
                      const int32_t* perm, void* z, void* workspace, int64_t workspace_bytes, void* stream) {
-  int rc = check_common("gs_switched_lora", dtype, num_tokens, num_slices, num_adapters, max_rank);
+  return switched_lora_impl("gs_switched_lora", dtype, x, ldx, y, ldy, num_tokens, hidden, out_total, slice_bounds,
+                            num_slices, a_pack, a_off, b_pack, b_off, ranks, num_adapters, max_rank, seg_offsets, perm,
+                            z, workspace, workspace_bytes, stream);
+}
+
+int gs_switched_lora_noalloc(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t num_tokens,
+                             int32_t hidden, int32_t out_total, const int32_t* slice_bounds, int32_t num_slices,
+                             const void* a_pack, const int64_t* a_off, const void* b_pack, const int64_t* b_off,
+                             const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* seg_offsets,
+                             const int32_t* perm, void* stream) {
+  const char* who = "gs_switched_lora_noalloc";
+  int rc = check_common(who, dtype, num_tokens, num_slices, num_adapters, max_rank);
   if (rc != GS_OK) return rc;
-  rc = check_shrink(dtype, x, ldx, hidden, a_pack);
-  if (rc != GS_OK) return rc;
-  ExpandParams ep{};
-  rc = prepare_expand(ep, "gs_switched_lora", dtype, y, ldy, num_tokens, out_total, slice_bounds, num_slices, b_pack,
-                      b_off, ranks, num_adapters, max_rank, seg_offsets, perm);
-  if (rc != GS_OK) return rc;
-  GS_CHECK_ARG(aligned16(z), "gs_switched_lora: z must be 16-byte aligned");
+  GS_CHECK_ARG(hidden > 0, "%s: hidden=%d", who, hidden);
   if (num_tokens == 0) return GS_OK;
-  const bool bf16 = dtype == GS_DTYPE_BF16;
-  const ShrinkPlan pl = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, bf16);
-  rc = check_workspace(pl, workspace, workspace_bytes);
+  // scratch layout: [split-K partials][z], each 256-byte aligned
+  const ShrinkPlan pl = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, dtype == GS_DTYPE_BF16);
+  const int64_t part = (pl.part_bytes + 255) & ~int64_t(255);
+  const int64_t zbytes = num_tokens * int64_t(num_slices) * max_rank * (dtype == GS_DTYPE_BF16 ? 2 : 4);
+  if (part + zbytes > kNoallocScratchBytes) {
+    set_error("%s: this shape needs %lld bytes of scratch (split-K partials %lld + z %lld); the static scratch "
+              "holds %lld (use gs_switched_lora with a caller workspace)", who, (long long)(part + zbytes),
+              (long long)pl.part_bytes, (long long)zbytes, (long long)kNoallocScratchBytes);
+    return GS_ERR_WORKSPACE;
+  }
+  char* base = nullptr;
+  rc = noalloc_scratch(who, &base);
   if (rc != GS_OK) return rc;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t ldz = static_cast<int64_t>(num_slices) * max_rank;
-  const ShrinkParams sp = make_shrink_params(pl, x, ldx, hidden, a_pack, a_off, ranks, num_slices, num_adapters,
-                                             seg_offsets, perm, z, ldz, workspace, num_tokens);
-  launch_shrink(bf16, pl, sp, st);
-  GS_CHECK_LAUNCH("gs_switched_lora (shrink)");
-  ep.z = z;
-  ep.ldz = ldz;
-  ep.z_by_token = 0;
-  ep.z_off = nullptr;
-  ep.part = sp.part;
-  ep.part_stride = sp.part_stride;
-  ep.zw = sp.zw;
-  ep.nparts = pl.KS > 1 ? pl.KS : 0;
-  launch_expand(bf16, num_tokens, ep, st);
-  GS_CHECK_LAUNCH("gs_switched_lora (expand)");
-  return GS_OK;
+  return switched_lora_impl(who, dtype, x, ldx, y, ldy, num_tokens, hidden, out_total, slice_bounds, num_slices,
+                            a_pack, a_off, b_pack, b_off, ranks, num_adapters, max_rank, seg_offsets, perm,
+                            base + part, base, part, stream);
 }
 
 }  // extern "C"

@@ -742,6 +742,38 @@ def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed:
     return y
 
 
+def switched_lora_noalloc_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed: PackedAdapters) -> torch.Tensor:
+    """In place: y += switched-LoRA delta of x, allocating nothing.
+
+    The segment path's two kernels with their scratch (split-K partials and
+    the shrink output) in the library's static per-GPU array
+    (``gs_switched_lora_noalloc``) -- for code that must not allocate, such as
+    a region under HIP graph capture.  No tensor is created or copied here:
+    x and y must already have unit column stride.  Shapes whose scratch would
+    exceed the array (``_lib.GS_NOALLOC_SCRATCH_BYTES``) raise.  Calls that
+    overlap in time on one GPU share the array and race.
+    """
+    _require_cuda(x, y)
+    if x.stride(-1) != 1 or y.stride(-1) != 1:
+        raise ValueError("switched_lora_noalloc_: x and y need unit column stride (nothing is copied)")
+    x2 = x.view(-1, x.shape[-1])
+    y2 = y.view(-1, y.shape[-1])
+    if x2.dtype != packed.dtype or y2.dtype != packed.dtype:
+        raise TypeError("x, y and the packed adapters must share a dtype")
+    if x2.shape[1] != packed.hidden or y2.shape != (x2.shape[0], packed.out_total):
+        raise ValueError("x / y shapes do not match the adapters")
+    T = x2.shape[0]
+    if T != segments.num_tokens:
+        raise ValueError("x / y shapes do not match the segments")
+    _check_segments(segments, packed)
+    _lib.call("gs_switched_lora_noalloc", _dtype_code(x2), x2.data_ptr(), x2.stride(0), y2.data_ptr(), y2.stride(0),
+              T, packed.hidden, packed.out_total, _i32_array(packed.slice_bounds), packed.num_slices,
+              packed.a_pack.data_ptr(), packed.a_off.data_ptr(), packed.b_pack.data_ptr(), packed.b_off.data_ptr(),
+              packed.ranks.data_ptr(), packed.num_adapters, packed.max_rank, segments.seg_offsets.data_ptr(),
+              segments.perm.data_ptr(), _lib.stream_ptr(x2.device))
+    return y
+
+
 def _check_segments(segments: Segments, packed: PackedAdapters) -> None:
     """The kernels read seg_offsets[0..NA] and perm[0..T): both must match the pack."""
     if segments.num_adapters != packed.num_adapters or segments.seg_offsets.numel() != packed.num_adapters + 1:
@@ -824,6 +856,7 @@ __all__ = [
     "expand_add_",
     "switched_lora_",
     "switched_lora_routed_",
+    "switched_lora_noalloc_",
     "small_eligible",
     "small_preferred",
     "small_workspace_bytes",

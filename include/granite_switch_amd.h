@@ -181,6 +181,24 @@ int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t
                      const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* seg_offsets,
                      const int32_t* perm, void* z, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* The same op with its scratch (split-K partials and z) in a static device
+ * array of GS_NOALLOC_SCRATCH_BYTES per GPU, so it allocates nothing: no
+ * workspace, no z, no hipMalloc.  No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation).  The array is looked up once per
+ * device (hipGetSymbolAddress, on the first call with that device current);
+ * launch on a stream of the current device.  Shapes whose partials plus z
+ * exceed the array are rejected with GS_ERR_WORKSPACE (use gs_switched_lora
+ * with a workspace then).  Every call on a GPU shares that GPU's array, which
+ * keeps the last call's contents (nothing needs to start at zero): calls that
+ * overlap in time on one GPU race; stream order keeps them apart. */
+#define GS_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int gs_switched_lora_noalloc(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t num_tokens,
+                             int32_t hidden, int32_t out_total, const int32_t* slice_bounds, int32_t num_slices,
+                             const void* a_pack, const int64_t* a_off, const void* b_pack, const int64_t* b_off,
+                             const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* seg_offsets,
+                             const int32_t* perm, void* stream);
+
 /* ------------------------------------------------------------------------
  * Small-batch switched-LoRA in ONE launch, no segment build (decode-sized
  * batches).  Same result as gs_build_segments + gs_switched_lora: every
