@@ -125,6 +125,25 @@ struct Elt<false> {
   static constexpr int kSize = 4;
 };
 
+// ---- direct global -> LDS transfers -----------------------------------------
+// s_waitcnt immediate for "vmcnt <= n" (expcnt and lgkmcnt not waited on)
+constexpr int wait_vm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// One wave-wide global_load_lds_dwordx4: lane i moves the 16 bytes at its src
+// to LDS at M0 + 16 i, where M0 holds the wave's (uniform) destination.  The
+// transfer counts in vmcnt until the bytes are in LDS; it is written as
+// assembly, so the compiler neither waits for it nor orders LDS reads
+// against it -- wait with s_waitcnt(wait_vm(n)) and a barrier.
+__device__ __forceinline__ void dma16(const char* src, char* lds_dst) {
+  const uint32_t dst =
+      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)(lds_dst))));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(dst) : "memory", "m0");
+}
+
+__device__ __forceinline__ void mem_fence_compiler() { asm volatile("" ::: "memory"); }
+
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ u32x4 sel16(bool keep, const u32x4& v) {

@@ -194,19 +194,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tn_kernel(GemmParams p
 constexpr int kDBK = 64;                        // k per tile
 constexpr int kDRow = kDBK * 2;                 // bytes of one operand row per tile (one cache line)
 constexpr int kDOp = kGBM * kDRow;              // one operand of one stage
-// s_waitcnt immediate for "vmcnt <= n" (expcnt and lgkmcnt not waited on)
-constexpr int wait_vm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-// M0 holds the wave's LDS destination: lane i writes 16 bytes at M0 + 16 i.
-__device__ __forceinline__ void dma16(const char* src, char* lds_dst) {
-  const uint32_t dst =
-      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)(lds_dst))));
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(dst) : "memory", "m0");
-}
-
-__device__ __forceinline__ void mem_fence_compiler() { asm volatile("" ::: "memory"); }
 
 template <int WM, int WN>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tn_dma_kernel(GemmParams p) {

@@ -217,6 +217,156 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NB <= 
   }
 }
 
+// ----------------------------------------------------------------------------
+// Shrink, bf16 with H % 64 == 0: the same work items, tile placement,
+// k-split and outputs as shrink_kernel, but the operands travel through a
+// ring of LDS stages filled by direct global -> LDS transfers, so several
+// stages are in flight per workgroup without staging registers.  A stage is
+// 64 k of the tile's 64 x rows and its COLS lora_A rows, one 128-byte line per
+// row (whole-line requests); a wave moves 16 x rows and COLS/4 lora_A rows of
+// every stage (1 KB per transfer: 8 rows, lane l row l/8 position l%8).
+// Pieces are XOR-swizzled (piece p of row r at position p ^ (r & 7)) so the
+// 16 rows an MFMA operand read touches fall in distinct banks.  NST stages
+// form a ring with NST - 1 in flight: iteration s waits for its own stage
+// (vmcnt), passes one barrier -- after which every wave is done with stage
+// s - 1, whose slot then receives stage s + NST - 1 -- and runs its MFMAs
+// from LDS.  The waiting in the old kernel was one memory round trip per
+// batch: the next batch's lora_A had to be in registers before it could be
+// staged.  Rows past the tile (x) or past the adapter's S*r (lora_A) re-read
+// a valid row; their results are never stored.
+// ----------------------------------------------------------------------------
+constexpr int kDmaBK = 64;                 // k per stage
+constexpr int kDmaRow = kDmaBK * 2;        // bytes of a bf16 row per stage (one cache line)
+
+// ring depth per column width: about 72 KB of LDS, two workgroups per CU
+#ifndef GS_DMA_NST1
+#define GS_DMA_NST1 6
+#endif
+#ifndef GS_DMA_NST2
+#define GS_DMA_NST2 4
+#endif
+#ifndef GS_DMA_NST3
+#define GS_DMA_NST3 3
+#endif
+#ifndef GS_DMA_NST4
+#define GS_DMA_NST4 3
+#endif
+template <int NB>
+struct DmaRing {
+  static constexpr int NST = NB == 1 ? GS_DMA_NST1 : (NB == 2 ? GS_DMA_NST2 : (NB == 3 ? GS_DMA_NST3 : GS_DMA_NST4));
+};
+
+// s_waitcnt until at most `after` stages (TPW transfers each) are outstanding
+template <int TPW, int N>
+__device__ __forceinline__ void wait_stages(int after) {
+  if constexpr (N >= 0) {
+    if (after >= N) {
+      __builtin_amdgcn_s_waitcnt(wait_vm(N * TPW));
+      return;
+    }
+    wait_stages<TPW, N - 1>(after);
+  }
+}
+
+template <int NB>
+__global__ __launch_bounds__(kThreads) void shrink_dma_kernel(ShrinkParams p) {
+  constexpr int COLS = 32 * NB;
+  constexpr int NC16 = COLS / 16;
+  constexpr int ROWS = kTMS + COLS;        // LDS rows of a stage: x rows, then lora_A rows
+  constexpr int STAGE = ROWS * kDmaRow;
+  constexpr int NST = DmaRing<NB>::NST;
+  constexpr int XT = kTMS / 4 / 8;         // x transfers per wave and stage
+  constexpr int ARW = COLS / 4;            // lora_A rows per wave and stage
+  constexpr int AT = ARW / 8;              // lora_A transfers per wave and stage
+  constexpr int TPW = XT + AT;
+  static_assert(TPW * (NST - 2) <= 63, "vmcnt counts at most 63 outstanding transfers");
+  __shared__ __align__(16) char ring[NST * STAGE];
+
+  int sub = 0;
+  const TileRef tr =
+      locate_tile<kTMS>(p.seg, p.ranks, p.a_off, p.NA, static_cast<int>(blockIdx.x), p.n_chunks * p.KS, sub);
+  if (tr.g == 0) return;
+  const int chunk = sub % p.n_chunks;
+  const int ks = sub / p.n_chunks;
+  const int ncols = p.S * tr.rank;
+  const int col0 = chunk * COLS;
+  if (col0 >= ncols) return;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int l = tid & 63;
+  const int i16 = l & 15;
+  const int q4 = l >> 4;
+  const int64_t k_lo = static_cast<int64_t>(ks) * p.KC;
+  const int64_t k_hi = min(static_cast<int64_t>(p.H), k_lo + p.KC);
+  const int nst = static_cast<int>((k_hi - k_lo) / kDmaBK);
+
+  // this lane's source in each transfer: row 8t + l/8 of the wave's rows,
+  // global piece (l % 8) ^ (row % 8), so LDS position l % 8 holds it swizzled
+  const int trow = l >> 3;
+  const int gpiece = ((l & 7) ^ trow) * 16;
+  const char* xsrc[XT];
+#pragma unroll
+  for (int t = 0; t < XT; ++t) {
+    const int r = 16 * wave + 8 * t + trow;
+    const int token = p.perm[tr.slot0 + (r < tr.nrows ? r : 0)];
+    xsrc[t] = static_cast<const char*>(p.x) + (static_cast<int64_t>(token) * p.ldx + k_lo) * 2 + gpiece;
+  }
+  const char* asrc[AT];
+#pragma unroll
+  for (int t = 0; t < AT; ++t) {
+    const int arow = min(col0 + ARW * wave + 8 * t + trow, ncols - 1);
+    asrc[t] = static_cast<const char*>(p.a_pack) + (tr.off + static_cast<int64_t>(arow) * p.H + k_lo) * 2 + gpiece;
+  }
+  auto issue = [&](int st) {
+    char* slot = ring + (st % NST) * STAGE;
+    const int64_t off = static_cast<int64_t>(st) * kDmaRow;
+#pragma unroll
+    for (int t = 0; t < XT; ++t) dma16(xsrc[t] + off, slot + (16 * wave + 8 * t) * kDmaRow);
+#pragma unroll
+    for (int t = 0; t < AT; ++t) dma16(asrc[t] + off, slot + (kTMS + ARW * wave + 8 * t) * kDmaRow);
+  };
+
+  f32x4 acc[NC16];
+#pragma unroll
+  for (int c = 0; c < NC16; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int sw = i16 & 7;                  // swizzle of every row this lane reads
+  for (int st = 0; st < NST - 1 && st < nst; ++st) issue(st);
+  for (int st = 0; st < nst; ++st) {
+    wait_stages<TPW, NST - 2>(min(NST - 2, nst - 1 - st));
+    mem_fence_compiler();
+    __builtin_amdgcn_s_barrier();
+    mem_fence_compiler();
+    if (st + NST - 1 < nst) issue(st + NST - 1);
+    const char* slot = ring + (st % NST) * STAGE;
+    const char* xs = slot + (16 * wave + i16) * kDmaRow;
+    const char* as = slot + (kTMS + i16) * kDmaRow;
+#pragma unroll
+    for (int kk = 0; kk < kDmaBK / 32; ++kk) {
+      const int pos = ((4 * kk + q4) ^ sw) * 16;
+      const u32x4 xa = *reinterpret_cast<const u32x4*>(xs + pos);
+#pragma unroll
+      for (int c = 0; c < NC16; ++c)
+        acc[c] = mfma16<true>(xa, *reinterpret_cast<const u32x4*>(as + 16 * c * kDmaRow + pos), acc[c]);
+    }
+  }
+
+  // lane (i16, q4) holds slots 16*wave + 4*q4 + e, column col0 + 16*c + i16
+#pragma unroll
+  for (int c = 0; c < NC16; ++c) {
+    const int col = col0 + 16 * c + i16;
+    if (col >= ncols) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = 16 * wave + 4 * q4 + e;
+      if (row >= tr.nrows) continue;
+      const int64_t slot = tr.slot0 + row;
+      if (p.KS == 1) static_cast<uint16_t*>(p.z)[slot * p.ldz + col] = f32_to_bf16_bits(acc[c][e]);
+      else p.part[static_cast<int64_t>(ks) * p.part_stride + slot * p.zw + col] = acc[c][e];
+    }
+  }
+}
+
 // z[slot][col] = sum_ks part[ks][slot][col] (fixed order), for active slots.
 template <bool BF16>
 __global__ __launch_bounds__(kThreads) void reduce_parts_kernel(const float* __restrict__ part, int64_t part_stride,
@@ -536,11 +686,20 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
 // ----------------------------------------------------------------------------
 struct ShrinkPlan {
   int max_tiles, n_chunks, KS, KC, zw, NB;
+  bool dma;               // shrink_dma_kernel (bf16, H % 64 == 0) instead of shrink_kernel
   int64_t part_bytes;
 };
 
+#ifndef GS_SHRINK_DMA
+#define GS_SHRINK_DMA 1
+#endif
+#ifndef GS_SHRINK_DMA_WGS_PER_4CU
+#define GS_SHRINK_DMA_WGS_PER_4CU 8
+#endif
+
 static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, bool bf16) {
   ShrinkPlan pl{};
+  pl.dma = GS_SHRINK_DMA && bf16 && H % kDmaBK == 0;
   pl.max_tiles = static_cast<int>((T + kTMS - 1) / kTMS + (NA < T ? NA : T));
   pl.zw = S * max_rank;
   const int nblk = (pl.zw + 31) / 32;         // 32-column blocks of the widest adapter
@@ -555,7 +714,9 @@ static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, boo
   // spread over enough streaming; measured on the prefill and decoder-step
   // shapes
   const int64_t wgs = static_cast<int64_t>(pl.max_tiles) * pl.n_chunks;
-  int ks = static_cast<int>((kShrinkTargetWgs + wgs / 2) / (wgs > 0 ? wgs : 1));
+  // the ring kernel holds two workgroups per CU: aim for one round of them
+  const int64_t target = pl.dma ? int64_t(GS_SHRINK_DMA_WGS_PER_4CU) * device_cus() / 4 : kShrinkTargetWgs;
+  int ks = static_cast<int>((target + wgs / 2) / (wgs > 0 ? wgs : 1));
   if (ks < 1) ks = 1;
   if (ks > 16) ks = 16;
   if (ks > units) ks = units;
@@ -637,6 +798,13 @@ int check_workspace(const ShrinkPlan& pl, const void* workspace, int64_t workspa
 template <bool BF16>
 void launch_shrink_t(const ShrinkPlan& pl, const ShrinkParams& p, hipStream_t st) {
   dim3 grid(8 * ((pl.max_tiles + 7) / 8) * pl.n_chunks * pl.KS);
+  if (BF16 && pl.dma) {
+    if (pl.NB == 4) hipLaunchKernelGGL(shrink_dma_kernel<4>, grid, dim3(kThreads), 0, st, p);
+    else if (pl.NB == 3) hipLaunchKernelGGL(shrink_dma_kernel<3>, grid, dim3(kThreads), 0, st, p);
+    else if (pl.NB == 2) hipLaunchKernelGGL(shrink_dma_kernel<2>, grid, dim3(kThreads), 0, st, p);
+    else hipLaunchKernelGGL(shrink_dma_kernel<1>, grid, dim3(kThreads), 0, st, p);
+    return;
+  }
   if (pl.NB == 4) hipLaunchKernelGGL((shrink_kernel<BF16, 4>), grid, dim3(kThreads), 0, st, p);
   else if (pl.NB == 3) hipLaunchKernelGGL((shrink_kernel<BF16, 3>), grid, dim3(kThreads), 0, st, p);
   else if (pl.NB == 2) hipLaunchKernelGGL((shrink_kernel<BF16, 2>), grid, dim3(kThreads), 0, st, p);
