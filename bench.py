@@ -585,8 +585,7 @@ def main():
         per_kernel_bytes[f"small_fused:{spec.name}"] = algorithmic_bytes(eff, pk0, spec.ranks, e)
     if only is not None and not kern_us:
         raise SystemExit(f"--kernel-only {only}: no such kernel on this workload")
-    if small:
-        switched.check(dev)
+    switched.check(dev)
     for name, us in kern_us.items():
         log(f"kernel {name}: {us:.2f} us/launch, {per_kernel_bytes[name] / us / 1e3:.0f} GB/s algorithmic")
     # every single kernel competes (the pair is two kernels): the split
@@ -641,7 +640,8 @@ def main():
         "data": "synthetic (seeded; random-init adapters in the composed-checkpoint layout)",
         "config": {"workload": wl_name, "tokens": T, "active_tokens": t_act, "adapters": NA,
                    "projections": [f"{s.name} {s.hidden}->{sum(s.output_slices)}" for s in specs],
-                   "layers": layers, "buffer_sets": nsets},
+                   "layers": layers, "buffer_sets": nsets,
+                   "path": "small-batch" if small else "segments"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": dom_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": dom_gbs / HBM_PEAK_GBS, "traffic": measured_traffic(WORKLOAD_KEY[cfg], dom),
                      "algorithmic_bytes": per_kernel_bytes[dom], "avg_us": kern_us[dom]},
