@@ -238,6 +238,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NB <= 
 constexpr int kDmaBK = 64;                 // k per stage
 constexpr int kDmaRow = kDmaBK * 2;        // bytes of a bf16 row per stage (one cache line)
 
+
 // ring depth per column width: about 72 KB of LDS, two workgroups per CU
 #ifndef GS_DMA_NST1
 #define GS_DMA_NST1 6
@@ -297,9 +298,12 @@ __global__ __launch_bounds__(kThreads) void shrink_dma_kernel(ShrinkParams p) {
   const int l = tid & 63;
   const int i16 = l & 15;
   const int q4 = l >> 4;
-  const int64_t k_lo = static_cast<int64_t>(ks) * p.KC;
-  const int64_t k_hi = min(static_cast<int64_t>(p.H), k_lo + p.KC);
-  const int nst = static_cast<int>((k_hi - k_lo) / kDmaBK);
+  // k-chunk ks: stages [ks * all / KS, (ks + 1) * all / KS) of the all = H / 64
+  // stages, so the chunks differ by at most one stage
+  const int all_st = p.H / kDmaBK;
+  const int s_lo = (ks * all_st) / p.KS;
+  const int nst = ((ks + 1) * all_st) / p.KS - s_lo;
+  const int64_t k_lo = static_cast<int64_t>(s_lo) * kDmaBK;
 
   // this lane's source in each transfer: row 8t + l/8 of the wave's rows,
   // global piece (l % 8) ^ (row % 8), so LDS position l % 8 holds it swizzled
@@ -351,18 +355,33 @@ __global__ __launch_bounds__(kThreads) void shrink_dma_kernel(ShrinkParams p) {
     }
   }
 
-  // lane (i16, q4) holds slots 16*wave + 4*q4 + e, column col0 + 16*c + i16
+  // Results go through LDS (the ring is free once every wave is past its last
+  // stage) so that each thread stores whole 16-byte pieces of output rows:
+  // lane (i16, q4) holds slots 16*wave + 4*q4 + e, column 16*c + i16.
+  constexpr int OLD = COLS + 4;            // fp32 row stride of the staged results
+  static_assert(kTMS * OLD * 4 <= NST * STAGE, "staged results must fit the ring");
+  float* res = reinterpret_cast<float*>(ring);
+  lds_barrier();
 #pragma unroll
-  for (int c = 0; c < NC16; ++c) {
-    const int col = col0 + 16 * c + i16;
-    if (col >= ncols) continue;
+  for (int c = 0; c < NC16; ++c)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = 16 * wave + 4 * q4 + e;
-      if (row >= tr.nrows) continue;
-      const int64_t slot = tr.slot0 + row;
-      if (p.KS == 1) static_cast<uint16_t*>(p.z)[slot * p.ldz + col] = f32_to_bf16_bits(acc[c][e]);
-      else p.part[static_cast<int64_t>(ks) * p.part_stride + slot * p.zw + col] = acc[c][e];
+    for (int e = 0; e < 4; ++e) res[(16 * wave + 4 * q4 + e) * OLD + 16 * c + i16] = acc[c][e];
+  lds_barrier();
+  constexpr int PPR4 = COLS / 4;           // 4-column pieces per row
+  const int wcols = min(COLS, ncols - col0);
+#pragma unroll
+  for (int it = 0; it < kTMS * PPR4 / kThreads; ++it) {
+    const int pc = tid + it * kThreads;
+    const int row = pc / PPR4;
+    const int c4 = (pc % PPR4) * 4;
+    if (row >= tr.nrows || c4 >= wcols) continue;
+    const f32x4 v = *reinterpret_cast<const f32x4*>(res + row * OLD + c4);
+    const int64_t slot = tr.slot0 + row;
+    if (p.KS == 1) {
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.z) + slot * p.ldz + col0 + c4) =
+          make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+    } else {
+      *reinterpret_cast<f32x4*>(p.part + static_cast<int64_t>(ks) * p.part_stride + slot * p.zw + col0 + c4) = v;
     }
   }
 }
@@ -720,6 +739,14 @@ static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, boo
   if (ks < 1) ks = 1;
   if (ks > 16) ks = 16;
   if (ks > units) ks = units;
+  if (pl.dma) {
+    // the ring kernel splits the 64-k stages evenly over the KS chunks (at
+    // least 4 stages each: ks <= units)
+    pl.KS = ks;
+    pl.KC = 0;
+    pl.part_bytes = pl.KS > 1 ? static_cast<int64_t>(pl.KS) * T * pl.zw * 4 : 0;
+    return pl;
+  }
   int per = (units + ks - 1) / ks;
   if (per < 3 && units >= 3 && wgs * ((units + 2) / 3) >= 512) per = 3;
   pl.KC = per * unit;
