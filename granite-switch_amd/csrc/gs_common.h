@@ -273,7 +273,23 @@ __device__ __forceinline__ XcdItem xcd_item(int lin, int total_tiles, int nsub) 
   return it;
 }
 
-template <int TM>
+// Tile jj of an adapter whose slots are [lo, hi): TM consecutive slots (the
+// last tile shorter), or, with BAL, one of ceil(n / TM) tiles of near-equal
+// size (rows spread evenly, at most TM each).
+template <int TM, bool BAL>
+__device__ __forceinline__ void tile_span(int lo, int hi, int jj, int& slot0, int& nrows) {
+  if constexpr (BAL) {
+    const int n = hi - lo;
+    const int nt = (n + TM - 1) / TM;
+    slot0 = lo + (jj * n) / nt;
+    nrows = lo + ((jj + 1) * n) / nt - slot0;
+  } else {
+    slot0 = lo + jj * TM;
+    nrows = min(TM, hi - slot0);
+  }
+}
+
+template <int TM, bool BAL = false>
 __device__ __forceinline__ TileRef find_tile(const int32_t* __restrict__ seg, const int32_t* __restrict__ ranks,
                                              const int64_t* __restrict__ offs, int num_adapters, int tile_id) {
   TileRef ref{0, 0, 0, 0, 0};
@@ -308,8 +324,7 @@ __device__ __forceinline__ TileRef find_tile(const int32_t* __restrict__ seg, co
       const int slo = __shfl(lo, src, 64);
       const int shi = __shfl(hi, src, 64);
       ref.g = g0 + src;
-      ref.slot0 = slo + jj * TM;
-      ref.nrows = min(TM, shi - ref.slot0);
+      tile_span<TM, BAL>(slo, shi, jj, ref.slot0, ref.nrows);
       ref.rank = __shfl(rk, src, 64);
       ref.off = __shfl(of, src, 64);
       return ref;
@@ -324,7 +339,7 @@ __device__ __forceinline__ TileRef find_tile(const int32_t* __restrict__ seg, co
 // (<= 64 adapters): the tile count and the tile's lookup share the same
 // loads.  nsub_of(total tiles) gives the number of subs per tile (every wave
 // computes the same value).  Returns g = 0 when the item has no tile.
-template <int TM, typename NsubOf>
+template <int TM, bool BAL = false, typename NsubOf>
 __device__ __forceinline__ TileRef locate_tile_by(const int32_t* __restrict__ seg, const int32_t* __restrict__ ranks,
                                                   const int64_t* __restrict__ offs, int num_adapters, int lin,
                                                   NsubOf nsub_of, int& sub) {
@@ -333,7 +348,7 @@ __device__ __forceinline__ TileRef locate_tile_by(const int32_t* __restrict__ se
     const int total = count_tiles<TM>(seg, ranks, num_adapters);
     const XcdItem it = xcd_item(lin, total, nsub_of(total));
     sub = it.sub;
-    return it.tile < 0 ? ref : find_tile<TM>(seg, ranks, offs, num_adapters, it.tile);
+    return it.tile < 0 ? ref : find_tile<TM, BAL>(seg, ranks, offs, num_adapters, it.tile);
   }
   const int l = __lane_id();
   const int g = 1 + l;
@@ -364,8 +379,7 @@ __device__ __forceinline__ TileRef locate_tile_by(const int32_t* __restrict__ se
   const int slo = __shfl(lo, src, 64);
   const int shi = __shfl(hi, src, 64);
   ref.g = 1 + src;
-  ref.slot0 = slo + jj * TM;
-  ref.nrows = min(TM, shi - ref.slot0);
+  tile_span<TM, BAL>(slo, shi, jj, ref.slot0, ref.nrows);
   ref.rank = __shfl(rk, src, 64);
   ref.off = __shfl(of, src, 64);
   return ref;

@@ -538,6 +538,14 @@ __host__ __device__ inline int expand_groups(int tiles, int n_sub, int wt) {
   return g;
 }
 
+// An adapter's slots are cut into 32-slot tiles of near-equal size (the
+// short last tile of a plain cut left the CUs holding one with less work
+// than the rest, and the launch waited for the others).
+#ifndef GS_EXPAND_BALANCED
+#define GS_EXPAND_BALANCED 1
+#endif
+constexpr bool kExpandBalanced = GS_EXPAND_BALANCED;
+
 template <bool BF16, int NBW, int PRE>
 __global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
   constexpr int NT = 4 * NBW * 32;           // columns per sub-tile
@@ -555,7 +563,7 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
 
   const int n_sub = (p.out_total + NT - 1) / NT;
   int sub = 0, groups = 1;
-  const TileRef tr = locate_tile_by<kTM>(p.seg, p.ranks, p.b_off, p.NA, static_cast<int>(blockIdx.x),
+  const TileRef tr = locate_tile_by<kTM, kExpandBalanced>(p.seg, p.ranks, p.b_off, p.NA, static_cast<int>(blockIdx.x),
                                          [&](int total) {
                                            groups = expand_groups(total, n_sub, p.wt);
                                            return groups;
