@@ -9,6 +9,8 @@
 // the rows of other adapters fed as zeros, so a row only ever receives its own
 // adapter's delta.  The delta goes through LDS to a row-major tile and is
 // added to x_ext in one bf16 read-modify-write per element.
+#include <type_traits>
+
 #include "gs_common.h"
 
 namespace gs {
@@ -79,6 +81,117 @@ __device__ f32x16 xext_block_delta(const XextArgs& a, const int* scr, int64_t m0
   return acc;
 }
 
+// Tier of kernel-local id kid (ids are numbered 1.. across the tiers in
+// ascending-rank order): tier t holds rank 16 << t; first = the tier's first
+// id; lb_off = the tier's offset in the packed lora_B.  Returns false for an
+// id past the last tier.
+__device__ __forceinline__ bool xext_tier(const XextArgs& a, int kid, int& t, int& first, int64_t& lb_off) {
+  t = 0;
+  first = 1;
+  lb_off = 0;
+  while (t < 6 && kid >= first + a.na[t]) {
+    first += a.na[t];
+    lb_off += static_cast<int64_t>(a.na[t]) * a.N * (16 << t);
+    ++t;
+  }
+  return t < 6;
+}
+
+// Fast path for modules whose tiers all have rank <= 16 KK.  A row only ever
+// receives its own adapter's delta, so each lane loads its row's shrink
+// values once (KK 16-byte pieces of slice s, zero when the row's adapter is
+// not followed), and the lora_B blocks of up to BA followed adapters are
+// loaded together, so a tile with several adapters costs one memory trip per
+// BA adapters instead of one per adapter.  The MFMA per adapter feeds the
+// rows of other adapters as zeros, as in the general path.
+// lora_B pieces one lane holds in flight per batch of adapters (registers)
+#ifndef GS_XEXT_SLOTS
+#define GS_XEXT_SLOTS 16
+#endif
+constexpr int kXextSlots = GS_XEXT_SLOTS;
+#ifndef GS_XEXT_COLS
+#define GS_XEXT_COLS 1
+#endif
+
+template <int KK>
+__device__ __forceinline__ void xext_own_z(const XextArgs& a, const int* scr, int64_t m0, int s, int id, bool row_ok,
+                                           uint64_t todo, u32x4 (&z)[KK]) {
+  const int l = __lane_id();
+  const int i = l & 31;
+  const int h = l >> 5;
+  bool ok = row_ok && id >= 1 && id <= 64 && ((todo >> (id - 1)) & 1ull);
+  int t = 0, first = 1;
+  int64_t lb_off = 0;
+  ok = xext_tier(a, ok ? id : 1, t, first, lb_off) && ok;
+  const int r = 16 << t;
+  const int64_t c0 = static_cast<int64_t>(scr[s * 6 + t]) + static_cast<int64_t>((ok ? id : first) - first) * a.S * r;
+  const uint16_t* xrow = static_cast<const uint16_t*>(a.x_ext) + (row_ok ? m0 + i : m0) * a.stride_m;
+  // unmasked (a clamped address when the row's adapter is not followed):
+  // a value is only used by the MFMA of the row's own adapter, k-step by
+  // k-step within its rank, so the loads need no wait before that
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) {
+    const bool kin = ok && kk * 16 < r;
+    z[kk] = *reinterpret_cast<const u32x4*>(xrow + (kin ? c0 + kk * 16 + 8 * h : 0));
+  }
+}
+
+// NS column blocks at once (the SwiGLU form computes the gate and the up
+// block of the same rows): n0[j] is block j's first column, z[j] the rows'
+// shrink values of its slice.
+template <int KK, int BA, int NS>
+__device__ void xext_block_delta_fast(const XextArgs& a, const int (&n0)[NS], int id, uint64_t todo,
+                                      const u32x4 (&z)[NS][KK], f32x16 (&acc)[NS]) {
+  const int l = __lane_id();
+  const int i = l & 31;
+  const int h = l >> 5;
+#pragma unroll
+  for (int j = 0; j < NS; ++j) acc[j] = f32x16{};
+  while (todo) {
+    int kid[BA], rk[BA];
+    const uint16_t* bp[BA];
+#pragma unroll
+    for (int b = 0; b < BA; ++b) {
+      kid[b] = 0;
+      rk[b] = 0;
+      bp[b] = a.lb;
+      if (todo) {   // uniform
+        const int bit = __builtin_amdgcn_readfirstlane(__ffsll(static_cast<long long>(todo)) - 1);
+        todo &= todo - 1;
+        int t, first;
+        int64_t lb_off;
+        if (xext_tier(a, bit + 1, t, first, lb_off)) {
+          kid[b] = bit + 1;
+          rk[b] = 16 << t;
+          bp[b] = a.lb + lb_off + static_cast<int64_t>(bit + 1 - first) * a.N * rk[b] + static_cast<int64_t>(i) * rk[b] +
+                  8 * h;
+        }
+      }
+    }
+    // every followed adapter's lora_B pieces in flight at once (unconditional
+    // loads; pieces past an adapter's rank read the packed array's first line)
+    u32x4 bb[NS][BA][KK];
+#pragma unroll
+    for (int j = 0; j < NS; ++j)
+#pragma unroll
+      for (int b = 0; b < BA; ++b)
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+          bb[j][b][kk] = *reinterpret_cast<const u32x4*>(
+              kk * 16 < rk[b] ? bp[b] + static_cast<int64_t>(n0[j]) * rk[b] + kk * 16 : a.lb);
+#pragma unroll
+    for (int b = 0; b < BA; ++b) {
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        if (kk * 16 < rk[b]) {   // uniform
+#pragma unroll
+          for (int j = 0; j < NS; ++j) acc[j] = mfma32_bf16(sel16(id == kid[b], z[j][kk]), bb[j][b][kk], acc[j]);
+        }
+      }
+    }
+  }
+}
+
 // Only bits for kernel-local ids that exist (1..sum(na)) may be followed.
 __device__ __forceinline__ uint64_t valid_bits(const int na[6]) {
   int tot = 0;
@@ -86,50 +199,327 @@ __device__ __forceinline__ uint64_t valid_bits(const int na[6]) {
   return tot >= 64 ? ~0ull : ((1ull << tot) - 1ull);
 }
 
+// KK = 0: the general path (one memory trip per adapter present in the
+// tile); KK > 0: the fast path above (every tier of rank <= 16 KK).
+template <int KK>
+__device__ __forceinline__ f32x16 xext_delta(const XextArgs& a, const int* scr, int64_t m0, int n0, int s, int id,
+                                             bool row_ok, uint64_t bm) {
+  if constexpr (KK == 0) {
+    return xext_block_delta(a, scr, m0, n0, s, id, row_ok, bm);
+  } else {
+    constexpr int BA = kXextSlots / KK;
+    uint64_t mine = (row_ok && id >= 1 && id <= 64) ? (1ull << (id - 1)) : 0ull;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) mine |= __shfl_xor(mine, d, 64);
+    const uint64_t todo = mine & bm;
+    u32x4 z[1][KK];
+    xext_own_z<KK>(a, scr, m0, s, id, row_ok, todo, z[0]);
+    const int n0s[1] = {n0};
+    f32x16 acc[1];
+    xext_block_delta_fast<KK, BA, 1>(a, n0s, id, todo, z, acc);
+    return acc[0];
+  }
+}
+
+// Gate and up deltas of the SwiGLU form (columns h0 of slice 0 and H + h0 of
+// slice 1).
+template <int KK>
+__device__ __forceinline__ void xext_delta_gate_up(const XextArgs& a, const int* scr, int64_t m0, int h0, int H, int id,
+                                                   bool row_ok, uint64_t bm, f32x16& ag, f32x16& au) {
+  if constexpr (KK == 0) {
+    ag = xext_block_delta(a, scr, m0, h0, 0, id, row_ok, bm);
+    au = xext_block_delta(a, scr, m0, H + h0, 1, id, row_ok, bm);
+  } else {
+    constexpr int BA = kXextSlots / 2 / KK;
+    uint64_t mine = (row_ok && id >= 1 && id <= 64) ? (1ull << (id - 1)) : 0ull;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) mine |= __shfl_xor(mine, d, 64);
+    const uint64_t todo = mine & bm;
+    u32x4 z[2][KK];
+    xext_own_z<KK>(a, scr, m0, 0, id, row_ok, todo, z[0]);
+    xext_own_z<KK>(a, scr, m0, 1, id, row_ok, todo, z[1]);
+    const int n0s[2] = {h0, H + h0};
+    f32x16 acc[2];
+    xext_block_delta_fast<KK, BA, 2>(a, n0s, id, todo, z, acc);
+    ag = acc[0];
+    au = acc[1];
+  }
+}
+
+template <int KK>
 __global__ __launch_bounds__(256) void xext_expand_kernel(XextArgs a, uint16_t* x_out, const int32_t* __restrict__ tile_slice,
                                                           int block_n) {
   __shared__ float dtile[32][128 + 4];
   __shared__ int scr[GS_MAX_SLICES * 6];
   const int64_t pm = blockIdx.y;
-  const uint64_t bm = static_cast<uint64_t>(a.bitmask[pm * a.stride_bm]) & valid_bits(a.na);
-  if (a.bitmask[pm * a.stride_bm] == 0) return;
-  // the slice column table, staged once (the adapter loop reads it per adapter)
-  if (threadIdx.x < a.S * 6) scr[threadIdx.x] = a.slice_col_r[threadIdx.x];
   const int n_tile0 = blockIdx.x * 128;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int l = tid & 63;
   const int i = l & 31;
   const int64_t m0 = pm * 32;
+  // everything that depends on no earlier load goes out first: the tile
+  // mask, the rows' ids, the slice tables and this thread's read-modify-write
+  // piece (row tid / 8, 16 columns, from a clamped in-bounds address)
+  const int64_t bm_raw = a.bitmask[pm * a.stride_bm];
   const bool row_ok = (m0 + i) < a.M;
   const int id = row_ok ? load_id(a.ids, a.idx_bytes, m0 + i) : 0;
-
+  if (tid < a.S * 6) scr[tid] = a.slice_col_r[tid];
   const int n0 = n_tile0 + 32 * wave;
   const int s = tile_slice[(n0 < a.N ? n0 : n_tile0) / block_n];
+  const int row = tid >> 3;
+  const int cx = (tid & 7) * 16;
+  const int64_t m = m0 + row;
+  const bool out_ok = m < a.M && n_tile0 + cx < a.N;
+  uint16_t* p = x_out + (out_ok ? m : m0) * a.stride_m + (out_ok ? n_tile0 + cx : n_tile0);
+  const int out_id = out_ok ? load_id(a.ids, a.idx_bytes, m) : 0;
+  u32x4 in[2];
+#pragma unroll
+  for (int half = 0; half < 2; ++half) in[half] = *reinterpret_cast<const u32x4*>(p + half * 8);
+  if (bm_raw == 0) return;
+  const uint64_t bm = static_cast<uint64_t>(bm_raw) & valid_bits(a.na);
   lds_barrier();
   f32x16 acc = f32x16{};
-  if (n0 < a.N) acc = xext_block_delta(a, scr, m0, n0, s, id, row_ok, bm);
+  if (n0 < a.N) acc = xext_delta<KK>(a, scr, m0, n0, s, id, row_ok, bm);
 #pragma unroll
   for (int v = 0; v < 16; ++v) dtile[mfma32_row(v, l)][32 * wave + i] = acc[v];
   lds_barrier();
 
-  const int row = tid >> 3;
-  const int cx = (tid & 7) * 16;
-  const int64_t m = m0 + row;
-  if (m >= a.M || n_tile0 + cx >= a.N) return;
-  if (load_id(a.ids, a.idx_bytes, m) == 0) return;   // base rows are never written
-  uint16_t* p = x_out + m * a.stride_m + n_tile0 + cx;
+  if (!out_ok || out_id == 0) return;   // base rows are never written
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
-    const u32x4 in = *reinterpret_cast<const u32x4*>(p + half * 8);
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float lo = bf16_bits_to_f32(static_cast<uint16_t>(in[e] & 0xffffu)) + dtile[row][cx + half * 8 + 2 * e];
-      const float hi = bf16_bits_to_f32(static_cast<uint16_t>(in[e] >> 16)) + dtile[row][cx + half * 8 + 2 * e + 1];
+      const float lo = bf16_bits_to_f32(static_cast<uint16_t>(in[half][e] & 0xffffu)) + dtile[row][cx + half * 8 + 2 * e];
+      const float hi = bf16_bits_to_f32(static_cast<uint16_t>(in[half][e] >> 16)) + dtile[row][cx + half * 8 + 2 * e + 1];
       o[e] = static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
     }
     *reinterpret_cast<u32x4*>(p + half * 8) = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Column-block form of the in-place expand, for modules whose tiers all have
+// rank <= 16 KK.  A workgroup owns 32 CB columns over kColsRT = 4
+// consecutive 32-row tiles, one wave per row tile.  The lora_B blocks of the
+// adapters followed in any of its tiles are staged in LDS once per workgroup
+// (an adapter's block for 32 CB consecutive columns is one contiguous run of
+// the packed array), so a column's lora_B is read once per four row tiles
+// instead of once per tile -- in a decode batch every tile holds most
+// adapters, and the per-tile form moved ~7x the unique lora_B bytes.  Each
+// lane loads its own row's shrink values once (a row only receives its own
+// adapter's delta); the per-adapter MFMA feeds the rows of other adapters as
+// zeros, as in the per-tile form.  At most kColsChunk(KK) adapters are staged
+// at a time.  Results go through LDS to row-major pieces for the
+// read-modify-write, whose loads are issued first.
+// ----------------------------------------------------------------------------
+constexpr int kColsRT = 4;
+
+// The id of row i: int64 ids are read as their low 32-bit word (little
+// endian), which is exactly static_cast<int> of the value, so no load leaves
+// a dead high half whose register reuse would force a wait.
+template <bool I64>
+__device__ __forceinline__ int load_id_t(const void* p, int64_t i) {
+  return static_cast<const int32_t*>(p)[I64 ? 2 * i : i];
+}
+
+template <int KK, int CB, bool I64>
+__global__ __launch_bounds__(256) void xext_cols_kernel(XextArgs a, uint16_t* x_out,
+                                                        const int32_t* __restrict__ tile_slice, int block_n) {
+  constexpr int NC = 32 * CB;                  // columns of the workgroup
+  constexpr int RMAX = 16 * KK;                // largest rank of the module
+  constexpr int CST = RMAX * 2 + 16;           // LDS bytes per column of a staged block (padded)
+  constexpr int ABLK = NC * CST;               // LDS bytes per staged adapter
+  constexpr int CA = CB == 1 ? 16 : 8;         // adapters staged at a time
+  constexpr int CAW = CA / kColsRT;            // adapters each wave stages
+  constexpr int QP = NC * RMAX / 8 / 64;       // 16-byte pieces per lane of one block at rank RMAX
+  constexpr int DLD = NC + 4;                  // fp32 row stride of the transposed delta
+  constexpr int LPR = NC / 16;                 // lanes per row in the read-modify-write
+  constexpr int PASSES = 32 * LPR / 64;        // rows per lane
+  static_assert(kColsRT * 32 * DLD * 4 <= CA * ABLK, "the delta tile must fit the staging buffer");
+  __shared__ __align__(16) char bs[CA * ABLK + 64 * 16];   // + a sink for masked-off pieces
+  __shared__ int scr[GS_MAX_SLICES * 6];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63;
+  const int i = l & 31;
+  const int h = l >> 5;
+  const int n_blk0 = blockIdx.x * NC;
+  const int64_t pm0 = static_cast<int64_t>(blockIdx.y) * kColsRT;
+  const int64_t pm = pm0 + wave;               // this wave's row tile
+  const int64_t m0 = pm * 32;
+  const int64_t n_tiles = (a.M + 31) / 32;
+  const int ncols = min(NC, a.N - n_blk0);
+
+  // The tile masks (uniform) name the adapters the reference's loop follows
+  // in each tile; their union over the workgroup's tiles is staged.
+  int64_t bmt[kColsRT];
+#pragma unroll
+  for (int w = 0; w < kColsRT; ++w) bmt[w] = pm0 + w < n_tiles ? a.bitmask[(pm0 + w) * a.stride_bm] : 0;
+  // loads that depend on nothing: ids, slice tables, this lane's
+  // read-modify-write pieces (clamped in-bounds addresses, masked afterwards)
+  const bool row_ok = (m0 + i) < a.M;
+  const int id_raw = load_id_t<I64>(a.ids, row_ok ? m0 + i : 0);
+  const int scr_v = a.slice_col_r[tid < a.S * 6 ? tid : 0];
+  int sc[CB];
+#pragma unroll
+  for (int c = 0; c < CB; ++c) {
+    const int n0 = n_blk0 + 32 * c;
+    sc[c] = tile_slice[(n0 < a.N ? n0 : n_blk0) / block_n];
+  }
+  const int cx = (l % LPR) * 16;
+  int64_t orow[PASSES];
+  bool ook[PASSES];
+  int oid[PASSES];
+  u32x4 in[PASSES][2];
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const int64_t m = m0 + ps * (64 / LPR) + l / LPR;
+    ook[ps] = m < a.M && n_blk0 + cx < a.N;
+    orow[ps] = ook[ps] ? m : 0;
+    const uint16_t* src = x_out + orow[ps] * a.stride_m + (ook[ps] ? n_blk0 + cx : 0);
+    in[ps][0] = *reinterpret_cast<const u32x4*>(src);
+    in[ps][1] = *reinterpret_cast<const u32x4*>(src + 8);
+    oid[ps] = load_id_t<I64>(a.ids, orow[ps]);
+  }
+  __builtin_amdgcn_sched_barrier(0);   // all of the above in flight before any of it is used
+
+  const uint64_t valid = valid_bits(a.na);
+  const int64_t bm_tile = bmt[0] * (wave == 0) + bmt[1] * (wave == 1) + bmt[2] * (wave == 2) + bmt[3] * (wave == 3);
+  const uint64_t todo = static_cast<uint64_t>(bm_tile) & valid;
+  uint64_t all = (static_cast<uint64_t>(bmt[0]) | static_cast<uint64_t>(bmt[1]) | static_cast<uint64_t>(bmt[2]) |
+                  static_cast<uint64_t>(bmt[3])) & valid;
+
+  f32x16 acc[2][CB];
+#pragma unroll
+  for (int c = 0; c < CB; ++c) acc[0][c] = acc[1][c] = f32x16{};
+  u32x4 z[CB][KK];
+  int id = 0;
+  // one chunk of up to CA adapters; the first is straight-line code (its
+  // staging loads go out right behind the first loads, before the ids are
+  // used), later chunks run in a loop
+  auto chunk = [&](auto first_tag) {
+    constexpr bool FIRST = decltype(first_tag)::value;
+    // lane j < CA describes the chunk's j-th adapter: kernel-local id, rank
+    // and the offset of its block for this workgroup's columns
+    int my_kid = 0, my_r = 0;
+    int64_t my_off = 0;
+    if (l < CA) {
+      uint64_t mm = all;
+      for (int k = 0; k < l; ++k) mm &= mm - 1;
+      if (mm) {
+        const int bit = __ffsll(static_cast<long long>(mm)) - 1;
+        int t, first;
+        int64_t lb_off;
+        if (xext_tier(a, bit + 1, t, first, lb_off)) {
+          my_kid = bit + 1;
+          my_r = 16 << t;
+          my_off = lb_off + (static_cast<int64_t>(bit + 1 - first) * a.N + n_blk0) * my_r;
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < CA; ++k) all &= all - 1;
+    // wave w stages adapters w, w + 4, ...: lane l moves pieces l + 64 q of
+    // each block (pieces past the adapter's ncols * r / 8 read the first line)
+    u32x4 v[CAW][QP];
+#pragma unroll
+    for (int jw = 0; jw < CAW; ++jw) {
+      const int j = kColsRT * jw + wave;
+      const int r = __builtin_amdgcn_readlane(my_r, j);
+      const int64_t off = static_cast<int64_t>(
+          (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(my_off >> 32), j))) << 32) |
+          static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(my_off & 0xffffffff), j)));
+      const uint16_t* base = a.lb + off;
+#pragma unroll
+      for (int q = 0; q < QP; ++q) {
+        const int pc = l + 64 * q;
+        v[jw][q] = *reinterpret_cast<const u32x4*>(pc < ncols * r / 8 ? base + 8 * pc : a.lb);
+      }
+    }
+    if constexpr (FIRST) {
+      // the rows' own shrink values: they need the ids and the slice table,
+      // whose loads were issued before the staging loads
+      if (tid < a.S * 6) scr[tid] = scr_v;
+      id = row_ok && pm < n_tiles ? id_raw : 0;
+      lds_barrier();   // scr
+#pragma unroll
+      for (int c = 0; c < CB; ++c) xext_own_z<KK>(a, scr, m0, sc[c], id, row_ok, todo, z[c]);
+    }
+    // every lane stores every piece: masked-off ones go to the sink, so no
+    // store sits under a branch (r / 8 = 2 << tier pieces per column)
+#pragma unroll
+    for (int jw = 0; jw < CAW; ++jw) {
+      const int j = kColsRT * jw + wave;
+      const int r = __builtin_amdgcn_readlane(my_r, j);
+      const int sh = 31 - __builtin_clz(r > 0 ? r / 8 : 1);
+#pragma unroll
+      for (int q = 0; q < QP; ++q) {
+        const int pc = l + 64 * q;
+        char* dst = pc < ncols * r / 8 ? bs + j * ABLK + (pc >> sh) * CST + (pc & ((1 << sh) - 1)) * 16
+                                       : bs + CA * ABLK + l * 16;
+        *reinterpret_cast<u32x4*>(dst) = v[jw][q];
+      }
+    }
+    lds_barrier();
+    // adapters this wave's tile follows, two accumulation chains; each
+    // adapter's operands are read from LDS one adapter ahead
+    u32x4 bn[CB][KK];
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk)
+        bn[c][kk] = *reinterpret_cast<const u32x4*>(bs + (32 * c + i) * CST + (kk * 16 + 8 * h) * 2);
+#pragma unroll
+    for (int j = 0; j < CA; ++j) {
+      u32x4 bc[CB][KK];
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) bc[c][kk] = bn[c][kk];
+      if (j + 1 < CA) {
+#pragma unroll
+        for (int c = 0; c < CB; ++c)
+#pragma unroll
+          for (int kk = 0; kk < KK; ++kk)
+            bn[c][kk] = *reinterpret_cast<const u32x4*>(bs + (j + 1) * ABLK + (32 * c + i) * CST + (kk * 16 + 8 * h) * 2);
+      }
+      const int kid = __builtin_amdgcn_readlane(my_kid, j);
+      const int r = __builtin_amdgcn_readlane(my_r, j);
+      if (kid == 0 || !((todo >> (kid - 1)) & 1ull)) continue;   // uniform
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        if (kk * 16 >= r) break;
+#pragma unroll
+        for (int c = 0; c < CB; ++c)
+          acc[j & 1][c] = mfma32_bf16(sel16(id == kid, z[c][kk]), bc[c][kk], acc[j & 1][c]);
+      }
+    }
+    lds_barrier();   // the staging buffer is refilled (or becomes the delta tile)
+  };
+  if (all) {
+    chunk(std::true_type{});
+    while (all) chunk(std::false_type{});
+  }
+
+  if (bm_tile == 0) return;   // the reference skips a tile whose mask is 0
+  float* dt = reinterpret_cast<float*>(bs) + wave * 32 * DLD;
+#pragma unroll
+  for (int c = 0; c < CB; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dt[mfma32_row(e, l) * DLD + 32 * c + i] = acc[0][c][e] + acc[1][c][e];
+  __builtin_amdgcn_wave_barrier();
+  // rows with an adapter get x + delta rounded once (a zero delta stores x
+  // back, as the reference's read-modify-write does); base rows are untouched
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    if (!ook[ps] || oid[ps] == 0) continue;
+    const int row = ps * (64 / LPR) + l / LPR;
+    uint16_t* dst = x_out + orow[ps] * a.stride_m + n_blk0 + cx;
+    *reinterpret_cast<u32x4*>(dst) = add_y16<true>(in[ps][0], dt + row * DLD + cx);
+    *reinterpret_cast<u32x4*>(dst + 8) = add_y16<true>(in[ps][1], dt + row * DLD + cx + 8);
   }
 }
 
@@ -139,7 +529,7 @@ __global__ __launch_bounds__(256) void xext_expand_kernel(XextArgs a, uint16_t* 
 // here every workgroup stores its whole 32 x 128 tile -- the delta, exactly
 // zero for base rows (they select no adapter), and zeros for a tile whose
 // bitmask is 0 -- so out is written once and no zeroing pass is needed.
-template <bool F32OUT>
+template <bool F32OUT, int KK>
 __global__ __launch_bounds__(256) void xext_shrink_expand_kernel(XextArgs a, void* out, int64_t stride_om,
                                                                  const int32_t* __restrict__ tile_slice,
                                                                  int block_n) {
@@ -162,7 +552,7 @@ __global__ __launch_bounds__(256) void xext_shrink_expand_kernel(XextArgs a, voi
     const int s = tile_slice[(n0 < a.N ? n0 : n_tile0) / block_n];
     lds_barrier();
     f32x16 acc = f32x16{};
-    if (n0 < a.N) acc = xext_block_delta(a, scr, m0, n0, s, id, row_ok, bm);
+    if (n0 < a.N) acc = xext_delta<KK>(a, scr, m0, n0, s, id, row_ok, bm);
 #pragma unroll
     for (int v = 0; v < 16; ++v) dtile[mfma32_row(v, l)][32 * wave + i] = acc[v];
     lds_barrier();
@@ -194,6 +584,7 @@ __global__ __launch_bounds__(256) void xext_shrink_expand_kernel(XextArgs a, voi
   }
 }
 
+template <int KK>
 __global__ __launch_bounds__(256) void xext_swiglu_kernel(XextArgs a, uint16_t* out, int64_t stride_om, int H) {
   __shared__ float dg[32][128 + 4];
   __shared__ float du[32][128 + 4];
@@ -229,10 +620,7 @@ __global__ __launch_bounds__(256) void xext_swiglu_kernel(XextArgs a, uint16_t* 
     lds_barrier();
     const int h0 = h_tile0 + 32 * wave;
     f32x16 ag = f32x16{}, au = f32x16{};
-    if (h0 < H) {
-      ag = xext_block_delta(a, scr, m0, h0, 0, id, row_ok, bm);
-      au = xext_block_delta(a, scr, m0, H + h0, 1, id, row_ok, bm);
-    }
+    if (h0 < H) xext_delta_gate_up<KK>(a, scr, m0, h0, H, id, row_ok, bm, ag, au);
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       dg[mfma32_row(v, l)][32 * wave + i] = ag[v];
@@ -264,6 +652,20 @@ __global__ __launch_bounds__(256) void xext_swiglu_kernel(XextArgs a, uint16_t* 
     }
     *reinterpret_cast<u32x4*>(orow + half * 8) = u32x4{o[0], o[1], o[2], o[3]};
   }
+}
+
+// Fast-path width for the module's tiers: 2 pieces (rank <= 32), 4 (<= 64),
+// or 0 (a tier of rank 128 or more is used: the general path).
+// Only decode-sized batches take it: with many tokens a 32-row tile holds one
+// or two adapters, the per-adapter trips are few, and the general kernels'
+// higher occupancy wins.
+constexpr int64_t kFastMaxRows = 1024;
+int xext_kk(const int32_t* na, int64_t M) {
+  if (M > kFastMaxRows) return 0;
+  int top = -1;
+  for (int t = 0; t < 6; ++t)
+    if (na[t] > 0) top = t;
+  return top <= 1 ? 2 : (top == 2 ? 4 : 0);
 }
 
 int check_xext(const char* who, const void* x_ext, int64_t stride_n, int64_t stride_m, int64_t M, int32_t idx_bytes,
@@ -313,8 +715,31 @@ int gs_switch_lora_expand(void* x_ext, int64_t stride_m, int64_t stride_n, int64
   a.S = S;
   a.N = N;
   dim3 grid((N + 127) / 128, static_cast<unsigned>((M + 31) / 32));
-  hipLaunchKernelGGL(xext_expand_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a,
-                     static_cast<uint16_t*>(x_ext), tile_slice, block_n);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  uint16_t* xo = static_cast<uint16_t*>(x_ext);
+  const int kk = xext_kk(na, M);
+  if (kk > 0 && GS_XEXT_COLS) {
+    // 64-column blocks (whole 128-byte row pieces) once they give two
+    // workgroups per CU; 32-column blocks otherwise
+    const unsigned row_groups = static_cast<unsigned>(((M + 31) / 32 + kColsRT - 1) / kColsRT);
+    const bool wide = int64_t(N / 64) * row_groups >= 2 * int64_t(device_cus());
+    const dim3 g2(static_cast<unsigned>((N + 63) / 64), row_groups), g1(static_cast<unsigned>(N / 32), row_groups);
+    auto go = [&](auto kern, dim3 g) { hipLaunchKernelGGL(kern, g, dim3(256), 0, st, a, xo, tile_slice, block_n); };
+    if (idx_bytes == 8) {
+      if (kk == 2) wide ? go(xext_cols_kernel<2, 2, true>, g2) : go(xext_cols_kernel<2, 1, true>, g1);
+      else wide ? go(xext_cols_kernel<4, 2, true>, g2) : go(xext_cols_kernel<4, 1, true>, g1);
+    } else {
+      if (kk == 2) wide ? go(xext_cols_kernel<2, 2, false>, g2) : go(xext_cols_kernel<2, 1, false>, g1);
+      else wide ? go(xext_cols_kernel<4, 2, false>, g2) : go(xext_cols_kernel<4, 1, false>, g1);
+    }
+    GS_CHECK_LAUNCH("gs_switch_lora_expand");
+    return GS_OK;
+  }
+  switch (kk) {
+    case 2: hipLaunchKernelGGL(xext_expand_kernel<2>, grid, dim3(256), 0, st, a, xo, tile_slice, block_n); break;
+    case 4: hipLaunchKernelGGL(xext_expand_kernel<4>, grid, dim3(256), 0, st, a, xo, tile_slice, block_n); break;
+    default: hipLaunchKernelGGL(xext_expand_kernel<0>, grid, dim3(256), 0, st, a, xo, tile_slice, block_n); break;
+  }
   GS_CHECK_LAUNCH("gs_switch_lora_expand");
   return GS_OK;
 }
@@ -348,10 +773,16 @@ int gs_switch_lora_shrink_expand(void* out, int32_t out_dtype, int64_t stride_om
   a.N = N;
   dim3 grid((N + 127) / 128, static_cast<unsigned>((M + 31) / 32));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (out_dtype == GS_DTYPE_FP32)
-    hipLaunchKernelGGL(xext_shrink_expand_kernel<true>, grid, dim3(256), 0, st, a, out, stride_om, tile_slice, block_n);
-  else
-    hipLaunchKernelGGL(xext_shrink_expand_kernel<false>, grid, dim3(256), 0, st, a, out, stride_om, tile_slice, block_n);
+  const int kk = xext_kk(na, M);
+  if (out_dtype == GS_DTYPE_FP32) {
+    if (kk == 2) hipLaunchKernelGGL((xext_shrink_expand_kernel<true, 2>), grid, dim3(256), 0, st, a, out, stride_om, tile_slice, block_n);
+    else if (kk == 4) hipLaunchKernelGGL((xext_shrink_expand_kernel<true, 4>), grid, dim3(256), 0, st, a, out, stride_om, tile_slice, block_n);
+    else hipLaunchKernelGGL((xext_shrink_expand_kernel<true, 0>), grid, dim3(256), 0, st, a, out, stride_om, tile_slice, block_n);
+  } else {
+    if (kk == 2) hipLaunchKernelGGL((xext_shrink_expand_kernel<false, 2>), grid, dim3(256), 0, st, a, out, stride_om, tile_slice, block_n);
+    else if (kk == 4) hipLaunchKernelGGL((xext_shrink_expand_kernel<false, 4>), grid, dim3(256), 0, st, a, out, stride_om, tile_slice, block_n);
+    else hipLaunchKernelGGL((xext_shrink_expand_kernel<false, 0>), grid, dim3(256), 0, st, a, out, stride_om, tile_slice, block_n);
+  }
   GS_CHECK_LAUNCH(who);
   return GS_OK;
 }
@@ -381,8 +812,13 @@ int gs_switch_lora_expand_swiglu(void* out, int64_t stride_om, int64_t stride_on
   a.S = S;
   a.N = N;
   dim3 grid((H + 127) / 128, static_cast<unsigned>((M + 31) / 32));
-  hipLaunchKernelGGL(xext_swiglu_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a,
-                     static_cast<uint16_t*>(out), stride_om, H);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  uint16_t* o = static_cast<uint16_t*>(out);
+  switch (xext_kk(na, M)) {
+    case 2: hipLaunchKernelGGL(xext_swiglu_kernel<2>, grid, dim3(256), 0, st, a, o, stride_om, H); break;
+    case 4: hipLaunchKernelGGL(xext_swiglu_kernel<4>, grid, dim3(256), 0, st, a, o, stride_om, H); break;
+    default: hipLaunchKernelGGL(xext_swiglu_kernel<0>, grid, dim3(256), 0, st, a, o, stride_om, H); break;
+  }
   GS_CHECK_LAUNCH("gs_switch_lora_expand_swiglu");
   return GS_OK;
 }
