@@ -44,7 +44,6 @@ class _SwitchedBase(nn.Module):
         self._packed = None
         self._auto_pack = None
         self._auto_key = None
-        self._auto_pack = None
 
     def _weights_key(self):
         A_sl, B_sl = self._slices()
