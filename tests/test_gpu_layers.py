@@ -125,6 +125,44 @@ def test_switch_lora_expand_op_matches_oracle(dev):
         assert np.array_equal(_np(xe)[:, layer._N_total:], x_ext0[:, layer._N_total:])
 
 
+@pytest.mark.parametrize("slices,ranks,T", [
+    ((4096, 96), [32, 16, 32, 8], 1000),      # column blocks of 64 (a partial last one), ragged last row group
+    ((512,), [64, 16, 64], 700),              # rank-64 tier, 32-column blocks
+    ((256, 128), [128, 16], 300),             # a rank-128 tier: the per-tile kernel at decode sizes
+    ((1024, 256), [32, 16, 8], 1500),         # past 1024 rows: the per-tile kernel
+])
+def test_switch_lora_expand_op_kernel_forms(dev, slices, ranks, T):
+    """Each kernel form of the reference op (column-block at decode batch
+    sizes with 32- and 64-column blocks, per-tile past 1024 rows or with a tier
+    above rank 64) vs the oracle, with int64 and int32 ids; base rows and the
+    shrink columns are untouched."""
+    K = 256
+    layer, W, A, B = _make_vllm_layer(dev, K, slices, ranks, seed=31 + T)
+    g = torch.Generator(device=dev).manual_seed(T)
+    x = torch.randn(T, K, generator=g, device=dev).to(torch.bfloat16)
+    ids = torch.randint(0, len(ranks) + 1, (T,), generator=g, device=dev)
+    ids[T // 3: T // 3 + 40] = 0                     # a run of base rows (an all-base tile)
+    ctx = _ctx_for(dev, layer, ids)
+    x_ext = torch.mm(x, layer.w_ext.T)
+    x_ext0 = _np(x_ext)
+    loc = ctx.remapped_indices[0]
+    ref = olora.switch_lora_expand_xext(x_ext0, loc.cpu().numpy(), ctx.per_module_bitmasks[0].cpu().numpy(),
+                                        _np(layer._lb_packed), layer.tile_to_slice.cpu().numpy(),
+                                        layer.slice_col_r.cpu().numpy(), layer._na, layer._S, layer._block_n,
+                                        layer._N_total)
+    base = (loc == 0).cpu().numpy()
+    for idx in (loc, loc.to(torch.int32)):
+        _say(f"expand op forms: slices={slices} ranks={ranks} T={T} ids={idx.dtype}")
+        xe = x_ext.clone()
+        ops.op("switch_lora_expand")(xe, idx, ctx.per_module_bitmasks[0], layer._lb_packed, layer.tile_to_slice,
+                                      layer.slice_col_r, *layer._na, layer._S, layer._block_n, layer._N_total)
+        torch.cuda.synchronize()
+        got = _np(xe)
+        _close(got, ref, 2e-2, "switch_lora_expand")
+        assert np.array_equal(got[base], x_ext0[base]), "base rows touched"
+        assert np.array_equal(got[:, layer._N_total:], x_ext0[:, layer._N_total:]), "shrink columns written"
+
+
 def test_switch_lora_expand_zero_bitmask_skips(dev):
     slices, ranks, K, T = (128,), [16, 16], 256, 64
     layer, W, A, B = _make_vllm_layer(dev, K, slices, ranks, seed=12)
