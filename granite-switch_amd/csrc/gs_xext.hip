@@ -125,7 +125,9 @@ __device__ __forceinline__ void xext_own_z(const XextArgs& a, const int* scr, in
   ok = xext_tier(a, ok ? id : 1, t, first, lb_off) && ok;
   const int r = 16 << t;
   const int64_t c0 = static_cast<int64_t>(scr[s * 6 + t]) + static_cast<int64_t>((ok ? id : first) - first) * a.S * r;
-  const uint16_t* xrow = static_cast<const uint16_t*>(a.x_ext) + (row_ok ? m0 + i : m0) * a.stride_m;
+  // a row past the batch (row_ok false: also the idle waves of a column-block
+  // workgroup, whose whole tile lies past it) reads row 0
+  const uint16_t* xrow = static_cast<const uint16_t*>(a.x_ext) + (row_ok ? m0 + i : 0) * a.stride_m;
   // unmasked (a clamped address when the row's adapter is not followed):
   // a value is only used by the MFMA of the row's own adapter, k-step by
   // k-step within its rank, so the loads need no wait before that
