@@ -35,8 +35,9 @@ GS_NOALLOC_SCRATCH_BYTES = 64 << 20
 SIGNATURES = {
     "gs_version": (c_i32, []),
     "gs_last_error": (ctypes.c_char_p, []),
+    "gs_build_segments_workspace_bytes": (c_i64, [c_i64, c_i32]),
     "gs_build_segments": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, c_i64, c_i32, c_i32, c_void_p, c_void_p,
-                                  c_void_p, c_void_p]),
+                                  c_void_p, c_void_p, c_i64, c_void_p]),
     "gs_route_latest_wins": (c_i32, [c_void_p, c_void_p, c_i64, c_i32, c_void_p, c_i32, c_i32, c_void_p, c_void_p,
                                      c_void_p]),
     "gs_shrink_workspace_bytes": (c_i64, [c_i64, c_i32, c_i32, c_i32, c_i32]),

@@ -85,6 +85,51 @@ __device__ __forceinline__ uint64_t match_id(int id, bool active, int nbits) {
   return match;
 }
 
+// Segment starts from the per-adapter totals (an exclusive scan by wave 0;
+// workgroup 0 writes seg), the chunk's cursor per adapter (segment start +
+// tokens of the adapter before the chunk, already in cursor), then the
+// chunk's stable scatter: a token's rank among equal ids of lower lanes is a
+// popcount, per-wave counts in LDS give the rank across waves.
+__device__ __forceinline__ void finish_chunk(const BuildArgs& a, const int* total, int* cursor,
+                                             int (*wcnt)[GS_MAX_ADAPTERS + 1], int mine, int c0, int nbits) {
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int NA = a.NA;
+  if (wave == 0) {
+    const int lane = tid & 63;
+    int carry = 0;
+    if (lane == 0 && blockIdx.x == 0) a.seg[0] = 0;
+    for (int g0 = 1; g0 <= NA; g0 += 64) {
+      const int g = g0 + lane;
+      const int v = (g <= NA) ? total[g] : 0;
+      int incl = v;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        int u = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += u;
+      }
+      if (g <= NA) {
+        cursor[g] += carry + incl - v;
+        if (blockIdx.x == 0) a.seg[g] = carry + incl;
+      }
+      carry += __shfl(incl, 63, 64);
+    }
+  }
+  lds_barrier();
+
+  const int t = c0 + tid;
+  const bool active = t < a.T && mine > 0;
+  const uint64_t match = match_id(mine, active, nbits);
+  const uint64_t below = match & lanemask_lt();
+  if (active && below == 0) wcnt[wave][mine] = __popcll(match);
+  lds_barrier();
+  if (active) {
+    int pp = cursor[mine] + __popcll(below);
+    for (int w = 0; w < wave; ++w) pp += wcnt[w][mine];   // zero where wave w has none of this id
+    a.perm[pp] = t;
+  }
+}
+
 __global__ __launch_bounds__(kBuildThreads) void build_segments_kernel(BuildArgs a) {
   __shared__ int total[GS_MAX_ADAPTERS + 1];
   __shared__ int cursor[GS_MAX_ADAPTERS + 1];     // counts before this chunk, then the chunk's cursors
@@ -155,42 +200,101 @@ __global__ __launch_bounds__(kBuildThreads) void build_segments_kernel(BuildArgs
   }
   lds_barrier();
 
-  // Exclusive scan of total[1..NA] by wave 0: segment starts; the chunk's
-  // cursor = segment start + tokens of the adapter before the chunk.
-  if (wave == 0) {
-    const int lane = tid & 63;
-    int carry = 0;
-    if (lane == 0 && blockIdx.x == 0) a.seg[0] = 0;
-    for (int g0 = 1; g0 <= NA; g0 += 64) {
-      const int g = g0 + lane;
-      const int v = (g <= NA) ? total[g] : 0;
-      int incl = v;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        int u = __shfl_up(incl, d, 64);
-        if (lane >= d) incl += u;
-      }
-      if (g <= NA) {
-        cursor[g] += carry + incl - v;
-        if (blockIdx.x == 0) a.seg[g] = carry + incl;
-      }
-      carry += __shfl(incl, 63, 64);
+  finish_chunk(a, total, cursor, wcnt, mine, c0, nbits);
+}
+
+// ---------------------------------------------------------------------------
+// Two-launch form for long batches, where every workgroup re-reading the
+// whole batch would cost more than a second launch: build_count_kernel gates
+// one chunk per workgroup and writes the chunk's per-adapter histogram to a
+// workspace ([chunks][NA+1] int32); build_scatter_kernel sums the histograms
+// (all chunks: totals; chunks before its own: cursors) and scatters its chunk
+// exactly as the one-launch kernel does.  The workspace is written in full by
+// the first launch before the second reads it, so it needs no clearing.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kBuildThreads) void build_count_kernel(BuildArgs a, int32_t* __restrict__ hist) {
+  __shared__ int cnt[GS_MAX_ADAPTERS + 1];
+  __shared__ int32_t cu_s[kCuCap];
+  __shared__ int64_t off_s[kCuCap];
+  const int tid = threadIdx.x;
+  const int NA = a.NA;
+  const int t = static_cast<int>(blockIdx.x) * kBuildThreads + tid;
+  const int tc = min(t, a.T - 1);
+  const int64_t rq = a.req[tc];
+  const int64_t ps = (a.pos != nullptr && a.act_off != nullptr) ? a.pos[tc] : 0;
+  for (int i = tid; i <= NA; i += kBuildThreads) cnt[i] = 0;
+  const int nseq = a.cu != nullptr ? a.num_seqs : 1;
+  const bool seq_in_lds = a.act_off != nullptr && nseq <= kCuCap;
+  if (seq_in_lds) {
+    for (int i = tid; i < nseq; i += kBuildThreads) {
+      cu_s[i] = a.cu != nullptr ? a.cu[i] : 0;
+      off_s[i] = a.act_off[i];
     }
   }
   lds_barrier();
-
-  // Pass 2: stable scatter of this chunk.
-  const int t = c0 + tid;
-  const bool active = t < T && mine > 0;
-  const uint64_t match = match_id(mine, active, nbits);
-  const uint64_t below = match & lanemask_lt();
-  if (active && below == 0) wcnt[wave][mine] = __popcll(match);
+  int nbits = 0;
+  while ((1 << nbits) <= NA) ++nbits;
+  const int id = t < a.T ? gate_id(a, seq_in_lds && a.cu != nullptr ? cu_s : nullptr, seq_in_lds ? off_s : nullptr, t,
+                                   rq, ps)
+                         : 0;
+  if (t < a.T) a.eff[t] = id;
+  const bool active = id > 0;
+  const uint64_t match = match_id(id, active, nbits);
+  if (active && (match & lanemask_lt()) == 0) atomicAdd(&cnt[id], __popcll(match));
   lds_barrier();
-  if (active) {
-    int pp = cursor[mine] + __popcll(below);
-    for (int w = 0; w < wave; ++w) pp += wcnt[w][mine];   // zero where wave w has none of this id
-    a.perm[pp] = t;
+  for (int i = tid; i <= NA; i += kBuildThreads) hist[static_cast<int64_t>(blockIdx.x) * (NA + 1) + i] = cnt[i];
+}
+
+constexpr int kHistPre = 8;
+
+// Chunks from which the two-launch form is the faster one (its workspace
+// query returns 0 below), and its workspace size.
+#ifndef GS_BUILD_SPLIT_CHUNKS
+#define GS_BUILD_SPLIT_CHUNKS 2
+#endif
+constexpr int64_t kBuildSplitChunks = GS_BUILD_SPLIT_CHUNKS;
+inline int64_t build_hist_bytes(int64_t chunks, int num_adapters) { return chunks * (num_adapters + 1) * 4; }   // histogram entries loaded per thread before any is added
+
+__global__ __launch_bounds__(kBuildThreads) void build_scatter_kernel(BuildArgs a, const int32_t* __restrict__ hist,
+                                                                      int nchunks) {
+  __shared__ int total[GS_MAX_ADAPTERS + 1];
+  __shared__ int cursor[GS_MAX_ADAPTERS + 1];
+  __shared__ int wcnt[kBuildWaves][GS_MAX_ADAPTERS + 1];
+  const int tid = threadIdx.x;
+  const int NA = a.NA;
+  const int c = static_cast<int>(blockIdx.x);
+  const int c0 = c * kBuildThreads;
+  const int mine = c0 + tid < a.T ? a.eff[c0 + tid] : 0;
+  for (int i = tid; i <= NA; i += kBuildThreads) {
+    total[i] = 0;
+    cursor[i] = 0;
   }
+  for (int i = tid; i < kBuildWaves * (GS_MAX_ADAPTERS + 1); i += kBuildThreads) (&wcnt[0][0])[i] = 0;
+  lds_barrier();
+  const int width = NA + 1;
+  const int n = nchunks * width;
+  for (int i0 = 0; i0 < n; i0 += kHistPre * kBuildThreads) {
+    int v[kHistPre];
+#pragma unroll
+    for (int u = 0; u < kHistPre; ++u) {
+      const int i = i0 + u * kBuildThreads + tid;
+      v[u] = i < n ? hist[i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kHistPre; ++u) {
+      const int i = i0 + u * kBuildThreads + tid;
+      if (v[u] != 0) {
+        const int cc = i / width;
+        const int g = i - cc * width;
+        atomicAdd(&total[g], v[u]);
+        if (cc < c) atomicAdd(&cursor[g], v[u]);
+      }
+    }
+  }
+  lds_barrier();
+  int nbits = 0;
+  while ((1 << nbits) <= NA) ++nbits;
+  finish_chunk(a, total, cursor, wcnt, mine, c0, nbits);
 }
 
 // ---------------------------------------------------------------------------
@@ -363,9 +467,16 @@ int gs_split_adapter_indices(const uint8_t* kind_lut, int32_t lut_len, const voi
 
 const char* gs_last_error(void) { return g_err; }
 
+int64_t gs_build_segments_workspace_bytes(int64_t num_tokens, int32_t num_adapters) {
+  if (num_tokens <= 0 || num_tokens >= (int64_t(1) << 31) || num_adapters < 1 || num_adapters > GS_MAX_ADAPTERS) return 0;
+  const int64_t chunks = (num_tokens + kBuildThreads - 1) / kBuildThreads;
+  return chunks >= kBuildSplitChunks ? build_hist_bytes(chunks, num_adapters) : 0;
+}
+
 int gs_build_segments(const int64_t* req_ids, const int64_t* positions, const int32_t* cu_seqlens,
                       const int64_t* act_offsets, int64_t num_tokens, int32_t num_seqs, int32_t num_adapters,
-                      int32_t* eff_ids, int32_t* seg_offsets, int32_t* perm, void* stream) {
+                      int32_t* eff_ids, int32_t* seg_offsets, int32_t* perm, void* workspace, int64_t workspace_bytes,
+                      void* stream) {
   GS_CHECK_ARG(num_adapters >= 1 && num_adapters <= GS_MAX_ADAPTERS, "gs_build_segments: num_adapters=%d not in [1,%d]",
                num_adapters, GS_MAX_ADAPTERS);
   GS_CHECK_ARG(num_tokens >= 0 && num_tokens < (int64_t(1) << 31), "gs_build_segments: num_tokens=%lld out of range",
@@ -374,10 +485,29 @@ int gs_build_segments(const int64_t* req_ids, const int64_t* positions, const in
   GS_CHECK_ARG(num_tokens == 0 || (req_ids && eff_ids && perm), "gs_build_segments: NULL token array");
   GS_CHECK_ARG(act_offsets == nullptr || cu_seqlens == nullptr || num_seqs >= 1,
                "gs_build_segments: num_seqs=%d with cu_seqlens", num_seqs);
+  GS_CHECK_ARG(workspace == nullptr || (reinterpret_cast<uintptr_t>(workspace) & 3) == 0,
+               "gs_build_segments: workspace must be 4-byte aligned");
   BuildArgs a{req_ids, positions, cu_seqlens, act_offsets, static_cast<int>(num_tokens), cu_seqlens ? num_seqs : 1,
               num_adapters, eff_ids, seg_offsets, perm};
-  const unsigned chunks = num_tokens > 0 ? static_cast<unsigned>((num_tokens + kBuildThreads - 1) / kBuildThreads) : 1u;
-  hipLaunchKernelGGL(build_segments_kernel, dim3(chunks), dim3(kBuildThreads), 0, static_cast<hipStream_t>(stream), a);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t chunks = num_tokens > 0 ? (num_tokens + kBuildThreads - 1) / kBuildThreads : 1;
+  if (workspace != nullptr && num_tokens > 0) {
+    const int64_t need = build_hist_bytes(chunks, num_adapters);
+    if (workspace_bytes < need) {
+      set_error("gs_build_segments: workspace of %lld bytes, the two-launch form needs %lld "
+                "(see gs_build_segments_workspace_bytes; NULL selects the one-launch form)",
+                (long long)workspace_bytes, (long long)need);
+      return GS_ERR_WORKSPACE;
+    }
+    int32_t* hist = static_cast<int32_t*>(workspace);
+    hipLaunchKernelGGL(build_count_kernel, dim3(static_cast<unsigned>(chunks)), dim3(kBuildThreads), 0, st, a, hist);
+    GS_CHECK_LAUNCH("gs_build_segments (count)");
+    hipLaunchKernelGGL(build_scatter_kernel, dim3(static_cast<unsigned>(chunks)), dim3(kBuildThreads), 0, st, a,
+                       static_cast<const int32_t*>(hist), static_cast<int>(chunks));
+    GS_CHECK_LAUNCH("gs_build_segments (scatter)");
+    return GS_OK;
+  }
+  hipLaunchKernelGGL(build_segments_kernel, dim3(static_cast<unsigned>(chunks)), dim3(kBuildThreads), 0, st, a);
   GS_CHECK_LAUNCH("gs_build_segments");
   return GS_OK;
 }

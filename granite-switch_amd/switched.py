@@ -54,6 +54,8 @@ class Segments:
     eff_ids     [T] int32  effective per-token global id (0 = base)
     seg_offsets [NA+1] int32: adapter g owns perm[seg_offsets[g-1]:seg_offsets[g]]
     perm        [T] int32  token indices grouped by adapter, ascending within
+    work        int32 per-chunk histograms of the builder's two-launch form
+                (None: the one-launch form, which needs no workspace)
     """
 
     eff_ids: torch.Tensor
@@ -61,6 +63,7 @@ class Segments:
     perm: torch.Tensor
     num_tokens: int
     num_adapters: int
+    work: torch.Tensor | None = None
 
 
 def _as_i64(t, device):
@@ -110,16 +113,19 @@ def build_segments(adapter_ids: torch.Tensor, num_adapters: int, positions=None,
     elif off is not None and off.numel() != 1:
         raise ValueError("act_offsets without cu_seqlens describes one sequence")
     if out is None:
+        ws = int(_lib.load().gs_build_segments_workspace_bytes(T, num_adapters))
         out = Segments(
             eff_ids=torch.empty(T, dtype=torch.int32, device=dev),
             seg_offsets=torch.empty(num_adapters + 1, dtype=torch.int32, device=dev),
             perm=torch.empty(max(T, 1), dtype=torch.int32, device=dev),
             num_tokens=T,
             num_adapters=num_adapters,
+            work=torch.empty((ws + 3) // 4, dtype=torch.int32, device=dev) if ws > 0 else None,
         )
+    work = out.work
     _lib.call("gs_build_segments", ids.data_ptr(), _lib.ptr(pos), _lib.ptr(cu), _lib.ptr(off), T, num_seqs,
               num_adapters, out.eff_ids.data_ptr(), out.seg_offsets.data_ptr(), out.perm.data_ptr(),
-              _lib.stream_ptr(dev))
+              _lib.ptr(work), 0 if work is None else work.numel() * 4, _lib.stream_ptr(dev))
     return out
 
 

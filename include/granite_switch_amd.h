@@ -91,10 +91,21 @@ const char* gs_last_error(void);
  * int32 or NULL (one sequence); act_offsets [num_seqs] int64 or NULL.
  * Outputs: eff_ids [T] int32, seg_offsets [num_adapters+1] int32, perm [T] int32.
  * Limits: 1 <= num_adapters <= GS_MAX_ADAPTERS; 0 <= T < 2^31.
+ *
+ * workspace NULL: one launch, in which every 1024-token chunk's workgroup
+ * counts the whole batch (its cost grows with T per workgroup).  Non-NULL
+ * (4-byte aligned, at least ceil(T/1024) * (num_adapters+1) * 4 bytes, else
+ * GS_ERR_WORKSPACE): two launches, each workgroup counting only its chunk,
+ * through per-chunk histograms in the workspace.  Both give identical
+ * outputs.  gs_build_segments_workspace_bytes returns the size to pass for
+ * batches where the two-launch form is the faster one, and 0 where the
+ * one-launch form is (pass NULL then).
  * ---------------------------------------------------------------------- */
+int64_t gs_build_segments_workspace_bytes(int64_t num_tokens, int32_t num_adapters);
 int gs_build_segments(const int64_t* req_ids, const int64_t* positions, const int32_t* cu_seqlens,
                       const int64_t* act_offsets, int64_t num_tokens, int32_t num_seqs, int32_t num_adapters,
-                      int32_t* eff_ids, int32_t* seg_offsets, int32_t* perm, void* stream);
+                      int32_t* eff_ids, int32_t* seg_offsets, int32_t* perm, void* workspace, int64_t workspace_bytes,
+                      void* stream);
 
 /* ------------------------------------------------------------------------
  * Probe-slot split of the per-token index stream (reference ids, 0 = base).

@@ -63,6 +63,45 @@ def test_build_segments_random(dev, T, NA, seed):
     _check_segments(segs, eff, NA)
 
 
+def _segments_buffers(T, NA, dev, two_launch):
+    chunks = max(1, -(-T // 1024))
+    return switched.Segments(
+        eff_ids=torch.full((T,), -7, dtype=torch.int32, device=dev),
+        seg_offsets=torch.full((NA + 1,), -7, dtype=torch.int32, device=dev),
+        perm=torch.full((max(T, 1),), -7, dtype=torch.int32, device=dev),
+        num_tokens=T, num_adapters=NA,
+        # garbage in the histogram workspace: the count launch writes all of it
+        work=torch.full((chunks * (NA + 1),), 12345, dtype=torch.int32, device=dev) if two_launch else None)
+
+
+@pytest.mark.parametrize("T,NA,seed,gating", [(1, 1, 11, True), (1023, 7, 12, True), (1025, 255, 13, True),
+                                              (4144, 24, 14, True), (9000, 256, 15, True), (20000, 24, 16, False),
+                                              (65536, 24, 17, True), (131072, 3, 18, False)])
+def test_build_segments_one_and_two_launch_forms(dev, T, NA, seed, gating):
+    """The two-launch form (per-chunk histograms in a workspace) against the
+    oracle and against the one-launch form, at batch sizes on both sides of
+    the size from which the library recommends it."""
+    rng = np.random.default_rng(seed)
+    req = rng.integers(-2, NA + 3, size=T)
+    cu = np.concatenate([[0], np.sort(rng.choice(np.arange(1, T), size=min(T - 1, max(1, T // 300)), replace=False))
+                         if T > 1 else np.zeros(0, np.int64), [T]]).astype(np.int32)
+    lens = np.diff(cu)
+    pos = np.concatenate([c + np.arange(l) for c, l in zip(rng.integers(0, 64, size=lens.size), lens)])
+    offs = rng.integers(0, 200, size=lens.size) if gating else None
+    args = (torch.tensor(req, device=dev), NA, torch.tensor(pos, device=dev), torch.tensor(cu, device=dev),
+            None if offs is None else torch.tensor(offs, device=dev))
+    eff = omap.alora_effective_ids(req, pos, cu, offs) if gating else req
+    eff = np.where((eff < 0) | (eff > NA), 0, eff)
+    outs = []
+    for two in (False, True):
+        _say(f"build_segments {'two' if two else 'one'}-launch T={T} NA={NA} seqs={lens.size} gating={gating}")
+        segs = switched.build_segments(*args, out=_segments_buffers(T, NA, dev, two))
+        torch.cuda.synchronize()
+        _check_segments(segs, eff, NA)
+        outs.append(segs)
+    assert torch.equal(outs[0].perm, outs[1].perm) and torch.equal(outs[0].seg_offsets, outs[1].seg_offsets)
+
+
 def test_build_segments_no_gating_all_base_and_all_one(dev):
     for ids, NA in ((np.zeros(300, np.int64), 5), (np.ones(3000, np.int64), 5), (np.arange(2048) % 9, 8)):
         _say(f"build_segments plain T={ids.size}")

@@ -50,8 +50,22 @@ def test_library_shares_torchs_hip_runtime():
 
 def test_validation_errors_without_launch():
     with pytest.raises(_lib.GraniteSwitchError) as e:
-        _lib.call("gs_build_segments", None, None, None, None, 4, 1, 0, None, None, None, None)
+        _lib.call("gs_build_segments", None, None, None, None, 4, 1, 0, None, None, None, None, 0, None)
     assert e.value.status == _lib.GS_ERR_INVALID and "num_adapters" in str(e.value)
+    # the two-launch builder's workspace: 0 below the batch size where it pays,
+    # ceil(T/1024) * (NA+1) int32 histograms from there
+    lib = _lib.load()
+    assert lib.gs_build_segments_workspace_bytes(0, 24) == 0
+    assert lib.gs_build_segments_workspace_bytes(1024, 24) == 0
+    assert lib.gs_build_segments_workspace_bytes(1025, 24) == 2 * 25 * 4
+    assert lib.gs_build_segments_workspace_bytes(1 << 16, 24) == 64 * 25 * 4
+    assert lib.gs_build_segments_workspace_bytes(1 << 16, 0) == 0
+    # a workspace smaller than the histograms is refused before any launch
+    fake = ctypes.c_void_p(256)
+    with pytest.raises(_lib.GraniteSwitchError) as e:
+        _lib.call("gs_build_segments", fake, None, None, None, 5000, 1, 24, fake, fake, fake, fake, 5 * 25 * 4 - 4,
+                  None)
+    assert e.value.status == _lib.GS_ERR_WORKSPACE and "workspace" in str(e.value)
     with pytest.raises(_lib.GraniteSwitchError) as e:
         _lib.call("gs_shrink", 0, None, 16, 4, 12, None, None, None, 1, 4, 16, None, None, None, 16, None, 0, None)
     assert "hidden" in str(e.value)
