@@ -112,6 +112,9 @@ constexpr int kXextSlots = GS_XEXT_SLOTS;
 #ifndef GS_XEXT_COLS
 #define GS_XEXT_COLS 1
 #endif
+#ifndef GS_XEXT_GATE_UP_ONE_TRIP
+#define GS_XEXT_GATE_UP_ONE_TRIP 1
+#endif
 
 template <int KK>
 __device__ __forceinline__ void xext_own_z(const XextArgs& a, const int* scr, int64_t m0, int s, int id, bool row_ok,
@@ -225,12 +228,70 @@ __device__ __forceinline__ f32x16 xext_delta(const XextArgs& a, const int* scr, 
 
 // Gate and up deltas of the SwiGLU form (columns h0 of slice 0 and H + h0 of
 // slice 1).
+// General path of the SwiGLU form: per followed adapter, the gate block's and
+// the up block's shrink values and lora_B for two k-steps are loaded in one
+// memory trip (eight 16-byte pieces per lane), then the four MFMAs run; a
+// rank of 32 costs one trip per adapter instead of one per k-step and slice.
+__device__ __forceinline__ void xext_gate_up_general(const XextArgs& a, const int* scr, int64_t m0, int h0, int H,
+                                                     int id, bool row_ok, uint64_t bm, f32x16& ag, f32x16& au) {
+  const int l = __lane_id();
+  const int i = l & 31;
+  const int h = l >> 5;
+  ag = f32x16{};
+  au = f32x16{};
+  uint64_t mine = (row_ok && id >= 1 && id <= 64) ? (1ull << (id - 1)) : 0ull;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) mine |= __shfl_xor(mine, d, 64);
+  uint64_t todo = mine & bm;
+  const uint16_t* xrow = static_cast<const uint16_t*>(a.x_ext) + (row_ok ? m0 + i : 0) * a.stride_m;
+  while (todo) {
+    const int kid = __builtin_amdgcn_readfirstlane(__ffsll(static_cast<long long>(todo)));   // uniform
+    todo &= todo - 1;
+    int t, first;
+    int64_t lb_off;
+    if (!xext_tier(a, kid, t, first, lb_off)) break;   // cannot happen: only valid bits are followed
+    const int r = 16 << t;
+    const int idx = kid - first;
+    const int64_t cg = static_cast<int64_t>(scr[t]) + static_cast<int64_t>(idx) * a.S * r;
+    const int64_t cu = static_cast<int64_t>(scr[6 + t]) + static_cast<int64_t>(idx) * a.S * r;
+    const uint16_t* bblk = a.lb + lb_off + static_cast<int64_t>(idx) * a.N * r;
+    const uint16_t* bg = bblk + static_cast<int64_t>(h0 + i) * r;
+    const uint16_t* bu = bblk + static_cast<int64_t>(H + h0 + i) * r;
+    const bool sel = row_ok && id == kid;
+    for (int kb = 0; kb < r; kb += 32) {
+      // all eight pieces load unconditionally (clamped addresses), so that
+      // none is deferred behind a branch; the second k-step exists unless
+      // the rank is 16, and a missing step feeds zeros
+      const bool two = kb + 16 < r;
+      const int k0 = kb + 8 * h;
+      const int k1 = two ? k0 + 16 : k0;
+      const int64_t og = sel ? cg : 0, ou = sel ? cu : 0;
+      const u32x4 zg0 = ld16(xrow + og + k0);
+      const u32x4 zu0 = ld16(xrow + ou + k0);
+      const u32x4 zg1 = ld16(xrow + og + k1);
+      const u32x4 zu1 = ld16(xrow + ou + k1);
+      const u32x4 bg0 = ld16(bg + k0);
+      const u32x4 bu0 = ld16(bu + k0);
+      const u32x4 bg1 = ld16(bg + k1);
+      const u32x4 bu1 = ld16(bu + k1);
+      ag = mfma32_bf16(sel16(sel, zg0), bg0, ag);
+      au = mfma32_bf16(sel16(sel, zu0), bu0, au);
+      ag = mfma32_bf16(sel16(sel && two, zg1), bg1, ag);
+      au = mfma32_bf16(sel16(sel && two, zu1), bu1, au);
+    }
+  }
+}
+
 template <int KK>
 __device__ __forceinline__ void xext_delta_gate_up(const XextArgs& a, const int* scr, int64_t m0, int h0, int H, int id,
                                                    bool row_ok, uint64_t bm, f32x16& ag, f32x16& au) {
   if constexpr (KK == 0) {
+#if GS_XEXT_GATE_UP_ONE_TRIP
+    xext_gate_up_general(a, scr, m0, h0, H, id, row_ok, bm, ag, au);
+#else
     ag = xext_block_delta(a, scr, m0, h0, 0, id, row_ok, bm);
     au = xext_block_delta(a, scr, m0, H + h0, 1, id, row_ok, bm);
+#endif
   } else {
     constexpr int BA = kXextSlots / 2 / KK;
     uint64_t mine = (row_ok && id >= 1 && id <= 64) ? (1ull << (id - 1)) : 0ull;
@@ -592,8 +653,6 @@ __global__ __launch_bounds__(256) void xext_swiglu_kernel(XextArgs a, uint16_t* 
   __shared__ float du[32][128 + 4];
   __shared__ int scr[GS_MAX_SLICES * 6];
   const int64_t pm = blockIdx.y;
-  const int64_t bm_raw = a.bitmask[pm * a.stride_bm];
-  const uint64_t bm = static_cast<uint64_t>(bm_raw) & valid_bits(a.na);
   const int h_tile0 = blockIdx.x * 128;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -602,23 +661,32 @@ __global__ __launch_bounds__(256) void xext_swiglu_kernel(XextArgs a, uint16_t* 
   const int64_t m0 = pm * 32;
   const bool row_ok = (m0 + i) < a.M;
   // this thread's gate and up pieces (row tid / 8, 16 columns) do not depend
-  // on the delta: they go out first, from a clamped in-bounds address
+  // on the delta: they go out early, from a clamped in-bounds address
   const int row = tid >> 3;
   const int cx = (tid & 7) * 16;
   const int64_t m = m0 + row;
   const bool out_ok = m < a.M && h_tile0 + cx < H;
   const uint16_t* xr = static_cast<const uint16_t*>(a.x_ext) + (out_ok ? m : m0) * a.stride_m +
                        (out_ok ? h_tile0 + cx : h_tile0);
+  // the ids and the slice table go out first, then the gate and up pieces,
+  // then the tile mask (a scalar load: the wait for the kernel arguments
+  // before the first vector loads must not include it), so the delta's
+  // inputs are one trip away
+  const int id = load_id(a.ids, a.idx_bytes, row_ok ? m0 + i : 0);
+  const int scr_v = a.slice_col_r[tid < a.S * 6 ? tid : 0];
+  __builtin_amdgcn_sched_barrier(0);
   u32x4 gi[2], ui[2];
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
     gi[half] = *reinterpret_cast<const u32x4*>(xr + half * 8);
     ui[half] = *reinterpret_cast<const u32x4*>(xr + H + half * 8);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  const int64_t bm_raw = a.bitmask[pm * a.stride_bm];
+  const uint64_t bm = static_cast<uint64_t>(bm_raw) & valid_bits(a.na);
 
   if (bm_raw != 0) {
-    if (tid < a.S * 6) scr[tid] = a.slice_col_r[tid];
-    const int id = row_ok ? load_id(a.ids, a.idx_bytes, m0 + i) : 0;
+    if (tid < a.S * 6) scr[tid] = scr_v;
     lds_barrier();
     const int h0 = h_tile0 + 32 * wave;
     f32x16 ag = f32x16{}, au = f32x16{};

@@ -218,6 +218,49 @@ def test_swiglu_op_matches_oracle(dev):
     _close(_np(out), ref, 2e-2, "swiglu op")
 
 
+def _runs_of_ids(T, NA, seed, max_run=300):
+    """Per-token ids as runs (prefill sequences of one request each), with
+    single tokens of random requests in between (decode rows): tiles holding
+    one adapter, several, or only base rows."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < T:
+        if rng.random() < 0.3:
+            out.extend(rng.integers(0, NA + 1, size=int(rng.integers(1, 40))).tolist())
+        else:
+            out.extend([int(rng.integers(0, NA + 1))] * int(rng.integers(1, max_run)))
+    return np.asarray(out[:T], np.int64)
+
+
+@pytest.mark.parametrize("M,H,ranks,idx32", [(2000, 1376, [16, 32, 32, 16], False), (1500, 256, [64, 16, 8], True),
+                                             (1100, 512, [128, 32], False), (1056, 640, [16] * 5, True),
+                                             (1200, 384, [256, 16], False)])
+def test_swiglu_op_large_batch_forms(dev, M, H, ranks, idx32):
+    """The row-strip SwiGLU kernel (above 1024 rows, tiers up to rank 128:
+    LDS shrink widths 32, 64 and 128, h not a multiple of 128, a partial last
+    row tile, tiles of one, several or no adapters, int32 and int64 ids) and
+    the per-tile kernel it leaves rank 256 to, against the oracle."""
+    K = 256
+    _say(f"swiglu op M={M} H={H} ranks={ranks} idx32={idx32}")
+    layer, W, A, B = _make_vllm_layer(dev, K, (H, H), ranks, seed=17 + M, fuse_swiglu=True)
+    g = torch.Generator(device=dev).manual_seed(M)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    ids = torch.tensor(_runs_of_ids(M, len(ranks), M), device=dev)
+    ctx = _ctx_for(dev, layer, ids)
+    x_ext = torch.mm(x, layer.w_ext.T)
+    loc = ctx.remapped_indices[0]
+    if idx32:
+        loc = loc.to(torch.int32)
+    out = torch.full((M, H), 7.0, dtype=torch.bfloat16, device=dev)
+    ops.op("switch_lora_expand_swiglu")(out, x_ext, loc, ctx.per_module_bitmasks[0], layer._lb_packed,
+                                         layer.slice_col_r, *layer._na, 2, 32, H, 2 * H)
+    torch.cuda.synchronize()
+    ref = olora.expand_swiglu_xext(_np(x_ext), ctx.remapped_indices[0].cpu().numpy(),
+                                   ctx.per_module_bitmasks[0].cpu().numpy(), _np(layer._lb_packed),
+                                   layer.slice_col_r.cpu().numpy(), layer._na, 2, H, 2 * H)
+    _close(_np(out), ref, 2e-2, "swiglu op")
+
+
 @pytest.mark.parametrize("merged", [False, True])
 def test_hf_layers_match_hf_loop(dev, merged):
     K, NA, R = 384, 5, 16
