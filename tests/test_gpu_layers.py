@@ -261,6 +261,42 @@ def test_swiglu_op_large_batch_forms(dev, M, H, ranks, idx32):
     _close(_np(out), ref, 2e-2, "swiglu op")
 
 
+@pytest.mark.parametrize("M", [96, 1500])
+def test_swiglu_op_extreme_gates(dev, M):
+    """silu(g) * u for gates from -300 to 300 (e^-g overflowing and
+    underflowing fp32), tiny gates and zero, on base rows (no delta), both
+    kernel forms: every output within one bf16 ulp of the exact value, and
+    the exact value's sign where it is zero."""
+    H, K = 256, 128
+    layer, W, A, B = _make_vllm_layer(dev, K, (H, H), [16], seed=31, fuse_swiglu=True)
+    ids = torch.zeros(M, dtype=torch.int64, device=dev)
+    ctx = _ctx_for(dev, layer, ids)
+    x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+    x_ext = torch.mm(x, layer.w_ext.T)
+    rng = np.random.default_rng(5)
+    special = np.array([-300, -120, -89, -87, -20, -1, -1e-3, -1e-30, 0, 1e-30, 1e-3, 1, 20, 87, 89, 120, 300],
+                       np.float64)
+    g = np.concatenate([special, rng.uniform(-12, 12, size=M * H - special.size)]).reshape(M, H)
+    u = rng.uniform(-4, 4, size=(M, H))
+    x_ext[:, :H] = torch.tensor(g, dtype=torch.float32, device=dev).to(torch.bfloat16)
+    x_ext[:, H:2 * H] = torch.tensor(u, dtype=torch.float32, device=dev).to(torch.bfloat16)
+    out = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
+    ops.op("switch_lora_expand_swiglu")(out, x_ext, ctx.remapped_indices[0], ctx.per_module_bitmasks[0],
+                                         layer._lb_packed, layer.slice_col_r, *layer._na, 2, 32, H, 2 * H)
+    torch.cuda.synchronize()
+    gb = _np(x_ext[:, :H]).astype(np.float64)
+    ub = _np(x_ext[:, H:2 * H]).astype(np.float64)
+    with np.errstate(over="ignore"):
+        exact = gb / (1.0 + np.exp(-gb)) * ub
+    got = _np(out).astype(np.float64)
+    # one bf16 ulp (or less) of the exact value; below 1e-30 (gates under
+    # about -70, where fp32's e^-g overflows past -88.7 as in the reference's
+    # own fp32 evaluation) any result of that size or zero
+    ulp = np.maximum(np.abs(exact) * 2.0 ** -7, 1e-30)
+    assert np.all(np.abs(got - exact) <= ulp), float(np.max(np.abs(got - exact) / ulp))
+    assert np.array_equal(np.signbit(got[exact == 0]), np.signbit(exact[exact == 0]))
+
+
 @pytest.mark.parametrize("merged", [False, True])
 def test_hf_layers_match_hf_loop(dev, merged):
     K, NA, R = 384, 5, 16
