@@ -127,6 +127,7 @@ constexpr int kXextSlots = GS_XEXT_SLOTS;
 #define GS_XEXT_GATE_UP_ONE_TRIP 1
 #endif
 
+
 template <int KK>
 __device__ __forceinline__ void xext_own_z(const XextArgs& a, const int* scr, int64_t m0, int s, int id, bool row_ok,
                                            uint64_t todo, u32x4 (&z)[KK]) {
@@ -341,15 +342,22 @@ __global__ __launch_bounds__(256) void xext_expand_kernel(XextArgs a, uint16_t* 
   if (tid < a.S * 6) scr[tid] = a.slice_col_r[tid];
   const int n0 = n_tile0 + 32 * wave;
   const int s = tile_slice[(n0 < a.N ? n0 : n_tile0) / block_n];
-  const int row = tid >> 3;
-  const int cx = (tid & 7) * 16;
-  const int64_t m = m0 + row;
-  const bool out_ok = m < a.M && n_tile0 + cx < a.N;
-  uint16_t* p = x_out + (out_ok ? m : m0) * a.stride_m + (out_ok ? n_tile0 + cx : n_tile0);
-  const int out_id = out_ok ? load_id(a.ids, a.idx_bytes, m) : 0;
+  // piece q of this thread: row (tid + 256 q) / 16, columns 8 ((tid + 256 q)
+  // % 16) on, so every wave access covers whole 256-byte row segments
+  int prow[2], pc[2], out_id[2];
+  bool out_ok[2];
+  uint16_t* p[2];
   u32x4 in[2];
 #pragma unroll
-  for (int half = 0; half < 2; ++half) in[half] = *reinterpret_cast<const u32x4*>(p + half * 8);
+  for (int q = 0; q < 2; ++q) {
+    prow[q] = (tid + 256 * q) >> 4;
+    pc[q] = ((tid + 256 * q) & 15) * 8;
+    const int64_t m = m0 + prow[q];
+    out_ok[q] = m < a.M && n_tile0 + pc[q] < a.N;
+    p[q] = x_out + (out_ok[q] ? m : m0) * a.stride_m + (out_ok[q] ? n_tile0 + pc[q] : n_tile0);
+    out_id[q] = out_ok[q] ? load_id(a.ids, a.idx_bytes, m) : 0;
+    in[q] = *reinterpret_cast<const u32x4*>(p[q]);
+  }
   if (bm_raw == 0) return;
   const uint64_t bm = static_cast<uint64_t>(bm_raw) & valid_bits(a.na);
   lds_barrier();
@@ -359,17 +367,17 @@ __global__ __launch_bounds__(256) void xext_expand_kernel(XextArgs a, uint16_t* 
   for (int v = 0; v < 16; ++v) dtile[mfma32_row(v, l)][32 * wave + i] = acc[v];
   lds_barrier();
 
-  if (!out_ok || out_id == 0) return;   // base rows are never written
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
+  for (int q = 0; q < 2; ++q) {
+    if (!out_ok[q] || out_id[q] == 0) continue;   // base rows are never written
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float lo = bf16_bits_to_f32(static_cast<uint16_t>(in[half][e] & 0xffffu)) + dtile[row][cx + half * 8 + 2 * e];
-      const float hi = bf16_bits_to_f32(static_cast<uint16_t>(in[half][e] >> 16)) + dtile[row][cx + half * 8 + 2 * e + 1];
+      const float lo = bf16_bits_to_f32(static_cast<uint16_t>(in[q][e] & 0xffffu)) + dtile[prow[q]][pc[q] + 2 * e];
+      const float hi = bf16_bits_to_f32(static_cast<uint16_t>(in[q][e] >> 16)) + dtile[prow[q]][pc[q] + 2 * e + 1];
       o[e] = static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
     }
-    *reinterpret_cast<u32x4*>(p + half * 8) = u32x4{o[0], o[1], o[2], o[3]};
+    *reinterpret_cast<u32x4*>(p[q]) = u32x4{o[0], o[1], o[2], o[3]};
   }
 }
 
@@ -671,14 +679,16 @@ __global__ __launch_bounds__(256) void xext_swiglu_kernel(XextArgs a, uint16_t* 
   const int i = l & 31;
   const int64_t m0 = pm * 32;
   const bool row_ok = (m0 + i) < a.M;
-  // this thread's gate and up pieces (row tid / 8, 16 columns) do not depend
-  // on the delta: they go out early, from a clamped in-bounds address
-  const int row = tid >> 3;
-  const int cx = (tid & 7) * 16;
-  const int64_t m = m0 + row;
-  const bool out_ok = m < a.M && h_tile0 + cx < H;
-  const uint16_t* xr = static_cast<const uint16_t*>(a.x_ext) + (out_ok ? m : m0) * a.stride_m +
-                       (out_ok ? h_tile0 + cx : h_tile0);
+  // this thread's two 8-column pieces of gate and up do not depend on the
+  // delta: they go out early, from clamped in-bounds addresses.  Piece q is
+  // row (tid + 256 q) / 16, columns 8 ((tid + 256 q) % 16) on, so that every
+  // wave access covers whole 256-byte row segments.
+  int prow[2], pc[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    prow[q] = (tid + 256 * q) >> 4;
+    pc[q] = ((tid + 256 * q) & 15) * 8;
+  }
   // the ids and the slice table go out first, then the gate and up pieces,
   // then the tile mask (a scalar load: the wait for the kernel arguments
   // before the first vector loads must not include it), so the delta's
@@ -687,15 +697,26 @@ __global__ __launch_bounds__(256) void xext_swiglu_kernel(XextArgs a, uint16_t* 
   const int scr_v = a.slice_col_r[tid < a.S * 6 ? tid : 0];
   __builtin_amdgcn_sched_barrier(0);
   u32x4 gi[2], ui[2];
+  bool pok[2];
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    gi[half] = *reinterpret_cast<const u32x4*>(xr + half * 8);
-    ui[half] = *reinterpret_cast<const u32x4*>(xr + H + half * 8);
+  for (int q = 0; q < 2; ++q) {
+    const int64_t m = m0 + prow[q];
+    pok[q] = m < a.M && h_tile0 + pc[q] < H;
+    const uint16_t* src = static_cast<const uint16_t*>(a.x_ext) + (pok[q] ? m : m0) * a.stride_m +
+                          (pok[q] ? h_tile0 + pc[q] : h_tile0);
+    gi[q] = *reinterpret_cast<const u32x4*>(src);
+    ui[q] = *reinterpret_cast<const u32x4*>(src + H);
   }
   __builtin_amdgcn_sched_barrier(0);
   const int64_t bm_raw = a.bitmask[pm * a.stride_bm];
   const uint64_t bm = static_cast<uint64_t>(bm_raw) & valid_bits(a.na);
 
+  // the deltas through LDS to this thread's pieces (held as fp32)
+  float gadd[2][8], uadd[2][8];
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) gadd[q][c] = uadd[q][c] = 0.f;
   if (bm_raw != 0) {
     if (tid < a.S * 6) scr[tid] = scr_v;
     lds_barrier();
@@ -707,31 +728,33 @@ __global__ __launch_bounds__(256) void xext_swiglu_kernel(XextArgs a, uint16_t* 
       dg[mfma32_row(v, l)][32 * wave + i] = ag[v];
       du[mfma32_row(v, l)][32 * wave + i] = au[v];
     }
-  }
-  lds_barrier();
-
-  if (!out_ok) return;
-  uint16_t* orow = out + m * stride_om + h_tile0 + cx;
+    lds_barrier();
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        gadd[q][c] = dg[prow[q]][pc[q] + c];
+        uadd[q][c] = du[prow[q]][pc[q] + c];
+      }
+  }
+
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    if (!pok[q]) continue;
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float r2[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const int c = half * 8 + 2 * e + j;
-        float g = bf16_bits_to_f32(static_cast<uint16_t>((gi[half][e] >> (16 * j)) & 0xffffu));
-        float u = bf16_bits_to_f32(static_cast<uint16_t>((ui[half][e] >> (16 * j)) & 0xffffu));
-        if (bm_raw != 0) {
-          g += dg[row][cx + c];
-          u += du[row][cx + c];
-        }
+        const int c = 2 * e + j;
+        const float g = bf16_bits_to_f32(static_cast<uint16_t>((gi[q][e] >> (16 * j)) & 0xffffu)) + gadd[q][c];
+        const float u = bf16_bits_to_f32(static_cast<uint16_t>((ui[q][e] >> (16 * j)) & 0xffffu)) + uadd[q][c];
         r2[j] = silu_mul(g, u);
       }
       o[e] = static_cast<uint32_t>(f32_to_bf16_bits(r2[0])) | (static_cast<uint32_t>(f32_to_bf16_bits(r2[1])) << 16);
     }
-    *reinterpret_cast<u32x4*>(orow + half * 8) = u32x4{o[0], o[1], o[2], o[3]};
+    *reinterpret_cast<u32x4*>(out + (m0 + prow[q]) * stride_om + h_tile0 + pc[q]) = u32x4{o[0], o[1], o[2], o[3]};
   }
 }
 
