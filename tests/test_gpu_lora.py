@@ -268,6 +268,43 @@ def test_graph_capture_replays(dev):
 
 
 @pytest.mark.parametrize("path", ["small", "segments"])
+def test_graph_replay_after_workspace_growth(dev, path):
+    """A graph captured at a small batch, then an eager call at a much larger
+    batch that outgrows the per-device workspace, then replays: the replays
+    still write into the captured (retired, kept alive) buffer and equal the
+    eager result of the small batch."""
+    NA = 6
+    spec = workloads.ModuleSpec("t", 1024, (512, 256), [16, 32, 8, 32, 16, 32], 32)
+    small = workloads.make_module(spec, 200, NA, torch.bfloat16, dev, seed=91)
+    big = workloads.make_module(spec, 3000 if path == "segments" else 1000, NA, torch.bfloat16, dev, seed=92)
+    pk_s = switched.PackedAdapters.from_slices(small.lora_A_slices, small.lora_B_slices, spec.ranks)
+    pk_b = switched.PackedAdapters.from_slices(big.lora_A_slices, big.lora_B_slices, spec.ranks)
+    g_ids = torch.Generator(device=dev).manual_seed(93)
+    ids_s = torch.randint(0, NA + 1, (200,), generator=g_ids, device=dev)
+    ids_b = torch.randint(0, NA + 1, (big.x.shape[0],), generator=g_ids, device=dev)
+    y_eager = small.y.clone()
+    switched.switched_lora_routed_(y_eager, small.x, ids_s, pk_s, path=path)
+    torch.cuda.synchronize()
+    y = small.y.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        switched.switched_lora_routed_(y, small.x, ids_s, pk_s, path=path)
+    # an eager call whose workspace need exceeds the captured one
+    _say(f"{path}: eager call at T={big.x.shape[0]} after capture")
+    y_big = big.y.clone()
+    switched.switched_lora_routed_(y_big, big.x, ids_b, pk_b, path=path)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        y.copy_(small.y)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        _say(f"{path}: replay {rep} after the workspace grew")
+        assert torch.equal(y, y_eager), f"replay {rep} differs from eager"
+    switched.check(dev)
+
+
+@pytest.mark.parametrize("path", ["small", "segments"])
 def test_slice_independence(dev, path):
     """LoRA weights on slice 0 only (reference tests/hf/test_lora.py:133-168):
     slice 0 changes, slices 1+ come back bit-identical, on both kernel paths."""
