@@ -919,8 +919,13 @@ void launch_expand_pre(int max_tiles, size_t lds, const ExpandParams& p, hipStre
 
 void launch_expand(bool bf16, int64_t T, ExpandParams p, hipStream_t st) {
   const int max_tiles = max_tiles_for(T, p.NA);
-  // wider column tiles halve the z / partial reads per output byte
-  const bool wide = T >= 2048 || p.nparts > 1;
+  // wider column tiles halve the z / partial reads per output byte, but
+  // their lora_B registers grow with the rank: above rank 32 (bf16; 16 fp32
+  // k per group) the wide kernel drops to 2 or 1 resident waves per SIMD and
+  // the narrow one streams faster (multiswitch down, ranks to 64: expand
+  // 21.5 -> 16.7 us)
+  const int kstep = bf16 ? 16 : 8;
+  const bool wide = (T >= 2048 || p.nparts > 1) && (p.max_rank + kstep - 1) / kstep <= 2;
   const size_t lds = expand_lds_bytes(bf16, p.si.S, p.max_rank);
   if (bf16) {
     if (wide) launch_expand_pre<true, 2>(max_tiles, lds, p, st);
