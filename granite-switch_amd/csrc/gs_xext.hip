@@ -120,6 +120,9 @@ __device__ __forceinline__ bool xext_tier(const XextArgs& a, int kid, int& t, in
 #define GS_XEXT_SLOTS 16
 #endif
 constexpr int kXextSlots = GS_XEXT_SLOTS;
+#ifndef GS_XEXT_RT8
+#define GS_XEXT_RT8 1
+#endif
 #ifndef GS_XEXT_COLS
 #define GS_XEXT_COLS 1
 #endif
@@ -383,11 +386,11 @@ __global__ __launch_bounds__(256) void xext_expand_kernel(XextArgs a, uint16_t* 
 
 // ----------------------------------------------------------------------------
 // Column-block form of the in-place expand, for modules whose tiers all have
-// rank <= 16 KK.  A workgroup owns 32 CB columns over kColsRT = 4
+// rank <= 16 KK.  A workgroup owns 32 CB columns over RT = 4 or 8
 // consecutive 32-row tiles, one wave per row tile.  The lora_B blocks of the
 // adapters followed in any of its tiles are staged in LDS once per workgroup
 // (an adapter's block for 32 CB consecutive columns is one contiguous run of
-// the packed array), so a column's lora_B is read once per four row tiles
+// the packed array), so a column's lora_B is read once per RT row tiles
 // instead of once per tile -- in a decode batch every tile holds most
 // adapters, and the per-tile form moved ~7x the unique lora_B bytes.  Each
 // lane loads its own row's shrink values once (a row only receives its own
@@ -396,7 +399,6 @@ __global__ __launch_bounds__(256) void xext_expand_kernel(XextArgs a, uint16_t* 
 // at a time.  Results go through LDS to row-major pieces for the
 // read-modify-write, whose loads are issued first.
 // ----------------------------------------------------------------------------
-constexpr int kColsRT = 4;
 
 // The id of row i: int64 ids are read as their low 32-bit word (little
 // endian), which is exactly static_cast<int> of the value, so no load leaves
@@ -406,20 +408,20 @@ __device__ __forceinline__ int load_id_t(const void* p, int64_t i) {
   return static_cast<const int32_t*>(p)[I64 ? 2 * i : i];
 }
 
-template <int KK, int CB, bool I64>
-__global__ __launch_bounds__(256) void xext_cols_kernel(XextArgs a, uint16_t* x_out,
-                                                        const int32_t* __restrict__ tile_slice, int block_n) {
+template <int KK, int CB, int RT, bool I64>
+__global__ __launch_bounds__(64 * RT) void xext_cols_kernel(XextArgs a, uint16_t* x_out,
+                                                            const int32_t* __restrict__ tile_slice, int block_n) {
   constexpr int NC = 32 * CB;                  // columns of the workgroup
   constexpr int RMAX = 16 * KK;                // largest rank of the module
   constexpr int CST = RMAX * 2 + 16;           // LDS bytes per column of a staged block (padded)
   constexpr int ABLK = NC * CST;               // LDS bytes per staged adapter
   constexpr int CA = CB == 1 ? 16 : 8;         // adapters staged at a time
-  constexpr int CAW = CA / kColsRT;            // adapters each wave stages
+  constexpr int CAW = CA / RT;                 // adapters each wave stages
   constexpr int QP = NC * RMAX / 8 / 64;       // 16-byte pieces per lane of one block at rank RMAX
   constexpr int DLD = NC + 4;                  // fp32 row stride of the transposed delta
   constexpr int LPR = NC / 16;                 // lanes per row in the read-modify-write
   constexpr int PASSES = 32 * LPR / 64;        // rows per lane
-  static_assert(kColsRT * 32 * DLD * 4 <= CA * ABLK, "the delta tile must fit the staging buffer");
+  static_assert(RT * 32 * DLD * 4 <= CA * ABLK, "the delta tile must fit the staging buffer");
   __shared__ __align__(16) char bs[CA * ABLK + 64 * 16];   // + a sink for masked-off pieces
   __shared__ int scr[GS_MAX_SLICES * 6];
 
@@ -429,7 +431,7 @@ __global__ __launch_bounds__(256) void xext_cols_kernel(XextArgs a, uint16_t* x_
   const int i = l & 31;
   const int h = l >> 5;
   const int n_blk0 = blockIdx.x * NC;
-  const int64_t pm0 = static_cast<int64_t>(blockIdx.y) * kColsRT;
+  const int64_t pm0 = static_cast<int64_t>(blockIdx.y) * RT;
   const int64_t pm = pm0 + wave;               // this wave's row tile
   const int64_t m0 = pm * 32;
   const int64_t n_tiles = (a.M + 31) / 32;
@@ -437,9 +439,9 @@ __global__ __launch_bounds__(256) void xext_cols_kernel(XextArgs a, uint16_t* x_
 
   // The tile masks (uniform) name the adapters the reference's loop follows
   // in each tile; their union over the workgroup's tiles is staged.
-  int64_t bmt[kColsRT];
+  int64_t bmt[RT];
 #pragma unroll
-  for (int w = 0; w < kColsRT; ++w) bmt[w] = pm0 + w < n_tiles ? a.bitmask[(pm0 + w) * a.stride_bm] : 0;
+  for (int w = 0; w < RT; ++w) bmt[w] = pm0 + w < n_tiles ? a.bitmask[(pm0 + w) * a.stride_bm] : 0;
   // loads that depend on nothing: ids, slice tables, this lane's
   // read-modify-write pieces (clamped in-bounds addresses, masked afterwards)
   const bool row_ok = (m0 + i) < a.M;
@@ -469,10 +471,15 @@ __global__ __launch_bounds__(256) void xext_cols_kernel(XextArgs a, uint16_t* x_
   __builtin_amdgcn_sched_barrier(0);   // all of the above in flight before any of it is used
 
   const uint64_t valid = valid_bits(a.na);
-  const int64_t bm_tile = bmt[0] * (wave == 0) + bmt[1] * (wave == 1) + bmt[2] * (wave == 2) + bmt[3] * (wave == 3);
+  int64_t bm_tile = 0;
+  uint64_t all = 0;
+#pragma unroll
+  for (int w = 0; w < RT; ++w) {
+    bm_tile = wave == w ? bmt[w] : bm_tile;   // uniform
+    all |= static_cast<uint64_t>(bmt[w]);
+  }
   const uint64_t todo = static_cast<uint64_t>(bm_tile) & valid;
-  uint64_t all = (static_cast<uint64_t>(bmt[0]) | static_cast<uint64_t>(bmt[1]) | static_cast<uint64_t>(bmt[2]) |
-                  static_cast<uint64_t>(bmt[3])) & valid;
+  all &= valid;
 
   f32x16 acc[2][CB];
 #pragma unroll
@@ -504,12 +511,12 @@ __global__ __launch_bounds__(256) void xext_cols_kernel(XextArgs a, uint16_t* x_
     }
 #pragma unroll
     for (int k = 0; k < CA; ++k) all &= all - 1;
-    // wave w stages adapters w, w + 4, ...: lane l moves pieces l + 64 q of
+    // wave w stages adapters w, w + RT, ...: lane l moves pieces l + 64 q of
     // each block (pieces past the adapter's ncols * r / 8 read the first line)
     u32x4 v[CAW][QP];
 #pragma unroll
     for (int jw = 0; jw < CAW; ++jw) {
-      const int j = kColsRT * jw + wave;
+      const int j = RT * jw + wave;
       const int r = __builtin_amdgcn_readlane(my_r, j);
       const int64_t off = static_cast<int64_t>(
           (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(my_off >> 32), j))) << 32) |
@@ -534,7 +541,7 @@ __global__ __launch_bounds__(256) void xext_cols_kernel(XextArgs a, uint16_t* x_
     // store sits under a branch (r / 8 = 2 << tier pieces per column)
 #pragma unroll
     for (int jw = 0; jw < CAW; ++jw) {
-      const int j = kColsRT * jw + wave;
+      const int j = RT * jw + wave;
       const int r = __builtin_amdgcn_readlane(my_r, j);
       const int sh = 31 - __builtin_clz(r > 0 ? r / 8 : 1);
 #pragma unroll
@@ -824,18 +831,32 @@ int gs_switch_lora_expand(void* x_ext, int64_t stride_m, int64_t stride_n, int64
   const int kk = xext_kk(na, M);
   if (kk > 0 && GS_XEXT_COLS) {
     // 64-column blocks (whole 128-byte row pieces) once they give two
-    // workgroups per CU; 32-column blocks otherwise
-    const unsigned row_groups = static_cast<unsigned>(((M + 31) / 32 + kColsRT - 1) / kColsRT);
-    const bool wide = int64_t(N / 64) * row_groups >= 2 * int64_t(device_cus());
-    const dim3 g2(static_cast<unsigned>((N + 63) / 64), row_groups), g1(static_cast<unsigned>(N / 32), row_groups);
-    auto go = [&](auto kern, dim3 g) { hipLaunchKernelGGL(kern, g, dim3(256), 0, st, a, xo, tile_slice, block_n); };
-    if (idx_bytes == 8) {
-      if (kk == 2) wide ? go(xext_cols_kernel<2, 2, true>, g2) : go(xext_cols_kernel<2, 1, true>, g1);
-      else wide ? go(xext_cols_kernel<4, 2, true>, g2) : go(xext_cols_kernel<4, 1, true>, g1);
-    } else {
-      if (kk == 2) wide ? go(xext_cols_kernel<2, 2, false>, g2) : go(xext_cols_kernel<2, 1, false>, g1);
-      else wide ? go(xext_cols_kernel<4, 2, false>, g2) : go(xext_cols_kernel<4, 1, false>, g1);
-    }
+    // workgroups per CU; 32-column blocks otherwise, over eight row tiles
+    // when four would take more than one round of workgroups (each column's
+    // lora_B is then staged half as often, and no CU runs two workgroups'
+    // worth of staging where one would do)
+    const int64_t tiles = (M + 31) / 32, cus = device_cus();
+    const unsigned rg4 = static_cast<unsigned>((tiles + 3) / 4), rg8 = static_cast<unsigned>((tiles + 7) / 8);
+    const bool wide = int64_t(N / 64) * rg4 >= 2 * cus;
+    const bool eight = !wide && GS_XEXT_RT8 && int64_t(N / 32) * rg4 > cus;
+    const dim3 g2(static_cast<unsigned>((N + 63) / 64), rg4), g1(static_cast<unsigned>(N / 32), eight ? rg8 : rg4);
+    auto go = [&](auto kern, dim3 g, int rt) {
+      hipLaunchKernelGGL(kern, g, dim3(64 * rt), 0, st, a, xo, tile_slice, block_n);
+    };
+    auto pick = [&](auto i64) {
+      constexpr bool I64 = decltype(i64)::value;
+      if (kk == 2) {
+        if (wide) go(xext_cols_kernel<2, 2, 4, I64>, g2, 4);
+        else if (eight) go(xext_cols_kernel<2, 1, 8, I64>, g1, 8);
+        else go(xext_cols_kernel<2, 1, 4, I64>, g1, 4);
+      } else {
+        if (wide) go(xext_cols_kernel<4, 2, 4, I64>, g2, 4);
+        else if (eight) go(xext_cols_kernel<4, 1, 8, I64>, g1, 8);
+        else go(xext_cols_kernel<4, 1, 4, I64>, g1, 4);
+      }
+    };
+    if (idx_bytes == 8) pick(std::true_type{});
+    else pick(std::false_type{});
     GS_CHECK_LAUNCH("gs_switch_lora_expand");
     return GS_OK;
   }

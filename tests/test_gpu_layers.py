@@ -128,12 +128,15 @@ def test_switch_lora_expand_op_matches_oracle(dev):
 @pytest.mark.parametrize("slices,ranks,T", [
     ((4096, 96), [32, 16, 32, 8], 1000),      # column blocks of 64 (a partial last one), ragged last row group
     ((512,), [64, 16, 64], 700),              # rank-64 tier, 32-column blocks
+    ((4096, 1024, 1024), [32, 16, 32, 8], 300),   # 32-column blocks over eight row tiles, ragged last group
+    ((4096, 2048), [64, 16, 8], 400),         # eight row tiles with a rank-64 tier
     ((256, 128), [128, 16], 300),             # a rank-128 tier: the per-tile kernel at decode sizes
     ((1024, 256), [32, 16, 8], 1500),         # past 1024 rows: the per-tile kernel
 ])
 def test_switch_lora_expand_op_kernel_forms(dev, slices, ranks, T):
     """Each kernel form of the reference op (column-block at decode batch
-    sizes with 32- and 64-column blocks, per-tile past 1024 rows or with a tier
+    sizes with 32- and 64-column blocks, over four or eight row tiles;
+    per-tile past 1024 rows or with a tier
     above rank 64) vs the oracle, with int64 and int32 ids; base rows and the
     shrink columns are untouched."""
     K = 256
@@ -161,6 +164,41 @@ def test_switch_lora_expand_op_kernel_forms(dev, slices, ranks, T):
         _close(got, ref, 2e-2, "switch_lora_expand")
         assert np.array_equal(got[base], x_ext0[base]), "base rows touched"
         assert np.array_equal(got[:, layer._N_total:], x_ext0[:, layer._N_total:]), "shrink columns written"
+
+
+@pytest.mark.parametrize("slices,T", [
+    ((4096, 96), 1000),     # 64-column blocks
+    ((512,), 700),          # 32-column blocks
+    ((2048, 1024), 500),    # 32-column blocks over eight row tiles
+])
+def test_switch_lora_expand_op_runs_of_adapters(dev, slices, T):
+    """The column-block form with 20 adapters (more than one staging chunk)
+    and ids in runs, so a workgroup's tiles follow a few adapters, some past
+    the first chunk, and tiles that follow none of the first ones; vs the
+    oracle."""
+    K, ranks = 256, [16, 32] * 10
+    layer, W, A, B = _make_vllm_layer(dev, K, slices, ranks, seed=77 + T)
+    g = torch.Generator(device=dev).manual_seed(5 + T)
+    x = torch.randn(T, K, generator=g, device=dev).to(torch.bfloat16)
+    order = [19, 3, 17, 0, 18, 20, 9, 16, 2, 20, 13, 1, 19, 18, 11, 17, 20, 4]
+    ids = torch.tensor([order[(m // 57) % len(order)] for m in range(T)], device=dev)
+    ctx = _ctx_for(dev, layer, ids)
+    x_ext = torch.mm(x, layer.w_ext.T)
+    x_ext0 = _np(x_ext)
+    loc = ctx.remapped_indices[0]
+    ref = olora.switch_lora_expand_xext(x_ext0, loc.cpu().numpy(), ctx.per_module_bitmasks[0].cpu().numpy(),
+                                        _np(layer._lb_packed), layer.tile_to_slice.cpu().numpy(),
+                                        layer.slice_col_r.cpu().numpy(), layer._na, layer._S, layer._block_n,
+                                        layer._N_total)
+    base = (loc == 0).cpu().numpy()
+    _say(f"expand op runs of adapters: slices={slices} T={T}")
+    xe = x_ext.clone()
+    ops.op("switch_lora_expand")(xe, loc, ctx.per_module_bitmasks[0], layer._lb_packed, layer.tile_to_slice,
+                                  layer.slice_col_r, *layer._na, layer._S, layer._block_n, layer._N_total)
+    torch.cuda.synchronize()
+    got = _np(xe)
+    _close(got, ref, 2e-2, "switch_lora_expand")
+    assert np.array_equal(got[base], x_ext0[base]), "base rows touched"
 
 
 def test_switch_lora_expand_zero_bitmask_skips(dev):
