@@ -215,6 +215,25 @@ def test_switch_lora_expand_zero_bitmask_skips(dev):
     assert torch.equal(xe, x_ext)
 
 
+def test_reference_ops_zero_rows(dev):
+    """The reference ops on a batch of no rows return without a launch and
+    leave their outputs as they were (the expand) or empty."""
+    slices, ranks, K = (128,), [16, 16], 256
+    layer, W, A, B = _make_vllm_layer(dev, K, slices, ranks, seed=21)
+    x_ext = torch.zeros(0, layer.w_ext.shape[0], dtype=torch.bfloat16, device=dev)
+    ids = torch.zeros(0, dtype=torch.int64, device=dev)
+    bm = torch.zeros(0, dtype=torch.int64, device=dev)
+    ops.op("switch_lora_expand")(x_ext, ids, bm, layer._lb_packed, layer.tile_to_slice, layer.slice_col_r, *layer._na,
+                                  layer._S, layer._block_n, layer._N_total)
+    H = 128
+    lg, _, _, _ = _make_vllm_layer(dev, K, (H, H), [16, 32], seed=22, fuse_swiglu=True)
+    xg = torch.zeros(0, lg.w_ext.shape[0], dtype=torch.bfloat16, device=dev)
+    out = torch.empty(0, H, dtype=torch.bfloat16, device=dev)
+    ops.op("switch_lora_expand_swiglu")(out, xg, ids, bm, lg._lb_packed, lg.slice_col_r, *lg._na, 2, 32, H, 2 * H)
+    torch.cuda.synchronize()
+    assert x_ext.shape[0] == 0 and out.shape == (0, H)
+
+
 @pytest.mark.parametrize("with_ctx", [True, False])
 def test_swiglu_path(dev, with_ctx):
     H, K, T = 1280, 512, 150

@@ -168,6 +168,11 @@ def test_small_all_base_and_no_tokens_for_some_adapters(dev):
     switched.switched_lora_routed_(y, md.x, torch.tensor(ids, device=dev), pk, path="small")
     torch.cuda.synchronize()
     _check(md, y, ids, torch.bfloat16)
+    # no tokens at all: nothing to do, no error
+    y0 = md.y[:0].clone()
+    switched.switched_lora_routed_(y0, md.x[:0], torch.zeros(0, dtype=torch.int64, device=dev), pk, path="small")
+    torch.cuda.synchronize()
+    assert y0.shape[0] == 0
 
 
 def test_small_graph_replays(dev):
