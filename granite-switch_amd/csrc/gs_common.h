@@ -142,10 +142,27 @@ __device__ __forceinline__ void dma16(const char* src, char* lds_dst) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(dst) : "memory", "m0");
 }
 
+// As dma16 for data read once (streamed: the nt policy keeps it from
+// displacing data that other workgroups re-read from L2).
+__device__ __forceinline__ void dma16_nt(const char* src, char* lds_dst) {
+  const uint32_t dst =
+      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)(lds_dst))));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(dst) : "memory", "m0");
+}
+
 __device__ __forceinline__ void mem_fence_compiler() { asm volatile("" ::: "memory"); }
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+// 16-byte load and store with the streaming (nt) cache policy, for data a
+// launch touches once: it does not displace what other workgroups re-read
+// from L2.
+__device__ __forceinline__ u32x4 ld16_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ void st16_nt(void* p, const u32x4& v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
 __device__ __forceinline__ u32x4 sel16(bool keep, const u32x4& v) {
   return keep ? v : u32x4{0u, 0u, 0u, 0u};
 }
@@ -155,7 +172,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 // y piece (16 bytes = 8 bf16 / 4 fp32) + delta, rounded once, stored back.
-template <bool BF16>
+template <bool BF16, bool NT = false>
 __device__ __forceinline__ void add_store_y(void* y, int64_t off, const u32x4& in, const float* d) {
   u32x4* p = reinterpret_cast<u32x4*>(static_cast<char*>(y) + off * Elt<BF16>::kSize);
   if constexpr (BF16) {
@@ -167,10 +184,14 @@ __device__ __forceinline__ void add_store_y(void* y, int64_t off, const u32x4& i
       const float hi = bf16_bits_to_f32(static_cast<uint16_t>(w >> 16)) + d[2 * e + 1];
       o[e] = pack_bf16x2(lo, hi);
     }
-    *p = u32x4{o[0], o[1], o[2], o[3]};
+    const u32x4 v = u32x4{o[0], o[1], o[2], o[3]};
+    if constexpr (NT) st16_nt(p, v);
+    else *p = v;
   } else {
     const f32x4 f = __builtin_bit_cast(f32x4, in);
-    *p = __builtin_bit_cast(u32x4, f32x4{f.x + d[0], f.y + d[1], f.z + d[2], f.w + d[3]});
+    const u32x4 v = __builtin_bit_cast(u32x4, f32x4{f.x + d[0], f.y + d[1], f.z + d[2], f.w + d[3]});
+    if constexpr (NT) st16_nt(p, v);
+    else *p = v;
   }
 }
 

@@ -326,7 +326,8 @@ __global__ __launch_bounds__(kThreads) void shrink_dma_kernel(ShrinkParams p) {
     char* slot = ring + (st % NST) * STAGE;
     const int64_t off = static_cast<int64_t>(st) * kDmaRow;
 #pragma unroll
-    for (int t = 0; t < XT; ++t) dma16(xsrc[t] + off, slot + (16 * wave + 8 * t) * kDmaRow);
+    for (int t = 0; t < XT; ++t)   // x is read once per launch: streamed, so lora_A stays in L2
+      dma16_nt(xsrc[t] + off, slot + (16 * wave + 8 * t) * kDmaRow);
 #pragma unroll
     for (int t = 0; t < AT; ++t) dma16(asrc[t] + off, slot + (kTMS + ARW * wave + 8 * t) * kDmaRow);
   };
@@ -558,6 +559,11 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
   constexpr int PASSES = kTM / RPI;           // rows per thread
   constexpr int KSTEP = BF16 ? 16 : 8;       // k per MFMA group (both lane halves)
   constexpr int KHALF = KSTEP / 2;
+  // y rows with the streaming policy in the 256-column form: the lora_B
+  // blocks and partials that the workgroups share stay in L2 (decoder step
+  // 7 000 -> 6 544 us).  The 128-column form (ranks above 32) measured
+  // slower with it (multiswitch down expand 16.3 -> 18.8 us).
+  constexpr bool YNT = NBW == 2;
   __shared__ float dtile[kTM][NT + kOutPad];
   extern __shared__ __align__(16) char zs[];   // [32][S*max_rank + 8] element type
 
@@ -599,8 +605,10 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
   auto load_y = [&](int sub, u32x4 (&yv)[PASSES]) {
     const int64_t col = min(static_cast<int64_t>(sub) * NT + cx, static_cast<int64_t>(p.out_total) - EPL);
 #pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps)
-      yv[ps] = ld16(static_cast<const char*>(p.y) + (yrow[ps] + col) * Elt<BF16>::kSize);
+    for (int ps = 0; ps < PASSES; ++ps) {
+      const char* src = static_cast<const char*>(p.y) + (yrow[ps] + col) * Elt<BF16>::kSize;
+      yv[ps] = YNT ? ld16_nt(src) : ld16(src);
+    }
   };
   // B k-groups [kc*PRE, kc*PRE + PRE) of this wave's n-blocks in sub-tile sub
   auto load_b = [&](int sub, int kc, u32x4 (&bp)[NBW][PRE]) {
@@ -688,7 +696,7 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
       float d[EPL];
 #pragma unroll
       for (int e = 0; e < EPL; ++e) d[e] = dtile[row][cx + e];
-      if (rok[ps] && col < p.out_total) add_store_y<BF16>(p.y, yrow[ps] + col, ycur[ps], d);
+      if (rok[ps] && col < p.out_total) add_store_y<BF16, YNT>(p.y, yrow[ps] + col, ycur[ps], d);
     }
     lds_barrier();                          // dtile is rewritten by the next sub-tile
   };
