@@ -132,6 +132,8 @@ def test_switch_lora_expand_op_matches_oracle(dev):
     ((4096, 2048), [64, 16, 8], 400),         # eight row tiles with a rank-64 tier
     ((256, 128), [128, 16], 300),             # a rank-128 tier: the per-tile kernel at decode sizes
     ((1024, 256), [32, 16, 8], 1500),         # past 1024 rows: the per-tile kernel
+    ((1024, 32), [32, 16], 1100),             # per-tile kernel, last 128-column tile a quarter full
+    ((1024, 32), [32, 16], 600),              # column-block kernel, N = 33 blocks of 32
 ])
 def test_switch_lora_expand_op_kernel_forms(dev, slices, ranks, T):
     """Each kernel form of the reference op (column-block at decode batch
