@@ -21,6 +21,7 @@ library must be built.
 from __future__ import annotations
 
 import ctypes
+import math
 import os
 from dataclasses import dataclass
 
@@ -385,7 +386,18 @@ def _small_plan(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None,
         plan = (False, 1)
     else:
         spread = packed.num_adapters if not num_seqs else min(packed.num_adapters, num_seqs)
-        largest = (T + spread - 1) // spread if largest_group is None else max(1, min(int(largest_group), T))
+        if largest_group is not None:
+            largest = max(1, min(int(largest_group), T))
+        elif num_seqs:
+            largest = (T + spread - 1) // spread
+        else:
+            # ids drawn per token: at a mean of one chunk or less the largest
+            # group runs over it by a few tokens (2 adapters, 64 tokens: 35
+            # against 32), and the second chunk then doubles a workgroup's
+            # walk, so a margin of two standard deviations is added there
+            largest = (T + spread - 1) // spread
+            if largest <= 32:
+                largest = min(T, largest + int(2 * math.sqrt(largest)))
         chunks = (largest + 31) // 32                   # 32-token chunks in the estimated largest group
         cus = _device_cus(packed.a_pack.device)
         rs = 1
@@ -393,7 +405,11 @@ def _small_plan(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None,
             rs *= 2
         per_wg = -(-chunks // rs)
         fits = small_workgroups(packed, T, rs) <= (8 if T <= 256 else 4) * cus
-        plan = (fits and (per_wg <= 2 or (rs == 1 and chunks <= 3)), rs)
+        # the kernel streams lora_A through ~128 producer workgroups; past
+        # ~28 MiB of it the segment shrink's wider grid is faster
+        a_bytes = sum(int(r) for r in packed.ranks_host) * packed.num_slices * packed.hidden * \
+            (4 if packed.dtype == torch.float32 else 2)
+        plan = (fits and a_bytes <= _SMALL_MAX_A_BYTES and (per_wg <= 2 or (rs == 1 and chunks <= 3)), rs)
     if len(_small_plans) >= _SMALL_PLAN_CAP:     # batch sizes vary per step: keep the cache bounded
         _small_plans.clear()
     _small_plans[key] = plan
@@ -402,6 +418,12 @@ def _small_plan(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None,
 
 _small_plans: dict = {}
 _SMALL_PLAN_CAP = 4096
+# lora_A bytes (all the module's adapters) past which the segment kernels are
+# taken: measured 48 adapters of ranks 8-64 on a 12800-wide down projection
+# (36.9 MB) 36-37 us one-launch against 27.3 us segments at 128-256 tokens;
+# at 12.6-19.7 MB (gate_up, qkv at rank 64, down with 24 adapters) the
+# one-launch kernel stays 20-40 % faster
+_SMALL_MAX_A_BYTES = 28 << 20
 
 
 def small_row_split(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None = None,
@@ -429,8 +451,12 @@ def small_preferred(packed: "PackedAdapters", num_tokens: int, num_seqs: int | N
     it is below the estimate's chunk count and the grid stays within 3
     workgroups per CU (the kernel holds 2 per CU at a time); the one-launch
     kernel is taken when it is eligible, its grid is within 4 workgroups per
-    CU (8 for batches of up to 256 tokens), and each workgroup is left with at
-    most 2 chunks (3 without a split).
+    CU (8 for batches of up to 256 tokens), each workgroup is left with at
+    most 2 chunks (3 without a split), and the module's lora_A is at most
+    28 MiB (its ~128 producer workgroups stream it slower than the segment
+    shrink's grid past that).  For per-token ids (no ``num_seqs``), an
+    estimated group of one chunk or less gets a margin of two standard
+    deviations, since one token over the chunk doubles a workgroup's walk.
 
     Measured on one MI355X (H = 2048..12800, 2..48 adapters, T = 64..1024):
     past these grids a second round of workgroups costs more than it saves

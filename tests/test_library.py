@@ -286,6 +286,8 @@ def _packed_stub(H, slices, NA, max_rank, dtype=torch.bfloat16):
     (12800, (4096,), 12, 16, 1024, 8, True, 2),                 # 128-token groups: split 2 fits 3 WG/CU
     (12800, (4096,), 12, 16, 1024, 4, False, 1),                # 256-token groups: 4 chunks per WG, segments
     (4096, (4096,), 4, 128, 64, None, False, 1),                # rank past the small kernel's limit
+    (12800, (4096,), 48, 32, 128, None, False, 1),              # 48 adapters: 39 MB of lora_A, segments
+    (12800, (4096,), 24, 32, 128, None, True, 1),               # 24 adapters: 19.7 MB, one launch
 ])
 def test_small_path_plan(monkeypatch, H, slices, NA, r, T, seqs, small, rs):
     """The host's path choice and row split on a 256-CU part (the decisions
