@@ -29,6 +29,7 @@ GS_DTYPE_FP32 = 1
 GS_MAX_ADAPTERS = 256
 GS_MAX_SLICES = 8
 GS_MAX_RANK = 512
+GS_RANK_CLASS_SPLIT = 64
 GS_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 # name -> (restype, argtypes); mirrors include/granite_switch_amd.h
@@ -40,17 +41,18 @@ SIGNATURES = {
                                   c_void_p, c_void_p, c_i64, c_void_p]),
     "gs_route_latest_wins": (c_i32, [c_void_p, c_void_p, c_i64, c_i32, c_void_p, c_i32, c_i32, c_void_p, c_void_p,
                                      c_void_p]),
-    "gs_shrink_workspace_bytes": (c_i64, [c_i64, c_i32, c_i32, c_i32, c_i32]),
+    "gs_shrink_workspace_bytes": (c_i64, [c_i64, c_i32, c_i32, c_i32, c_i32, c_void_p]),
+    "gs_shrink_ksplits": (c_i32, [c_i32, c_i64, c_i32, c_i32, c_i32, c_i32, c_void_p, c_void_p]),
     "gs_shrink": (c_i32, [c_i32, c_void_p, c_i64, c_i64, c_i32, c_void_p, c_void_p, c_void_p, c_i32, c_i32, c_i32,
-                          c_void_p, c_void_p, c_void_p, c_i64, c_void_p, c_i64, c_void_p]),
+                          c_void_p, c_void_p, c_void_p, c_void_p, c_i64, c_void_p, c_i64, c_void_p]),
     "gs_expand_add": (c_i32, [c_i32, c_void_p, c_i64, c_i64, c_i32, c_void_p, c_i32, c_void_p, c_i64, c_i32, c_void_p,
-                              c_void_p, c_void_p, c_void_p, c_i32, c_i32, c_void_p, c_void_p, c_void_p]),
+                              c_void_p, c_void_p, c_void_p, c_i32, c_i32, c_void_p, c_void_p, c_void_p, c_void_p]),
     "gs_switched_lora": (c_i32, [c_i32, c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i32, c_i32, c_void_p, c_i32,
                                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_i32, c_i32, c_void_p, c_void_p,
-                                 c_void_p, c_void_p, c_i64, c_void_p]),
+                                 c_void_p, c_void_p, c_void_p, c_i64, c_void_p]),
     "gs_switched_lora_noalloc": (c_i32, [c_i32, c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i32, c_i32, c_void_p,
                                          c_i32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_i32, c_i32,
-                                         c_void_p, c_void_p, c_void_p]),
+                                         c_void_p, c_void_p, c_void_p, c_void_p]),
     "gs_small_eligible": (c_i32, [c_i64, c_i32, c_i32, c_void_p, c_i32, c_i32]),
     "gs_small_workspace_bytes": (c_i64, [c_i32, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_void_p]),
     "gs_small_sync_bytes": (c_i64, []),
@@ -107,6 +109,11 @@ def load() -> ctypes.CDLL:
             fn.argtypes = args
         _lib = lib
     return _lib
+
+
+def last_error() -> str:
+    msg = load().gs_last_error()
+    return msg.decode() if msg else ""
 
 
 def call(name: str, *args) -> int:

@@ -239,10 +239,20 @@ struct SliceInfo {
 
 // ---------------------------------------------------------------------------
 // Segment work lists. Adapter g (1..NA) owns slots [seg[g-1], seg[g]) of the
-// adapter-sorted token permutation. A module skips adapters with rank 0 (not
-// applicable to it). Tiles are TM consecutive slots of one adapter. Every wave
-// computes the same answer, so no LDS or barrier is needed.
+// adapter-sorted token permutation. A launch covers the adapters whose rank in
+// this module lies in its rank window [rw.lo, rw.hi] (lo >= 1, so adapters of
+// rank 0 -- not applicable here -- are always skipped): a module whose ranks
+// differ widely runs one launch per rank class, each sized for its own ranks.
+// Tiles are TM consecutive slots of one adapter. Every wave computes the same
+// answer, so no LDS or barrier is needed.
 // ---------------------------------------------------------------------------
+struct RankWindow {
+  int lo;
+  int hi;
+};
+
+__host__ __device__ __forceinline__ bool in_window(const RankWindow& rw, int r) { return r >= rw.lo && r <= rw.hi; }
+
 struct TileRef {
   int g;        // global adapter id (0 = no tile: the workgroup exits)
   int slot0;    // first slot of the tile
@@ -255,13 +265,13 @@ struct TileRef {
 // computes the same value).
 template <int TM>
 __device__ __forceinline__ int count_tiles(const int32_t* __restrict__ seg, const int32_t* __restrict__ ranks,
-                                           int num_adapters) {
+                                           int num_adapters, RankWindow rw) {
   const int l = __lane_id();
   int total = 0;
   for (int g0 = 1; g0 <= num_adapters; g0 += 64) {
     const int g = g0 + l;
     int ntiles = 0;
-    if (g <= num_adapters && ranks[g] > 0) ntiles = (seg[g] - seg[g - 1] + TM - 1) / TM;
+    if (g <= num_adapters && in_window(rw, ranks[g])) ntiles = (seg[g] - seg[g - 1] + TM - 1) / TM;
 #pragma unroll
     for (int d = 32; d > 0; d >>= 1) ntiles += __shfl_xor(ntiles, d, 64);
     total += ntiles;
@@ -294,6 +304,29 @@ __device__ __forceinline__ XcdItem xcd_item(int lin, int total_tiles, int nsub) 
   return it;
 }
 
+// Item layout of a launch over (tile, sub) pairs.  The XCD form (xcd_item)
+// gives each XCD a contiguous range of tiles, so an adapter's tiles share one
+// L2: for launches of many tiles.  The flat form makes item lin the pair
+// (lin / nsub, lin % nsub), so consecutive items -- and workgroups, which are
+// dealt to the XCDs round-robin -- fall on different XCDs: for a launch of a
+// few tiles with many subs each (a rank class of one large adapter), which
+// the XCD form would leave to one XCD.
+__device__ __forceinline__ XcdItem work_item(int lin, int total_tiles, int nsub, bool flat) {
+  if (!flat) return xcd_item(lin, total_tiles, nsub);
+  XcdItem it{-1, 0};
+  if (lin >= 0 && lin < total_tiles * nsub) {
+    it.tile = lin / nsub;
+    it.sub = lin - it.tile * nsub;
+  }
+  return it;
+}
+
+// Items a launch over `total_tiles` tiles must cover (ids at or past it have
+// no work in either form).
+__device__ __forceinline__ int work_items(int total_tiles, int nsub, bool flat) {
+  return flat ? total_tiles * nsub : 8 * ((total_tiles + 7) >> 3) * nsub;
+}
+
 // Tile jj of an adapter whose slots are [lo, hi): TM consecutive slots (the
 // last tile shorter), or, with BAL, one of ceil(n / TM) tiles of near-equal
 // size (rows spread evenly, at most TM each).
@@ -312,7 +345,8 @@ __device__ __forceinline__ void tile_span(int lo, int hi, int jj, int& slot0, in
 
 template <int TM, bool BAL = false>
 __device__ __forceinline__ TileRef find_tile(const int32_t* __restrict__ seg, const int32_t* __restrict__ ranks,
-                                             const int64_t* __restrict__ offs, int num_adapters, int tile_id) {
+                                             const int64_t* __restrict__ offs, int num_adapters, RankWindow rw,
+                                             int tile_id) {
   TileRef ref{0, 0, 0, 0, 0};
   const int l = __lane_id();
   int carry = 0;
@@ -326,7 +360,7 @@ __device__ __forceinline__ TileRef find_tile(const int32_t* __restrict__ seg, co
       hi = seg[g];
       rk = ranks[g];
       of = offs[g];
-      ntiles = (rk > 0) ? (hi - lo + TM - 1) / TM : 0;
+      ntiles = in_window(rw, rk) ? (hi - lo + TM - 1) / TM : 0;
     }
     // inclusive scan over the wave
     int incl = ntiles;
@@ -356,20 +390,23 @@ __device__ __forceinline__ TileRef find_tile(const int32_t* __restrict__ seg, co
 }
 
 // The tile of work item `lin` of a 1-D launch over (tile, sub) pairs (see
-// xcd_item), in one pass over the adapter table when it fits one wave
+// work_item), in one pass over the adapter table when it fits one wave
 // (<= 64 adapters): the tile count and the tile's lookup share the same
 // loads.  nsub_of(total tiles) gives the number of subs per tile (every wave
-// computes the same value).  Returns g = 0 when the item has no tile.
+// computes the same value); the tile count is returned in `total_out` (a
+// workgroup that loops over items finds its later tiles with tile_at).
+// Returns g = 0 when the item has no tile.
 template <int TM, bool BAL = false, typename NsubOf>
 __device__ __forceinline__ TileRef locate_tile_by(const int32_t* __restrict__ seg, const int32_t* __restrict__ ranks,
-                                                  const int64_t* __restrict__ offs, int num_adapters, int lin,
-                                                  NsubOf nsub_of, int& sub) {
+                                                  const int64_t* __restrict__ offs, int num_adapters, RankWindow rw,
+                                                  int lin, bool flat, NsubOf nsub_of, int& sub, int& total_out) {
   TileRef ref{0, 0, 0, 0, 0};
   if (num_adapters > 64) {
-    const int total = count_tiles<TM>(seg, ranks, num_adapters);
-    const XcdItem it = xcd_item(lin, total, nsub_of(total));
+    const int total = count_tiles<TM>(seg, ranks, num_adapters, rw);
+    total_out = total;
+    const XcdItem it = work_item(lin, total, nsub_of(total), flat);
     sub = it.sub;
-    return it.tile < 0 ? ref : find_tile<TM, BAL>(seg, ranks, offs, num_adapters, it.tile);
+    return it.tile < 0 ? ref : find_tile<TM, BAL>(seg, ranks, offs, num_adapters, rw, it.tile);
   }
   const int l = __lane_id();
   const int g = 1 + l;
@@ -380,7 +417,7 @@ __device__ __forceinline__ TileRef locate_tile_by(const int32_t* __restrict__ se
     hi = seg[g];
     rk = ranks[g];
     of = offs[g];
-    ntiles = (rk > 0) ? (hi - lo + TM - 1) / TM : 0;
+    ntiles = in_window(rw, rk) ? (hi - lo + TM - 1) / TM : 0;
   }
   int incl = ntiles;
 #pragma unroll
@@ -389,7 +426,8 @@ __device__ __forceinline__ TileRef locate_tile_by(const int32_t* __restrict__ se
     if (l >= d) incl += v;
   }
   const int total = __shfl(incl, 63, 64);
-  const XcdItem it = xcd_item(lin, total, nsub_of(total));
+  total_out = total;
+  const XcdItem it = work_item(lin, total, nsub_of(total), flat);
   sub = it.sub;
   if (it.tile < 0) return ref;
   const int excl = incl - ntiles;
@@ -409,9 +447,21 @@ __device__ __forceinline__ TileRef locate_tile_by(const int32_t* __restrict__ se
 // As locate_tile_by with a fixed number of subs per tile.
 template <int TM>
 __device__ __forceinline__ TileRef locate_tile(const int32_t* __restrict__ seg, const int32_t* __restrict__ ranks,
-                                               const int64_t* __restrict__ offs, int num_adapters, int lin, int nsub,
-                                               int& sub) {
-  return locate_tile_by<TM>(seg, ranks, offs, num_adapters, lin, [nsub](int) { return nsub; }, sub);
+                                               const int64_t* __restrict__ offs, int num_adapters, RankWindow rw,
+                                               int lin, bool flat, int nsub, int& sub, int& total) {
+  return locate_tile_by<TM>(seg, ranks, offs, num_adapters, rw, lin, flat, [nsub](int) { return nsub; }, sub, total);
+}
+
+// The tile of a later item `lin` of a workgroup that loops over items, the
+// batch's tile count already known.
+template <int TM, bool BAL = false>
+__device__ __forceinline__ TileRef tile_at(const int32_t* __restrict__ seg, const int32_t* __restrict__ ranks,
+                                           const int64_t* __restrict__ offs, int num_adapters, RankWindow rw, int lin,
+                                           bool flat, int total, int nsub, int& sub) {
+  const XcdItem it = work_item(lin, total, nsub, flat);
+  sub = it.sub;
+  if (it.tile < 0) return TileRef{0, 0, 0, 0, 0};
+  return find_tile<TM, BAL>(seg, ranks, offs, num_adapters, rw, it.tile);
 }
 
 }  // namespace gs

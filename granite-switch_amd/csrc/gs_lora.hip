@@ -71,6 +71,8 @@ struct ShrinkParams {
   int KS;
   int KC;
   int n_chunks;
+  RankWindow rw;          // adapters of this launch's rank class
+  int flat;               // flat item layout (work_item) instead of tile ranges per XCD
 };
 
 // 16x16 MFMA over one 16-byte piece of each operand (K = 32 bf16, or four
@@ -112,9 +114,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NB <= 
   static_assert(COLS * PPR % kThreads == 0, "lora_A pieces must split evenly over the workgroup");
   __shared__ __align__(16) char a_s[COLS * ALD];
 
-  int sub = 0;
-  const TileRef tr =
-      locate_tile<kTMS>(p.seg, p.ranks, p.a_off, p.NA, static_cast<int>(blockIdx.x), p.n_chunks * p.KS, sub);
+  int sub = 0, total = 0;
+  const TileRef tr = locate_tile<kTMS>(p.seg, p.ranks, p.a_off, p.NA, p.rw, static_cast<int>(blockIdx.x), p.flat != 0,
+                                       p.n_chunks * p.KS, sub, total);
   if (tr.g == 0) return;
   const int chunk = sub % p.n_chunks;
   const int ks = sub / p.n_chunks;
@@ -269,8 +271,9 @@ __device__ __forceinline__ void wait_stages(int after) {
   }
 }
 
+// One work item of shrink_dma_kernel: tile tr, sub = (k-chunk, column chunk).
 template <int NB>
-__global__ __launch_bounds__(kThreads) void shrink_dma_kernel(ShrinkParams p) {
+__device__ __forceinline__ void shrink_dma_item(const ShrinkParams& p, const TileRef& tr, int sub, char* ring) {
   constexpr int COLS = 32 * NB;
   constexpr int NC16 = COLS / 16;
   constexpr int ROWS = kTMS + COLS;        // LDS rows of a stage: x rows, then lora_A rows
@@ -281,12 +284,7 @@ __global__ __launch_bounds__(kThreads) void shrink_dma_kernel(ShrinkParams p) {
   constexpr int AT = ARW / 8;              // lora_A transfers per wave and stage
   constexpr int TPW = XT + AT;
   static_assert(TPW * (NST - 2) <= 63, "vmcnt counts at most 63 outstanding transfers");
-  __shared__ __align__(16) char ring[NST * STAGE];
 
-  int sub = 0;
-  const TileRef tr =
-      locate_tile<kTMS>(p.seg, p.ranks, p.a_off, p.NA, static_cast<int>(blockIdx.x), p.n_chunks * p.KS, sub);
-  if (tr.g == 0) return;
   const int chunk = sub % p.n_chunks;
   const int ks = sub / p.n_chunks;
   const int ncols = p.S * tr.rank;
@@ -387,15 +385,54 @@ __global__ __launch_bounds__(kThreads) void shrink_dma_kernel(ShrinkParams p) {
   }
 }
 
-// z[slot][col] = sum_ks part[ks][slot][col] (fixed order), for active slots.
+// LOOP = false: one item per workgroup (the launch is sized for every tile
+// the batch can have).  LOOP = true (a rank class expected to hold far fewer
+// tiles than it could, whose grid the host caps): a workgroup takes items
+// blockIdx.x, + gridDim.x, ... while they lie in the batch's item range.  The
+// loop is a separate instantiation: its live state would cost the one-item
+// form registers.
+template <int NB, bool LOOP>
+__global__ __launch_bounds__(kThreads) void shrink_dma_kernel(ShrinkParams p) {
+  __shared__ __align__(16) char ring[DmaRing<NB>::NST * (kTMS + 32 * NB) * kDmaRow];
+  const int nsub = p.n_chunks * p.KS;
+  const bool flat = LOOP && p.flat != 0;       // the one-item form is never flat
+  int lin = static_cast<int>(blockIdx.x);
+  int sub = 0, total = 0;
+  TileRef tr = locate_tile<kTMS>(p.seg, p.ranks, p.a_off, p.NA, p.rw, lin, flat, nsub, sub, total);
+  if constexpr (!LOOP) {
+    if (tr.g != 0) shrink_dma_item<NB>(p, tr, sub, ring);
+    return;
+  }
+  const int items = work_items(total, nsub, flat);
+  for (;;) {
+    if (tr.g != 0) shrink_dma_item<NB>(p, tr, sub, ring);
+    lin += static_cast<int>(gridDim.x);
+    if (lin >= items) break;
+    lds_barrier();                         // every wave is done with the ring before the next item's transfers
+    tr = tile_at<kTMS>(p.seg, p.ranks, p.a_off, p.NA, p.rw, lin, flat, total, nsub, sub);
+  }
+}
+
+// z[slot][col] = sum_ks part[ks][slot][col] (fixed order), for the active
+// slots of the adapters in the launch's rank window (the other classes' slots
+// are written by their own launches).
 template <bool BF16>
 __global__ __launch_bounds__(kThreads) void reduce_parts_kernel(const float* __restrict__ part, int64_t part_stride,
                                                                int KS, int zw, const int32_t* __restrict__ seg,
+                                                               const int32_t* __restrict__ ranks, RankWindow rw,
                                                                int NA, void* z, int64_t ldz) {
   const int64_t e8 = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * 8;   // 8 elements
   const int64_t slot = e8 / zw;
   const int col = static_cast<int>(e8 % zw);
   if (slot >= seg[NA]) return;
+  // the slot's adapter: the smallest g with seg[g] > slot
+  int glo = 1, ghi = NA;
+  while (glo < ghi) {
+    const int mid = (glo + ghi) >> 1;
+    if (seg[mid] > slot) ghi = mid;
+    else glo = mid + 1;
+  }
+  if (!in_window(rw, ranks[glo])) return;
   // all partial loads in flight at once (KS <= 16), summed in ks order
   f32x4 a[16], b[16];
 #pragma unroll
@@ -464,6 +501,8 @@ struct ExpandParams {
   int wt;                 // workgroups that fill the GPU once
   const int32_t* seg;
   const int32_t* perm;
+  RankWindow rw;          // adapters of this launch's rank class
+  int flat;               // flat item layout, one sub-tile per item (work_item)
 };
 
 // Shrink values of the tile for slices s_lo..s_hi (the ones the workgroup's
@@ -547,8 +586,13 @@ __host__ __device__ inline int expand_groups(int tiles, int n_sub, int wt) {
 #endif
 constexpr bool kExpandBalanced = GS_EXPAND_BALANCED;
 
-template <bool BF16, int NBW, int PRE>
-__global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
+// One work item of expand_kernel: tile tr, sub-tiles [sub0, sub0 + nsub).
+// PIPE: ranks above PRE k-groups load lora_B chunk kc + 1 before chunk kc is
+// multiplied (the looping form for large ranks); otherwise each later chunk
+// is loaded where it is used, which keeps the one-item forms' registers.
+template <bool BF16, int NBW, int PRE, bool PIPE>
+__device__ __forceinline__ void expand_item(const ExpandParams& p, const TileRef& tr, int sub0, int nsub,
+                                            float (&dtile)[kTM][4 * NBW * 32 + kOutPad], char* zs) {
   constexpr int NT = 4 * NBW * 32;           // columns per sub-tile
   // read-modify-write mapping: each lane owns one 16-byte piece per row it
   // touches, consecutive lanes consecutive pieces, so every wave access
@@ -564,23 +608,8 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
   // 7 000 -> 6 544 us).  The 128-column form (ranks above 32) measured
   // slower with it (multiswitch down expand 16.3 -> 18.8 us).
   constexpr bool YNT = NBW == 2;
-  __shared__ float dtile[kTM][NT + kOutPad];
-  extern __shared__ __align__(16) char zs[];   // [32][S*max_rank + 8] element type
 
-  const int n_sub = (p.out_total + NT - 1) / NT;
-  int sub = 0, groups = 1;
-  const TileRef tr = locate_tile_by<kTM, kExpandBalanced>(p.seg, p.ranks, p.b_off, p.NA, static_cast<int>(blockIdx.x),
-                                         [&](int total) {
-                                           groups = expand_groups(total, n_sub, p.wt);
-                                           return groups;
-                                         }, sub);
-  if (tr.g == 0) return;
   const int r = tr.rank;
-  // group sub of `groups` covers sub-tiles [sub*n_sub/groups, (sub+1)*n_sub/groups)
-  const int sub0 = (sub * n_sub) / groups;
-  const int nsub = ((sub + 1) * n_sub) / groups - sub0;
-  if (nsub <= 0) return;
-
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int l = tid & 63;
@@ -650,22 +679,8 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
       while (s + 1 < p.si.S && n0 >= p.si.bounds[s + 1]) ++s;
       const char* zrow_s = zs + (static_cast<int64_t>(i) * zs_ld + s * r) * Elt<BF16>::kSize;
       acc[q] = f32x16{};
-      for (int kc = 0; kc < nchunk; ++kc) {
-        u32x4 bx[PRE];
-        if (kc == 0) {
-#pragma unroll
-          for (int st = 0; st < PRE; ++st) bx[st] = bcur[q][st];
-        } else {
-          // ranks above PRE k-groups: the later groups are loaded here
-          const int n = min(n0 + i, p.out_total - 1);
-          const char* br = static_cast<const char*>(p.b_pack) + (tr.off + static_cast<int64_t>(n) * r) * Elt<BF16>::kSize;
-#pragma unroll
-          for (int st = 0; st < PRE; ++st) {
-            const int k0 = (kc * PRE + st) * KSTEP + KHALF * h;
-            const bool kin = k0 < r;
-            bx[st] = sel16(kin, ld16(br + (kin ? k0 : 0) * Elt<BF16>::kSize));
-          }
-        }
+      // k-groups [kc*PRE, kc*PRE + PRE) of the rank against the staged shrink values
+      auto mma = [&](int kc, const u32x4 (&bx)[PRE]) {
 #pragma unroll
         for (int st = 0; st < PRE; ++st) {
           const int k0 = (kc * PRE + st) * KSTEP + KHALF * h;
@@ -681,6 +696,66 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
             acc[q] = mfma32_f32(zf.z, bf.z, acc[q]);
             acc[q] = mfma32_f32(zf.w, bf.w, acc[q]);
           }
+        }
+      };
+      if constexpr (!PIPE) {
+        for (int kc = 0; kc < nchunk; ++kc) {
+          u32x4 bx[PRE];
+          if (kc == 0) {
+#pragma unroll
+            for (int st = 0; st < PRE; ++st) bx[st] = bcur[q][st];
+          } else {
+            // ranks above PRE k-groups: the later groups are loaded here
+            const int n = min(n0 + i, p.out_total - 1);
+            const char* br =
+                static_cast<const char*>(p.b_pack) + (tr.off + static_cast<int64_t>(n) * r) * Elt<BF16>::kSize;
+#pragma unroll
+            for (int st = 0; st < PRE; ++st) {
+              const int k0 = (kc * PRE + st) * KSTEP + KHALF * h;
+              const bool kin = k0 < r;
+              bx[st] = sel16(kin, ld16(br + (kin ? k0 : 0) * Elt<BF16>::kSize));
+            }
+          }
+#pragma unroll
+          for (int st = 0; st < PRE; ++st) {
+            const int k0 = (kc * PRE + st) * KSTEP + KHALF * h;
+            const bool kin = k0 < r;
+            const u32x4 za = sel16(kin, *reinterpret_cast<const u32x4*>(zrow_s + (kin ? k0 : 0) * Elt<BF16>::kSize));
+            if constexpr (BF16) {
+              acc[q] = mfma32_bf16(za, bx[st], acc[q]);
+            } else {
+              const f32x4 zf = __builtin_bit_cast(f32x4, za);
+              const f32x4 bf = __builtin_bit_cast(f32x4, bx[st]);
+              acc[q] = mfma32_f32(zf.x, bf.x, acc[q]);
+              acc[q] = mfma32_f32(zf.y, bf.y, acc[q]);
+              acc[q] = mfma32_f32(zf.z, bf.z, acc[q]);
+              acc[q] = mfma32_f32(zf.w, bf.w, acc[q]);
+            }
+          }
+        }
+      } else if (nchunk == 1) {
+        mma(0, bcur[q]);
+      } else {
+        // ranks above PRE k-groups: chunk kc + 1 of lora_B is loaded before
+        // chunk kc is multiplied, so two chunks are in flight (the last
+        // iteration re-reads its own chunk: no branch around the loads)
+        const int n = min(n0 + i, p.out_total - 1);
+        const char* br = static_cast<const char*>(p.b_pack) + (tr.off + static_cast<int64_t>(n) * r) * Elt<BF16>::kSize;
+        u32x4 bx[PRE];
+#pragma unroll
+        for (int st = 0; st < PRE; ++st) bx[st] = bcur[q][st];
+        for (int kc = 0; kc < nchunk; ++kc) {
+          const int kn = min(kc + 1, nchunk - 1);
+          u32x4 bnx[PRE];
+#pragma unroll
+          for (int st = 0; st < PRE; ++st) {
+            const int k0 = (kn * PRE + st) * KSTEP + KHALF * h;
+            const bool kin = k0 < r;
+            bnx[st] = sel16(kin, ld16(br + (kin ? k0 : 0) * Elt<BF16>::kSize));
+          }
+          mma(kc, bx);
+#pragma unroll
+          for (int st = 0; st < PRE; ++st) bx[st] = bnx[st];
         }
       }
     }
@@ -716,12 +791,60 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(ExpandParams p) {
   compute(sub0 + nsub - 1, bc, yc);
 }
 
+// LOOP = false: one item per workgroup (the grid covers the items).  LOOP =
+// true (a rank class expected to hold few tiles, laid out flat with one
+// sub-tile per item, grid capped at one round): a workgroup takes items
+// blockIdx.x, + gridDim.x, ... while they lie in the batch's item range.  A
+// separate instantiation, so the one-item form keeps its registers.
+// The narrow bf16 forms up to rank 64 hold 4 workgroups per CU (<= 128
+// registers per lane; the rank-64 multiswitch projection measured faster at
+// 4 than at 3).
+template <bool BF16, int NBW, int PRE, bool LOOP>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BF16 && NBW == 1 && PRE <= 4 && !LOOP ? 4 : 1)))
+void expand_kernel(ExpandParams p) {
+  constexpr int NT = 4 * NBW * 32;
+  __shared__ float dtile[kTM][NT + kOutPad];
+  extern __shared__ __align__(16) char zs[];   // [32][S*max_rank + 8] element type
+  const int n_sub = (p.out_total + NT - 1) / NT;
+  const bool flat = LOOP;                      // the looping form is the flat one
+  int lin = static_cast<int>(blockIdx.x);
+  int sub = 0, groups = 1, total = 0;
+  TileRef tr = locate_tile_by<kTM, kExpandBalanced>(p.seg, p.ranks, p.b_off, p.NA, p.rw, lin, flat,
+                                                    [&](int tot) {
+                                                      groups = flat ? n_sub : expand_groups(tot, n_sub, p.wt);
+                                                      return groups;
+                                                    }, sub, total);
+  if constexpr (!LOOP) {
+    if (tr.g == 0) return;
+    // group sub of `groups` covers sub-tiles [sub*n_sub/groups, (sub+1)*n_sub/groups)
+    const int sub0 = (sub * n_sub) / groups;
+    const int nsub = ((sub + 1) * n_sub) / groups - sub0;
+    if (nsub > 0) expand_item<BF16, NBW, PRE, false>(p, tr, sub0, nsub, dtile, zs);
+    return;
+  }
+  const int items = work_items(total, groups, flat);
+  for (;;) {
+    if (tr.g != 0) {
+      const int sub0 = (sub * n_sub) / groups;
+      const int nsub = ((sub + 1) * n_sub) / groups - sub0;
+      if (nsub > 0) expand_item<BF16, NBW, PRE, true>(p, tr, sub0, nsub, dtile, zs);
+    }
+    lin += static_cast<int>(gridDim.x);
+    if (lin >= items) break;
+    lds_barrier();                         // every wave is done with zs and dtile before the next item
+    tr = tile_at<kTM, kExpandBalanced>(p.seg, p.ranks, p.b_off, p.NA, p.rw, lin, flat, total, groups, sub);
+  }
+}
+
 // ----------------------------------------------------------------------------
 // Host-side planning (shared by the workspace query and the launches).
 // ----------------------------------------------------------------------------
 struct ShrinkPlan {
   int max_tiles, n_chunks, KS, KC, zw, NB;
   bool dma;               // shrink_dma_kernel (bf16, H % 64 == 0) instead of shrink_kernel
+  bool flat;              // flat item layout (work_item)
+  bool loop;              // the ring kernel's looping form (a capped grid)
+  int64_t grid;           // workgroups launched
   int64_t part_bytes;
 };
 
@@ -732,13 +855,27 @@ struct ShrinkPlan {
 #define GS_SHRINK_DMA_WGS_PER_4CU 8
 #endif
 
-static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, bool bf16) {
+// est_tokens: the tokens the launch's rank class is expected to hold (the
+// k-split is sized for them); the items cover every tile the class can have
+// (all T tokens over its NA adapters).  large: the class of ranks above
+// GS_RANK_CLASS_SPLIT.
+static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, bool bf16, int64_t est_tokens,
+                              bool large = false) {
   ShrinkPlan pl{};
   pl.dma = GS_SHRINK_DMA && bf16 && H % kDmaBK == 0;
   pl.max_tiles = static_cast<int>((T + kTMS - 1) / kTMS + (NA < T ? NA : T));
+  const int64_t est_tiles = (est_tokens + kTMS - 1) / kTMS + (NA < est_tokens ? NA : est_tokens);
+  // the ring kernel holds two workgroups per CU: aim for one round of them
+  const int64_t target = pl.dma ? int64_t(GS_SHRINK_DMA_WGS_PER_4CU) * device_cus() / 4 : kShrinkTargetWgs;
   pl.zw = S * max_rank;
   const int nblk = (pl.zw + 31) / 32;         // 32-column blocks of the widest adapter
   pl.NB = nblk >= 4 ? 4 : nblk;
+  // A large-rank class expected to hold too few tiles to fill the GPU with
+  // 128-column chunks takes 32-column chunks: its parallelism then comes from
+  // its many columns instead of a deep k-split, and the expand adds fewer
+  // partial sums.  Few tiles are laid out flat, so they spread over the XCDs.
+  if (large && pl.dma && est_tiles * ((pl.zw + 127) / 128) < target) pl.NB = 1;
+  pl.flat = large && pl.dma && est_tiles < 8;
   pl.n_chunks = (pl.zw + 32 * pl.NB - 1) / (32 * pl.NB);
   const int unit = bf16 ? 256 : 128;          // k per batch of the shrink kernel
   const int units = (H + unit - 1) / unit;
@@ -748,9 +885,7 @@ static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, boo
   // least 3 batches, so its start (tile lookup, token rows, first batch) is
   // spread over enough streaming; measured on the prefill and decoder-step
   // shapes
-  const int64_t wgs = static_cast<int64_t>(pl.max_tiles) * pl.n_chunks;
-  // the ring kernel holds two workgroups per CU: aim for one round of them
-  const int64_t target = pl.dma ? int64_t(GS_SHRINK_DMA_WGS_PER_4CU) * device_cus() / 4 : kShrinkTargetWgs;
+  const int64_t wgs = est_tiles * pl.n_chunks;
   int ks = static_cast<int>((target + wgs / 2) / (wgs > 0 ? wgs : 1));
   if (ks < 1) ks = 1;
   if (ks > 16) ks = 16;
@@ -761,6 +896,16 @@ static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, boo
     pl.KS = ks;
     pl.KC = 0;
     pl.part_bytes = pl.KS > 1 ? static_cast<int64_t>(pl.KS) * T * pl.zw * 4 : 0;
+    const int64_t nsub = static_cast<int64_t>(pl.n_chunks) * pl.KS;
+    const auto items = [&](int64_t tiles) { return (pl.flat ? tiles : 8 * ((tiles + 7) / 8)) * nsub; };
+    pl.grid = items(pl.max_tiles);
+    // a large-rank class is expected to hold far fewer tiles than it could:
+    // its grid is capped near the expected items and the workgroups loop
+    // (workgroups with no item would each hold a ring of LDS through a lookup)
+    if (large) {
+      pl.loop = true;
+      pl.grid = std::min(pl.grid, (std::max(target, std::min(items(est_tiles), 2 * target)) + 7) / 8 * 8);
+    }
     return pl;
   }
   int per = (units + ks - 1) / ks;
@@ -769,7 +914,69 @@ static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, boo
   pl.KS = (H + pl.KC - 1) / pl.KC;
   if (pl.KS < 1) pl.KS = 1;
   pl.part_bytes = pl.KS > 1 ? static_cast<int64_t>(pl.KS) * T * pl.zw * 4 : 0;
+  pl.grid = 8 * ((static_cast<int64_t>(pl.max_tiles) + 7) / 8) * pl.n_chunks * pl.KS;
   return pl;
+}
+
+// ----------------------------------------------------------------------------
+// Rank classes.  A module whose adapters' ranks differ widely (one rank-512
+// adapter among rank-32 ones) runs its shrink and expand once per class, each
+// planned for the class's own largest rank, so that the column tiles, k-split,
+// LDS and registers a large adapter needs never apply to the small adapters'
+// tokens: a large adapter costs large-rank work only for the tokens that use
+// it.  The classes are ranks <= 64 (the expand's register-resident forms) and
+// ranks above.  Without a host rank table a module is one class up to
+// max_rank, as before.
+// ----------------------------------------------------------------------------
+constexpr int kRankClassSplit = GS_RANK_CLASS_SPLIT;
+
+struct RankClass {
+  RankWindow rw;
+  int max_rank;         // the class's largest rank
+  int adapters;         // its adapters (the grid's bound on part-filled tiles)
+  int64_t est_tokens;   // the tokens it is expected to hold: ids spread evenly over the applicable adapters
+};
+
+// Fills cls[0..n) and sets n (0: no adapter is applicable, nothing to launch).
+static int rank_classes(const char* who, const int32_t* ranks_host, int NA, int max_rank, int64_t T,
+                        RankClass (&cls)[2], int& n) {
+  n = 0;
+  if (ranks_host == nullptr) {
+    cls[n++] = RankClass{{1, max_rank}, max_rank, NA, T};
+    return GS_OK;
+  }
+  RankClass c[2] = {RankClass{{1, kRankClassSplit}, 0, 0, 0}, RankClass{{kRankClassSplit + 1, GS_MAX_RANK}, 0, 0, 0}};
+  int applicable = 0;
+  for (int g = 1; g <= NA; ++g) {
+    const int r = ranks_host[g];
+    GS_CHECK_ARG(r >= 0 && r <= max_rank && r % 8 == 0, "%s: ranks_host[%d]=%d must be a multiple of 8 in [0, max_rank=%d]",
+                 who, g, r, max_rank);
+    if (r == 0) continue;
+    RankClass& k = c[r <= kRankClassSplit ? 0 : 1];
+    k.max_rank = r > k.max_rank ? r : k.max_rank;
+    ++k.adapters;
+    ++applicable;
+  }
+  for (RankClass& k : c) {
+    if (k.adapters == 0) continue;
+    k.est_tokens = (T * k.adapters + applicable - 1) / applicable;
+    cls[n++] = k;
+  }
+  return GS_OK;
+}
+
+static bool large_class(const RankClass& k) { return k.rw.lo > kRankClassSplit; }
+
+static ShrinkPlan plan_class(int64_t T, int H, int S, const RankClass& k, bool bf16) {
+  return plan_shrink(T, H, S, k.adapters, k.max_rank, bf16, k.est_tokens, large_class(k));
+}
+
+// The expand lays a large-rank class's tiles out flat, one sub-tile per item,
+// when it is expected to hold few of them (the grid is then capped at one
+// round of workgroups, which loop).
+static bool expand_flat(const RankClass& k) {
+  const int64_t est_tiles = (k.est_tokens + kTM - 1) / kTM + std::min<int64_t>(k.adapters, k.est_tokens);
+  return large_class(k) && est_tiles < 16;
 }
 
 }  // namespace gs
@@ -806,8 +1013,10 @@ int check_shrink(int32_t dtype, const void* x, int64_t ldx, int32_t hidden, cons
 ShrinkParams make_shrink_params(const ShrinkPlan& pl, const void* x, int64_t ldx, int32_t hidden, const void* a_pack,
                                 const int64_t* a_off, const int32_t* ranks, int32_t S, int32_t NA,
                                 const int32_t* seg, const int32_t* perm, void* z, int64_t ldz, void* workspace,
-                                int64_t T) {
+                                int64_t T, RankWindow rw) {
   ShrinkParams p{};
+  p.rw = rw;
+  p.flat = pl.flat ? 1 : 0;
   p.x = x;
   p.ldx = ldx;
   p.H = hidden;
@@ -840,12 +1049,19 @@ int check_workspace(const ShrinkPlan& pl, const void* workspace, int64_t workspa
 
 template <bool BF16>
 void launch_shrink_t(const ShrinkPlan& pl, const ShrinkParams& p, hipStream_t st) {
-  dim3 grid(8 * ((pl.max_tiles + 7) / 8) * pl.n_chunks * pl.KS);
+  dim3 grid(static_cast<unsigned>(pl.grid));
   if (BF16 && pl.dma) {
-    if (pl.NB == 4) hipLaunchKernelGGL(shrink_dma_kernel<4>, grid, dim3(kThreads), 0, st, p);
-    else if (pl.NB == 3) hipLaunchKernelGGL(shrink_dma_kernel<3>, grid, dim3(kThreads), 0, st, p);
-    else if (pl.NB == 2) hipLaunchKernelGGL(shrink_dma_kernel<2>, grid, dim3(kThreads), 0, st, p);
-    else hipLaunchKernelGGL(shrink_dma_kernel<1>, grid, dim3(kThreads), 0, st, p);
+    if (pl.loop) {
+      if (pl.NB == 4) hipLaunchKernelGGL((shrink_dma_kernel<4, true>), grid, dim3(kThreads), 0, st, p);
+      else if (pl.NB == 3) hipLaunchKernelGGL((shrink_dma_kernel<3, true>), grid, dim3(kThreads), 0, st, p);
+      else if (pl.NB == 2) hipLaunchKernelGGL((shrink_dma_kernel<2, true>), grid, dim3(kThreads), 0, st, p);
+      else hipLaunchKernelGGL((shrink_dma_kernel<1, true>), grid, dim3(kThreads), 0, st, p);
+      return;
+    }
+    if (pl.NB == 4) hipLaunchKernelGGL((shrink_dma_kernel<4, false>), grid, dim3(kThreads), 0, st, p);
+    else if (pl.NB == 3) hipLaunchKernelGGL((shrink_dma_kernel<3, false>), grid, dim3(kThreads), 0, st, p);
+    else if (pl.NB == 2) hipLaunchKernelGGL((shrink_dma_kernel<2, false>), grid, dim3(kThreads), 0, st, p);
+    else hipLaunchKernelGGL((shrink_dma_kernel<1, false>), grid, dim3(kThreads), 0, st, p);
     return;
   }
   if (pl.NB == 4) hipLaunchKernelGGL((shrink_kernel<BF16, 4>), grid, dim3(kThreads), 0, st, p);
@@ -892,12 +1108,13 @@ int prepare_expand(ExpandParams& p, const char* who, int32_t dtype, void* y, int
 
 template <bool BF16, int NBW, int PRE>
 void launch_expand_t(int max_tiles, size_t lds, ExpandParams p, hipStream_t st) {
-  auto kern = expand_kernel<BF16, NBW, PRE>;
+  auto kern = p.flat ? expand_kernel<BF16, NBW, PRE, true> : expand_kernel<BF16, NBW, PRE, false>;
   if (lds > 64 * 1024) (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   // workgroups resident per CU for this LDS size, queried once per size and
-  // kept as one word (lds << 16 | count) so concurrent callers read a
-  // consistent pair
-  static std::atomic<uint64_t> occ{0};
+  // kernel form and kept as one word (lds << 16 | count) so concurrent
+  // callers read a consistent pair
+  static std::atomic<uint64_t> occ_of[2];
+  std::atomic<uint64_t>& occ = occ_of[p.flat ? 1 : 0];
   uint64_t o = occ.load(std::memory_order_relaxed);
   if (o == 0 || (o >> 16) != lds) {
     int n = 0;
@@ -907,11 +1124,13 @@ void launch_expand_t(int max_tiles, size_t lds, ExpandParams p, hipStream_t st) 
   }
   p.wt = static_cast<int>(o & 0xffff) * device_cus();
   // the items never exceed wt (or one per tile slot when the tiles alone
-  // exceed it) nor one per (tile slot, sub-tile)
+  // exceed it) nor one per (tile slot, sub-tile); a flat launch is one round
+  // of workgroups that loop over its (tile, sub-tile) items
   const int t8 = 8 * ((max_tiles + 7) / 8);
   constexpr int NT = 4 * NBW * 32;
   const int64_t n_sub = (p.out_total + NT - 1) / NT;
-  const int64_t items = std::min<int64_t>(std::max(p.wt, t8), static_cast<int64_t>(t8) * n_sub);
+  const int64_t items = p.flat ? std::min<int64_t>(p.wt, static_cast<int64_t>(max_tiles) * n_sub)
+                               : std::min<int64_t>(std::max(p.wt, t8), static_cast<int64_t>(t8) * n_sub);
   const int grid = static_cast<int>((items + 7) / 8 * 8);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, st, p);
 }
@@ -925,8 +1144,9 @@ void launch_expand_pre(int max_tiles, size_t lds, const ExpandParams& p, hipStre
   else launch_expand_t<BF16, NBW, 8>(max_tiles, lds, p, st);
 }
 
-void launch_expand(bool bf16, int64_t T, ExpandParams p, hipStream_t st) {
-  const int max_tiles = max_tiles_for(T, p.NA);
+// adapters: the launch's rank class (bounds its part-filled tiles)
+void launch_expand(bool bf16, int64_t T, int adapters, ExpandParams p, hipStream_t st) {
+  const int max_tiles = max_tiles_for(T, adapters);
   // wider column tiles halve the z / partial reads per output byte, but
   // their lora_B registers grow with the rank: above rank 32 (bf16; 16 fp32
   // k per group) the wide kernel drops to 2 or 1 resident waves per SIMD and
@@ -991,14 +1211,16 @@ int noalloc_scratch(const char* who, char** out) {
   return GS_OK;
 }
 
-// Shrink, then the expand reading its output (shared by gs_switched_lora and
-// gs_switched_lora_noalloc, which differ only in where z and the partials live).
+// Shrink, then the expand reading its output, once per rank class (shared by
+// gs_switched_lora and gs_switched_lora_noalloc, which differ only in where z
+// and the partials live).  The classes run one after the other on the stream,
+// so they share z and the workspace.
 int switched_lora_impl(const char* who, int32_t dtype, const void* x, int64_t ldx, void* y, int64_t ldy,
                        int64_t num_tokens, int32_t hidden, int32_t out_total, const int32_t* slice_bounds,
                        int32_t num_slices, const void* a_pack, const int64_t* a_off, const void* b_pack,
                        const int64_t* b_off, const int32_t* ranks, int32_t num_adapters, int32_t max_rank,
-                       const int32_t* seg_offsets, const int32_t* perm, void* z, void* workspace,
-                       int64_t workspace_bytes, void* stream) {
+                       const int32_t* ranks_host, const int32_t* seg_offsets, const int32_t* perm, void* z,
+                       void* workspace, int64_t workspace_bytes, void* stream) {
   int rc = check_common(who, dtype, num_tokens, num_slices, num_adapters, max_rank);
   if (rc != GS_OK) return rc;
   rc = check_shrink(dtype, x, ldx, hidden, a_pack);
@@ -1008,27 +1230,40 @@ int switched_lora_impl(const char* who, int32_t dtype, const void* x, int64_t ld
                       num_adapters, max_rank, seg_offsets, perm);
   if (rc != GS_OK) return rc;
   GS_CHECK_ARG(aligned16(z), "%s: z must be 16-byte aligned", who);
+  RankClass cls[2];
+  int ncls = 0;
+  rc = rank_classes(who, ranks_host, num_adapters, max_rank, num_tokens, cls, ncls);
+  if (rc != GS_OK) return rc;
   if (num_tokens == 0) return GS_OK;
   const bool bf16 = dtype == GS_DTYPE_BF16;
-  const ShrinkPlan pl = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, bf16);
-  rc = check_workspace(pl, workspace, workspace_bytes);
-  if (rc != GS_OK) return rc;
+  for (int c = 0; c < ncls; ++c) {
+    rc = check_workspace(plan_class(num_tokens, hidden, num_slices, cls[c], bf16), workspace, workspace_bytes);
+    if (rc != GS_OK) return rc;
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t ldz = static_cast<int64_t>(num_slices) * max_rank;
-  const ShrinkParams sp = make_shrink_params(pl, x, ldx, hidden, a_pack, a_off, ranks, num_slices, num_adapters,
-                                             seg_offsets, perm, z, ldz, workspace, num_tokens);
-  launch_shrink(bf16, pl, sp, st);
-  GS_CHECK_LAUNCH(who);
-  ep.z = z;
-  ep.ldz = ldz;
-  ep.z_by_token = 0;
-  ep.z_off = nullptr;
-  ep.part = sp.part;
-  ep.part_stride = sp.part_stride;
-  ep.zw = sp.zw;
-  ep.nparts = pl.KS > 1 ? pl.KS : 0;
-  launch_expand(bf16, num_tokens, ep, st);
-  GS_CHECK_LAUNCH(who);
+  for (int c = 0; c < ncls; ++c) {
+    const RankClass& k = cls[c];
+    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, k, bf16);
+    const int64_t ldz = static_cast<int64_t>(num_slices) * k.max_rank;
+    const ShrinkParams sp = make_shrink_params(pl, x, ldx, hidden, a_pack, a_off, ranks, num_slices, num_adapters,
+                                               seg_offsets, perm, z, ldz, workspace, num_tokens, k.rw);
+    launch_shrink(bf16, pl, sp, st);
+    GS_CHECK_LAUNCH(who);
+    ExpandParams e = ep;
+    e.max_rank = k.max_rank;
+    e.rw = k.rw;
+    e.flat = expand_flat(k) ? 1 : 0;
+    e.z = z;
+    e.ldz = ldz;
+    e.z_by_token = 0;
+    e.z_off = nullptr;
+    e.part = sp.part;
+    e.part_stride = sp.part_stride;
+    e.zw = sp.zw;
+    e.nparts = pl.KS > 1 ? pl.KS : 0;
+    launch_expand(bf16, num_tokens, k.adapters, e, st);
+    GS_CHECK_LAUNCH(who);
+  }
   return GS_OK;
 }
 
@@ -1037,18 +1272,39 @@ int switched_lora_impl(const char* who, int32_t dtype, const void* x, int64_t ld
 extern "C" {
 
 int64_t gs_shrink_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t num_slices, int32_t num_adapters,
-                                  int32_t max_rank) {
+                                  int32_t max_rank, const int32_t* ranks_host) {
   if (num_tokens <= 0 || hidden <= 0) return 256;
-  const ShrinkPlan pl = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, true);
-  const ShrinkPlan pf = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, false);
-  int64_t b = pl.part_bytes > pf.part_bytes ? pl.part_bytes : pf.part_bytes;
-  return b < 256 ? 256 : b;
+  RankClass cls[2];
+  int ncls = 0;
+  if (rank_classes("gs_shrink_workspace_bytes", ranks_host, num_adapters, max_rank, num_tokens, cls, ncls) != GS_OK)
+    return -1;
+  int64_t b = 256;
+  for (int c = 0; c < ncls; ++c) {
+    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, cls[c], true);
+    const ShrinkPlan pf = plan_class(num_tokens, hidden, num_slices, cls[c], false);
+    b = std::max(b, std::max(pl.part_bytes, pf.part_bytes));
+  }
+  return b;
+}
+
+int32_t gs_shrink_ksplits(int32_t dtype, int64_t num_tokens, int32_t hidden, int32_t num_slices, int32_t num_adapters,
+                          int32_t max_rank, const int32_t* ranks_host, int32_t* ksplit) {
+  int rc = check_common("gs_shrink_ksplits", dtype, num_tokens, num_slices, num_adapters, max_rank);
+  if (rc != GS_OK) return -rc;
+  GS_CHECK_ARG(hidden > 0 && ksplit != nullptr, "gs_shrink_ksplits: hidden=%d / NULL ksplit", hidden);
+  RankClass cls[2];
+  int ncls = 0;
+  rc = rank_classes("gs_shrink_ksplits", ranks_host, num_adapters, max_rank, num_tokens, cls, ncls);
+  if (rc != GS_OK) return -rc;
+  for (int c = 0; c < ncls; ++c)
+    ksplit[c] = plan_class(num_tokens, hidden, num_slices, cls[c], dtype == GS_DTYPE_BF16).KS;
+  return ncls;
 }
 
 int gs_shrink(int32_t dtype, const void* x, int64_t ldx, int64_t num_tokens, int32_t hidden, const void* a_pack,
               const int64_t* a_off, const int32_t* ranks, int32_t num_slices, int32_t num_adapters,
-              int32_t max_rank, const int32_t* seg_offsets, const int32_t* perm, void* z, int64_t ldz,
-              void* workspace, int64_t workspace_bytes, void* stream) {
+              int32_t max_rank, const int32_t* ranks_host, const int32_t* seg_offsets, const int32_t* perm, void* z,
+              int64_t ldz, void* workspace, int64_t workspace_bytes, void* stream) {
   int rc = check_common("gs_shrink", dtype, num_tokens, num_slices, num_adapters, max_rank);
   if (rc != GS_OK) return rc;
   rc = check_shrink(dtype, x, ldx, hidden, a_pack);
@@ -1056,25 +1312,36 @@ int gs_shrink(int32_t dtype, const void* x, int64_t ldx, int64_t num_tokens, int
   const bool bf16 = dtype == GS_DTYPE_BF16;
   GS_CHECK_ARG(z == nullptr || (ldz >= int64_t(num_slices) * max_rank && ldz % 8 == 0 && aligned16(z)),
                "gs_shrink: ldz=%lld / z alignment", (long long)ldz);
-  if (num_tokens == 0) return GS_OK;
-  const ShrinkPlan pl = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, bf16);
-  GS_CHECK_ARG(z != nullptr || pl.KS > 1, "gs_shrink: z may be NULL only when the hidden dimension is split "
-               "(gs_shrink_workspace_bytes > 256)");
-  rc = check_workspace(pl, workspace, workspace_bytes);
+  RankClass cls[2];
+  int ncls = 0;
+  rc = rank_classes("gs_shrink", ranks_host, num_adapters, max_rank, num_tokens, cls, ncls);
   if (rc != GS_OK) return rc;
+  if (num_tokens == 0) return GS_OK;
+  for (int c = 0; c < ncls; ++c) {
+    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, cls[c], bf16);
+    GS_CHECK_ARG(z != nullptr || (pl.KS > 1 && ncls == 1),
+                 "gs_shrink: z may be NULL only when the module is one rank class whose hidden dimension is split "
+                 "(gs_shrink_ksplits)");
+    rc = check_workspace(pl, workspace, workspace_bytes);
+    if (rc != GS_OK) return rc;
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const ShrinkParams p = make_shrink_params(pl, x, ldx, hidden, a_pack, a_off, ranks, num_slices, num_adapters,
-                                            seg_offsets, perm, z, ldz, workspace, num_tokens);
-  launch_shrink(bf16, pl, p, st);
-  GS_CHECK_LAUNCH("gs_shrink");
-  if (pl.KS > 1 && z != nullptr) {
-    const int64_t n8 = (num_tokens * pl.zw) / 8;
-    const unsigned blocks = static_cast<unsigned>((n8 + kThreads - 1) / kThreads);
-    if (bf16) hipLaunchKernelGGL(reduce_parts_kernel<true>, dim3(blocks), dim3(kThreads), 0, st, p.part, p.part_stride,
-                                 pl.KS, pl.zw, seg_offsets, num_adapters, z, ldz);
-    else hipLaunchKernelGGL(reduce_parts_kernel<false>, dim3(blocks), dim3(kThreads), 0, st, p.part, p.part_stride,
-                            pl.KS, pl.zw, seg_offsets, num_adapters, z, ldz);
-    GS_CHECK_LAUNCH("gs_shrink (reduce)");
+  for (int c = 0; c < ncls; ++c) {
+    const RankClass& k = cls[c];
+    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, k, bf16);
+    const ShrinkParams p = make_shrink_params(pl, x, ldx, hidden, a_pack, a_off, ranks, num_slices, num_adapters,
+                                              seg_offsets, perm, z, ldz, workspace, num_tokens, k.rw);
+    launch_shrink(bf16, pl, p, st);
+    GS_CHECK_LAUNCH("gs_shrink");
+    if (pl.KS > 1 && z != nullptr) {
+      const int64_t n8 = (num_tokens * pl.zw) / 8;
+      const unsigned blocks = static_cast<unsigned>((n8 + kThreads - 1) / kThreads);
+      if (bf16) hipLaunchKernelGGL(reduce_parts_kernel<true>, dim3(blocks), dim3(kThreads), 0, st, p.part,
+                                   p.part_stride, pl.KS, pl.zw, seg_offsets, ranks, k.rw, num_adapters, z, ldz);
+      else hipLaunchKernelGGL(reduce_parts_kernel<false>, dim3(blocks), dim3(kThreads), 0, st, p.part, p.part_stride,
+                              pl.KS, pl.zw, seg_offsets, ranks, k.rw, num_adapters, z, ldz);
+      GS_CHECK_LAUNCH("gs_shrink (reduce)");
+    }
   }
   return GS_OK;
 }
@@ -1082,8 +1349,8 @@ int gs_shrink(int32_t dtype, const void* x, int64_t ldx, int64_t num_tokens, int
 int gs_expand_add(int32_t dtype, void* y, int64_t ldy, int64_t num_tokens, int32_t out_total,
                   const int32_t* slice_bounds, int32_t num_slices, const void* z, int64_t ldz, int32_t z_by_token,
                   const int32_t* z_off, const void* b_pack, const int64_t* b_off, const int32_t* ranks,
-                  int32_t num_adapters, int32_t max_rank, const int32_t* seg_offsets, const int32_t* perm,
-                  void* stream) {
+                  int32_t num_adapters, int32_t max_rank, const int32_t* ranks_host, const int32_t* seg_offsets,
+                  const int32_t* perm, void* stream) {
   int rc = check_common("gs_expand_add", dtype, num_tokens, num_slices, num_adapters, max_rank);
   if (rc != GS_OK) return rc;
   ExpandParams p{};
@@ -1091,52 +1358,73 @@ int gs_expand_add(int32_t dtype, void* y, int64_t ldy, int64_t num_tokens, int32
                       ranks, num_adapters, max_rank, seg_offsets, perm);
   if (rc != GS_OK) return rc;
   GS_CHECK_ARG(ldz % 8 == 0 && aligned16(z), "gs_expand_add: ldz=%lld / z alignment", (long long)ldz);
+  RankClass cls[2];
+  int ncls = 0;
+  rc = rank_classes("gs_expand_add", ranks_host, num_adapters, max_rank, num_tokens, cls, ncls);
+  if (rc != GS_OK) return rc;
   if (num_tokens == 0) return GS_OK;
   p.z = z;
   p.ldz = ldz;
   p.z_by_token = z_by_token;
   p.z_off = z_off;
   p.nparts = 0;
-  launch_expand(dtype == GS_DTYPE_BF16, num_tokens, p, static_cast<hipStream_t>(stream));
-  GS_CHECK_LAUNCH("gs_expand_add");
+  for (int c = 0; c < ncls; ++c) {
+    ExpandParams e = p;
+    e.max_rank = cls[c].max_rank;
+    e.rw = cls[c].rw;
+    e.flat = expand_flat(cls[c]) ? 1 : 0;
+    launch_expand(dtype == GS_DTYPE_BF16, num_tokens, cls[c].adapters, e, static_cast<hipStream_t>(stream));
+    GS_CHECK_LAUNCH("gs_expand_add");
+  }
   return GS_OK;
 }
 
 int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t num_tokens,
                      int32_t hidden, int32_t out_total, const int32_t* slice_bounds, int32_t num_slices,
                      const void* a_pack, const int64_t* a_off, const void* b_pack, const int64_t* b_off,
-                     const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* seg_offsets,
-                     const int32_t* perm, void* z, void* workspace, int64_t workspace_bytes, void* stream) {
+                     const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* ranks_host,
+                     const int32_t* seg_offsets, const int32_t* perm, void* z, void* workspace,
+                     int64_t workspace_bytes, void* stream) {
   return switched_lora_impl("gs_switched_lora", dtype, x, ldx, y, ldy, num_tokens, hidden, out_total, slice_bounds,
-                            num_slices, a_pack, a_off, b_pack, b_off, ranks, num_adapters, max_rank, seg_offsets, perm,
-                            z, workspace, workspace_bytes, stream);
+                            num_slices, a_pack, a_off, b_pack, b_off, ranks, num_adapters, max_rank, ranks_host,
+                            seg_offsets, perm, z, workspace, workspace_bytes, stream);
 }
 
 int gs_switched_lora_noalloc(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t num_tokens,
                              int32_t hidden, int32_t out_total, const int32_t* slice_bounds, int32_t num_slices,
                              const void* a_pack, const int64_t* a_off, const void* b_pack, const int64_t* b_off,
-                             const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* seg_offsets,
-                             const int32_t* perm, void* stream) {
+                             const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* ranks_host,
+                             const int32_t* seg_offsets, const int32_t* perm, void* stream) {
   const char* who = "gs_switched_lora_noalloc";
   int rc = check_common(who, dtype, num_tokens, num_slices, num_adapters, max_rank);
   if (rc != GS_OK) return rc;
   GS_CHECK_ARG(hidden > 0, "%s: hidden=%d", who, hidden);
-  if (num_tokens == 0) return GS_OK;
-  // scratch layout: [split-K partials][z], each 256-byte aligned
-  const ShrinkPlan pl = plan_shrink(num_tokens, hidden, num_slices, num_adapters, max_rank, dtype == GS_DTYPE_BF16);
-  const int64_t part = (pl.part_bytes + 255) & ~int64_t(255);
-  const int64_t zbytes = num_tokens * int64_t(num_slices) * max_rank * (dtype == GS_DTYPE_BF16 ? 2 : 4);
+  RankClass cls[2];
+  int ncls = 0;
+  rc = rank_classes(who, ranks_host, num_adapters, max_rank, num_tokens, cls, ncls);
+  if (rc != GS_OK) return rc;
+  if (num_tokens == 0 || ncls == 0) return GS_OK;
+  // scratch layout: [split-K partials][z], each 256-byte aligned; the rank
+  // classes run one after the other and share both
+  int64_t part_need = 0, zrank = 0;
+  for (int c = 0; c < ncls; ++c) {
+    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, cls[c], dtype == GS_DTYPE_BF16);
+    part_need = std::max(part_need, pl.part_bytes);
+    zrank = std::max<int64_t>(zrank, cls[c].max_rank);
+  }
+  const int64_t part = (part_need + 255) & ~int64_t(255);
+  const int64_t zbytes = num_tokens * int64_t(num_slices) * zrank * (dtype == GS_DTYPE_BF16 ? 2 : 4);
   if (part + zbytes > kNoallocScratchBytes) {
     set_error("%s: this shape needs %lld bytes of scratch (split-K partials %lld + z %lld); the static scratch "
               "holds %lld (use gs_switched_lora with a caller workspace)", who, (long long)(part + zbytes),
-              (long long)pl.part_bytes, (long long)zbytes, (long long)kNoallocScratchBytes);
+              (long long)part_need, (long long)zbytes, (long long)kNoallocScratchBytes);
     return GS_ERR_WORKSPACE;
   }
   char* base = nullptr;
   rc = noalloc_scratch(who, &base);
   if (rc != GS_OK) return rc;
   return switched_lora_impl(who, dtype, x, ldx, y, ldy, num_tokens, hidden, out_total, slice_bounds, num_slices,
-                            a_pack, a_off, b_pack, b_off, ranks, num_adapters, max_rank, seg_offsets, perm,
+                            a_pack, a_off, b_pack, b_off, ranks, num_adapters, max_rank, ranks_host, seg_offsets, perm,
                             base + part, base, part, stream);
 }
 

@@ -10,6 +10,13 @@ steps of ``switched`` (segments, shrink, expand-add), so forward never syncs
 once the adapters are packed: ``freeze()`` packs them once; without it the
 pack is cached and rebuilt only when a LoRA parameter changes.  The kernels
 compute no gradients, so a forward that autograd would track raises.
+
+The layers run the segment kernels (``path = "segments"``), in which no
+workgroup waits for another, so a forward either completes correctly or
+raises.  Setting a layer's ``path`` to ``"auto"`` lets decode-sized batches
+take the one-launch kernel, whose consumers wait for their producers with a
+bounded wait; a wait that runs out leaves a wrong output and sets an error
+word, which ``check()`` (or ``switched.check()``) turns into an exception.
 """
 
 from __future__ import annotations
@@ -82,8 +89,20 @@ class _SwitchedBase(nn.Module):
         if ids.numel() != x_flat.shape[0]:
             raise ValueError("adapter_indices must have one entry per token")
         segs = switched.build_segments(ids, self.num_adapters)
-        switched.switched_lora_(out_flat, x_flat.to(packed.dtype), segs, packed)
+        switched.switched_lora_(out_flat, x_flat.to(packed.dtype), segs, packed, path=self.path)
         return output
+
+    # "segments": no workgroup waits for another (a forward is correct or
+    # raises); "auto": decode-sized batches take the one-launch kernel -- call
+    # check() at a point that synchronises anyway
+    path = "segments"
+
+    def check(self) -> None:
+        """Raise ``switched.SmallPathError`` if a one-launch call on this layer's
+        device has reported a failed hand-off (its output was wrong) since the
+        last ``switched.small_reset``; synchronises.  Only ``path = "auto"``
+        can take that kernel."""
+        switched.check(self.base_layer.weight.device)
 
     @property
     def weight(self):

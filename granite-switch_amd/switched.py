@@ -21,6 +21,7 @@ library must be built.
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 import math
 import os
 from dataclasses import dataclass
@@ -123,11 +124,32 @@ def build_segments(adapter_ids: torch.Tensor, num_adapters: int, positions=None,
             num_adapters=num_adapters,
             work=torch.empty((ws + 3) // 4, dtype=torch.int32, device=dev) if ws > 0 else None,
         )
+    else:
+        _check_reused_segments(out, T, num_adapters, dev)
+        out.num_tokens = T
     work = out.work
     _lib.call("gs_build_segments", ids.data_ptr(), _lib.ptr(pos), _lib.ptr(cu), _lib.ptr(off), T, num_seqs,
               num_adapters, out.eff_ids.data_ptr(), out.seg_offsets.data_ptr(), out.perm.data_ptr(),
               _lib.ptr(work), 0 if work is None else work.numel() * 4, _lib.stream_ptr(dev))
     return out
+
+
+def _check_reused_segments(out: Segments, T: int, num_adapters: int, dev: torch.device) -> None:
+    """``out`` is written in place by the builder: its buffers must hold this
+    batch (T tokens, num_adapters adapters) before anything is launched."""
+    bufs = (("eff_ids", out.eff_ids, T), ("perm", out.perm, max(T, 1)),
+            ("seg_offsets", out.seg_offsets, num_adapters + 1))
+    if out.num_adapters != num_adapters or out.seg_offsets.numel() != num_adapters + 1:
+        raise ValueError(f"build_segments(out=...): the segments were allocated for {out.num_adapters} adapters, "
+                         f"this call has {num_adapters}")
+    for name, t, need in bufs:
+        if t.dtype != torch.int32 or t.device != dev or not t.is_contiguous():
+            raise ValueError(f"build_segments(out=...): {name} must be a contiguous int32 tensor on {dev}")
+        if t.numel() < need:
+            raise ValueError(f"build_segments(out=...): {name} holds {t.numel()} entries, this batch of {T} tokens "
+                             f"needs {need}")
+    if out.work is not None and (out.work.dtype != torch.int32 or out.work.device != dev):
+        raise ValueError(f"build_segments(out=...): work must be an int32 tensor on {dev}")
 
 
 def route_latest_wins(input_ids: torch.Tensor, control_tokens, id_offset: int = 1, cu_seqlens=None,
@@ -205,6 +227,22 @@ class PackedAdapters:
     @property
     def dtype(self) -> torch.dtype:
         return self.a_pack.dtype
+
+    def restricted(self, lo: int, hi: int) -> "PackedAdapters | None":
+        """The same pack limited to the adapters whose rank lies in [lo, hi]:
+        the others get rank 0 in the host tables, which the kernels skip (the
+        device tensors are shared).  None when no adapter's rank is in range."""
+        rk = [int(r) if lo <= int(r) <= hi else 0 for r in self.ranks_host]
+        if not any(rk):
+            return None
+        return dataclasses.replace(self, ranks_host=rk, max_rank=max(rk))
+
+    def rank_split(self) -> tuple:
+        """(adapters of rank <= 64, adapters of larger rank) as restricted packs
+        (either may be None).  The one-launch decode kernel takes the first;
+        the segment kernels plan and launch each class for its own ranks."""
+        cut = _lib.GS_RANK_CLASS_SPLIT
+        return self.restricted(1, cut), self.restricted(cut + 1, _lib.GS_MAX_RANK)
 
     @staticmethod
     def from_slices(lora_A_slices, lora_B_slices, adapter_ranks=None, applicable=None) -> "PackedAdapters":
@@ -320,15 +358,28 @@ def _workspace(device: torch.device, need: int) -> torch.Tensor:
 
 
 def shrink_workspace(num_tokens: int, hidden: int, num_slices: int, num_adapters: int, max_rank: int,
-                     device: torch.device) -> torch.Tensor:
+                     device: torch.device, ranks_host=None) -> torch.Tensor:
     """A workspace big enough for the split-K partials of one shrink of this shape.
 
     One buffer per device is reused by every call (stream order keeps calls on
     one stream apart); calls on different streams that may overlap in time
     must not share it.
     """
-    need = int(_lib.load().gs_shrink_workspace_bytes(num_tokens, hidden, num_slices, num_adapters, max_rank))
+    need = int(_lib.load().gs_shrink_workspace_bytes(num_tokens, hidden, num_slices, num_adapters, max_rank,
+                                                     None if ranks_host is None else _i32_array(ranks_host)))
+    if need < 0:
+        raise _lib.GraniteSwitchError("gs_shrink_workspace_bytes", _lib.GS_ERR_INVALID, _lib.last_error())
     return _workspace(device, need)
+
+
+def shrink_ksplits(packed: "PackedAdapters", num_tokens: int) -> list:
+    """The hidden-dimension split of each rank class of ``packed`` at this batch size."""
+    out = (ctypes.c_int32 * 2)()
+    n = int(_lib.load().gs_shrink_ksplits(_DTYPES[packed.dtype], int(num_tokens), packed.hidden, packed.num_slices,
+                                          packed.num_adapters, packed.max_rank, _i32_array(packed.ranks_host), out))
+    if n < 0:
+        raise _lib.GraniteSwitchError("gs_shrink_ksplits", -n, _lib.last_error())
+    return [int(out[i]) for i in range(n)]
 
 
 def small_workspace_bytes(packed: "PackedAdapters", num_tokens: int) -> int:
@@ -378,7 +429,8 @@ def _small_plan(packed: "PackedAdapters", num_tokens: int, num_seqs: int | None,
     if packed.a_off_host is None or packed.b_off_host is None or not packed.ranks_host:
         return (False, 1)                             # no host tables: the small kernel cannot run
     key = (_dev_key(packed.a_pack.device), packed.dtype, packed.hidden, packed.num_slices, packed.num_adapters,
-           packed.max_rank, packed.out_total, tuple(packed.slice_bounds), T, num_seqs, largest_group)
+           packed.max_rank, tuple(packed.ranks_host), packed.out_total, tuple(packed.slice_bounds), T, num_seqs,
+           largest_group)
     plan = _small_plans.get(key)
     if plan is not None:
         return plan
@@ -611,9 +663,10 @@ def shrink(x: torch.Tensor, segments: Segments, packed: PackedAdapters, z: torch
            partials_only: bool = False) -> torch.Tensor | None:
     """z[slot, s*r_g + j] = x[perm[slot]] . A_{g,s}[j] (compact, slot-major).
 
-    ``partials_only``: when the hidden dimension is split, write only the fp32
-    split-K partials to the per-device workspace (the shrink half of
-    ``switched_lora_``) and return None; raises if this shape is not split.
+    ``partials_only``: when the module is one rank class whose hidden
+    dimension is split (``shrink_ksplits``), write only the fp32 split-K
+    partials to the per-device workspace (the shrink half of
+    ``switched_lora_``) and return None; raises otherwise.
     """
     _require_cuda(x)
     x2 = x.reshape(-1, x.shape[-1])
@@ -632,11 +685,12 @@ def shrink(x: torch.Tensor, segments: Segments, packed: PackedAdapters, z: torch
         z = torch.empty(max(T, 1), zw, dtype=x2.dtype, device=x2.device)
     elif z.dtype != x2.dtype or z.stride(-1) != 1 or z.dim() != 2 or z.shape[0] < T or z.shape[1] < zw:
         raise ValueError("z must be a [T, >= S*max_rank] buffer of x's dtype with unit column stride")
-    ws = shrink_workspace(T, H, packed.num_slices, packed.num_adapters, packed.max_rank, x2.device)
+    ws = shrink_workspace(T, H, packed.num_slices, packed.num_adapters, packed.max_rank, x2.device, packed.ranks_host)
     _lib.call("gs_shrink", _dtype_code(x2), x2.data_ptr(), x2.stride(0), T, H, packed.a_pack.data_ptr(),
               packed.a_off.data_ptr(), packed.ranks.data_ptr(), packed.num_slices, packed.num_adapters,
-              packed.max_rank, segments.seg_offsets.data_ptr(), segments.perm.data_ptr(), _lib.ptr(z),
-              zw if z is None else z.stride(0), ws.data_ptr(), ws.numel(), _lib.stream_ptr(x2.device))
+              packed.max_rank, _i32_array(packed.ranks_host), segments.seg_offsets.data_ptr(),
+              segments.perm.data_ptr(), _lib.ptr(z), zw if z is None else z.stride(0), ws.data_ptr(), ws.numel(),
+              _lib.stream_ptr(x2.device))
     return z
 
 
@@ -658,8 +712,8 @@ def expand_add_(y: torch.Tensor, z: torch.Tensor, segments: Segments, packed: Pa
     bounds = _i32_array(packed.slice_bounds)
     _lib.call("gs_expand_add", _dtype_code(y2), y2.data_ptr(), y2.stride(0), T, O, bounds, packed.num_slices,
               z.data_ptr(), z.stride(0), 0, None, packed.b_pack.data_ptr(), packed.b_off.data_ptr(),
-              packed.ranks.data_ptr(), packed.num_adapters, packed.max_rank, segments.seg_offsets.data_ptr(),
-              segments.perm.data_ptr(), _lib.stream_ptr(y2.device))
+              packed.ranks.data_ptr(), packed.num_adapters, packed.max_rank, _i32_array(packed.ranks_host),
+              segments.seg_offsets.data_ptr(), segments.perm.data_ptr(), _lib.stream_ptr(y2.device))
     return y
 
 
@@ -696,6 +750,18 @@ def _call_small(x2, y2, packed, eff_ids=None, req=None, pos=None, cu=None, off=N
         check(x2.device)
 
 
+def path_plan(packed: PackedAdapters, num_tokens: int, num_seqs: int | None = None,
+              largest_group: int | None = None) -> str:
+    """The kernels ``path="auto"`` runs for this module and batch: "small" (the
+    one-launch kernel for every adapter), "split" (the one-launch kernel for
+    the adapters of rank <= 64, the segment kernels for the larger ones) or
+    "segments"."""
+    small_v, large_v = packed.rank_split()
+    if small_v is None or not num_tokens or not small_preferred(small_v, num_tokens, num_seqs, largest_group):
+        return "segments"
+    return "small" if large_v is None else "split"
+
+
 def switched_lora_routed_(y: torch.Tensor, x: torch.Tensor, adapter_ids: torch.Tensor, packed: PackedAdapters,
                           positions=None, cu_seqlens=None, act_offsets=None, path: str = "auto",
                           largest_group: int | None = None) -> torch.Tensor:
@@ -705,9 +771,12 @@ def switched_lora_routed_(y: torch.Tensor, x: torch.Tensor, adapter_ids: torch.T
     meaning of ``build_segments``.  ``path="auto"``: decode-sized batches
     (``small_preferred``) run in one launch that gates and groups the tokens
     itself; larger ones build segments first and run ``switched_lora_``.
-    ``"small"`` / ``"segments"`` force one of the two.  ``largest_group``
-    (optional): the most tokens any one adapter has in the batch, when the
-    caller knows it on the host; it replaces the path choice's estimate.
+    ``"small"`` / ``"segments"`` force one of the two.  The one-launch kernel
+    takes the adapters of rank <= 64; a module that also holds larger ones
+    runs those through segments built for them (``path_plan`` "split").
+    ``largest_group`` (optional): the most tokens any one adapter has in the
+    batch, when the caller knows it on the host; it replaces the path choice's
+    estimate.
     """
     if path not in ("auto", "small", "segments"):
         raise ValueError(f"unknown path {path!r}")
@@ -726,13 +795,19 @@ def switched_lora_routed_(y: torch.Tensor, x: torch.Tensor, adapter_ids: torch.T
     if off is not None and off.numel() != num_seqs:
         raise ValueError("act_offsets must have one entry per sequence")
     nseq_hint = num_seqs if cu is not None else None
-    if path == "small" or (path == "auto" and small_preferred(packed, T, nseq_hint, largest_group)):
-        if not small_eligible(packed, T, num_seqs):
+    small_v, large_v = packed.rank_split()
+    if path == "small" and small_v is None:
+        raise ValueError("the one-launch kernel takes adapters of rank <= 64; this module has none")
+    if path == "small" or (path == "auto" and path_plan(packed, T, nseq_hint, largest_group) != "segments"):
+        if not small_eligible(small_v, T, num_seqs):
             raise ValueError("this module / batch is outside the small-batch kernel's limits")
-        _call_small(x2, y2, packed, req=ids, pos=pos, cu=cu if off is not None else None, off=off,
+        _call_small(x2, y2, small_v, req=ids, pos=pos, cu=cu if off is not None else None, off=off,
                     num_seqs=num_seqs if off is not None else 1,
-                    row_split=small_row_split(packed, T, nseq_hint, largest_group))
-        return y
+                    row_split=small_row_split(small_v, T, nseq_hint, largest_group))
+        if large_v is None:
+            return y
+        segs = build_segments(ids, packed.num_adapters, pos, cu, off)
+        return switched_lora_(y, x, segs, large_v, path="segments")
     segs = build_segments(ids, packed.num_adapters, pos, cu, off)
     return switched_lora_(y, x, segs, packed, path="segments")
 
@@ -744,11 +819,14 @@ def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed:
     ``path="auto"``: decode-sized batches (``small_preferred``) take the
     one-launch small-batch kernel, which groups tokens from
     ``segments.eff_ids`` itself; larger ones the two segment kernels.
-    ``"small"`` / ``"segments"`` force one of the two.  On the segment path ``z`` is optional scratch
-    [T, S*max_rank] of y's dtype (allocated when omitted) -- when the shrink
-    is split over the hidden dimension the expand reads the fp32 partials from
-    the workspace and z is not written.  ``largest_group`` as for
-    ``switched_lora_routed_``.
+    ``"small"`` / ``"segments"`` force one of the two.  The one-launch kernel
+    takes the adapters of rank <= 64 and the segment kernels the rest
+    (``path_plan`` "split").  The segment kernels run once per rank class
+    (ranks <= 64 and above), each planned for its own largest rank.  On the
+    segment path ``z`` is optional scratch [T, S*max_rank] of y's dtype
+    (allocated when omitted) -- when the shrink is split over the hidden
+    dimension the expand reads the fp32 partials from the workspace and z is
+    not written.  ``largest_group`` as for ``switched_lora_routed_``.
     """
     if path not in ("auto", "small", "segments"):
         raise ValueError(f"unknown path {path!r}")
@@ -757,33 +835,43 @@ def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed:
     if T != segments.num_tokens:
         raise ValueError("x / y shapes do not match the segments")
     _check_segments(segments, packed)
-    if path == "small" or (path == "auto" and T and small_preferred(packed, T, None, largest_group)):
-        _call_small(x2, y2, packed, eff_ids=segments.eff_ids, row_split=small_row_split(packed, T, None, largest_group))
-        return y
+    rest = packed
+    if path != "segments" and T:
+        small_v, large_v = packed.rank_split()
+        if path == "small" and small_v is None:
+            raise ValueError("the one-launch kernel takes adapters of rank <= 64; this module has none")
+        if path == "small" or path_plan(packed, T, None, largest_group) != "segments":
+            _call_small(x2, y2, small_v, eff_ids=segments.eff_ids,
+                        row_split=small_row_split(small_v, T, None, largest_group))
+            if large_v is None:
+                return y
+            rest = large_v
     zw = packed.num_slices * packed.max_rank
     if z is None:
-        z = torch.empty(max(T, 1), zw, dtype=x2.dtype, device=x2.device)
+        z = torch.empty(max(T, 1), rest.num_slices * rest.max_rank, dtype=x2.dtype, device=x2.device)
     elif z.stride(-1) != 1 or z.shape[-1] < zw or (T and z.stride(0) != zw):
         raise ValueError("z must be a contiguous [T, S*max_rank] buffer")
-    ws = shrink_workspace(T, H, packed.num_slices, packed.num_adapters, packed.max_rank, x2.device)
+    ws = shrink_workspace(T, H, rest.num_slices, rest.num_adapters, rest.max_rank, x2.device, rest.ranks_host)
     _lib.call("gs_switched_lora", _dtype_code(x2), x2.data_ptr(), x2.stride(0), y2.data_ptr(), y2.stride(0), T, H,
-              packed.out_total, _i32_array(packed.slice_bounds), packed.num_slices, packed.a_pack.data_ptr(),
-              packed.a_off.data_ptr(), packed.b_pack.data_ptr(), packed.b_off.data_ptr(), packed.ranks.data_ptr(),
-              packed.num_adapters, packed.max_rank, segments.seg_offsets.data_ptr(), segments.perm.data_ptr(),
-              z.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(x2.device))
+              rest.out_total, _i32_array(rest.slice_bounds), rest.num_slices, rest.a_pack.data_ptr(),
+              rest.a_off.data_ptr(), rest.b_pack.data_ptr(), rest.b_off.data_ptr(), rest.ranks.data_ptr(),
+              rest.num_adapters, rest.max_rank, _i32_array(rest.ranks_host), segments.seg_offsets.data_ptr(),
+              segments.perm.data_ptr(), z.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(x2.device))
     return y
 
 
 def switched_lora_noalloc_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed: PackedAdapters) -> torch.Tensor:
     """In place: y += switched-LoRA delta of x, allocating nothing.
 
-    The segment path's two kernels with their scratch (split-K partials and
-    the shrink output) in the library's static per-GPU array
-    (``gs_switched_lora_noalloc``) -- for code that must not allocate, such as
-    a region under HIP graph capture.  No tensor is created or copied here:
-    x and y must already have unit column stride.  Shapes whose scratch would
-    exceed the array (``_lib.GS_NOALLOC_SCRATCH_BYTES``) raise.  Calls that
-    overlap in time on one GPU share the array and race.
+    The segment path's two kernels (per rank class) with their scratch
+    (split-K partials and the shrink output) in the library's static per-GPU
+    array (``gs_switched_lora_noalloc``) -- for code that must not allocate,
+    such as a region under HIP graph capture.  No tensor is created or copied
+    here: x and y must already have unit column stride.  Shapes whose scratch
+    would exceed the array (``_lib.GS_NOALLOC_SCRATCH_BYTES``) raise.  Calls
+    that overlap in time on one GPU share the array and race.  The array is
+    looked up on the first call on a device: make that call (or any call)
+    eagerly before capturing one in a graph.
     """
     _require_cuda(x, y)
     if x.stride(-1) != 1 or y.stride(-1) != 1:
@@ -801,8 +889,8 @@ def switched_lora_noalloc_(y: torch.Tensor, x: torch.Tensor, segments: Segments,
     _lib.call("gs_switched_lora_noalloc", _dtype_code(x2), x2.data_ptr(), x2.stride(0), y2.data_ptr(), y2.stride(0),
               T, packed.hidden, packed.out_total, _i32_array(packed.slice_bounds), packed.num_slices,
               packed.a_pack.data_ptr(), packed.a_off.data_ptr(), packed.b_pack.data_ptr(), packed.b_off.data_ptr(),
-              packed.ranks.data_ptr(), packed.num_adapters, packed.max_rank, segments.seg_offsets.data_ptr(),
-              segments.perm.data_ptr(), _lib.stream_ptr(x2.device))
+              packed.ranks.data_ptr(), packed.num_adapters, packed.max_rank, _i32_array(packed.ranks_host),
+              segments.seg_offsets.data_ptr(), segments.perm.data_ptr(), _lib.stream_ptr(x2.device))
     return y
 
 
@@ -891,6 +979,8 @@ __all__ = [
     "switched_lora_noalloc_",
     "small_eligible",
     "small_preferred",
+    "path_plan",
+    "shrink_ksplits",
     "small_workspace_bytes",
     "small_sync_buffer",
     "small_workspace",

@@ -272,6 +272,7 @@ class SwitchedLoRALinear(nn.Module):
         self._seg_boff = torch.tensor(seg_boff, dtype=torch.int64, device=dev)
         self._seg_zoff = torch.tensor(seg_zoff, dtype=torch.int32, device=dev)
         self._seg_max_rank = max([16] + seg_rank)
+        self._seg_ranks_host = _i32_array(seg_rank)
         self._slice_bounds = _i32_array(plan.bounds)
 
         if self.fuse_swiglu:
@@ -362,6 +363,7 @@ class SwitchedLoRALinear(nn.Module):
         _lib.call("gs_expand_add", _dtype_code(x_ext), x_ext.data_ptr(), x_ext.stride(0), M, self._N_total,
                   self._slice_bounds, self._S, x_ext.data_ptr(), x_ext.stride(0), 1, self._seg_zoff.data_ptr(),
                   self._lb_packed.data_ptr(), self._seg_boff.data_ptr(), self._seg_ranks.data_ptr(),
-                  self.num_adapters, self._seg_max_rank, segs.seg_offsets.data_ptr(), segs.perm.data_ptr(),
+                  self.num_adapters, self._seg_max_rank, self._seg_ranks_host, segs.seg_offsets.data_ptr(),
+                  segs.perm.data_ptr(),
                   _lib.stream_ptr(x_ext.device))
 

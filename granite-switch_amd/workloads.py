@@ -115,10 +115,13 @@ def _loguniform_lengths(rng, n, lo, hi, total):
     return lens
 
 
-def routing_for(config: int, seed: int = 0) -> Routing:
+def routing_for(config: int, seed: int = 0, num_adapters: int | None = None) -> Routing:
+    """Seeded routing of one workload; ``num_adapters`` widens (or narrows)
+    the range the adapter ids are drawn from (default: the workload's own)."""
     rng = np.random.default_rng(1000 + 17 * config + seed)
+    na = num_adapters
     if config == 0:
-        B, L, NA = 4, 128, 4
+        B, L, NA = 4, 128, na or 4
         lens = np.full(B, L)
         adapters = rng.integers(1, NA + 1, size=B)
         offsets = rng.integers(0, L, size=B)
@@ -127,7 +130,7 @@ def routing_for(config: int, seed: int = 0) -> Routing:
         return Routing(req.astype(np.int64), np.concatenate([[0], np.cumsum(lens)]).astype(np.int32),
                        pos.astype(np.int64), offsets.astype(np.int64))
     if config == 1:
-        T, NA = 256, 12
+        T, NA = 256, na or 12
         req = rng.integers(1, NA + 1, size=T)
         ctx_len = rng.integers(16, 2048, size=T)           # decode position of each request
         inactive = np.zeros(T, dtype=bool)
@@ -138,7 +141,7 @@ def routing_for(config: int, seed: int = 0) -> Routing:
         return Routing(req.astype(np.int64), np.arange(T + 1, dtype=np.int32), ctx_len.astype(np.int64),
                        offsets.astype(np.int64))
     if config == 2:
-        B, T, NA = 16, 8192, 12
+        B, T, NA = 16, 8192, na or 12
         lens = _loguniform_lengths(rng, B, 64, 2048, T)
         adapters = rng.integers(1, NA + 1, size=B)
         offsets = np.array([rng.integers(0, l) for l in lens])
@@ -147,7 +150,7 @@ def routing_for(config: int, seed: int = 0) -> Routing:
         return Routing(req.astype(np.int64), np.concatenate([[0], np.cumsum(lens)]).astype(np.int32),
                        pos.astype(np.int64), offsets.astype(np.int64))
     if config == 3:
-        B, L, NA = 64, 64, 48
+        B, L, NA = 64, 64, na or 48
         req = np.zeros(B * L, dtype=np.int64)
         for s in range(B):
             p = 0
@@ -159,7 +162,7 @@ def routing_for(config: int, seed: int = 0) -> Routing:
         pos = np.tile(np.arange(L), B)
         return Routing(req, np.arange(0, B * L + 1, L).astype(np.int32), pos.astype(np.int64), None)
     if config == 4:
-        NA, ND, NP, C = 24, 48, 16, 256
+        NA, ND, NP, C = na or 24, 48, 16, 256
         dec_adapters = rng.integers(1, NA + 1, size=ND)
         dec_pos = rng.integers(16, 4096, size=ND)
         dec_off = np.array([rng.integers(0, p + 64) for p in dec_pos])   # some not yet activated
@@ -210,6 +213,42 @@ def num_adapters_for(config: int) -> int:
 
 def dtype_for(config: int) -> torch.dtype:
     return torch.float32 if config == 0 else torch.bfloat16
+
+
+# Adapter populations on a workload's shapes (src/granite_switch docs/
+# SWITCH_KERNELS.md "Methodology": balanced N x rank 32; imbalanced N x rank 32
+# plus one larger adapter, N + 1 loaded, ids drawn uniformly over those
+# loaded; and the idle batch, in which no token has an adapter).
+POPULATIONS = ("balanced", "all_base", "r512")
+
+
+def population_routing(config: int, population: str = "balanced") -> Routing:
+    """Routing of ``population`` on workload ``config``'s shapes.
+
+    balanced: the workload itself; all_base: the same batch with every token on
+    the base model; r512: ids drawn over the workload's adapters plus one more
+    (the rank-512 one), with the workload's activation offsets and positions.
+    """
+    if population == "balanced":
+        return routing_for(config)
+    if population == "all_base":
+        r = routing_for(config)
+        return Routing(np.zeros_like(r.req_ids), r.cu_seqlens, r.positions, r.act_offsets)
+    if population == "r512":
+        return routing_for(config, num_adapters=num_adapters_for(config) + 1)
+    raise ValueError(f"unknown population {population!r}")
+
+
+def population_adapters(config: int, population: str = "balanced") -> int:
+    return num_adapters_for(config) + (1 if population == "r512" else 0)
+
+
+def population_specs(config: int, population: str = "balanced") -> list:
+    """Module specs of ``population``: r512 appends one adapter of rank 512 (storage rank 512)."""
+    specs = module_specs(config)
+    if population != "r512":
+        return specs
+    return [ModuleSpec(s.name, s.hidden, s.output_slices, list(s.ranks) + [512], 512) for s in specs]
 
 
 def make_workload(config: int, device="cuda", seed: int = 0, layers: int | None = None) -> Workload:

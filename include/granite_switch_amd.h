@@ -149,7 +149,16 @@ int gs_route_latest_wins(const int64_t* input_ids, const int32_t* cu_seqlens, in
  *       layout), already scaled by alpha/r.
  *   slice_bounds [S+1] int32 (host array): output column where each slice
  *       starts; every slice width must be a multiple of 32.
+ *   ranks_host [num_adapters+1] int32 (host array) or NULL: the same values
+ *       as ranks, on the host.  With it the module's adapters are split into
+ *       rank classes (ranks <= 64 and ranks above) and each class is planned
+ *       and launched for its own largest rank, so a large adapter's tile
+ *       widths, k-split, LDS and registers apply only to its own tokens (the
+ *       reference's per-adapter rank tiers, docs/SWITCH_KERNELS.md "per-adapter
+ *       rank tiers").  An entry of 0 skips that adapter.  NULL: one class of
+ *       every rank up to max_rank.
  * ---------------------------------------------------------------------- */
+#define GS_RANK_CLASS_SPLIT 64
 
 /* Workspace for gs_shrink / gs_switched_lora: fp32 split-K partial sums.
  * The hidden dimension is split over several workgroups when there are too
@@ -158,18 +167,27 @@ int gs_route_latest_wins(const int64_t* input_ids, const int32_t* cu_seqlens, in
  * No initialisation is needed.  Calls that share a workspace must not overlap
  * in time (stream order is enough). */
 int64_t gs_shrink_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t num_slices, int32_t num_adapters,
-                                  int32_t max_rank);
+                                  int32_t max_rank, const int32_t* ranks_host);
+
+/* The hidden-dimension split (k-chunks) of each rank class of a module for
+ * this batch size and dtype: writes ksplit[0..n) (n <= 2) and returns n (0
+ * when no adapter is applicable, a negated GS_* status on bad arguments).  No
+ * counterpart in the reference (its shrink is the fused GEMM); it tells a
+ * caller whether gs_shrink may write partials only (one class split >1). */
+int32_t gs_shrink_ksplits(int32_t dtype, int64_t num_tokens, int32_t hidden, int32_t num_slices,
+                          int32_t num_adapters, int32_t max_rank, const int32_t* ranks_host, int32_t* ksplit);
 
 /* z[slot, s*r_g + j] = sum_k x[perm[slot], k] * lora_A_{g,s}[j, k] for every
  * active slot (slot < seg_offsets[num_adapters]) whose adapter is applicable.
  * x [T, hidden] (ld ldx); z [T, ldz] with ldz >= S*max_rank; same dtype.
- * When the hidden dimension is split (gs_shrink_workspace_bytes > 256), z
- * may be NULL: only the fp32 partials [KS][T][S*max_rank] are written to the
- * workspace, the shrink half of gs_switched_lora. */
+ * When the module is one rank class whose hidden dimension is split
+ * (gs_shrink_ksplits), z may be NULL: only the fp32 partials
+ * [KS][T][S*max_rank] are written to the workspace, the shrink half of
+ * gs_switched_lora. */
 int gs_shrink(int32_t dtype, const void* x, int64_t ldx, int64_t num_tokens, int32_t hidden, const void* a_pack,
               const int64_t* a_off, const int32_t* ranks, int32_t num_slices, int32_t num_adapters,
-              int32_t max_rank, const int32_t* seg_offsets, const int32_t* perm, void* z, int64_t ldz,
-              void* workspace, int64_t workspace_bytes, void* stream);
+              int32_t max_rank, const int32_t* ranks_host, const int32_t* seg_offsets, const int32_t* perm, void* z,
+              int64_t ldz, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* y[perm[slot], n] = round(y + sum_k z[row, zcol + k] * B_g[n, k]) for every
  * active slot and output column n, k < r_g, where n lies in slice s,
@@ -179,18 +197,20 @@ int gs_shrink(int32_t dtype, const void* x, int64_t ldx, int64_t num_tokens, int
 int gs_expand_add(int32_t dtype, void* y, int64_t ldy, int64_t num_tokens, int32_t out_total,
                   const int32_t* slice_bounds, int32_t num_slices, const void* z, int64_t ldz, int32_t z_by_token,
                   const int32_t* z_off, const void* b_pack, const int64_t* b_off, const int32_t* ranks,
-                  int32_t num_adapters, int32_t max_rank, const int32_t* seg_offsets, const int32_t* perm,
-                  void* stream);
+                  int32_t num_adapters, int32_t max_rank, const int32_t* ranks_host, const int32_t* seg_offsets,
+                  const int32_t* perm, void* stream);
 
 /* The whole switched-LoRA delta added into y in two launches: the shrink,
  * then the expand reading the shrink's output directly (split-K partials are
  * summed while they are staged, so z is only written when the shrink is not
- * split).  z [T, S*max_rank] scratch of the same dtype. */
+ * split), once per rank class (two launches per class).  z [T, S*max_rank]
+ * scratch of the same dtype. */
 int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t num_tokens,
                      int32_t hidden, int32_t out_total, const int32_t* slice_bounds, int32_t num_slices,
                      const void* a_pack, const int64_t* a_off, const void* b_pack, const int64_t* b_off,
-                     const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* seg_offsets,
-                     const int32_t* perm, void* z, void* workspace, int64_t workspace_bytes, void* stream);
+                     const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* ranks_host,
+                     const int32_t* seg_offsets, const int32_t* perm, void* z, void* workspace,
+                     int64_t workspace_bytes, void* stream);
 
 /* The same op with its scratch (split-K partials and z) in a static device
  * array of GS_NOALLOC_SCRATCH_BYTES per GPU, so it allocates nothing: no
@@ -207,8 +227,8 @@ int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t
 int gs_switched_lora_noalloc(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t num_tokens,
                              int32_t hidden, int32_t out_total, const int32_t* slice_bounds, int32_t num_slices,
                              const void* a_pack, const int64_t* a_off, const void* b_pack, const int64_t* b_off,
-                             const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* seg_offsets,
-                             const int32_t* perm, void* stream);
+                             const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* ranks_host,
+                             const int32_t* seg_offsets, const int32_t* perm, void* stream);
 
 /* ------------------------------------------------------------------------
  * Small-batch switched-LoRA in ONE launch, no segment build (decode-sized

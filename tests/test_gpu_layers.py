@@ -432,3 +432,49 @@ def test_segment_op_surface(dev):
     assert seg.cpu().tolist() == [0, 2, 4, 4]
     assert perm.cpu().tolist()[:4] == [2, 5, 1, 3]
     _ = switched
+
+
+@pytest.mark.gpu
+def test_hf_layer_path_and_check(dev):
+    """The HF layer takes the segment kernels by default, which never wait
+    across workgroups: with the one-launch kernel's wait bound forced to 0
+    from the host its output stays right and check() passes.  With
+    path = "auto" a decode-sized batch takes the one-launch kernel, and the
+    forced give-up is reported by check()."""
+    K, NA, R = 256, 3, 16
+    torch.manual_seed(3)
+    layer = hf_layers.MergedSwitchedLoRALinear(K, (256, 128), NA, R).to(dev).to(torch.bfloat16)
+    with torch.no_grad():
+        for B in layer.lora_B_slices:
+            B.copy_(torch.randn_like(B) * 0.1)
+    layer.freeze()
+    x = torch.randn(64, K, device=dev, dtype=torch.bfloat16)
+    ids = torch.randint(0, NA + 1, (64,), device=dev)
+    assert layer.path == "segments"
+    switched.small_reset(dev)
+    prev = switched.set_small_wait_limit(0)
+    try:
+        with torch.no_grad():
+            out = layer(x, ids)
+            base = layer.base_layer(x)
+        torch.cuda.synchronize()
+        layer.check()                             # the segment kernels never wait
+        ref = olora.switched_lora_apply(_np(base), _np(x), ids.cpu().numpy(),
+                                        [_np(a) for a in layer.lora_A_slices], [_np(b) for b in layer.lora_B_slices],
+                                        (256, 128), None, "bf16")
+        _close(_np(out), ref, 2e-2, "hf layer, segment path")
+        layer.path = "auto"
+        assert switched.small_preferred(layer._packed, 64)
+        with torch.no_grad():
+            layer(x, ids)
+        torch.cuda.synchronize()
+    finally:
+        switched.set_small_wait_limit(prev)
+    with pytest.raises(switched.SmallPathError):
+        layer.check()
+    switched.small_reset(dev)
+    with torch.no_grad():
+        out_auto = layer(x, ids)
+    torch.cuda.synchronize()
+    layer.check()
+    _close(_np(out_auto), ref, 2e-2, "hf layer, one-launch path")

@@ -162,7 +162,10 @@ def test_production_adapter_sets(dev, variant, size, proj):
     x = (torch.randn(M, H, generator=g, device=dev) * 0.1).to(torch.bfloat16)
     y0 = torch.randn(M, sum(slices), generator=g, device=dev).to(torch.bfloat16)
     xn, y0n = x.float().cpu().numpy(), y0.float().cpu().numpy()
-    paths = ["auto", "segments"] + (["small"] if switched.small_eligible(pk, M) else [])
+    # "small": the one-launch kernel for the adapters of rank <= 64 (and the
+    # segment kernels for larger ones, the "split" plan)
+    small_v = pk.rank_split()[0]
+    paths = ["auto", "segments"] + (["small"] if small_v is not None and switched.small_eligible(small_v, M) else [])
     scen = HAND + ([sc_only_large] if variant in LARGE else []) + RANDOM
     if size == "30B":
         scen = [sc_many_with_base, sc_all_one, RANDOM[0]]

@@ -1,0 +1,188 @@
+"""Modules whose adapters' ranks differ widely, on the GPU (rank classes).
+
+The reference's imbalanced population -- N rank-32 adapters plus one rank-512
+adapter, ids drawn over all of them (docs/SWITCH_KERNELS.md "Methodology";
+"a rank-512 adapter costs rank-512 work only for the tokens that use it",
+"Per-adapter rank tiers") -- and other mixes.  The segment kernels run once
+per rank class (ranks <= 64 and above), each planned for its own ranks; the
+one-launch decode kernel takes the rank <= 64 class and the segment kernels
+the larger adapters.  Every path is checked against the oracle
+(|got - ref| <= 2e-2 + 2e-2 |ref| in bf16, 1e-5 in fp32) with base rows
+bit-identical.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from granite_switch_amd import switched, workloads
+from oracle import lora as olora
+from oracle import mapping as omap
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.bfloat16: 2e-2, torch.float32: 1e-5}
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _check(md, y, eff, dtype, what):
+    dt = "bf16" if dtype == torch.bfloat16 else "fp32"
+    ref = olora.switched_lora_apply(_np(md.y), _np(md.x), eff, [_np(a) for a in md.lora_A_slices],
+                                    [_np(b) for b in md.lora_B_slices], md.spec.output_slices, md.spec.ranks, dt)
+    got = _np(y).astype(np.float64)
+    err = np.abs(got - ref)
+    tol = TOL[dtype]
+    bad = err > tol + tol * np.abs(ref)
+    assert not bad.any(), f"{what}: {int(bad.sum())} out of tolerance, max abs err {err.max():.3e}"
+    base = eff == 0
+    assert np.array_equal(got[base], _np(md.y)[base]), f"{what}: base rows modified"
+    return float(err.max())
+
+
+@pytest.mark.parametrize("path", ["auto", "small", "segments"])
+def test_decode_population_with_a_rank512_adapter(dev, path):
+    """12 rank-32 adapters + 1 rank-512 on the decode QKV shape (T = 256)."""
+    r = workloads.population_routing(1, "r512")
+    NA = workloads.population_adapters(1, "r512")
+    spec = workloads.population_specs(1, "r512")[0]
+    md = workloads.make_module(spec, r.num_tokens, NA, torch.bfloat16, dev, seed=501)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, spec.ranks)
+    assert pk.max_rank == 512 and pk.rank_split()[1].ranks_host[NA] == 512
+    if path == "auto":
+        assert switched.path_plan(pk, r.num_tokens, r.num_tokens) == "split"
+    args = [torch.tensor(v, device=dev) for v in (r.req_ids, r.positions, r.cu_seqlens, r.act_offsets)]
+    eff = omap.alora_effective_ids(r.req_ids, r.positions, r.cu_seqlens, r.act_offsets)
+    assert (eff == NA).sum() > 0, "the rank-512 adapter has tokens"
+    _say(f"decode r512 population, path={path}: {int((eff > 0).sum())} adapted, {int((eff == NA).sum())} on rank 512")
+    y = md.y.clone()
+    switched.switched_lora_routed_(y, md.x, args[0], pk, args[1], args[2], args[3], path=path)
+    torch.cuda.synchronize()
+    switched.check(dev)
+    err = _check(md, y, eff, torch.bfloat16, f"routed path={path}")
+    # with prebuilt segments (the one-launch kernel reads their effective ids)
+    segs = switched.build_segments(args[0], NA, args[1], args[2], args[3])
+    y2 = md.y.clone()
+    switched.switched_lora_(y2, md.x, segs, pk, path=path)
+    torch.cuda.synchronize()
+    switched.check(dev)
+    _check(md, y2, eff, torch.bfloat16, f"segments given, path={path}")
+    _say(f"  max abs err {err:.3e}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("path", ["auto", "segments"])
+def test_mixed_ranks_prefill_batch(dev, dtype, path):
+    """Sequences of 256 tokens, one adapter each, over ranks 8..512; T = 2048
+    (above the one-launch kernel's batch limit, so both rank classes run the
+    segment kernels), and T = 512 (auto: the split)."""
+    # (fp32 stages its shrink values in LDS at 4 bytes: 2 slices x rank 256 at most)
+    top = 512 if dtype == torch.bfloat16 else 256
+    ranks = [32, 8, top, 64, 128, 16, 32, 256]
+    NA = len(ranks)
+    H, slices = (1024, (512, 256)) if dtype == torch.bfloat16 else (512, (256, 128))
+    spec = workloads.ModuleSpec("mixed", H, slices, ranks, top)
+    for T in (2048, 512):
+        L = 256
+        nseq = T // L
+        rng = np.random.default_rng(T)
+        adapters = np.array([3, 1, 5, 8, 2, 4, 6, 7])[:nseq]           # the largest adapter (3) first
+        req = np.repeat(adapters, L).astype(np.int64)
+        req[rng.random(T) < 0.1] = 0
+        md = workloads.make_module(spec, T, NA, dtype, dev, seed=600 + T)
+        pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, ranks)
+        _say(f"mixed ranks {ranks}, T={T}, {dtype}, path={path} (plan {switched.path_plan(pk, T)})")
+        segs = switched.build_segments(torch.tensor(req, device=dev), NA)
+        y = md.y.clone()
+        switched.switched_lora_(y, md.x, segs, pk, path=path)
+        torch.cuda.synchronize()
+        switched.check(dev)
+        _check(md, y, req, dtype, f"T={T} path={path}")
+
+
+def test_shrink_materialises_z_per_class(dev):
+    """gs_shrink with z requested on a two-class module whose hidden dimension
+    is split in both classes: each class's partials are reduced into its own
+    adapters' z rows only (the other class's rows are not overwritten), and
+    the expand from that z matches the oracle."""
+    ranks = [32, 256, 16, 32]
+    NA = len(ranks)
+    spec = workloads.ModuleSpec("two_class", 4096, (512, 512), ranks, 256)
+    T = 300
+    md = workloads.make_module(spec, T, NA, torch.bfloat16, dev, seed=77)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, ranks)
+    ks = switched.shrink_ksplits(pk, T)
+    assert len(ks) == 2 and min(ks) > 1, ks
+    rng = np.random.default_rng(9)
+    req = rng.integers(0, NA + 1, size=T)
+    segs = switched.build_segments(torch.tensor(req, device=dev), NA)
+    with pytest.raises(switched._lib.GraniteSwitchError, match="one rank class"):
+        switched.shrink(md.x, segs, pk, partials_only=True)
+    zw = pk.num_slices * pk.max_rank
+    z = torch.full((T, zw), float("nan"), dtype=torch.bfloat16, device=dev)
+    switched.shrink(md.x, segs, pk, z)
+    torch.cuda.synchronize()
+    seg_h, perm_h = segs.seg_offsets.cpu().numpy(), segs.perm.cpu().numpy()
+    ref = olora.shrink_rows(_np(md.x), perm_h, seg_h, [_np(a) for a in md.lora_A_slices], ranks, zw)
+    got = _np(z)
+    for g in range(1, NA + 1):
+        lo, hi = seg_h[g - 1], seg_h[g]
+        cols = pk.num_slices * pk.ranks_host[g]
+        err = np.abs(got[lo:hi, :cols] - olora.bf16_round(ref[lo:hi, :cols]))
+        assert np.all(err <= 2e-2 + 2e-2 * np.abs(ref[lo:hi, :cols])), f"z of adapter {g}"
+    y = md.y.clone()
+    switched.expand_add_(y, z, segs, pk)
+    torch.cuda.synchronize()
+    _check(md, y, req, torch.bfloat16, "expand from the materialised z")
+
+
+def test_noalloc_two_classes_equals_workspace_path(dev):
+    """gs_switched_lora_noalloc on a two-class module: the same kernels per
+    class, scratch in the static array, bit-identical to gs_switched_lora."""
+    ranks = [32] * 6 + [512]
+    NA = len(ranks)
+    spec = workloads.ModuleSpec("qkv", 4096, (4096, 1024, 1024), ranks, 512)
+    T = 400
+    md = workloads.make_module(spec, T, NA, torch.bfloat16, dev, seed=88)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, ranks)
+    req = np.random.default_rng(3).integers(0, NA + 1, size=T)
+    segs = switched.build_segments(torch.tensor(req, device=dev), NA)
+    y_ref = md.y.clone()
+    switched.switched_lora_(y_ref, md.x, segs, pk, path="segments")
+    y = md.y.clone()
+    switched.switched_lora_noalloc_(y, md.x, segs, pk)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref), "noalloc differs from gs_switched_lora"
+    _check(md, y, req, torch.bfloat16, "noalloc, two classes")
+
+
+def test_only_large_adapters_and_no_applicable_adapter(dev):
+    """A module whose every adapter is above rank 64 is one (large) class;
+    one with no applicable adapter launches nothing and leaves y as it was."""
+    ranks = [128, 512]
+    spec = workloads.ModuleSpec("large", 1024, (1024,), ranks, 512)
+    T = 200
+    md = workloads.make_module(spec, T, 2, torch.bfloat16, dev, seed=5)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, ranks)
+    assert pk.rank_split()[0] is None and switched.path_plan(pk, T) == "segments"
+    req = np.random.default_rng(1).integers(0, 3, size=T)
+    for path in ("auto", "segments"):
+        y = md.y.clone()
+        switched.switched_lora_routed_(y, md.x, torch.tensor(req, device=dev), pk, path=path)
+        torch.cuda.synchronize()
+        _check(md, y, req, torch.bfloat16, f"large only, path={path}")
+    with pytest.raises(ValueError, match="rank <= 64"):
+        switched.switched_lora_routed_(md.y.clone(), md.x, torch.tensor(req, device=dev), pk, path="small")
+    none = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, ranks, applicable=[False, False])
+    y = md.y.clone()
+    switched.switched_lora_routed_(y, md.x, torch.tensor(req, device=dev), none, path="segments")
+    torch.cuda.synchronize()
+    assert torch.equal(y, md.y)

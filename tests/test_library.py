@@ -67,11 +67,12 @@ def test_validation_errors_without_launch():
                   None)
     assert e.value.status == _lib.GS_ERR_WORKSPACE and "workspace" in str(e.value)
     with pytest.raises(_lib.GraniteSwitchError) as e:
-        _lib.call("gs_shrink", 0, None, 16, 4, 12, None, None, None, 1, 4, 16, None, None, None, 16, None, 0, None)
+        _lib.call("gs_shrink", 0, None, 16, 4, 12, None, None, None, 1, 4, 16, None, None, None, None, 16, None, 0,
+                  None)
     assert "hidden" in str(e.value)
     with pytest.raises(_lib.GraniteSwitchError) as e:
         _lib.call("gs_expand_add", 0, None, 64, 4, 48, (ctypes.c_int32 * 2)(0, 48), 1, None, 16, 0, None, None,
-                  None, None, 4, 16, None, None, None)
+                  None, None, 4, 16, None, None, None, None)
     assert "multiple of 32" in str(e.value)
     na = (ctypes.c_int32 * 6)(65, 0, 0, 0, 0, 0)
     with pytest.raises(_lib.GraniteSwitchError) as e:
@@ -90,10 +91,57 @@ def test_validation_errors_without_launch():
 
 def test_workspace_plan_is_consistent():
     lib = _lib.load()
-    small = lib.gs_shrink_workspace_bytes(256, 4096, 3, 12, 32)
-    big = lib.gs_shrink_workspace_bytes(8192, 4096, 2, 12, 32)
+    small = lib.gs_shrink_workspace_bytes(256, 4096, 3, 12, 32, None)
+    big = lib.gs_shrink_workspace_bytes(8192, 4096, 2, 12, 32, None)
     assert small > 0 and big > 0
-    assert lib.gs_shrink_workspace_bytes(0, 4096, 3, 12, 32) == 256
+    assert lib.gs_shrink_workspace_bytes(0, 4096, 3, 12, 32, None) == 256
+
+
+def _ranks(vals):
+    return (ctypes.c_int32 * len(vals))(*vals)
+
+
+def test_rank_classes_plan_each_class_for_its_own_rank():
+    """A module of rank-32 adapters plus one rank-512 adapter is planned as two
+    rank classes.  The rank-32 class keeps the k-split and workspace of the
+    module without the large adapter; the large class, expected to hold its
+    adapter's share of the tokens, gets a deep k-split."""
+    lib = _lib.load()
+    ks = (ctypes.c_int32 * 2)()
+    r32 = [0] + [32] * 12
+    mixed = r32 + [512]
+    bf16 = _lib.GS_DTYPE_BF16
+    for T, H, S in ((256, 4096, 3), (4144, 4096, 3), (4144, 12800, 1), (4144, 4096, 2)):
+        assert lib.gs_shrink_ksplits(bf16, T, H, S, 12, 32, _ranks(r32), ks) == 1
+        ks_alone = ks[0]
+        # the host-table class of a uniform module equals the table-less plan
+        assert lib.gs_shrink_ksplits(bf16, T, H, S, 12, 32, None, ks) == 1 and ks[0] == ks_alone
+        assert lib.gs_shrink_ksplits(bf16, T, H, S, 13, 512, _ranks(mixed), ks) == 2
+        assert ks[0] == ks_alone, (T, H, S, ks[0], ks_alone)
+        assert ks[1] >= 2, (T, H, S, ks[1])
+        ws_mixed = lib.gs_shrink_workspace_bytes(T, H, S, 13, 512, _ranks(mixed))
+        assert ws_mixed >= lib.gs_shrink_workspace_bytes(T, H, S, 12, 32, _ranks(r32))
+    # no applicable adapter: no class, nothing to launch
+    assert lib.gs_shrink_ksplits(bf16, 256, 4096, 1, 3, 32, _ranks([0, 0, 0, 0]), ks) == 0
+    # a host table that disagrees with max_rank is refused
+    assert lib.gs_shrink_ksplits(bf16, 256, 4096, 1, 2, 32, _ranks([0, 32, 64]), ks) == -_lib.GS_ERR_INVALID
+    assert lib.gs_shrink_workspace_bytes(256, 4096, 1, 2, 32, _ranks([0, 32, 64])) < 0
+
+
+def test_rank_split_views():
+    """PackedAdapters.rank_split: the <= 64 view and the larger view share the
+    device tensors and zero the other class's host ranks."""
+    spec = workloads.ModuleSpec("m", 64, (64,), [16, 512, 64, 0], 512)
+    md = workloads.make_module(spec, 4, 4, torch.float32, "cpu", seed=1)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, spec.ranks,
+                                             applicable=[True, True, True, False])
+    small, large = pk.rank_split()
+    assert small.ranks_host == [0, 16, 0, 64, 0] and small.max_rank == 64
+    assert large.ranks_host == [0, 0, 512, 0, 0] and large.max_rank == 512
+    assert small.a_pack is pk.a_pack and large.b_off is pk.b_off
+    only_small = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, [16, 0, 64, 0],
+                                                     applicable=[True, False, True, False])
+    assert only_small.rank_split()[1] is None
 
 
 # -- host mirrors of the reference API ---------------------------------------
@@ -346,3 +394,48 @@ def test_wait_limit_setter_round_trips():
         assert switched.set_small_wait_limit(None) == prev        # None restores the default
     finally:
         switched.set_small_wait_limit(prev)
+
+
+def test_reused_segments_are_checked_before_any_launch():
+    """build_segments(out=...) writes eff_ids / perm / seg_offsets in place: a
+    Segments allocated for a smaller batch or another adapter count is refused
+    before the builder runs (the kernels would write past its buffers)."""
+    dev = torch.device("cpu")
+
+    def segs(T, NA):
+        return switched.Segments(eff_ids=torch.empty(T, dtype=torch.int32), seg_offsets=torch.empty(NA + 1, dtype=torch.int32),
+                                 perm=torch.empty(max(T, 1), dtype=torch.int32), num_tokens=T, num_adapters=NA)
+
+    switched._check_reused_segments(segs(64, 4), 64, 4, dev)
+    switched._check_reused_segments(segs(64, 4), 10, 4, dev)       # a larger buffer holds a smaller batch
+    with pytest.raises(ValueError, match="eff_ids holds 64"):
+        switched._check_reused_segments(segs(64, 4), 65, 4, dev)
+    with pytest.raises(ValueError, match="allocated for 4 adapters"):
+        switched._check_reused_segments(segs(64, 4), 64, 5, dev)
+    s = segs(64, 4)
+    s.perm = torch.empty(32, dtype=torch.int32)
+    with pytest.raises(ValueError, match="perm holds 32"):
+        switched._check_reused_segments(s, 64, 4, dev)
+    s = segs(64, 4)
+    s.seg_offsets = torch.empty(5, dtype=torch.int64)
+    with pytest.raises(ValueError, match="seg_offsets must be a contiguous int32"):
+        switched._check_reused_segments(s, 64, 4, dev)
+    with pytest.raises(ValueError, match="on cuda"):
+        switched._check_reused_segments(segs(64, 4), 64, 4, torch.device("cuda", 0))
+
+
+def test_population_workloads():
+    """The bench's adapter populations: the rank-512 one adds adapter N+1 of
+    rank 512 and draws ids over N+1; the idle one keeps the batch, all base."""
+    for cfg in (1, 4):
+        na = workloads.num_adapters_for(cfg)
+        r = workloads.population_routing(cfg, "r512")
+        assert workloads.population_adapters(cfg, "r512") == na + 1
+        assert r.req_ids.max() == na + 1 and r.req_ids.min() >= 0
+        assert r.num_tokens == workloads.routing_for(cfg).num_tokens
+        for spec, base in zip(workloads.population_specs(cfg, "r512"), workloads.module_specs(cfg)):
+            assert spec.ranks == list(base.ranks) + [512] and spec.max_rank == 512
+        idle = workloads.population_routing(cfg, "all_base")
+        assert not idle.req_ids.any()
+        assert np.array_equal(idle.positions, workloads.routing_for(cfg).positions)
+    assert workloads.population_specs(2, "balanced") == workloads.module_specs(2)

@@ -86,5 +86,6 @@ def test_noalloc_rejects_shapes_beyond_the_scratch(dev):
     T = 1 << 20
     with pytest.raises(_lib.GraniteSwitchError) as e:
         _lib.call("gs_switched_lora_noalloc", _lib.GS_DTYPE_BF16, None, 4096, None, 6144, T, 4096, 6144,
-                  (_lib.c_i32 * 4)(0, 4096, 5120, 6144), 3, None, None, None, None, None, 24, 64, None, None, None)
+                  (_lib.c_i32 * 4)(0, 4096, 5120, 6144), 3, None, None, None, None, None, 24, 64, None, None, None,
+                  None)
     assert e.value.status == _lib.GS_ERR_WORKSPACE and "static scratch" in str(e.value)
