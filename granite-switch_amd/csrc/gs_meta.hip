@@ -420,7 +420,9 @@ __global__ __launch_bounds__(256) void bitmask_kernel(const void* __restrict__ i
 }
 
 // Probe-slot split: one thread per token.  The kind table (<= 257 bytes) is
-// staged in LDS; an index outside the table is not a probe.
+// staged in LDS.  An index outside the table (negative or past its last
+// slot) is neither a probe nor an adapter: both streams get 0, so the token
+// takes the base model, as the segment builder treats such ids.
 __global__ __launch_bounds__(256) void split_indices_kernel(const uint8_t* __restrict__ kind_lut, int lut_len,
                                                             const void* __restrict__ ids, int idx_bytes, int64_t n,
                                                             void* lora_out, void* probe_out) {
@@ -430,12 +432,14 @@ __global__ __launch_bounds__(256) void split_indices_kernel(const uint8_t* __res
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t >= n) return;
   const int64_t v = load_idx(ids, idx_bytes, t);
-  const bool probe = v >= 0 && v < lut_len && lut[v] != 0;
+  const bool in_table = v >= 0 && v < lut_len;
+  const bool probe = in_table && lut[v] != 0;
+  const int64_t lora = in_table && !probe ? v : 0;
   if (idx_bytes == 8) {
-    if (lora_out) static_cast<int64_t*>(lora_out)[t] = probe ? 0 : v;
+    if (lora_out) static_cast<int64_t*>(lora_out)[t] = lora;
     if (probe_out) static_cast<int64_t*>(probe_out)[t] = probe ? v : 0;
   } else {
-    if (lora_out) static_cast<int32_t*>(lora_out)[t] = probe ? 0 : static_cast<int32_t>(v);
+    if (lora_out) static_cast<int32_t*>(lora_out)[t] = static_cast<int32_t>(lora);
     if (probe_out) static_cast<int32_t*>(probe_out)[t] = probe ? static_cast<int32_t>(v) : 0;
   }
 }

@@ -42,7 +42,10 @@ def split_adapter_indices(kind_lut: torch.Tensor | None,
     None the LoRA stream IS ``adapter_indices`` and the probe stream is zeros.
     Indices must be int32 or int64 on the GPU; ``kind_lut`` is moved to their
     device if it is not there (keep it there, e.g. as a module buffer, to stay
-    capture-safe).  An index outside the table is not a probe.
+    capture-safe).  An index outside the table (negative, or past the last
+    slot) is neither a probe nor an adapter: both streams hold 0 there, so the
+    token takes the base model.  (The reference indexes the table directly: a
+    negative index wraps and one past the end raises.)
     """
     if kind_lut is None:
         return adapter_indices, torch.zeros_like(adapter_indices)

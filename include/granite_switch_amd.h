@@ -114,8 +114,10 @@ int gs_build_segments(const int64_t* req_ids, const int64_t* positions, const in
  * an activation-probe slot (build_adapter_kind_lut; entry 0, base, is 0).
  * lora_indices[t] = 0 where adapter_indices[t] is a probe, else the index;
  * probe_indices[t] = the index where it is a probe, else 0.  Either output may
- * be NULL.  Indices outside [0, lut_len) are not probes (the reference's
- * table lookup would reject them).  adapter_indices and both outputs have
+ * be NULL.  Indices outside [0, lut_len) are neither probes nor adapters:
+ * both outputs hold 0 there, so the token takes the base model (the
+ * reference's table lookup would wrap a negative index and reject one past
+ * the end).  adapter_indices and both outputs have
  * element size idx_bytes (4 or 8).  Limits: 1 <= lut_len <= GS_MAX_ADAPTERS+1.
  * ---------------------------------------------------------------------- */
 int gs_split_adapter_indices(const uint8_t* kind_lut, int32_t lut_len, const void* adapter_indices,
@@ -217,8 +219,9 @@ int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t
  * workspace, no z, no hipMalloc.  No counterpart in the reference: it is for
  * callers that cannot allocate (code under HIP graph capture, tight serving
  * loops, harnesses that forbid allocation).  The array is looked up once per
- * device (hipGetSymbolAddress, on the first call with that device current);
- * launch on a stream of the current device.  Shapes whose partials plus z
+ * device (hipGetSymbolAddress, on the first call with that device current):
+ * make that first call outside graph capture (one eager call); launch on a
+ * stream of the current device.  Shapes whose partials plus z
  * exceed the array are rejected with GS_ERR_WORKSPACE (use gs_switched_lora
  * with a workspace then).  Every call on a GPU shares that GPU's array, which
  * keeps the last call's contents (nothing needs to start at zero): calls that

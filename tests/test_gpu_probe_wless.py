@@ -101,6 +101,10 @@ CASES = [
     ("two tiers", (16, 32), [0, 1, 2, 2, 0, 1] * 8, 512, 128),
     ("two adapters of one tier", (16, 16), [1, 2, 0, 1, 2, 0] * 8, 256, 64),
     ("three tiers, ragged", (16, 32, 64, 128), [3] * 5 + [0] * 40 + [1, 2, 4] * 11, 384, 4096),
+    # top tier 64 at <= 1024 rows: the 4-k-group form of the kernel
+    ("top tier 64", (32, 64), [0, 1, 2, 2, 1, 0] * 8, 256, 128),
+    # past 1024 rows: the general form (one pass per adapter present)
+    ("past 1024 rows", (16, 32), ([0, 1, 1, 2, 2, 2, 0] * 158)[:1100], 256, 128),
 ]
 
 
@@ -137,3 +141,18 @@ def test_shrink_expand_zeroes_a_larger_output_and_skips_zero_tiles(dev):
     o = out.float().cpu()
     assert torch.count_nonzero(o[32:]) == 0 and torch.count_nonzero(o[:, N:]) == 0
     assert torch.count_nonzero(o[:32, :N]) > 0
+
+
+def test_split_out_of_range_ids_go_to_neither_stream(dev):
+    """An index outside the kind table (negative, or past the last slot) is
+    neither a probe nor an adapter: both streams hold 0 there, so the token
+    takes the base model (the segment builder treats such ids as base too).
+    The reference indexes the table directly, so there a negative index wraps
+    and one past the end raises; this library's choice is pinned here."""
+    lut = probe_routing.build_adapter_kind_lut(["lora", "probe"]).to(dev)         # 3 entries
+    for dtype in (torch.int64, torch.int32):
+        ids = torch.tensor([-1, 3, 7, 0, 1, 2, -5], dtype=dtype, device=dev)
+        lora, probe = probe_routing.split_adapter_indices(lut, ids)
+        torch.cuda.synchronize()
+        assert lora.cpu().tolist() == [0, 0, 0, 0, 1, 0, 0]
+        assert probe.cpu().tolist() == [0, 0, 0, 0, 0, 2, 0]
