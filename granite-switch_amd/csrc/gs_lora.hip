@@ -73,7 +73,19 @@ struct ShrinkParams {
   int n_chunks;
   RankWindow rw;          // adapters of this launch's rank class
   int flat;               // flat item layout (work_item) instead of tile ranges per XCD
+  int ks_target;          // > 0: the k-split is chosen on the device (dyn_ksplit), KS is its maximum
 };
+
+// The k-split of a launch whose workgroups loop (a large-rank class): chosen
+// on the device from the batch's real tile count, as the host chooses it from
+// an estimate -- about `target` items, 1..KS_max -- so that a class holding
+// fewer tokens than expected still spreads over the GPU.  The expand of the
+// class computes the same value from the same count.
+__device__ __forceinline__ int dyn_ksplit(int tiles, int n_chunks, int target, int ks_max) {
+  const int w = tiles * n_chunks;
+  int ks = w > 0 ? (target + w / 2) / w : ks_max;
+  return ks < 1 ? 1 : (ks > ks_max ? ks_max : ks);
+}
 
 // 16x16 MFMA over one 16-byte piece of each operand (K = 32 bf16, or four
 // K = 4 fp32 steps).  Lane l supplies row l % 16 of each operand and elements
@@ -273,7 +285,8 @@ __device__ __forceinline__ void wait_stages(int after) {
 
 // One work item of shrink_dma_kernel: tile tr, sub = (k-chunk, column chunk).
 template <int NB>
-__device__ __forceinline__ void shrink_dma_item(const ShrinkParams& p, const TileRef& tr, int sub, char* ring) {
+__device__ __forceinline__ void shrink_dma_item(const ShrinkParams& p, const TileRef& tr, int sub, int KS,
+                                                char* ring) {
   constexpr int COLS = 32 * NB;
   constexpr int NC16 = COLS / 16;
   constexpr int ROWS = kTMS + COLS;        // LDS rows of a stage: x rows, then lora_A rows
@@ -299,8 +312,8 @@ __device__ __forceinline__ void shrink_dma_item(const ShrinkParams& p, const Til
   // k-chunk ks: stages [ks * all / KS, (ks + 1) * all / KS) of the all = H / 64
   // stages, so the chunks differ by at most one stage
   const int all_st = p.H / kDmaBK;
-  const int s_lo = (ks * all_st) / p.KS;
-  const int nst = ((ks + 1) * all_st) / p.KS - s_lo;
+  const int s_lo = (ks * all_st) / KS;
+  const int nst = ((ks + 1) * all_st) / KS - s_lo;
   const int64_t k_lo = static_cast<int64_t>(s_lo) * kDmaBK;
 
   // this lane's source in each transfer: row 8t + l/8 of the wave's rows,
@@ -376,7 +389,7 @@ __device__ __forceinline__ void shrink_dma_item(const ShrinkParams& p, const Til
     if (row >= tr.nrows || c4 >= wcols) continue;
     const f32x4 v = *reinterpret_cast<const f32x4*>(res + row * OLD + c4);
     const int64_t slot = tr.slot0 + row;
-    if (p.KS == 1) {
+    if (KS == 1) {
       *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.z) + slot * p.ldz + col0 + c4) =
           make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
     } else {
@@ -394,18 +407,25 @@ __device__ __forceinline__ void shrink_dma_item(const ShrinkParams& p, const Til
 template <int NB, bool LOOP>
 __global__ __launch_bounds__(kThreads) void shrink_dma_kernel(ShrinkParams p) {
   __shared__ __align__(16) char ring[DmaRing<NB>::NST * (kTMS + 32 * NB) * kDmaRow];
-  const int nsub = p.n_chunks * p.KS;
   const bool flat = LOOP && p.flat != 0;       // the one-item form is never flat
   int lin = static_cast<int>(blockIdx.x);
   int sub = 0, total = 0;
-  TileRef tr = locate_tile<kTMS>(p.seg, p.ranks, p.a_off, p.NA, p.rw, lin, flat, nsub, sub, total);
   if constexpr (!LOOP) {
-    if (tr.g != 0) shrink_dma_item<NB>(p, tr, sub, ring);
+    const TileRef tr =
+        locate_tile<kTMS>(p.seg, p.ranks, p.a_off, p.NA, p.rw, lin, false, p.n_chunks * p.KS, sub, total);
+    if (tr.g != 0) shrink_dma_item<NB>(p, tr, sub, p.KS, ring);
     return;
   }
+  int KS = p.KS;
+  TileRef tr = locate_tile_by<kTMS>(p.seg, p.ranks, p.a_off, p.NA, p.rw, lin, flat,
+                                    [&](int tot) {
+                                      if (p.ks_target > 0) KS = dyn_ksplit(tot, p.n_chunks, p.ks_target, p.KS);
+                                      return p.n_chunks * KS;
+                                    }, sub, total);
+  const int nsub = p.n_chunks * KS;
   const int items = work_items(total, nsub, flat);
   for (;;) {
-    if (tr.g != 0) shrink_dma_item<NB>(p, tr, sub, ring);
+    if (tr.g != 0) shrink_dma_item<NB>(p, tr, sub, KS, ring);
     lin += static_cast<int>(gridDim.x);
     if (lin >= items) break;
     lds_barrier();                         // every wave is done with the ring before the next item's transfers
@@ -503,6 +523,8 @@ struct ExpandParams {
   const int32_t* perm;
   RankWindow rw;          // adapters of this launch's rank class
   int flat;               // flat item layout, one sub-tile per item (work_item)
+  int ks_target;          // > 0: the shrink chose its k-split on the device (dyn_ksplit over
+  int ks_chunks;          //   its 64-slot tiles, ks_chunks column chunks, at most nparts)
 };
 
 // Shrink values of the tile for slices s_lo..s_hi (the ones the workgroup's
@@ -515,7 +537,7 @@ constexpr int kPartGroup = 8;
 
 template <bool BF16>
 __device__ __forceinline__ void z_stage(const ExpandParams& p, const TileRef& tr, int r, int zo, char* zs, int zs_ld,
-                                        int s_lo, int s_hi) {
+                                        int s_lo, int s_hi, int nparts) {
   const int per_row = ((s_hi - s_lo + 1) * r) >> 2;
   const int items = kTM * per_row;
   for (int it = threadIdx.x; it < items; it += kThreads) {
@@ -524,16 +546,16 @@ __device__ __forceinline__ void z_stage(const ExpandParams& p, const TileRef& tr
     float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (row < tr.nrows) {
       const int slot = tr.slot0 + row;
-      if (p.nparts > 0) {
+      if (nparts > 0) {
         const float* src = p.part + static_cast<int64_t>(slot) * p.zw + c4;
-        for (int ks0 = 0; ks0 < p.nparts; ks0 += kPartGroup) {
+        for (int ks0 = 0; ks0 < nparts; ks0 += kPartGroup) {
           f32x4 a[kPartGroup];
 #pragma unroll
           for (int u = 0; u < kPartGroup; ++u)
-            if (ks0 + u < p.nparts) a[u] = *reinterpret_cast<const f32x4*>(src + (ks0 + u) * p.part_stride);
+            if (ks0 + u < nparts) a[u] = *reinterpret_cast<const f32x4*>(src + (ks0 + u) * p.part_stride);
 #pragma unroll
           for (int u = 0; u < kPartGroup; ++u) {
-            if (ks0 + u < p.nparts) {
+            if (ks0 + u < nparts) {
               v[0] += a[u].x;
               v[1] += a[u].y;
               v[2] += a[u].z;
@@ -592,7 +614,7 @@ constexpr bool kExpandBalanced = GS_EXPAND_BALANCED;
 // is loaded where it is used, which keeps the one-item forms' registers.
 template <bool BF16, int NBW, int PRE, bool PIPE>
 __device__ __forceinline__ void expand_item(const ExpandParams& p, const TileRef& tr, int sub0, int nsub,
-                                            float (&dtile)[kTM][4 * NBW * 32 + kOutPad], char* zs) {
+                                            int nparts, float (&dtile)[kTM][4 * NBW * 32 + kOutPad], char* zs) {
   constexpr int NT = 4 * NBW * 32;           // columns per sub-tile
   // read-modify-write mapping: each lane owns one 16-byte piece per row it
   // touches, consecutive lanes consecutive pieces, so every wave access
@@ -666,7 +688,7 @@ __device__ __forceinline__ void expand_item(const ExpandParams& p, const TileRef
     s_hi = s_lo;
     while (s_hi + 1 < p.si.S && c_last >= p.si.bounds[s_hi + 1]) ++s_hi;
   }
-  z_stage<BF16>(p, tr, r, zo, zs, zs_ld, s_lo, s_hi);
+  z_stage<BF16>(p, tr, r, zo, zs, zs_ld, s_lo, s_hi, nparts);
   lds_barrier();
 
   auto compute = [&](int sub, u32x4 (&bcur)[NBW][PRE], u32x4 (&ycur)[PASSES]) {
@@ -819,20 +841,187 @@ void expand_kernel(ExpandParams p) {
     // group sub of `groups` covers sub-tiles [sub*n_sub/groups, (sub+1)*n_sub/groups)
     const int sub0 = (sub * n_sub) / groups;
     const int nsub = ((sub + 1) * n_sub) / groups - sub0;
-    if (nsub > 0) expand_item<BF16, NBW, PRE, false>(p, tr, sub0, nsub, dtile, zs);
+    if (nsub > 0) expand_item<BF16, NBW, PRE, false>(p, tr, sub0, nsub, p.nparts, dtile, zs);
     return;
+  }
+  // the shrink's k-split when it chose it on the device: the same function of
+  // the same 64-slot tile count
+  int nparts = p.nparts;
+  if (p.ks_target > 0) {
+    const int ks = dyn_ksplit(count_tiles<kTMS>(p.seg, p.ranks, p.NA, p.rw), p.ks_chunks, p.ks_target, p.nparts);
+    nparts = ks > 1 ? ks : 0;
   }
   const int items = work_items(total, groups, flat);
   for (;;) {
     if (tr.g != 0) {
       const int sub0 = (sub * n_sub) / groups;
       const int nsub = ((sub + 1) * n_sub) / groups - sub0;
-      if (nsub > 0) expand_item<BF16, NBW, PRE, true>(p, tr, sub0, nsub, dtile, zs);
+      if (nsub > 0) expand_item<BF16, NBW, PRE, true>(p, tr, sub0, nsub, nparts, dtile, zs);
     }
     lin += static_cast<int>(gridDim.x);
     if (lin >= items) break;
     lds_barrier();                         // every wave is done with zs and dtile before the next item
     tr = tile_at<kTM, kExpandBalanced>(p.seg, p.ranks, p.b_off, p.NA, p.rw, lin, flat, total, groups, sub);
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Expand of a sparse large-rank class (bf16; a few tiles of an adapter of rank
+// 72..512, e.g. one rank-512 adapter among rank-32 ones at decode).  One item
+// is (tile, 128-column sub-tile), laid out flat over a looping grid of one
+// round.  The 4 waves split the RANK instead of the columns: wave w takes
+// k-groups [w*KG, (w+1)*KG) of all 128 columns, so the item's whole lora_B
+// block (128 x r) is in flight in one memory trip (the column-split kernel
+// streams a large rank in dependent chunks).  The waves' partial deltas are
+// summed through LDS in a fixed order, (w0 + w2) + (w1 + w3), then every
+// thread read-modify-writes 16-byte pieces of its token rows.  Sub-tiles lie
+// inside one slice (slice widths are multiples of 128), so only that slice's
+// shrink values are staged.
+// ----------------------------------------------------------------------------
+constexpr int kSpNT = 128;                   // columns per item
+
+template <int KG>
+__global__ __launch_bounds__(kThreads) void expand_sparse_kernel(ExpandParams p) {
+  constexpr int KSTEP = 16;                  // bf16 k per MFMA group (both lane halves)
+  constexpr int KHALF = 8;
+  constexpr int EPL = 8;                     // bf16 elements per 16-byte piece
+  constexpr int LPR = kSpNT / EPL;           // lanes per row
+  constexpr int RPI = kThreads / LPR;        // rows per workgroup-wide access
+  constexpr int PASSES = kTM / RPI;
+  __shared__ float red[2][kTM][kSpNT + kOutPad];
+  extern __shared__ __align__(16) char zs[];   // [32][max_rank + 8] bf16: one slice's shrink values
+
+  const int n_sub = p.out_total / kSpNT;
+  int lin = static_cast<int>(blockIdx.x);
+  int sub = 0, total = 0;
+  TileRef tr = locate_tile_by<kTM, kExpandBalanced>(p.seg, p.ranks, p.b_off, p.NA, p.rw, lin, true,
+                                                    [&](int) { return n_sub; }, sub, total);
+  int nparts = p.nparts;
+  if (p.ks_target > 0) {
+    const int ks = dyn_ksplit(count_tiles<kTMS>(p.seg, p.ranks, p.NA, p.rw), p.ks_chunks, p.ks_target, p.nparts);
+    nparts = ks > 1 ? ks : 0;
+  }
+  const int items = work_items(total, n_sub, true);
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int l = tid & 63;
+  const int i = l & 31;
+  const int h = l >> 5;
+  const int zs_ld = p.max_rank + 8;
+  const int cx = (tid % LPR) * EPL;
+  for (;;) {
+    if (tr.g != 0) {
+      const int r = tr.rank;
+      const int n_tile0 = sub * kSpNT;
+      int s = 0;
+      while (s + 1 < p.si.S && n_tile0 >= p.si.bounds[s + 1]) ++s;
+      // this wave's k-groups of lora_B for the 4 column blocks (pieces past
+      // the rank read the row's first piece and are masked)
+      u32x4 bv[4][KG];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n_tile0 + 32 * q + i;
+        const char* br = static_cast<const char*>(p.b_pack) + (tr.off + static_cast<int64_t>(n) * r) * 2;
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) {
+          const int k0 = (wave * KG + kg) * KSTEP + KHALF * h;
+          const bool kin = k0 < r;
+          bv[q][kg] = sel16(kin, ld16(br + (kin ? k0 : 0) * 2));
+        }
+      }
+      // y pieces of the item's rows (rows past the tile re-read its first token)
+      int64_t yrow[PASSES];
+      bool rok[PASSES];
+      u32x4 yv[PASSES];
+#pragma unroll
+      for (int ps = 0; ps < PASSES; ++ps) {
+        const int row = ps * RPI + tid / LPR;
+        rok[ps] = row < tr.nrows;
+        yrow[ps] = static_cast<int64_t>(p.perm[tr.slot0 + (rok[ps] ? row : 0)]) * p.ldy;
+        yv[ps] = ld16(static_cast<const char*>(p.y) + (yrow[ps] + n_tile0 + cx) * 2);
+      }
+      // the slice's shrink values of the tile's rows: split-K partials summed
+      // in ks order (kPartGroup at a time) and rounded to bf16 as a stored z
+      // would be, or z itself
+      const int zo = (p.z_off != nullptr) ? p.z_off[tr.g] : 0;
+      const int per_row = r >> 2;
+      for (int it = tid; it < kTM * per_row; it += kThreads) {
+        const int row = it / per_row;
+        const int c4 = (it - row * per_row) * 4;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (row < tr.nrows) {
+          const int slot = tr.slot0 + row;
+          if (nparts > 0) {
+            const float* src = p.part + static_cast<int64_t>(slot) * p.zw + s * r + c4;
+            for (int ks0 = 0; ks0 < nparts; ks0 += kPartGroup) {
+              f32x4 a[kPartGroup];
+#pragma unroll
+              for (int u = 0; u < kPartGroup; ++u)
+                if (ks0 + u < nparts) a[u] = *reinterpret_cast<const f32x4*>(src + (ks0 + u) * p.part_stride);
+#pragma unroll
+              for (int u = 0; u < kPartGroup; ++u) {
+                if (ks0 + u < nparts) {
+                  v[0] += a[u].x;
+                  v[1] += a[u].y;
+                  v[2] += a[u].z;
+                  v[3] += a[u].w;
+                }
+              }
+            }
+          } else {
+            const int64_t zrow = p.z_by_token ? static_cast<int64_t>(p.perm[slot]) : static_cast<int64_t>(slot);
+            const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.z) + zrow * p.ldz + zo +
+                                                            s * r + c4);
+            v[0] = bf16_bits_to_f32(static_cast<uint16_t>(w.x & 0xffffu));
+            v[1] = bf16_bits_to_f32(static_cast<uint16_t>(w.x >> 16));
+            v[2] = bf16_bits_to_f32(static_cast<uint16_t>(w.y & 0xffffu));
+            v[3] = bf16_bits_to_f32(static_cast<uint16_t>(w.y >> 16));
+          }
+        }
+        *reinterpret_cast<uint2*>(zs + (static_cast<int64_t>(row) * zs_ld + c4) * 2) =
+            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      }
+      lds_barrier();
+      f32x16 acc[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = f32x16{};
+      const char* zrow_l = zs + static_cast<int64_t>(i) * zs_ld * 2;
+#pragma unroll
+      for (int kg = 0; kg < KG; ++kg) {
+        const int k0 = (wave * KG + kg) * KSTEP + KHALF * h;
+        const bool kin = k0 < r;
+        const u32x4 za = sel16(kin, *reinterpret_cast<const u32x4*>(zrow_l + (kin ? k0 : 0) * 2));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] = mfma32_bf16(za, bv[q][kg], acc[q]);
+      }
+      // fixed-order sum of the waves' partial deltas
+      if (wave < 2) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) red[wave][mfma32_row(v, l)][32 * q + i] = acc[q][v];
+      }
+      lds_barrier();
+      if (wave >= 2) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) red[wave - 2][mfma32_row(v, l)][32 * q + i] += acc[q][v];
+      }
+      lds_barrier();
+#pragma unroll
+      for (int ps = 0; ps < PASSES; ++ps) {
+        const int row = ps * RPI + tid / LPR;
+        float d[EPL];
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) d[e] = red[0][row][cx + e] + red[1][row][cx + e];
+        if (rok[ps]) add_store_y<true>(p.y, yrow[ps] + n_tile0 + cx, yv[ps], d);
+      }
+    }
+    lin += static_cast<int>(gridDim.x);
+    if (lin >= items) break;
+    lds_barrier();                         // every wave is done with zs and red before the next item
+    tr = tile_at<kTM, kExpandBalanced>(p.seg, p.ranks, p.b_off, p.NA, p.rw, lin, true, total, n_sub, sub);
   }
 }
 
@@ -844,6 +1033,7 @@ struct ShrinkPlan {
   bool dma;               // shrink_dma_kernel (bf16, H % 64 == 0) instead of shrink_kernel
   bool flat;              // flat item layout (work_item)
   bool loop;              // the ring kernel's looping form (a capped grid)
+  int ks_target;          // > 0: the k-split is chosen on the device, KS is its maximum
   int64_t grid;           // workgroups launched
   int64_t part_bytes;
 };
@@ -859,8 +1049,20 @@ struct ShrinkPlan {
 // k-split is sized for them); the items cover every tile the class can have
 // (all T tokens over its NA adapters).  large: the class of ranks above
 // GS_RANK_CLASS_SPLIT.
+// The device k-split of a sparse class aims at half the shrink's usual
+// workgroup target: its expand stages the split-K partials of every row for
+// each 128-column item, so fewer, longer k-chunks measured faster overall
+// (decode QKV with one rank-512 adapter: 49.9 -> 43.2 us; a quarter of the
+// target, 45.0 us).
+#ifndef GS_SPARSE_KS_DIV
+#define GS_SPARSE_KS_DIV 2
+#endif
+// sparse: a large-rank class expected to hold so few tokens that its tiles
+// are laid out flat and its k-split is chosen on the device from the real
+// count (ks_target, KS its maximum).  max_part_bytes caps the partial sums
+// (the allocation-free entry point's static scratch).
 static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, bool bf16, int64_t est_tokens,
-                              bool large = false) {
+                              bool large = false, bool sparse = false, int64_t max_part_bytes = INT64_MAX) {
   ShrinkPlan pl{};
   pl.dma = GS_SHRINK_DMA && bf16 && H % kDmaBK == 0;
   pl.max_tiles = static_cast<int>((T + kTMS - 1) / kTMS + (NA < T ? NA : T));
@@ -875,7 +1077,7 @@ static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, boo
   // its many columns instead of a deep k-split, and the expand adds fewer
   // partial sums.  Few tiles are laid out flat, so they spread over the XCDs.
   if (large && pl.dma && est_tiles * ((pl.zw + 127) / 128) < target) pl.NB = 1;
-  pl.flat = large && pl.dma && est_tiles < 8;
+  pl.flat = sparse && pl.dma;
   pl.n_chunks = (pl.zw + 32 * pl.NB - 1) / (32 * pl.NB);
   const int unit = bf16 ? 256 : 128;          // k per batch of the shrink kernel
   const int units = (H + unit - 1) / unit;
@@ -894,6 +1096,13 @@ static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, boo
     // the ring kernel splits the 64-k stages evenly over the KS chunks (at
     // least 4 stages each: ks <= units)
     pl.KS = ks;
+    if (pl.flat) {
+      // chosen on the device (dyn_ksplit): KS is the largest it may take,
+      // within the partial sums' budget
+      pl.ks_target = static_cast<int>(std::max<int64_t>(1, target / GS_SPARSE_KS_DIV));
+      const int64_t row = T * pl.zw * 4;
+      pl.KS = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(std::min(16, units), max_part_bytes / row)));
+    }
     pl.KC = 0;
     pl.part_bytes = pl.KS > 1 ? static_cast<int64_t>(pl.KS) * T * pl.zw * 4 : 0;
     const int64_t nsub = static_cast<int64_t>(pl.n_chunks) * pl.KS;
@@ -904,7 +1113,8 @@ static ShrinkPlan plan_shrink(int64_t T, int H, int S, int NA, int max_rank, boo
     // (workgroups with no item would each hold a ring of LDS through a lookup)
     if (large) {
       pl.loop = true;
-      pl.grid = std::min(pl.grid, (std::max(target, std::min(items(est_tiles), 2 * target)) + 7) / 8 * 8);
+      const int64_t cap = pl.flat ? target : std::max(target, std::min(items(est_tiles), 2 * target));
+      pl.grid = std::min(pl.grid, (cap + 7) / 8 * 8);
     }
     return pl;
   }
@@ -967,16 +1177,21 @@ static int rank_classes(const char* who, const int32_t* ranks_host, int NA, int 
 
 static bool large_class(const RankClass& k) { return k.rw.lo > kRankClassSplit; }
 
-static ShrinkPlan plan_class(int64_t T, int H, int S, const RankClass& k, bool bf16) {
-  return plan_shrink(T, H, S, k.adapters, k.max_rank, bf16, k.est_tokens, large_class(k));
+// A large-rank class expected to hold fewer than 8 tiles of 64 tokens: both
+// kernels lay its tiles out flat (its few tiles spread over the XCDs), their
+// workgroups loop over a grid of one round, and the shrink's k-split is
+// chosen on the device from the real tile count.
+static bool sparse_class(const RankClass& k) {
+  const int64_t est_tiles = (k.est_tokens + kTMS - 1) / kTMS + std::min<int64_t>(k.adapters, k.est_tokens);
+  return large_class(k) && est_tiles < 8;
 }
 
-// The expand lays a large-rank class's tiles out flat, one sub-tile per item,
-// when it is expected to hold few of them (the grid is then capped at one
-// round of workgroups, which loop).
-static bool expand_flat(const RankClass& k) {
-  const int64_t est_tiles = (k.est_tokens + kTM - 1) / kTM + std::min<int64_t>(k.adapters, k.est_tokens);
-  return large_class(k) && est_tiles < 16;
+// device_ks = false: the host's k-split even for a sparse class (gs_shrink,
+// whose reduce into z must know it).
+static ShrinkPlan plan_class(int64_t T, int H, int S, const RankClass& k, bool bf16,
+                             int64_t max_part_bytes = INT64_MAX, bool device_ks = true) {
+  return plan_shrink(T, H, S, k.adapters, k.max_rank, bf16, k.est_tokens, large_class(k),
+                     device_ks && sparse_class(k), max_part_bytes);
 }
 
 }  // namespace gs
@@ -1017,6 +1232,7 @@ ShrinkParams make_shrink_params(const ShrinkPlan& pl, const void* x, int64_t ldx
   ShrinkParams p{};
   p.rw = rw;
   p.flat = pl.flat ? 1 : 0;
+  p.ks_target = pl.ks_target;
   p.x = x;
   p.ldx = ldx;
   p.H = hidden;
@@ -1144,8 +1360,48 @@ void launch_expand_pre(int max_tiles, size_t lds, const ExpandParams& p, hipStre
   else launch_expand_t<BF16, NBW, 8>(max_tiles, lds, p, st);
 }
 
+// The rank-split expand takes a sparse bf16 class whose sub-tiles of 128
+// columns never straddle a slice.
+bool sparse_expand_fits(bool bf16, const ExpandParams& p) {
+  if (!bf16 || p.max_rank > 4 * 8 * 16) return false;
+  for (int s = 0; s < p.si.S; ++s)
+    if ((p.si.bounds[s + 1] - p.si.bounds[s]) % kSpNT != 0) return false;
+  return true;
+}
+
+template <int KG>
+void launch_sparse_t(int max_tiles, ExpandParams p, hipStream_t st) {
+  auto kern = expand_sparse_kernel<KG>;
+  const size_t lds = static_cast<size_t>(kTM) * (p.max_rank + 8) * 2;
+  // workgroups resident per CU for this LDS size (one word: lds << 16 | count)
+  static std::atomic<uint64_t> occ{0};
+  uint64_t o = occ.load(std::memory_order_relaxed);
+  if (o == 0 || (o >> 16) != lds) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kern), kThreads, lds) != hipSuccess || n < 1) n = 1;
+    o = (static_cast<uint64_t>(lds) << 16) | static_cast<uint64_t>(std::min(n, 0xffff));
+    occ.store(o, std::memory_order_relaxed);
+  }
+  // one round of workgroups looping over the flat (tile, sub-tile) items
+  const int64_t n_sub = p.out_total / kSpNT;
+  const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(static_cast<int64_t>(o & 0xffff) * device_cus(),
+                                                              static_cast<int64_t>(max_tiles) * n_sub));
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(kThreads), lds, st, p);
+}
+
+void launch_expand_sparse(int64_t T, int adapters, const ExpandParams& p, hipStream_t st) {
+  const int max_tiles = max_tiles_for(T, adapters);
+  if (p.max_rank <= 4 * 2 * 16) launch_sparse_t<2>(max_tiles, p, st);
+  else if (p.max_rank <= 4 * 4 * 16) launch_sparse_t<4>(max_tiles, p, st);
+  else launch_sparse_t<8>(max_tiles, p, st);
+}
+
 // adapters: the launch's rank class (bounds its part-filled tiles)
 void launch_expand(bool bf16, int64_t T, int adapters, ExpandParams p, hipStream_t st) {
+  if (p.flat && sparse_expand_fits(bf16, p)) {
+    launch_expand_sparse(T, adapters, p, st);
+    return;
+  }
   const int max_tiles = max_tiles_for(T, adapters);
   // wider column tiles halve the z / partial reads per output byte, but
   // their lora_B registers grow with the rank: above rank 32 (bf16; 16 fp32
@@ -1220,7 +1476,8 @@ int switched_lora_impl(const char* who, int32_t dtype, const void* x, int64_t ld
                        int32_t num_slices, const void* a_pack, const int64_t* a_off, const void* b_pack,
                        const int64_t* b_off, const int32_t* ranks, int32_t num_adapters, int32_t max_rank,
                        const int32_t* ranks_host, const int32_t* seg_offsets, const int32_t* perm, void* z,
-                       void* workspace, int64_t workspace_bytes, void* stream) {
+                       void* workspace, int64_t workspace_bytes, void* stream,
+                       int64_t max_part_bytes = INT64_MAX) {
   int rc = check_common(who, dtype, num_tokens, num_slices, num_adapters, max_rank);
   if (rc != GS_OK) return rc;
   rc = check_shrink(dtype, x, ldx, hidden, a_pack);
@@ -1237,13 +1494,14 @@ int switched_lora_impl(const char* who, int32_t dtype, const void* x, int64_t ld
   if (num_tokens == 0) return GS_OK;
   const bool bf16 = dtype == GS_DTYPE_BF16;
   for (int c = 0; c < ncls; ++c) {
-    rc = check_workspace(plan_class(num_tokens, hidden, num_slices, cls[c], bf16), workspace, workspace_bytes);
+    rc = check_workspace(plan_class(num_tokens, hidden, num_slices, cls[c], bf16, max_part_bytes), workspace,
+                         workspace_bytes);
     if (rc != GS_OK) return rc;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   for (int c = 0; c < ncls; ++c) {
     const RankClass& k = cls[c];
-    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, k, bf16);
+    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, k, bf16, max_part_bytes);
     const int64_t ldz = static_cast<int64_t>(num_slices) * k.max_rank;
     const ShrinkParams sp = make_shrink_params(pl, x, ldx, hidden, a_pack, a_off, ranks, num_slices, num_adapters,
                                                seg_offsets, perm, z, ldz, workspace, num_tokens, k.rw);
@@ -1252,7 +1510,9 @@ int switched_lora_impl(const char* who, int32_t dtype, const void* x, int64_t ld
     ExpandParams e = ep;
     e.max_rank = k.max_rank;
     e.rw = k.rw;
-    e.flat = expand_flat(k) ? 1 : 0;
+    e.flat = pl.flat ? 1 : 0;
+    e.ks_target = pl.ks_target;
+    e.ks_chunks = pl.n_chunks;
     e.z = z;
     e.ldz = ldz;
     e.z_by_token = 0;
@@ -1297,7 +1557,7 @@ int32_t gs_shrink_ksplits(int32_t dtype, int64_t num_tokens, int32_t hidden, int
   rc = rank_classes("gs_shrink_ksplits", ranks_host, num_adapters, max_rank, num_tokens, cls, ncls);
   if (rc != GS_OK) return -rc;
   for (int c = 0; c < ncls; ++c)
-    ksplit[c] = plan_class(num_tokens, hidden, num_slices, cls[c], dtype == GS_DTYPE_BF16).KS;
+    ksplit[c] = plan_class(num_tokens, hidden, num_slices, cls[c], dtype == GS_DTYPE_BF16, INT64_MAX, false).KS;
   return ncls;
 }
 
@@ -1318,7 +1578,7 @@ int gs_shrink(int32_t dtype, const void* x, int64_t ldx, int64_t num_tokens, int
   if (rc != GS_OK) return rc;
   if (num_tokens == 0) return GS_OK;
   for (int c = 0; c < ncls; ++c) {
-    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, cls[c], bf16);
+    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, cls[c], bf16, INT64_MAX, false);
     GS_CHECK_ARG(z != nullptr || (pl.KS > 1 && ncls == 1),
                  "gs_shrink: z may be NULL only when the module is one rank class whose hidden dimension is split "
                  "(gs_shrink_ksplits)");
@@ -1328,7 +1588,7 @@ int gs_shrink(int32_t dtype, const void* x, int64_t ldx, int64_t num_tokens, int
   hipStream_t st = static_cast<hipStream_t>(stream);
   for (int c = 0; c < ncls; ++c) {
     const RankClass& k = cls[c];
-    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, k, bf16);
+    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, k, bf16, INT64_MAX, false);
     const ShrinkParams p = make_shrink_params(pl, x, ldx, hidden, a_pack, a_off, ranks, num_slices, num_adapters,
                                               seg_offsets, perm, z, ldz, workspace, num_tokens, k.rw);
     launch_shrink(bf16, pl, p, st);
@@ -1372,7 +1632,7 @@ int gs_expand_add(int32_t dtype, void* y, int64_t ldy, int64_t num_tokens, int32
     ExpandParams e = p;
     e.max_rank = cls[c].max_rank;
     e.rw = cls[c].rw;
-    e.flat = expand_flat(cls[c]) ? 1 : 0;
+    e.flat = sparse_class(cls[c]) ? 1 : 0;
     launch_expand(dtype == GS_DTYPE_BF16, num_tokens, cls[c].adapters, e, static_cast<hipStream_t>(stream));
     GS_CHECK_LAUNCH("gs_expand_add");
   }
@@ -1407,13 +1667,15 @@ int gs_switched_lora_noalloc(int32_t dtype, const void* x, int64_t ldx, void* y,
   // scratch layout: [split-K partials][z], each 256-byte aligned; the rank
   // classes run one after the other and share both
   int64_t part_need = 0, zrank = 0;
+  for (int c = 0; c < ncls; ++c) zrank = std::max<int64_t>(zrank, cls[c].max_rank);
+  const int64_t zbytes = num_tokens * int64_t(num_slices) * zrank * (dtype == GS_DTYPE_BF16 ? 2 : 4);
+  // a k-split chosen on the device is capped by what the array holds beside z
+  const int64_t part_budget = std::max<int64_t>(0, (kNoallocScratchBytes - zbytes) & ~int64_t(255));
   for (int c = 0; c < ncls; ++c) {
-    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, cls[c], dtype == GS_DTYPE_BF16);
+    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, cls[c], dtype == GS_DTYPE_BF16, part_budget);
     part_need = std::max(part_need, pl.part_bytes);
-    zrank = std::max<int64_t>(zrank, cls[c].max_rank);
   }
   const int64_t part = (part_need + 255) & ~int64_t(255);
-  const int64_t zbytes = num_tokens * int64_t(num_slices) * zrank * (dtype == GS_DTYPE_BF16 ? 2 : 4);
   if (part + zbytes > kNoallocScratchBytes) {
     set_error("%s: this shape needs %lld bytes of scratch (split-K partials %lld + z %lld); the static scratch "
               "holds %lld (use gs_switched_lora with a caller workspace)", who, (long long)(part + zbytes),
@@ -1425,7 +1687,7 @@ int gs_switched_lora_noalloc(int32_t dtype, const void* x, int64_t ldx, void* y,
   if (rc != GS_OK) return rc;
   return switched_lora_impl(who, dtype, x, ldx, y, ldy, num_tokens, hidden, out_total, slice_bounds, num_slices,
                             a_pack, a_off, b_pack, b_off, ranks, num_adapters, max_rank, ranks_host, seg_offsets, perm,
-                            base + part, base, part, stream);
+                            base + part, base, part, stream, part_budget);
 }
 
 }  // extern "C"
