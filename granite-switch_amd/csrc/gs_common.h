@@ -289,7 +289,7 @@ struct XcdItem {
   int tile;
   int sub;
 };
-__device__ __forceinline__ XcdItem xcd_item(int lin, int total_tiles, int nsub) {
+__host__ __device__ __forceinline__ XcdItem xcd_item(int lin, int total_tiles, int nsub) {
   const int tpx = (total_tiles + 7) >> 3;
   XcdItem it{-1, 0};
   if (tpx == 0) return it;
@@ -311,7 +311,7 @@ __device__ __forceinline__ XcdItem xcd_item(int lin, int total_tiles, int nsub) 
 // dealt to the XCDs round-robin -- fall on different XCDs: for a launch of a
 // few tiles with many subs each (a rank class of one large adapter), which
 // the XCD form would leave to one XCD.
-__device__ __forceinline__ XcdItem work_item(int lin, int total_tiles, int nsub, bool flat) {
+__host__ __device__ __forceinline__ XcdItem work_item(int lin, int total_tiles, int nsub, bool flat) {
   if (!flat) return xcd_item(lin, total_tiles, nsub);
   XcdItem it{-1, 0};
   if (lin >= 0 && lin < total_tiles * nsub) {
@@ -323,7 +323,7 @@ __device__ __forceinline__ XcdItem work_item(int lin, int total_tiles, int nsub,
 
 // Items a launch over `total_tiles` tiles must cover (ids at or past it have
 // no work in either form).
-__device__ __forceinline__ int work_items(int total_tiles, int nsub, bool flat) {
+__host__ __device__ __forceinline__ int work_items(int total_tiles, int nsub, bool flat) {
   return flat ? total_tiles * nsub : 8 * ((total_tiles + 7) >> 3) * nsub;
 }
 
@@ -331,7 +331,7 @@ __device__ __forceinline__ int work_items(int total_tiles, int nsub, bool flat) 
 // last tile shorter), or, with BAL, one of ceil(n / TM) tiles of near-equal
 // size (rows spread evenly, at most TM each).
 template <int TM, bool BAL>
-__device__ __forceinline__ void tile_span(int lo, int hi, int jj, int& slot0, int& nrows) {
+__host__ __device__ __forceinline__ void tile_span(int lo, int hi, int jj, int& slot0, int& nrows) {
   if constexpr (BAL) {
     const int n = hi - lo;
     const int nt = (n + TM - 1) / TM;

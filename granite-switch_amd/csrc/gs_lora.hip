@@ -11,10 +11,14 @@
 // writes fp32 partial sums; the consumer -- the expand kernel, or a small
 // reduce kernel when z itself is asked for -- adds the partials in a fixed
 // order, so results are deterministic and need no cross-XCD fences.
+#include <stdarg.h>
+
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <vector>
 
+#include "gs_addr.h"
 #include "gs_common.h"
 
 namespace gs {
@@ -81,7 +85,7 @@ struct ShrinkParams {
 // an estimate -- about `target` items, 1..KS_max -- so that a class holding
 // fewer tokens than expected still spreads over the GPU.  The expand of the
 // class computes the same value from the same count.
-__device__ __forceinline__ int dyn_ksplit(int tiles, int n_chunks, int target, int ks_max) {
+__host__ __device__ __forceinline__ int dyn_ksplit(int tiles, int n_chunks, int target, int ks_max) {
   const int w = tiles * n_chunks;
   int ks = w > 0 ? (target + w / 2) / w : ks_max;
   return ks < 1 ? 1 : (ks > ks_max ? ks_max : ks);
@@ -148,7 +152,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NB <= 
   // this lane's x row (slots past the tile re-read the tile's first token)
   const int srow = 16 * wave + i16;
   const bool row_ok = srow < tr.nrows;
-  const int token = p.perm[tr.slot0 + (row_ok ? srow : 0)];
+  const int token = p.perm[tr.slot0 + addr::tile_row(srow, tr.nrows)];
   // this thread's lora_A pieces: flat piece f = tid + 256*j of the COLS x PPR
   // batch tile is row tid/PPR + j*(256/PPR), piece tid % PPR of the row, so
   // PPR consecutive threads read one row's 512 contiguous bytes
@@ -166,7 +170,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NB <= 
 #pragma unroll
     for (int j = 0; j < APT; ++j) {
       const bool ok = j * RSTEP < arows && kp < k_hi;
-      av[j] = sel16(ok, ld16(abase + (ok ? j * astep + kp * ES : k_lo * ES)));
+      av[j] = sel16(ok, ld16(abase + addr::reg_a_elem(ok, j, astep / ES, kp, k_lo) * ES));
     }
   };
   // lora_A of the first batch goes out before the wait for the token index
@@ -179,7 +183,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NB <= 
     for (int pp = 0; pp < NPB; ++pp) {
       const int64_t kp = kb + pp * KSTEP + q4 * P;
       const bool ok = row_ok && kp < k_hi;
-      xv[pp] = sel16(ok, ld16(xrow + (ok ? kp : k_lo) * ES));
+      xv[pp] = sel16(ok, ld16(xrow + addr::reg_x_elem(ok, kp, k_lo) * ES));
     }
   };
   auto stage_a = [&](const u32x4 (&av)[APT]) {
@@ -311,26 +315,24 @@ __device__ __forceinline__ void shrink_dma_item(const ShrinkParams& p, const Til
   const int q4 = l >> 4;
   // k-chunk ks: stages [ks * all / KS, (ks + 1) * all / KS) of the all = H / 64
   // stages, so the chunks differ by at most one stage
-  const int all_st = p.H / kDmaBK;
-  const int s_lo = (ks * all_st) / KS;
-  const int nst = ((ks + 1) * all_st) / KS - s_lo;
+  int s_lo = 0, nst = 0;
+  addr::dma_kchunk(p.H, ks, KS, s_lo, nst);
   const int64_t k_lo = static_cast<int64_t>(s_lo) * kDmaBK;
 
   // this lane's source in each transfer: row 8t + l/8 of the wave's rows,
   // global piece (l % 8) ^ (row % 8), so LDS position l % 8 holds it swizzled
-  const int trow = l >> 3;
-  const int gpiece = ((l & 7) ^ trow) * 16;
+  const int trow = addr::dma_trow(l);
+  const int gpiece = addr::dma_gpiece_bytes(l);
   const char* xsrc[XT];
 #pragma unroll
   for (int t = 0; t < XT; ++t) {
-    const int r = 16 * wave + 8 * t + trow;
-    const int token = p.perm[tr.slot0 + (r < tr.nrows ? r : 0)];
+    const int token = p.perm[tr.slot0 + addr::tile_row(addr::dma_x_row(wave, t, trow), tr.nrows)];
     xsrc[t] = static_cast<const char*>(p.x) + (static_cast<int64_t>(token) * p.ldx + k_lo) * 2 + gpiece;
   }
   const char* asrc[AT];
 #pragma unroll
   for (int t = 0; t < AT; ++t) {
-    const int arow = min(col0 + ARW * wave + 8 * t + trow, ncols - 1);
+    const int arow = addr::dma_a_row(col0, ARW, wave, t, trow, ncols);
     asrc[t] = static_cast<const char*>(p.a_pack) + (tr.off + static_cast<int64_t>(arow) * p.H + k_lo) * 2 + gpiece;
   }
   auto issue = [&](int st) {
@@ -384,8 +386,8 @@ __device__ __forceinline__ void shrink_dma_item(const ShrinkParams& p, const Til
 #pragma unroll
   for (int it = 0; it < kTMS * PPR4 / kThreads; ++it) {
     const int pc = tid + it * kThreads;
-    const int row = pc / PPR4;
-    const int c4 = (pc % PPR4) * 4;
+    const int row = addr::dma_res_row(pc, PPR4);
+    const int c4 = addr::dma_res_col(pc, PPR4);
     if (row >= tr.nrows || c4 >= wcols) continue;
     const f32x4 v = *reinterpret_cast<const f32x4*>(res + row * OLD + c4);
     const int64_t slot = tr.slot0 + row;
@@ -541,8 +543,8 @@ __device__ __forceinline__ void z_stage(const ExpandParams& p, const TileRef& tr
   const int per_row = ((s_hi - s_lo + 1) * r) >> 2;
   const int items = kTM * per_row;
   for (int it = threadIdx.x; it < items; it += kThreads) {
-    const int row = it / per_row;
-    const int c4 = s_lo * r + (it - row * per_row) * 4;
+    const int row = addr::stage_row(it, per_row);
+    const int c4 = addr::stage_col(it, row, per_row, s_lo * r);
     float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (row < tr.nrows) {
       const int slot = tr.slot0 + row;
@@ -650,11 +652,11 @@ __device__ __forceinline__ void expand_item(const ExpandParams& p, const TileRef
   for (int ps = 0; ps < PASSES; ++ps) {
     const int row = ps * RPI + tid / LPR;
     rok[ps] = row < tr.nrows;
-    yrow[ps] = static_cast<int64_t>(p.perm[tr.slot0 + (rok[ps] ? row : 0)]) * p.ldy;
+    yrow[ps] = static_cast<int64_t>(p.perm[tr.slot0 + addr::tile_row(row, tr.nrows)]) * p.ldy;
   }
 
   auto load_y = [&](int sub, u32x4 (&yv)[PASSES]) {
-    const int64_t col = min(static_cast<int64_t>(sub) * NT + cx, static_cast<int64_t>(p.out_total) - EPL);
+    const int64_t col = addr::y_col(sub, NT, cx, p.out_total, EPL);
 #pragma unroll
     for (int ps = 0; ps < PASSES; ++ps) {
       const char* src = static_cast<const char*>(p.y) + (yrow[ps] + col) * Elt<BF16>::kSize;
@@ -665,13 +667,12 @@ __device__ __forceinline__ void expand_item(const ExpandParams& p, const TileRef
   auto load_b = [&](int sub, int kc, u32x4 (&bp)[NBW][PRE]) {
 #pragma unroll
     for (int q = 0; q < NBW; ++q) {
-      const int n = min(sub * NT + 32 * (wave * NBW + q) + i, p.out_total - 1);
+      const int n = addr::b_col(sub * NT + 32 * (wave * NBW + q) + i, p.out_total);
       const char* br = static_cast<const char*>(p.b_pack) + (tr.off + static_cast<int64_t>(n) * r) * Elt<BF16>::kSize;
 #pragma unroll
       for (int st = 0; st < PRE; ++st) {
         const int k0 = (kc * PRE + st) * KSTEP + KHALF * h;
-        const bool kin = k0 < r;
-        bp[q][st] = sel16(kin, ld16(br + (kin ? k0 : 0) * Elt<BF16>::kSize));
+        bp[q][st] = sel16(k0 < r, ld16(br + addr::k_or_zero(k0, r) * Elt<BF16>::kSize));
       }
     }
   };
@@ -728,14 +729,13 @@ __device__ __forceinline__ void expand_item(const ExpandParams& p, const TileRef
             for (int st = 0; st < PRE; ++st) bx[st] = bcur[q][st];
           } else {
             // ranks above PRE k-groups: the later groups are loaded here
-            const int n = min(n0 + i, p.out_total - 1);
+            const int n = addr::b_col(n0 + i, p.out_total);
             const char* br =
                 static_cast<const char*>(p.b_pack) + (tr.off + static_cast<int64_t>(n) * r) * Elt<BF16>::kSize;
 #pragma unroll
             for (int st = 0; st < PRE; ++st) {
               const int k0 = (kc * PRE + st) * KSTEP + KHALF * h;
-              const bool kin = k0 < r;
-              bx[st] = sel16(kin, ld16(br + (kin ? k0 : 0) * Elt<BF16>::kSize));
+              bx[st] = sel16(k0 < r, ld16(br + addr::k_or_zero(k0, r) * Elt<BF16>::kSize));
             }
           }
 #pragma unroll
@@ -761,7 +761,7 @@ __device__ __forceinline__ void expand_item(const ExpandParams& p, const TileRef
         // ranks above PRE k-groups: chunk kc + 1 of lora_B is loaded before
         // chunk kc is multiplied, so two chunks are in flight (the last
         // iteration re-reads its own chunk: no branch around the loads)
-        const int n = min(n0 + i, p.out_total - 1);
+        const int n = addr::b_col(n0 + i, p.out_total);
         const char* br = static_cast<const char*>(p.b_pack) + (tr.off + static_cast<int64_t>(n) * r) * Elt<BF16>::kSize;
         u32x4 bx[PRE];
 #pragma unroll
@@ -772,8 +772,7 @@ __device__ __forceinline__ void expand_item(const ExpandParams& p, const TileRef
 #pragma unroll
           for (int st = 0; st < PRE; ++st) {
             const int k0 = (kn * PRE + st) * KSTEP + KHALF * h;
-            const bool kin = k0 < r;
-            bnx[st] = sel16(kin, ld16(br + (kin ? k0 : 0) * Elt<BF16>::kSize));
+            bnx[st] = sel16(k0 < r, ld16(br + addr::k_or_zero(k0, r) * Elt<BF16>::kSize));
           }
           mma(kc, bx);
 #pragma unroll
@@ -925,8 +924,7 @@ __global__ __launch_bounds__(kThreads) void expand_sparse_kernel(ExpandParams p)
 #pragma unroll
         for (int kg = 0; kg < KG; ++kg) {
           const int k0 = (wave * KG + kg) * KSTEP + KHALF * h;
-          const bool kin = k0 < r;
-          bv[q][kg] = sel16(kin, ld16(br + (kin ? k0 : 0) * 2));
+          bv[q][kg] = sel16(k0 < r, ld16(br + addr::k_or_zero(k0, r) * 2));
         }
       }
       // y pieces of the item's rows (rows past the tile re-read its first token)
@@ -937,7 +935,7 @@ __global__ __launch_bounds__(kThreads) void expand_sparse_kernel(ExpandParams p)
       for (int ps = 0; ps < PASSES; ++ps) {
         const int row = ps * RPI + tid / LPR;
         rok[ps] = row < tr.nrows;
-        yrow[ps] = static_cast<int64_t>(p.perm[tr.slot0 + (rok[ps] ? row : 0)]) * p.ldy;
+        yrow[ps] = static_cast<int64_t>(p.perm[tr.slot0 + addr::tile_row(row, tr.nrows)]) * p.ldy;
         yv[ps] = ld16(static_cast<const char*>(p.y) + (yrow[ps] + n_tile0 + cx) * 2);
       }
       // the slice's shrink values of the tile's rows: split-K partials summed
@@ -946,8 +944,8 @@ __global__ __launch_bounds__(kThreads) void expand_sparse_kernel(ExpandParams p)
       const int zo = (p.z_off != nullptr) ? p.z_off[tr.g] : 0;
       const int per_row = r >> 2;
       for (int it = tid; it < kTM * per_row; it += kThreads) {
-        const int row = it / per_row;
-        const int c4 = (it - row * per_row) * 4;
+        const int row = addr::stage_row(it, per_row);
+        const int c4 = addr::stage_col(it, row, per_row, 0);
         float v[4] = {0.f, 0.f, 0.f, 0.f};
         if (row < tr.nrows) {
           const int slot = tr.slot0 + row;
@@ -1322,6 +1320,23 @@ int prepare_expand(ExpandParams& p, const char* who, int32_t dtype, void* y, int
   return GS_OK;
 }
 
+// Workgroups of a column-split expand launch: the items never exceed wt (or
+// one per tile slot when the tiles alone exceed it) nor one per (tile slot,
+// sub-tile); a flat launch is one round of workgroups that loop over its
+// (tile, sub-tile) items.
+int64_t expand_grid(int64_t wt, int max_tiles, int64_t n_sub, bool flat) {
+  const int64_t t8 = 8 * ((static_cast<int64_t>(max_tiles) + 7) / 8);
+  const int64_t items = flat ? std::min<int64_t>(wt, static_cast<int64_t>(max_tiles) * n_sub)
+                             : std::min<int64_t>(std::max(wt, t8), t8 * n_sub);
+  return (items + 7) / 8 * 8;
+}
+
+// Workgroups of a rank-split (sparse) expand launch: one round, at most one
+// per (tile slot, sub-tile).
+int64_t sparse_grid(int64_t wt, int max_tiles, int64_t n_sub) {
+  return std::max<int64_t>(1, std::min<int64_t>(wt, static_cast<int64_t>(max_tiles) * n_sub));
+}
+
 template <bool BF16, int NBW, int PRE>
 void launch_expand_t(int max_tiles, size_t lds, ExpandParams p, hipStream_t st) {
   auto kern = p.flat ? expand_kernel<BF16, NBW, PRE, true> : expand_kernel<BF16, NBW, PRE, false>;
@@ -1339,15 +1354,8 @@ void launch_expand_t(int max_tiles, size_t lds, ExpandParams p, hipStream_t st) 
     occ.store(o, std::memory_order_relaxed);
   }
   p.wt = static_cast<int>(o & 0xffff) * device_cus();
-  // the items never exceed wt (or one per tile slot when the tiles alone
-  // exceed it) nor one per (tile slot, sub-tile); a flat launch is one round
-  // of workgroups that loop over its (tile, sub-tile) items
-  const int t8 = 8 * ((max_tiles + 7) / 8);
   constexpr int NT = 4 * NBW * 32;
-  const int64_t n_sub = (p.out_total + NT - 1) / NT;
-  const int64_t items = p.flat ? std::min<int64_t>(p.wt, static_cast<int64_t>(max_tiles) * n_sub)
-                               : std::min<int64_t>(std::max(p.wt, t8), static_cast<int64_t>(t8) * n_sub);
-  const int grid = static_cast<int>((items + 7) / 8 * 8);
+  const int grid = static_cast<int>(expand_grid(p.wt, max_tiles, (p.out_total + NT - 1) / NT, p.flat != 0));
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, st, p);
 }
 
@@ -1383,9 +1391,7 @@ void launch_sparse_t(int max_tiles, ExpandParams p, hipStream_t st) {
     occ.store(o, std::memory_order_relaxed);
   }
   // one round of workgroups looping over the flat (tile, sub-tile) items
-  const int64_t n_sub = p.out_total / kSpNT;
-  const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(static_cast<int64_t>(o & 0xffff) * device_cus(),
-                                                              static_cast<int64_t>(max_tiles) * n_sub));
+  const int64_t grid = sparse_grid(static_cast<int64_t>(o & 0xffff) * device_cus(), max_tiles, p.out_total / kSpNT);
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(kThreads), lds, st, p);
 }
 
@@ -1396,30 +1402,401 @@ void launch_expand_sparse(int64_t T, int adapters, const ExpandParams& p, hipStr
   else launch_sparse_t<8>(max_tiles, p, st);
 }
 
-// adapters: the launch's rank class (bounds its part-filled tiles)
-void launch_expand(bool bf16, int64_t T, int adapters, ExpandParams p, hipStream_t st) {
+// Which expand form a launch takes (shared by the launch and the address
+// model): the rank-split form for a sparse bf16 class, else the column-split
+// form with NBW 32-column blocks per wave and PRE k-groups of lora_B in
+// registers.
+struct ExpandForm {
+  bool sparse;
+  int NBW, PRE, KG;
+};
+ExpandForm expand_form(bool bf16, int64_t T, const ExpandParams& p) {
+  ExpandForm f{false, 1, 2, 0};
   if (p.flat && sparse_expand_fits(bf16, p)) {
-    launch_expand_sparse(T, adapters, p, st);
-    return;
+    f.sparse = true;
+    f.KG = p.max_rank <= 4 * 2 * 16 ? 2 : (p.max_rank <= 4 * 4 * 16 ? 4 : 8);
+    return f;
   }
-  const int max_tiles = max_tiles_for(T, adapters);
   // wider column tiles halve the z / partial reads per output byte, but
   // their lora_B registers grow with the rank: above rank 32 (bf16; 16 fp32
   // k per group) the wide kernel drops to 2 or 1 resident waves per SIMD and
   // the narrow one streams faster (multiswitch down, ranks to 64: expand
   // 21.5 -> 16.7 us)
   const int kstep = bf16 ? 16 : 8;
-  const bool wide = (T >= 2048 || p.nparts > 1) && (p.max_rank + kstep - 1) / kstep <= 2;
+  const int need = (p.max_rank + kstep - 1) / kstep;
+  f.NBW = ((T >= 2048 || p.nparts > 1) && need <= 2) ? 2 : 1;
+  f.PRE = need <= 2 ? 2 : (need <= 4 ? 4 : 8);
+  return f;
+}
+
+// adapters: the launch's rank class (bounds its part-filled tiles)
+void launch_expand(bool bf16, int64_t T, int adapters, ExpandParams p, hipStream_t st) {
+  const ExpandForm f = expand_form(bf16, T, p);
+  if (f.sparse) {
+    launch_expand_sparse(T, adapters, p, st);
+    return;
+  }
+  const int max_tiles = max_tiles_for(T, adapters);
   const size_t lds = expand_lds_bytes(bf16, p.si.S, p.max_rank);
   if (bf16) {
-    if (wide) launch_expand_pre<true, 2>(max_tiles, lds, p, st);
+    if (f.NBW == 2) launch_expand_pre<true, 2>(max_tiles, lds, p, st);
     else launch_expand_pre<true, 1>(max_tiles, lds, p, st);
   } else {
-    if (wide) launch_expand_pre<false, 2>(max_tiles, lds, p, st);
+    if (f.NBW == 2) launch_expand_pre<false, 2>(max_tiles, lds, p, st);
     else launch_expand_pre<false, 1>(max_tiles, lds, p, st);
   }
 }
 
+
+// ----------------------------------------------------------------------------
+// Address model (test support): replays the global and LDS accesses of the
+// segment kernels on the host, with the launch plans and the addr:: formulas
+// the kernels use, for every workgroup, wave, lane and loop step of every
+// launch a call makes, and checks each access against its buffer.  It also
+// checks that the launches cover every item of the batch (a one-item grid
+// smaller than the items would skip work).  No HIP call is made.
+// ----------------------------------------------------------------------------
+struct AddrModel {
+  // the call
+  bool bf16;
+  int64_t T;
+  int H;
+  int64_t ldx;
+  int out_total;
+  int64_t ldy;
+  SliceInfo si;
+  const int32_t* ranks;     // host copies of the module tables
+  const int64_t* a_off;
+  const int64_t* b_off;
+  int64_t a_elems, b_elems;
+  int NA;
+  int max_rank;
+  const int32_t* seg;
+  const int32_t* perm;
+  int64_t perm_len;
+  // outcome
+  int64_t checked = 0;
+  int64_t bad = 0;
+  char msg[512] = {0};
+
+  int es() const { return bf16 ? 2 : 4; }
+  void fail(const char* fmt, ...) {
+    ++bad;
+    if (bad > 1) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(msg, sizeof msg, fmt, ap);
+    va_end(ap);
+  }
+  // [lo, lo + len) inside [0, size)?
+  bool in(const char* what, int64_t lo, int64_t len, int64_t size) {
+    ++checked;
+    if (lo < 0 || len < 0 || lo + len > size) {
+      fail("%s: [%lld, %lld) outside [0, %lld)", what, (long long)lo, (long long)(lo + len), (long long)size);
+      return false;
+    }
+    return true;
+  }
+  int token_at(int64_t slot_idx) {
+    if (!in("perm", slot_idx, 1, perm_len)) return 0;
+    const int tok = perm[slot_idx];
+    in("token", tok, 1, T);
+    return tok;
+  }
+  // a 16-byte (or len-byte) piece of row `tok` of a [T, ld] matrix whose rows hold `cols` valid elements
+  void row_piece(const char* what, int64_t tok, int64_t elem, int64_t n_elems, int64_t cols) {
+    in(what, elem, n_elems, cols);
+    (void)tok;
+  }
+  // an adapter's block [off, off + rows * cols) inside a pack of `elems` elements
+  void pack_piece(const char* what, int64_t off, int64_t rows, int64_t cols, int64_t elem, int64_t n, int64_t elems) {
+    in(what, elem - off, n, rows * cols);
+    in(what, elem, n, elems);
+  }
+
+  template <int TM, bool BAL>
+  std::vector<TileRef> tiles(RankWindow rw, const int64_t* offs) const {
+    std::vector<TileRef> v;
+    for (int g = 1; g <= NA; ++g) {
+      if (!in_window(rw, ranks[g])) continue;
+      const int lo = seg[g - 1], hi = seg[g];
+      const int nt = (hi - lo + TM - 1) / TM;
+      for (int jj = 0; jj < nt; ++jj) {
+        TileRef t{g, 0, 0, ranks[g], offs[g]};
+        tile_span<TM, BAL>(lo, hi, jj, t.slot0, t.nrows);
+        v.push_back(t);
+      }
+    }
+    return v;
+  }
+
+  // Items processed by a grid: one per workgroup (loop = false) or
+  // blockIdx.x, + grid, ... (loop = true); every real item must be taken
+  // exactly once.
+  template <typename F>
+  void for_items(const char* who, int64_t grid, bool loop, int items, F&& fn) {
+    int64_t seen = 0;
+    for (int64_t b = 0; b < grid; ++b) {
+      for (int64_t lin = b; lin < items; lin += grid) {
+        fn(static_cast<int>(lin));
+        ++seen;
+        if (!loop) break;
+      }
+    }
+    if (seen != items) fail("%s: the grid of %lld workgroups takes %lld of %d items", who, (long long)grid,
+                            (long long)seen, items);
+  }
+
+  // ---- shrink_dma_kernel ----------------------------------------------------
+  void shrink_dma(const ShrinkPlan& pl, RankWindow rw, int64_t ldz, int64_t z_elems, int64_t part_elems) {
+    const std::vector<TileRef> tl = tiles<kTMS, false>(rw, a_off);
+    const int total = static_cast<int>(tl.size());
+    const int KS = pl.ks_target > 0 ? dyn_ksplit(total, pl.n_chunks, pl.ks_target, pl.KS) : pl.KS;
+    const int nsub = pl.n_chunks * KS;
+    const bool flat = pl.loop && pl.flat;
+    const int COLS = 32 * pl.NB, ARW = COLS / 4, XT = kTMS / 4 / 8, AT = ARW / 8;
+    const int NST = pl.NB == 1 ? GS_DMA_NST1 : (pl.NB == 2 ? GS_DMA_NST2 : (pl.NB == 3 ? GS_DMA_NST3 : GS_DMA_NST4));
+    const int64_t stage = static_cast<int64_t>(kTMS + COLS) * kDmaRow, ring = NST * stage;
+    const int64_t zw = pl.zw;
+    for_items("shrink_dma_kernel", pl.grid, pl.loop, work_items(total, nsub, flat), [&](int lin) {
+      const XcdItem it = work_item(lin, total, nsub, flat);
+      if (it.tile < 0) return;
+      const TileRef& tr = tl[it.tile];
+      const int chunk = it.sub % pl.n_chunks, ks = it.sub / pl.n_chunks;
+      const int ncols = si.S * tr.rank, col0 = chunk * COLS;
+      if (col0 >= ncols) return;
+      int s_lo = 0, nst = 0;
+      addr::dma_kchunk(H, ks, KS, s_lo, nst);
+      in("shrink k-chunk", static_cast<int64_t>(s_lo) * kDmaBK, static_cast<int64_t>(nst) * kDmaBK, H);
+      const int64_t k_lo = static_cast<int64_t>(s_lo) * kDmaBK;
+      for (int wave = 0; wave < 4; ++wave)
+        for (int l = 0; l < 64; ++l) {
+          const int trow = addr::dma_trow(l);
+          const int64_t gp = addr::dma_gpiece_bytes(l) / 2;
+          for (int t = 0; t < XT; ++t) {
+            const int tok = token_at(tr.slot0 + addr::tile_row(addr::dma_x_row(wave, t, trow), tr.nrows));
+            for (int st = 0; st < nst; ++st) row_piece("shrink x", tok, k_lo + st * 64 + gp, 8, H);
+            in("shrink x ring", (NST - 1) * stage + (16 * wave + 8 * t) * kDmaRow + 16 * l, 16, ring);
+          }
+          for (int t = 0; t < AT; ++t) {
+            const int arow = addr::dma_a_row(col0, ARW, wave, t, trow, ncols);
+            for (int st = 0; st < nst; ++st)
+              pack_piece("shrink lora_A", tr.off, ncols, H, tr.off + static_cast<int64_t>(arow) * H + k_lo + st * 64 + gp,
+                         8, a_elems);
+            in("shrink A ring", (NST - 1) * stage + (kTMS + ARW * wave + 8 * t) * kDmaRow + 16 * l, 16, ring);
+          }
+        }
+      const int PPR4 = COLS / 4, wcols = std::min(COLS, ncols - col0);
+      in("shrink staged results", 0, static_cast<int64_t>(kTMS) * (COLS + 4) * 4, ring);
+      for (int tid = 0; tid < kThreads; ++tid)
+        for (int k = 0; k < kTMS * PPR4 / kThreads; ++k) {
+          const int pc = tid + k * kThreads;
+          const int row = addr::dma_res_row(pc, PPR4), c4 = addr::dma_res_col(pc, PPR4);
+          if (row >= tr.nrows || c4 >= wcols) continue;
+          const int64_t slot = tr.slot0 + row;
+          if (KS == 1) {
+            in("shrink z column", col0 + c4, 4, ldz);
+            in("shrink z", slot * ldz + col0 + c4, 4, z_elems);
+          } else {
+            in("shrink partial column", col0 + c4, 4, zw);
+            in("shrink partials", ks * T * zw + slot * zw + col0 + c4, 4, part_elems);
+          }
+        }
+    });
+  }
+
+  // ---- shrink_kernel (register form) ----------------------------------------
+  void shrink_reg(const ShrinkPlan& pl, RankWindow rw, int64_t ldz, int64_t z_elems, int64_t part_elems) {
+    const std::vector<TileRef> tl = tiles<kTMS, false>(rw, a_off);
+    const int total = static_cast<int>(tl.size());
+    const int nsub = pl.n_chunks * pl.KS;
+    const int P = bf16 ? 8 : 4, KSTEP = 4 * P, NPB = 8, BK = NPB * KSTEP, COLS = 32 * pl.NB;
+    const int PPR = BK * es() / 16, RSTEP = kThreads / PPR, APT = COLS * PPR / kThreads;
+    for_items("shrink_kernel", pl.grid, false, work_items(total, nsub, false), [&](int lin) {
+      const XcdItem it = work_item(lin, total, nsub, false);
+      if (it.tile < 0) return;
+      const TileRef& tr = tl[it.tile];
+      const int chunk = it.sub % pl.n_chunks, ks = it.sub / pl.n_chunks;
+      const int ncols = si.S * tr.rank, col0 = chunk * COLS;
+      if (col0 >= ncols) return;
+      const int64_t k_lo = static_cast<int64_t>(ks) * pl.KC;
+      const int64_t k_hi = std::min<int64_t>(H, k_lo + pl.KC);
+      const int nbat = static_cast<int>((k_hi - k_lo + BK - 1) / BK);
+      for (int tid = 0; tid < kThreads; ++tid) {
+        const int wave = tid >> 6, l = tid & 63, i16 = l & 15, q4 = l >> 4;
+        const int srow = 16 * wave + i16;
+        const bool row_ok = srow < tr.nrows;
+        const int tok = token_at(tr.slot0 + addr::tile_row(srow, tr.nrows));
+        const int ar0 = tid / PPR, apc = tid % PPR, arows = ncols - col0 - ar0;
+        const int64_t abase = tr.off + static_cast<int64_t>(col0 + ar0) * H;
+        for (int b = 0; b <= nbat; ++b) {          // b = nbat: the prefetch past the chunk (masked)
+          const int64_t kp_a = k_lo + static_cast<int64_t>(b) * BK + apc * P;
+          for (int j = 0; j < APT; ++j) {
+            const bool ok = j * RSTEP < arows && kp_a < k_hi;
+            pack_piece("shrink lora_A", tr.off, ncols, H, abase + addr::reg_a_elem(ok, j, int64_t(RSTEP) * H, kp_a, k_lo),
+                       P, a_elems);
+          }
+          for (int pp = 0; pp < NPB; ++pp) {
+            const int64_t kp = k_lo + static_cast<int64_t>(b) * BK + pp * KSTEP + q4 * P;
+            const bool ok = row_ok && kp < k_hi;
+            row_piece("shrink x", tok, addr::reg_x_elem(ok, kp, k_lo), P, H);
+          }
+        }
+        for (int c = 0; c < COLS / 16; ++c) {
+          const int col = col0 + 16 * c + i16;
+          if (col >= ncols) continue;
+          for (int e = 0; e < 4; ++e) {
+            const int row = 16 * wave + 4 * q4 + e;
+            if (row >= tr.nrows) continue;
+            const int64_t slot = tr.slot0 + row;
+            if (pl.KS == 1) in("shrink z", slot * ldz + col, 1, z_elems);
+            else in("shrink partials", ks * T * pl.zw + slot * pl.zw + col, 1, part_elems);
+          }
+        }
+      }
+    });
+  }
+
+  // ---- reduce_parts_kernel ---------------------------------------------------
+  void reduce(const ShrinkPlan& pl, RankWindow rw, int64_t ldz, int64_t z_elems, int64_t part_elems) {
+    const int64_t n8 = T * pl.zw / 8;
+    const int64_t blocks = (n8 + kThreads - 1) / kThreads;
+    for (int64_t e = 0; e < blocks * kThreads; ++e) {
+      const int64_t e8 = e * 8, slot = e8 / pl.zw;
+      const int col = static_cast<int>(e8 % pl.zw);
+      if (!in("reduce seg", NA, 1, NA + 1) || slot >= seg[NA]) continue;
+      int glo = 1, ghi = NA;
+      while (glo < ghi) {
+        const int mid = (glo + ghi) >> 1;
+        if (seg[mid] > slot) ghi = mid;
+        else glo = mid + 1;
+      }
+      if (!in_window(rw, ranks[glo])) continue;
+      for (int ks = 0; ks < pl.KS; ++ks) in("reduce partials", ks * T * pl.zw + slot * pl.zw + col, 8, part_elems);
+      in("reduce z", slot * ldz + col, 8, z_elems);
+    }
+  }
+
+  // ---- expand_kernel and expand_sparse_kernel --------------------------------
+  // z source: partials [nparts][T][zw] (nparts > 0), else z [z_rows, ldz]
+  // by slot or by token (z_by_token), columns from z_off[g].
+  void expand(const ExpandParams& e, const ExpandForm& f, int adapters, int64_t wt, int64_t z_elems,
+              int64_t part_elems, const int32_t* z_off) {
+    const bool flat = e.flat != 0;
+    const int max_tiles = max_tiles_for(T, adapters);
+    const std::vector<TileRef> tl = tiles<kTM, kExpandBalanced>(e.rw, b_off);
+    const int total = static_cast<int>(tl.size());
+    int nparts = e.nparts;
+    if (flat && e.ks_target > 0) {
+      const int ks = dyn_ksplit(static_cast<int>(tiles<kTMS, false>(e.rw, a_off).size()), e.ks_chunks, e.ks_target,
+                                e.nparts);
+      nparts = ks > 1 ? ks : 0;
+    }
+    const int ES = es(), EPL = 16 / ES;
+    auto stage = [&](const TileRef& tr, int s_lo, int s_hi, int col_base_of_slice0, int64_t zs_ld, int64_t lds) {
+      const int r = tr.rank, zo = z_off ? z_off[tr.g] : 0;
+      const int per_row = ((s_hi - s_lo + 1) * r) >> 2;
+      for (int it = 0; it < kTM * per_row; ++it) {
+        const int row = addr::stage_row(it, per_row);
+        const int c4 = addr::stage_col(it, row, per_row, col_base_of_slice0);
+        in("expand staged shrink values", (row * zs_ld + c4) * ES, 4 * ES, lds);
+        if (row >= tr.nrows) continue;
+        const int64_t slot = tr.slot0 + row;
+        const int zc = c4 + (s_lo * r - col_base_of_slice0);   // the value's column in the adapter's S*r
+        if (nparts > 0) {
+          in("expand partial column", zc, 4, e.zw);
+          for (int ks = 0; ks < nparts; ++ks) in("expand partials", ks * e.part_stride + slot * e.zw + zc, 4, part_elems);
+        } else {
+          const int64_t zrow = e.z_by_token ? token_at(slot) : slot;
+          in("expand z column", zo + zc, 4, e.ldz);
+          in("expand z", zrow * e.ldz + zo + zc, 4, z_elems);
+        }
+      }
+    };
+    if (f.sparse) {
+      const int64_t n_sub = out_total / kSpNT;
+      const int64_t zs_ld = e.max_rank + 8, lds = kTM * zs_ld * 2;
+      const int LPR = kSpNT / 8, RPI = kThreads / LPR, PASSES = kTM / RPI;
+      for_items("expand_sparse_kernel", sparse_grid(wt, max_tiles, n_sub), true,
+                work_items(total, static_cast<int>(n_sub), true), [&](int lin) {
+        const XcdItem it = work_item(lin, total, static_cast<int>(n_sub), true);
+        if (it.tile < 0) return;
+        const TileRef& tr = tl[it.tile];
+        const int r = tr.rank, n_tile0 = it.sub * kSpNT;
+        int s = 0;
+        while (s + 1 < si.S && n_tile0 >= si.bounds[s + 1]) ++s;
+        in("sparse sub-tile inside its slice", n_tile0 - si.bounds[s], kSpNT, si.bounds[s + 1] - si.bounds[s]);
+        for (int wave = 0; wave < 4; ++wave)
+          for (int l = 0; l < 64; ++l) {
+            const int i = l & 31, h = l >> 5;
+            for (int q = 0; q < 4; ++q) {
+              const int64_t n = n_tile0 + 32 * q + i;
+              in("sparse lora_B column", n, 1, out_total);
+              for (int kg = 0; kg < f.KG; ++kg) {
+                const int k0 = (wave * f.KG + kg) * 16 + 8 * h;
+                pack_piece("sparse lora_B", tr.off, out_total, r, tr.off + n * r + addr::k_or_zero(k0, r), 8, b_elems);
+                in("sparse staged read", (static_cast<int64_t>(i) * zs_ld + addr::k_or_zero(k0, r)) * 2, 16, lds);
+              }
+            }
+          }
+        for (int tid = 0; tid < kThreads; ++tid)
+          for (int ps = 0; ps < PASSES; ++ps) {
+            const int row = ps * RPI + tid / LPR, cx = (tid % LPR) * 8;
+            const int tok = token_at(tr.slot0 + addr::tile_row(row, tr.nrows));
+            row_piece("sparse y", tok, n_tile0 + cx, 8, out_total);
+          }
+        stage(tr, s, s, 0, zs_ld, lds);
+      });
+      return;
+    }
+    const int NT = 4 * f.NBW * 32, n_sub = (out_total + NT - 1) / NT;
+    const int KSTEP = bf16 ? 16 : 8, KHALF = KSTEP / 2;
+    const int LPR = NT / EPL, RPI = kThreads / LPR, PASSES = kTM / RPI;
+    const int64_t zs_ld = static_cast<int64_t>(si.S) * e.max_rank + 8, lds = kTM * zs_ld * ES;
+    const int groups = flat ? n_sub : expand_groups(total, n_sub, static_cast<int>(wt));
+    for_items("expand_kernel", expand_grid(wt, max_tiles, n_sub, flat), flat, work_items(total, groups, flat),
+              [&](int lin) {
+      const XcdItem it = work_item(lin, total, groups, flat);
+      if (it.tile < 0) return;
+      const TileRef& tr = tl[it.tile];
+      const int r = tr.rank;
+      const int sub0 = (it.sub * n_sub) / groups, nsub = ((it.sub + 1) * n_sub) / groups - sub0;
+      if (nsub <= 0) return;
+      const int nchunk = (r + f.PRE * KSTEP - 1) / (f.PRE * KSTEP);
+      for (int sb = sub0; sb < sub0 + nsub; ++sb) {
+        for (int wave = 0; wave < 4; ++wave)
+          for (int l = 0; l < 64; ++l) {
+            const int i = l & 31, h = l >> 5;
+            for (int q = 0; q < f.NBW; ++q) {
+              const int n0 = sb * NT + 32 * (wave * f.NBW + q);
+              const int n = addr::b_col(n0 + i, out_total);
+              int s = 0;
+              while (s + 1 < si.S && n0 >= si.bounds[s + 1]) ++s;
+              for (int kc = 0; kc < nchunk; ++kc)
+                for (int st = 0; st < f.PRE; ++st) {
+                  const int k0 = (kc * f.PRE + st) * KSTEP + KHALF * h;
+                  pack_piece("expand lora_B", tr.off, out_total, r,
+                             tr.off + static_cast<int64_t>(n) * r + addr::k_or_zero(k0, r), EPL, b_elems);
+                  in("expand staged read", (i * zs_ld + s * r + addr::k_or_zero(k0, r)) * ES, 16, lds);
+                }
+            }
+          }
+        for (int tid = 0; tid < kThreads; ++tid)
+          for (int ps = 0; ps < PASSES; ++ps) {
+            const int row = ps * RPI + tid / LPR, cx = (tid % LPR) * EPL;
+            const int tok = token_at(tr.slot0 + addr::tile_row(row, tr.nrows));
+            row_piece("expand y", tok, addr::y_col(sb, NT, cx, out_total, EPL), EPL, out_total);
+          }
+      }
+      int s_lo = 0, s_hi = 0;
+      const int c_first = sub0 * NT, c_last = std::min((sub0 + nsub) * NT, out_total) - 1;
+      while (s_lo + 1 < si.S && c_first >= si.bounds[s_lo + 1]) ++s_lo;
+      s_hi = s_lo;
+      while (s_hi + 1 < si.S && c_last >= si.bounds[s_hi + 1]) ++s_hi;
+      stage(tr, s_lo, s_hi, s_lo * r, zs_ld, lds);
+    });
+  }
+};
 }  // namespace
 
 // ----------------------------------------------------------------------------
@@ -1688,6 +2065,116 @@ int gs_switched_lora_noalloc(int32_t dtype, const void* x, int64_t ldx, void* y,
   return switched_lora_impl(who, dtype, x, ldx, y, ldy, num_tokens, hidden, out_total, slice_bounds, num_slices,
                             a_pack, a_off, b_pack, b_off, ranks, num_adapters, max_rank, ranks_host, seg_offsets, perm,
                             base + part, base, part, stream, part_budget);
+}
+
+int64_t gs_check_segment_addresses(int32_t dtype, int64_t num_tokens, int32_t hidden, int64_t ldx, int32_t out_total,
+                                   int64_t ldy, const int32_t* slice_bounds, int32_t num_slices, const int64_t* a_off,
+                                   int64_t a_pack_elems, const int64_t* b_off, int64_t b_pack_elems,
+                                   const int32_t* ranks, int32_t num_adapters, int32_t max_rank,
+                                   const int32_t* seg_offsets, const int32_t* perm, const int32_t* z_off,
+                                   int64_t z_ld, char* msg, int64_t msg_len, int64_t* checked) {
+  const char* who = "gs_check_segment_addresses";
+  int rc = check_common(who, dtype, num_tokens, num_slices, num_adapters, max_rank);
+  if (rc != GS_OK) return -rc;
+  GS_CHECK_ARG(hidden > 0 && ldx >= hidden && out_total > 0 && ldy >= out_total, "%s: shape", who);
+  GS_CHECK_ARG(slice_bounds && a_off && b_off && ranks && seg_offsets && (perm || num_tokens == 0), "%s: NULL table",
+               who);
+  const bool bf16 = dtype == GS_DTYPE_BF16;
+  AddrModel m{};
+  m.bf16 = bf16;
+  m.T = num_tokens;
+  m.H = hidden;
+  m.ldx = ldx;
+  m.out_total = out_total;
+  m.ldy = ldy;
+  m.si.S = num_slices;
+  for (int s = 0; s <= num_slices; ++s) m.si.bounds[s] = slice_bounds[s];
+  m.ranks = ranks;
+  m.a_off = a_off;
+  m.b_off = b_off;
+  m.a_elems = a_pack_elems;
+  m.b_elems = b_pack_elems;
+  m.NA = num_adapters;
+  m.max_rank = max_rank;
+  m.seg = seg_offsets;
+  m.perm = perm;
+  m.perm_len = num_tokens > 0 ? num_tokens : 1;
+  RankClass cls[2];
+  int ncls = 0;
+  rc = rank_classes(who, ranks, num_adapters, max_rank, num_tokens, cls, ncls);
+  if (rc != GS_OK) return -rc;
+  const int64_t T = num_tokens;
+  const int cus = device_cus();
+  const int64_t z_elems = std::max<int64_t>(T, 1) * num_slices * max_rank;   // z as switched.py allocates it
+  const int64_t ws_elems = gs_shrink_workspace_bytes(T, hidden, num_slices, num_adapters, max_rank, ranks) / 4;
+  if (T > 0) {
+    // gs_switched_lora (caller workspace) and gs_switched_lora_noalloc (the
+    // static array: the partial budget left beside z)
+    for (int noalloc = 0; noalloc < 2; ++noalloc) {
+      int64_t budget = INT64_MAX, zrank = 0;
+      for (int c = 0; c < ncls; ++c) zrank = std::max<int64_t>(zrank, cls[c].max_rank);
+      const int64_t zbytes = T * int64_t(num_slices) * zrank * (bf16 ? 2 : 4);
+      if (noalloc) {
+        budget = std::max<int64_t>(0, (kNoallocScratchBytes - zbytes) & ~int64_t(255));
+        int64_t part = 0;
+        for (int c = 0; c < ncls; ++c)
+          part = std::max(part, plan_class(T, hidden, num_slices, cls[c], bf16, budget).part_bytes);
+        if (((part + 255) & ~int64_t(255)) + zbytes > kNoallocScratchBytes) continue;   // rejected by the call
+      }
+      for (int c = 0; c < ncls; ++c) {
+        const RankClass& k = cls[c];
+        const ShrinkPlan pl = plan_class(T, hidden, num_slices, k, bf16, budget);
+        const int64_t part_elems = noalloc ? budget / 4 : ws_elems;
+        const int64_t zl = static_cast<int64_t>(num_slices) * k.max_rank;
+        const int64_t zel = noalloc ? zbytes / (bf16 ? 2 : 4) : z_elems;
+        if (pl.part_bytes / 4 > part_elems) m.fail("%s: partials of %lld bytes exceed the workspace", who,
+                                                   (long long)pl.part_bytes);
+        if (pl.dma) m.shrink_dma(pl, k.rw, zl, zel, part_elems);
+        else m.shrink_reg(pl, k.rw, zl, zel, part_elems);
+        ExpandParams e{};
+        e.out_total = out_total;
+        e.si = m.si;
+        e.ldz = zl;
+        e.part_stride = T * pl.zw;
+        e.zw = pl.zw;
+        e.nparts = pl.KS > 1 ? pl.KS : 0;
+        e.max_rank = k.max_rank;
+        e.rw = k.rw;
+        e.flat = pl.flat ? 1 : 0;
+        e.ks_target = pl.ks_target;
+        e.ks_chunks = pl.n_chunks;
+        const ExpandForm f = expand_form(bf16, T, e);
+        for (int occ = 1; occ <= 4; ++occ) m.expand(e, f, k.adapters, int64_t(occ) * cus, zel, part_elems, nullptr);
+      }
+    }
+    // gs_shrink writing z (reduced when split), then gs_expand_add from it;
+    // and, when z_off is given, gs_expand_add reading its shrink values by
+    // token from a [T, z_ld] matrix (the vLLM layer's x_ext columns)
+    for (int c = 0; c < ncls; ++c) {
+      const RankClass& k = cls[c];
+      const ShrinkPlan pl = plan_class(T, hidden, num_slices, k, bf16, INT64_MAX, false);
+      const int64_t zl = static_cast<int64_t>(num_slices) * max_rank;
+      if (pl.dma) m.shrink_dma(pl, k.rw, zl, z_elems, ws_elems);
+      else m.shrink_reg(pl, k.rw, zl, z_elems, ws_elems);
+      if (pl.KS > 1) m.reduce(pl, k.rw, zl, z_elems, ws_elems);
+      for (int by_token = 0; by_token < (z_off ? 2 : 1); ++by_token) {
+        ExpandParams e{};
+        e.out_total = out_total;
+        e.si = m.si;
+        e.ldz = by_token ? z_ld : zl;
+        e.z_by_token = by_token;
+        e.max_rank = k.max_rank;
+        e.rw = k.rw;
+        e.flat = sparse_class(k) ? 1 : 0;
+        const ExpandForm f = expand_form(bf16, T, e);
+        for (int occ = 1; occ <= 4; ++occ)
+          m.expand(e, f, k.adapters, int64_t(occ) * cus, by_token ? T * z_ld : z_elems, 0, by_token ? z_off : nullptr);
+      }
+    }
+  }
+  if (checked) *checked = m.checked;
+  if (msg && msg_len > 0) snprintf(msg, static_cast<size_t>(msg_len), "%s", m.msg);
+  return m.bad;
 }
 
 }  // extern "C"

@@ -214,6 +214,28 @@ int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t
                      const int32_t* seg_offsets, const int32_t* perm, void* z, void* workspace,
                      int64_t workspace_bytes, void* stream);
 
+/* Test support (no counterpart in the reference; makes no HIP call).  Replays
+ * on the host every global and LDS access the segment kernels would make for
+ * this call -- the launches of gs_switched_lora with a caller workspace and
+ * with gs_switched_lora_noalloc's static scratch, and gs_shrink (z written,
+ * split partials reduced) followed by gs_expand_add; with z_off given, also
+ * gs_expand_add reading its shrink values by token from a [T, z_ld] matrix
+ * (the vLLM layer's x_ext columns) -- for every workgroup, wave, lane and loop
+ * step, with the launches' own plans and the kernels' address arithmetic
+ * (gs_addr.h), and for each possible number of resident expand workgroups
+ * per CU (1..4).  Host copies of the tables: a_off / b_off / ranks
+ * [num_adapters+1], seg_offsets [num_adapters+1], perm [num_tokens] (as
+ * gs_build_segments writes them).  Returns the number of accesses outside
+ * their buffers plus items a grid leaves uncovered (0: clean), the first one
+ * described in msg; *checked receives the number of accesses checked; a
+ * negated GS_* status on bad arguments. */
+int64_t gs_check_segment_addresses(int32_t dtype, int64_t num_tokens, int32_t hidden, int64_t ldx, int32_t out_total,
+                                   int64_t ldy, const int32_t* slice_bounds, int32_t num_slices, const int64_t* a_off,
+                                   int64_t a_pack_elems, const int64_t* b_off, int64_t b_pack_elems,
+                                   const int32_t* ranks, int32_t num_adapters, int32_t max_rank,
+                                   const int32_t* seg_offsets, const int32_t* perm, const int32_t* z_off,
+                                   int64_t z_ld, char* msg, int64_t msg_len, int64_t* checked);
+
 /* The same op with its scratch (split-K partials and z) in a static device
  * array of GS_NOALLOC_SCRATCH_BYTES per GPU, so it allocates nothing: no
  * workspace, no z, no hipMalloc.  No counterpart in the reference: it is for

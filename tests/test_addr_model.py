@@ -1,0 +1,177 @@
+"""CPU check of the segment kernels' memory accesses (no GPU needed).
+
+Every hot loop of the kernels loads unconditionally from clamped addresses
+and masks afterwards, so a wrong clamp is an out-of-bounds access.  The
+library's address model (``gs_check_segment_addresses``) replays, on the host,
+every global and LDS access of every launch a call makes -- every workgroup,
+wave, lane and loop step -- with the launches' own plans and the kernels' own
+address arithmetic (``csrc/gs_addr.h``, called by both), and reports any
+access outside its buffer and any item a grid leaves uncovered.  This test
+drives it at the benchmark shapes (the five workloads and the rank-512
+population) and at the edge cases the GPU tests run: ragged and tiny
+batches, one token, rank 8 to 512, odd hidden sizes, non-applicable
+adapters, 64 and 256 adapters, and the vLLM layer's by-token form.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from granite_switch_amd import _lib, vllm_layers, workloads
+from oracle import mapping as omap
+
+
+def _pack_tables(ranks, S, H, O):
+    """Host tables of PackedAdapters.from_slices: ranks rounded up to 8,
+    adapter g's S*r rows of lora_A at a_off[g], its [O, r] lora_B at b_off[g]."""
+    NA = len(ranks)
+    r8 = [0] + [((int(r) + 7) // 8) * 8 if r > 0 else 0 for r in ranks]
+    a_off, b_off = [0] * (NA + 1), [0] * (NA + 1)
+    a = b = 0
+    for g in range(1, NA + 1):
+        if r8[g] == 0:
+            continue
+        a_off[g], b_off[g] = a, b
+        a += S * r8[g] * H
+        b += O * r8[g]
+    return r8, a_off, b_off, max(a, 8 * H), max(b, 8 * O)
+
+
+def _check(T, H, slices, ranks, eff, dtype=_lib.GS_DTYPE_BF16, ldx=None, ldy=None, z_off=None, z_ld=0, b_tables=None):
+    NA = len(ranks)
+    S, O = len(slices), int(sum(slices))
+    r8, a_off, b_off, a_el, b_el = _pack_tables(ranks, S, H, O)
+    if b_tables is not None:
+        b_off, b_el = b_tables
+    max_rank = max([8] + r8)
+    seg, perm = omap.build_segments(np.asarray(eff, dtype=np.int64), NA)
+    perm_full = np.zeros(max(T, 1), dtype=np.int32)
+    perm_full[: len(perm)] = perm
+    bounds = np.concatenate([[0], np.cumsum(slices)]).astype(np.int32)
+    i32 = lambda v: (ctypes.c_int32 * len(v))(*[int(u) for u in v])
+    i64 = lambda v: (ctypes.c_int64 * len(v))(*[int(u) for u in v])
+    msg = ctypes.create_string_buffer(512)
+    checked = ctypes.c_int64(0)
+    bad = _lib.load().gs_check_segment_addresses(
+        dtype, T, H, ldx or H, O, ldy or O, i32(bounds), S, i64(a_off), a_el, i64(b_off), b_el, i32(r8), NA, max_rank,
+        i32(seg), i32(perm_full), None if z_off is None else i32(z_off), z_ld, msg, 512, ctypes.byref(checked))
+    assert bad >= 0, f"bad arguments: {_lib.last_error()}"
+    assert bad == 0, f"{bad} violations, first: {msg.value.decode()}"
+    assert T == 0 or int((np.asarray(eff) > 0).sum()) == 0 or checked.value > 0
+    return checked.value
+
+
+def _eff(routing):
+    return omap.alora_effective_ids(routing.req_ids, routing.positions, routing.cu_seqlens, routing.act_offsets)
+
+
+@pytest.mark.parametrize("config", [0, 1, 2, 3, 4])
+def test_benchmark_workloads(config):
+    r = workloads.routing_for(config)
+    eff = _eff(r)
+    dt = _lib.GS_DTYPE_FP32 if config == 0 else _lib.GS_DTYPE_BF16
+    for spec in workloads.module_specs(config):
+        n = _check(r.num_tokens, spec.hidden, spec.output_slices, spec.ranks, eff, dt)
+        print(f"config {config} {spec.name}: {n} accesses checked")
+
+
+@pytest.mark.parametrize("config", [1, 4])
+def test_rank512_population(config):
+    r = workloads.population_routing(config, "r512")
+    eff = _eff(r)
+    for spec in workloads.population_specs(config, "r512"):
+        _check(r.num_tokens, spec.hidden, spec.output_slices, spec.ranks, eff)
+
+
+def test_rank512_population_with_a_prefill_chunk_on_the_large_adapter():
+    """The large class holding far more tokens than expected: its looping
+    grids must still cover every item."""
+    r = workloads.population_routing(4, "r512")
+    req = r.req_ids.copy()
+    req[48:48 + 3 * 256] = 25                      # three prefill chunks on the rank-512 adapter
+    eff = omap.alora_effective_ids(req, r.positions, r.cu_seqlens, r.act_offsets)
+    for spec in workloads.population_specs(4, "r512"):
+        _check(r.num_tokens, spec.hidden, spec.output_slices, spec.ranks, eff)
+
+
+EDGE = [
+    # T, H, slices, ranks, seed, share of base tokens
+    (1, 4096, (4096, 1024, 1024), [32] * 12, 0, 0.0),
+    (7, 256, (128, 64), [8, 16, 32], 1, 0.2),
+    (96, 256, (128, 64), [8, 16, 32], 2, 0.3),
+    (300, 1000, (96, 32), [8, 24, 40], 3, 0.2),                  # H not a multiple of 64: register shrink
+    (130, 520, (64,), [512, 8], 4, 0.1),
+    (1100, 2048, (512, 256), [8, 16, 32, 64, 128, 16], 5, 0.2),
+    (2048, 1024, (512, 256), [32, 8, 512, 64, 128, 16, 32, 256], 6, 0.1),
+    (64, 4096, (4096,), [64] * 64, 7, 0.1),                       # every limit of the one-launch path
+    (5000, 512, (256,), [8] * 256, 8, 0.0),                      # 256 adapters: the multi-pass tile lookup
+    (4096, 12800, (4096,), [(8, 16, 32, 64)[a % 4] for a in range(48)], 9, 0.15),
+    (200, 1024, (1024,), [128, 512], 10, 0.3),                    # large class only
+    (400, 4096, (4096, 1024, 1024), [32] * 6 + [512], 11, 0.1),
+]
+
+
+@pytest.mark.parametrize("T,H,slices,ranks,seed,base", EDGE)
+def test_edge_shapes(T, H, slices, ranks, seed, base):
+    rng = np.random.default_rng(seed)
+    NA = len(ranks)
+    eff = rng.integers(1, NA + 1, size=T)
+    eff[rng.random(T) < base] = 0
+    for dt in (_lib.GS_DTYPE_BF16, _lib.GS_DTYPE_FP32):
+        if dt == _lib.GS_DTYPE_FP32 and len(slices) * max(ranks) > 512:
+            continue                                          # refused by the fp32 expand's LDS limit
+        _check(T, H, slices, ranks, eff, dt)
+    # a row stride wider than the row, and an all-base batch
+    _check(T, H, slices, ranks, eff, ldx=H + 64, ldy=int(sum(slices)) + 32)
+    _check(T, H, slices, ranks, np.zeros(T, dtype=np.int64))
+
+
+def test_non_applicable_adapter_and_empty_batch():
+    _check(0, 256, (128,), [16, 16], np.zeros(0, dtype=np.int64))
+    eff = np.array([1, 2, 2, 0, 1, 3, 3, 3] * 20)
+    _check(len(eff), 512, (256, 128), [32, 0, 16], eff)           # adapter 2 is not applicable here
+
+
+def test_vllm_layer_reads_shrink_values_by_token():
+    """The vLLM layer's segment expand reads each row's shrink values from
+    x_ext by token, at the columns its fusion plan gives each adapter."""
+    K, slices, ranks = 256, (256, 128, 128), [16, 512, 8, 32]
+    base = torch.nn.Linear(K, sum(slices), bias=False)
+    layer = vllm_layers.SwitchedLoRALinear(base, len(ranks), max(ranks), num_slices=3, output_slices=slices)
+    with torch.no_grad():
+        for A in layer.lora_A_slices:
+            A.data.normal_()
+    layer.finalize_weights(ranks)
+    # the layer's own segment tables: promoted (tier) ranks, lora_B blocks in
+    # lb_packed, first shrink column of each adapter in x_ext
+    seg_rank = layer._seg_ranks.tolist()[1:]
+    b_tables = (layer._seg_boff.tolist(), layer._lb_packed.numel())
+    x_ext_cols = layer.w_ext.shape[0]
+    rng = np.random.default_rng(3)
+    for T in (100, 1500):
+        eff = rng.integers(0, len(ranks) + 1, size=T)
+        _check(T, K, slices, seg_rank, eff, z_off=layer._seg_zoff.tolist(), z_ld=x_ext_cols, b_tables=b_tables)
+
+
+def test_model_catches_a_planted_out_of_range_table():
+    """The model reports accesses outside their buffers: a lora_B offset that
+    puts the last adapter's block past the end of the pack is caught."""
+    T, H, slices, ranks = 64, 256, (128,), [16, 16]
+    S, O = 1, 128
+    r8, a_off, b_off, a_el, b_el = _pack_tables(ranks, S, H, O)
+    eff = np.array([1, 2] * 32)
+    seg, perm = omap.build_segments(eff, 2)
+    i32 = lambda v: (ctypes.c_int32 * len(v))(*[int(u) for u in v])
+    i64 = lambda v: (ctypes.c_int64 * len(v))(*[int(u) for u in v])
+    msg = ctypes.create_string_buffer(512)
+    checked = ctypes.c_int64(0)
+    b_off_bad = list(b_off)
+    b_off_bad[2] += O * 8                                          # half a block past the end
+    bad = _lib.load().gs_check_segment_addresses(
+        _lib.GS_DTYPE_BF16, T, H, H, O, O, i32([0, O]), S, i64(a_off), a_el, i64(b_off_bad), b_el, i32(r8), 2, 16,
+        i32(seg), i32(perm), None, 0, msg, 512, ctypes.byref(checked))
+    assert bad > 0 and "lora_B" in msg.value.decode()
