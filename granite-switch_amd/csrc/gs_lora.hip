@@ -914,8 +914,45 @@ __global__ __launch_bounds__(kThreads) void expand_sparse_kernel(ExpandParams p)
       const int n_tile0 = sub * kSpNT;
       int s = 0;
       while (s + 1 < p.si.S && n_tile0 >= p.si.bounds[s + 1]) ++s;
-      // this wave's k-groups of lora_B for the 4 column blocks (pieces past
-      // the rank read the row's first piece and are masked)
+      // the token rows of the item's y pieces (rows past the tile re-read its
+      // first token) and, when z is read by token, of its z pieces: the only
+      // loads the others wait for, so they go first
+      const int zo = (p.z_off != nullptr) ? p.z_off[tr.g] : 0;
+      const int per_row = r >> 2;
+      constexpr int ZIT = kTM * (4 * KG * KSTEP) / 4 / kThreads;   // z pieces per thread at the largest rank
+      int64_t yrow[PASSES];
+      bool rok[PASSES];
+#pragma unroll
+      for (int ps = 0; ps < PASSES; ++ps) {
+        const int row = ps * RPI + tid / LPR;
+        rok[ps] = row < tr.nrows;
+        yrow[ps] = static_cast<int64_t>(p.perm[tr.slot0 + addr::tile_row(row, tr.nrows)]) * p.ldy;
+      }
+      int64_t zrow[ZIT];
+#pragma unroll
+      for (int j = 0; j < ZIT; ++j)
+        zrow[j] = tr.slot0 + addr::tile_row(addr::stage_row(tid + j * kThreads, per_row), tr.nrows);
+      if (nparts == 0 && p.z_by_token) {   // uniform
+#pragma unroll
+        for (int j = 0; j < ZIT; ++j) zrow[j] = p.perm[zrow[j]];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // then, all in flight together: the slice's z pieces of the tile's rows
+      // (when z is given; the oldest, so staging them waits for nothing
+      // else; pieces past the rank read clamped addresses and are not
+      // stored), this wave's k-groups of lora_B for the 4 column blocks
+      // (pieces past the rank read the row's first piece and are masked) and
+      // the y pieces
+      uint2 w[ZIT];
+      if (nparts == 0) {
+        const uint16_t* zp = static_cast<const uint16_t*>(p.z) + zo + s * r;
+#pragma unroll
+        for (int j = 0; j < ZIT; ++j) {
+          const int it = tid + j * kThreads;
+          const int c4 = it < kTM * per_row ? addr::stage_col(it, addr::stage_row(it, per_row), per_row, 0) : 0;
+          w[j] = *reinterpret_cast<const uint2*>(zp + zrow[j] * p.ldz + c4);
+        }
+      }
       u32x4 bv[4][KG];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -927,57 +964,70 @@ __global__ __launch_bounds__(kThreads) void expand_sparse_kernel(ExpandParams p)
           bv[q][kg] = sel16(k0 < r, ld16(br + addr::k_or_zero(k0, r) * 2));
         }
       }
-      // y pieces of the item's rows (rows past the tile re-read its first token)
-      int64_t yrow[PASSES];
-      bool rok[PASSES];
       u32x4 yv[PASSES];
 #pragma unroll
-      for (int ps = 0; ps < PASSES; ++ps) {
-        const int row = ps * RPI + tid / LPR;
-        rok[ps] = row < tr.nrows;
-        yrow[ps] = static_cast<int64_t>(p.perm[tr.slot0 + addr::tile_row(row, tr.nrows)]) * p.ldy;
-        yv[ps] = ld16(static_cast<const char*>(p.y) + (yrow[ps] + n_tile0 + cx) * 2);
-      }
-      // the slice's shrink values of the tile's rows: split-K partials summed
-      // in ks order (kPartGroup at a time) and rounded to bf16 as a stored z
-      // would be, or z itself
-      const int zo = (p.z_off != nullptr) ? p.z_off[tr.g] : 0;
-      const int per_row = r >> 2;
-      for (int it = tid; it < kTM * per_row; it += kThreads) {
-        const int row = addr::stage_row(it, per_row);
-        const int c4 = addr::stage_col(it, row, per_row, 0);
-        float v[4] = {0.f, 0.f, 0.f, 0.f};
-        if (row < tr.nrows) {
-          const int slot = tr.slot0 + row;
-          if (nparts > 0) {
-            const float* src = p.part + static_cast<int64_t>(slot) * p.zw + s * r + c4;
-            for (int ks0 = 0; ks0 < nparts; ks0 += kPartGroup) {
-              f32x4 a[kPartGroup];
+      for (int ps = 0; ps < PASSES; ++ps) yv[ps] = ld16(static_cast<const char*>(p.y) + (yrow[ps] + n_tile0 + cx) * 2);
+      // the slice's shrink values of the tile's rows in LDS: the z pieces
+      // loaded above, or split-K partials summed in ks order (kPartGroup at a
+      // time) and rounded to bf16 as a stored z would be
+      if (nparts == 0) {
 #pragma unroll
-              for (int u = 0; u < kPartGroup; ++u)
-                if (ks0 + u < nparts) a[u] = *reinterpret_cast<const f32x4*>(src + (ks0 + u) * p.part_stride);
-#pragma unroll
-              for (int u = 0; u < kPartGroup; ++u) {
-                if (ks0 + u < nparts) {
-                  v[0] += a[u].x;
-                  v[1] += a[u].y;
-                  v[2] += a[u].z;
-                  v[3] += a[u].w;
-                }
-              }
-            }
-          } else {
-            const int64_t zrow = p.z_by_token ? static_cast<int64_t>(p.perm[slot]) : static_cast<int64_t>(slot);
-            const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.z) + zrow * p.ldz + zo +
-                                                            s * r + c4);
-            v[0] = bf16_bits_to_f32(static_cast<uint16_t>(w.x & 0xffffu));
-            v[1] = bf16_bits_to_f32(static_cast<uint16_t>(w.x >> 16));
-            v[2] = bf16_bits_to_f32(static_cast<uint16_t>(w.y & 0xffffu));
-            v[3] = bf16_bits_to_f32(static_cast<uint16_t>(w.y >> 16));
+        for (int j = 0; j < ZIT; ++j) {
+          const int it = tid + j * kThreads;
+          const int row = addr::stage_row(it, per_row);
+          if (it < kTM * per_row) {
+            const int c4 = addr::stage_col(it, row, per_row, 0);
+            *reinterpret_cast<uint2*>(zs + (static_cast<int64_t>(row) * zs_ld + c4) * 2) =
+                row < tr.nrows ? w[j] : make_uint2(0u, 0u);
           }
         }
-        *reinterpret_cast<uint2*>(zs + (static_cast<int64_t>(row) * zs_ld + c4) * 2) =
-            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      }
+      // partials: the tile's real rows only (the products of the rows past
+      // them are never stored), UNR passes' pieces in flight per trip (two
+      // at rank > 256, where the kernel holds one wave per SIMD anyway; one
+      // below, which keeps two)
+      constexpr int UNR = KG >= 8 ? 2 : 1;
+      const int npieces = nparts == 0 ? 0 : tr.nrows * per_row;
+      for (int it0 = tid; it0 < npieces; it0 += UNR * kThreads) {
+        float v[UNR][4];
+        const float* src[UNR];
+#pragma unroll
+        for (int w2 = 0; w2 < UNR; ++w2) {
+          const int it = it0 + w2 * kThreads < npieces ? it0 + w2 * kThreads : it0;
+          const int row = addr::stage_row(it, per_row);
+          src[w2] = p.part + static_cast<int64_t>(tr.slot0 + row) * p.zw + s * r +
+                    addr::stage_col(it, row, per_row, 0);
+          v[w2][0] = v[w2][1] = v[w2][2] = v[w2][3] = 0.f;
+        }
+        for (int ks0 = 0; ks0 < nparts; ks0 += kPartGroup) {
+          f32x4 a[UNR][kPartGroup];
+#pragma unroll
+          for (int w2 = 0; w2 < UNR; ++w2)
+#pragma unroll
+            for (int u = 0; u < kPartGroup; ++u)
+              if (ks0 + u < nparts) a[w2][u] = *reinterpret_cast<const f32x4*>(src[w2] + (ks0 + u) * p.part_stride);
+#pragma unroll
+          for (int w2 = 0; w2 < UNR; ++w2)
+#pragma unroll
+            for (int u = 0; u < kPartGroup; ++u) {
+              if (ks0 + u < nparts) {
+                v[w2][0] += a[w2][u].x;
+                v[w2][1] += a[w2][u].y;
+                v[w2][2] += a[w2][u].z;
+                v[w2][3] += a[w2][u].w;
+              }
+            }
+        }
+#pragma unroll
+        for (int w2 = 0; w2 < UNR; ++w2) {
+          const int it = it0 + w2 * kThreads;
+          if (it < npieces) {
+            const int row = addr::stage_row(it, per_row);
+            const int c4 = addr::stage_col(it, row, per_row, 0);
+            *reinterpret_cast<uint2*>(zs + (static_cast<int64_t>(row) * zs_ld + c4) * 2) =
+                make_uint2(pack_bf16x2(v[w2][0], v[w2][1]), pack_bf16x2(v[w2][2], v[w2][3]));
+          }
+        }
       }
       lds_barrier();
       f32x16 acc[4];
@@ -1191,6 +1241,7 @@ static ShrinkPlan plan_class(int64_t T, int H, int S, const RankClass& k, bool b
   return plan_shrink(T, H, S, k.adapters, k.max_rank, bf16, k.est_tokens, large_class(k),
                      device_ks && sparse_class(k), max_part_bytes);
 }
+
 
 }  // namespace gs
 
@@ -1428,6 +1479,7 @@ ExpandForm expand_form(bool bf16, int64_t T, const ExpandParams& p) {
   f.PRE = need <= 2 ? 2 : (need <= 4 ? 4 : 8);
   return f;
 }
+
 
 // adapters: the launch's rank class (bounds its part-filled tiles)
 void launch_expand(bool bf16, int64_t T, int adapters, ExpandParams p, hipStream_t st) {
@@ -1693,7 +1745,8 @@ struct AddrModel {
       nparts = ks > 1 ? ks : 0;
     }
     const int ES = es(), EPL = 16 / ES;
-    auto stage = [&](const TileRef& tr, int s_lo, int s_hi, int col_base_of_slice0, int64_t zs_ld, int64_t lds) {
+    auto stage = [&](const TileRef& tr, int s_lo, int s_hi, int col_base_of_slice0, int64_t zs_ld, int64_t lds,
+                     int nparts) {
       const int r = tr.rank, zo = z_off ? z_off[tr.g] : 0;
       const int per_row = ((s_hi - s_lo + 1) * r) >> 2;
       for (int it = 0; it < kTM * per_row; ++it) {
@@ -1745,7 +1798,24 @@ struct AddrModel {
             const int tok = token_at(tr.slot0 + addr::tile_row(row, tr.nrows));
             row_piece("sparse y", tok, n_tile0 + cx, 8, out_total);
           }
-        stage(tr, s, s, 0, zs_ld, lds);
+        if (nparts > 0) {
+          stage(tr, s, s, 0, zs_ld, lds, nparts);
+        } else {
+          // every piece of the 2 KG per thread loaded (rows past the tile
+          // and pieces past the rank read clamped addresses), then stored
+          const int per_row = r >> 2, ZIT = 2 * f.KG, zo = z_off ? z_off[tr.g] : 0;
+          for (int tid = 0; tid < kThreads; ++tid)
+            for (int j = 0; j < ZIT; ++j) {
+              const int it = tid + j * kThreads;
+              const int row = addr::stage_row(it, per_row);
+              const int64_t slot = tr.slot0 + addr::tile_row(row, tr.nrows);
+              const int64_t zrow = e.z_by_token ? token_at(slot) : slot;
+              const int c4 = it < kTM * per_row ? addr::stage_col(it, row, per_row, 0) : 0;
+              in("sparse z column", zo + s * r + c4, 4, e.ldz);
+              in("sparse z", zrow * e.ldz + zo + s * r + c4, 4, z_elems);
+              if (it < kTM * per_row) in("sparse staged z", (row * zs_ld + c4) * 2, 8, lds);
+            }
+        }
       });
       return;
     }
@@ -1793,7 +1863,7 @@ struct AddrModel {
       while (s_lo + 1 < si.S && c_first >= si.bounds[s_lo + 1]) ++s_lo;
       s_hi = s_lo;
       while (s_hi + 1 < si.S && c_last >= si.bounds[s_hi + 1]) ++s_hi;
-      stage(tr, s_lo, s_hi, s_lo * r, zs_ld, lds);
+      stage(tr, s_lo, s_hi, s_lo * r, zs_ld, lds, nparts);
     });
   }
 };
@@ -1848,13 +1918,77 @@ int noalloc_scratch(const char* who, char** out) {
 // gs_switched_lora and gs_switched_lora_noalloc, which differ only in where z
 // and the partials live).  The classes run one after the other on the stream,
 // so they share z and the workspace.
+// Side stream and fork / join events of a device, on which the large rank
+// class of a two-class module runs beside the small one (created on the
+// first such call; default priority, non-blocking).  The mutex makes a call's
+// record / wait / launch sequence atomic against other host threads.
+#ifndef GS_FORK_ORDER
+#define GS_FORK_ORDER 0
+#endif
+struct ForkState {
+  std::mutex mu;
+  hipStream_t side = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  bool failed = false;
+};
+ForkState g_fork[kMaxDevices];
+
+ForkState* fork_state() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  ForkState& f = g_fork[dev];
+  std::lock_guard<std::mutex> lock(f.mu);
+  if (f.side == nullptr && !f.failed) {
+    if (hipStreamCreateWithFlags(&f.side, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&f.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&f.join, hipEventDisableTiming) != hipSuccess) {
+      f.failed = true;
+      (void)hipGetLastError();
+    }
+  }
+  return f.failed ? nullptr : &f;
+}
+
+constexpr int64_t align256(int64_t b) { return (b + 255) & ~int64_t(255); }
+
+// Workspace bytes of each rank class's partials and where they start when
+// the classes run concurrently (side by side) or one after the other (both
+// at 0).
+struct ClassLayout {
+  int64_t off[2] = {0, 0};
+  int64_t bytes = 0;       // the span the call uses
+  bool concurrent = false;
+};
+ClassLayout class_layout(int64_t T, int H, int S, const RankClass* cls, int ncls, bool bf16, int64_t max_part_bytes,
+                         bool want_concurrent, int64_t workspace_bytes) {
+  ClassLayout L;
+  int64_t part[2] = {0, 0};
+  for (int c = 0; c < ncls; ++c) part[c] = plan_class(T, H, S, cls[c], bf16, max_part_bytes).part_bytes;
+  L.bytes = ncls == 2 ? std::max(part[0], part[1]) : part[0];
+  if (ncls == 2 && want_concurrent) {
+    const int64_t both = part[0] == 0 ? part[1] : align256(part[0]) + part[1];
+    if (both <= workspace_bytes || both == 0) {
+      L.concurrent = true;
+      L.off[1] = part[0] == 0 ? 0 : align256(part[0]);
+      L.bytes = both;
+    }
+  }
+  return L;
+}
+
+// concurrent: a two-class module runs its large class on the device's side
+// stream, forked from and joined back into `stream`, when the workspace holds
+// both classes' partials (gs_shrink_workspace_bytes); the classes touch
+// disjoint y rows, z rows (both at the stride S * max_rank) and workspace
+// ranges.  Otherwise (or with concurrent false) the classes run one after
+// the other on `stream`, sharing z and the workspace.
 int switched_lora_impl(const char* who, int32_t dtype, const void* x, int64_t ldx, void* y, int64_t ldy,
                        int64_t num_tokens, int32_t hidden, int32_t out_total, const int32_t* slice_bounds,
                        int32_t num_slices, const void* a_pack, const int64_t* a_off, const void* b_pack,
                        const int64_t* b_off, const int32_t* ranks, int32_t num_adapters, int32_t max_rank,
                        const int32_t* ranks_host, const int32_t* seg_offsets, const int32_t* perm, void* z,
                        void* workspace, int64_t workspace_bytes, void* stream,
-                       int64_t max_part_bytes = INT64_MAX) {
+                       int64_t max_part_bytes = INT64_MAX, bool concurrent = false) {
   int rc = check_common(who, dtype, num_tokens, num_slices, num_adapters, max_rank);
   if (rc != GS_OK) return rc;
   rc = check_shrink(dtype, x, ldx, hidden, a_pack);
@@ -1875,13 +2009,14 @@ int switched_lora_impl(const char* who, int32_t dtype, const void* x, int64_t ld
                          workspace_bytes);
     if (rc != GS_OK) return rc;
   }
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  for (int c = 0; c < ncls; ++c) {
-    const RankClass& k = cls[c];
+  const ClassLayout L = class_layout(num_tokens, hidden, num_slices, cls, ncls, bf16, max_part_bytes, concurrent,
+                                     workspace_bytes);
+  ForkState* fs = L.concurrent ? fork_state() : nullptr;
+  auto run_class = [&](const RankClass& k, hipStream_t st, int64_t part_off, int64_t ldz) -> int {
     const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, k, bf16, max_part_bytes);
-    const int64_t ldz = static_cast<int64_t>(num_slices) * k.max_rank;
+    void* ws = workspace ? static_cast<void*>(static_cast<char*>(workspace) + part_off) : nullptr;
     const ShrinkParams sp = make_shrink_params(pl, x, ldx, hidden, a_pack, a_off, ranks, num_slices, num_adapters,
-                                               seg_offsets, perm, z, ldz, workspace, num_tokens, k.rw);
+                                               seg_offsets, perm, z, ldz, ws, num_tokens, k.rw);
     launch_shrink(bf16, pl, sp, st);
     GS_CHECK_LAUNCH(who);
     ExpandParams e = ep;
@@ -1900,6 +2035,37 @@ int switched_lora_impl(const char* who, int32_t dtype, const void* x, int64_t ld
     e.nparts = pl.KS > 1 ? pl.KS : 0;
     launch_expand(bf16, num_tokens, k.adapters, e, st);
     GS_CHECK_LAUNCH(who);
+    return GS_OK;
+  };
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (fs == nullptr) {
+    for (int c = 0; c < ncls; ++c) {
+      rc = run_class(cls[c], st, 0, static_cast<int64_t>(num_slices) * cls[c].max_rank);
+      if (rc != GS_OK) return rc;
+    }
+    return GS_OK;
+  }
+  // the large class on the side stream once everything before this call on
+  // `stream` is done, issued after the small class's kernels (GS_FORK_ORDER
+  // 0; 1 issues it first); `stream` waits for it before anything after
+  // this call
+  const int64_t ldz = static_cast<int64_t>(num_slices) * max_rank;
+  std::lock_guard<std::mutex> lock(fs->mu);
+  if (hipEventRecord(fs->fork, st) != hipSuccess || hipStreamWaitEvent(fs->side, fs->fork, 0) != hipSuccess) {
+    set_error("%s: forking the side stream failed: %s", who, hipGetErrorString(hipGetLastError()));
+    return GS_ERR_HIP;
+  }
+  int rc0 = GS_OK, rc1 = GS_OK;
+  if (!GS_FORK_ORDER) rc0 = run_class(cls[0], st, L.off[0], ldz);
+  rc1 = run_class(cls[1], fs->side, L.off[1], ldz);
+  const hipError_t ej = hipEventRecord(fs->join, fs->side);
+  if (GS_FORK_ORDER) rc0 = run_class(cls[0], st, L.off[0], ldz);
+  const hipError_t ew = ej == hipSuccess ? hipStreamWaitEvent(st, fs->join, 0) : ej;
+  if (rc1 != GS_OK) return rc1;
+  if (rc0 != GS_OK) return rc0;
+  if (ew != hipSuccess) {
+    set_error("%s: joining the side stream failed: %s", who, hipGetErrorString(ew));
+    return GS_ERR_HIP;
   }
   return GS_OK;
 }
@@ -1915,12 +2081,11 @@ int64_t gs_shrink_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t nu
   int ncls = 0;
   if (rank_classes("gs_shrink_workspace_bytes", ranks_host, num_adapters, max_rank, num_tokens, cls, ncls) != GS_OK)
     return -1;
+  // both dtypes; two classes side by side (gs_switched_lora runs them
+  // concurrently in a workspace that holds both)
   int64_t b = 256;
-  for (int c = 0; c < ncls; ++c) {
-    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, cls[c], true);
-    const ShrinkPlan pf = plan_class(num_tokens, hidden, num_slices, cls[c], false);
-    b = std::max(b, std::max(pl.part_bytes, pf.part_bytes));
-  }
+  for (int bf16 = 0; bf16 < 2; ++bf16)
+    b = std::max(b, class_layout(num_tokens, hidden, num_slices, cls, ncls, bf16 != 0, INT64_MAX, true, INT64_MAX).bytes);
   return b;
 }
 
@@ -2024,7 +2189,7 @@ int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t
                      int64_t workspace_bytes, void* stream) {
   return switched_lora_impl("gs_switched_lora", dtype, x, ldx, y, ldy, num_tokens, hidden, out_total, slice_bounds,
                             num_slices, a_pack, a_off, b_pack, b_off, ranks, num_adapters, max_rank, ranks_host,
-                            seg_offsets, perm, z, workspace, workspace_bytes, stream);
+                            seg_offsets, perm, z, workspace, workspace_bytes, stream, INT64_MAX, true);
 }
 
 int gs_switched_lora_noalloc(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t num_tokens,
@@ -2121,11 +2286,15 @@ int64_t gs_check_segment_addresses(int32_t dtype, int64_t num_tokens, int32_t hi
           part = std::max(part, plan_class(T, hidden, num_slices, cls[c], bf16, budget).part_bytes);
         if (((part + 255) & ~int64_t(255)) + zbytes > kNoallocScratchBytes) continue;   // rejected by the call
       }
+      // gs_switched_lora runs two classes concurrently, their partials side
+      // by side (each checked against its own range) and z at one stride
+      const ClassLayout L = class_layout(T, hidden, num_slices, cls, ncls, bf16, budget, !noalloc, ws_elems * 4);
       for (int c = 0; c < ncls; ++c) {
         const RankClass& k = cls[c];
         const ShrinkPlan pl = plan_class(T, hidden, num_slices, k, bf16, budget);
-        const int64_t part_elems = noalloc ? budget / 4 : ws_elems;
-        const int64_t zl = static_cast<int64_t>(num_slices) * k.max_rank;
+        const int64_t part_hi = noalloc ? budget / 4 : (L.concurrent && c == 0 && L.off[1] > 0 ? L.off[1] / 4 : ws_elems);
+        const int64_t part_elems = part_hi - L.off[c] / 4;
+        const int64_t zl = static_cast<int64_t>(num_slices) * (L.concurrent ? max_rank : k.max_rank);
         const int64_t zel = noalloc ? zbytes / (bf16 ? 2 : 4) : z_elems;
         if (pl.part_bytes / 4 > part_elems) m.fail("%s: partials of %lld bytes exceed the workspace", who,
                                                    (long long)pl.part_bytes);

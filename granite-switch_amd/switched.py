@@ -540,6 +540,36 @@ def _dev_key(device: torch.device):
     return (device.type, device.index if device.index is not None else torch.cuda.current_device())
 
 
+_side_streams: dict = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """The per-device stream on which the "split" path runs the large rank
+    class's segment kernels beside the one-launch kernel (default priority)."""
+    key = _dev_key(device)
+    s = _side_streams.get(key)
+    if s is None:
+        s = _side_streams[key] = torch.cuda.Stream(device=torch.device(key[0], key[1]))
+    return s
+
+
+def _split_run(device: torch.device, large, small) -> None:
+    """The "split" path: ``large()`` (the segment kernels of the adapters above
+    rank 64) on the side stream, forked from the current stream, and
+    ``small()`` (the one-launch kernel of the rest) on the current stream,
+    then the current stream waits for the side stream.  The two touch disjoint
+    rows of y and separate scratch buffers; the large class goes first, its
+    kernels being the longer dependent chain.  Everything a later caller's
+    work may reuse is released to the current stream only after the join."""
+    cur = torch.cuda.current_stream(device)
+    side = _side_stream(device)
+    side.wait_stream(cur)
+    with torch.cuda.stream(side):
+        large()
+    small()
+    cur.wait_stream(side)
+
+
 def small_sync_buffer(device: torch.device) -> torch.Tensor:
     """The per-device sync buffer of the small-batch kernel (int32 words)."""
     key = _dev_key(device)
@@ -801,13 +831,21 @@ def switched_lora_routed_(y: torch.Tensor, x: torch.Tensor, adapter_ids: torch.T
     if path == "small" or (path == "auto" and path_plan(packed, T, nseq_hint, largest_group) != "segments"):
         if not small_eligible(small_v, T, num_seqs):
             raise ValueError("this module / batch is outside the small-batch kernel's limits")
-        _call_small(x2, y2, small_v, req=ids, pos=pos, cu=cu if off is not None else None, off=off,
-                    num_seqs=num_seqs if off is not None else 1,
-                    row_split=small_row_split(small_v, T, nseq_hint, largest_group))
+        def small():
+            _call_small(x2, y2, small_v, req=ids, pos=pos, cu=cu if off is not None else None, off=off,
+                        num_seqs=num_seqs if off is not None else 1,
+                        row_split=small_row_split(small_v, T, nseq_hint, largest_group))
+
         if large_v is None:
+            small()
             return y
-        segs = build_segments(ids, packed.num_adapters, pos, cu, off)
-        return switched_lora_(y, x, segs, large_v, path="segments")
+
+        def large():
+            segs = build_segments(ids, packed.num_adapters, pos, cu, off)
+            switched_lora_(y, x, segs, large_v, path="segments")
+
+        _split_run(dev, large, small)
+        return y
     segs = build_segments(ids, packed.num_adapters, pos, cu, off)
     return switched_lora_(y, x, segs, packed, path="segments")
 
@@ -835,27 +873,30 @@ def switched_lora_(y: torch.Tensor, x: torch.Tensor, segments: Segments, packed:
     if T != segments.num_tokens:
         raise ValueError("x / y shapes do not match the segments")
     _check_segments(segments, packed)
-    rest = packed
     if path != "segments" and T:
         small_v, large_v = packed.rank_split()
         if path == "small" and small_v is None:
             raise ValueError("the one-launch kernel takes adapters of rank <= 64; this module has none")
         if path == "small" or path_plan(packed, T, None, largest_group) != "segments":
-            _call_small(x2, y2, small_v, eff_ids=segments.eff_ids,
-                        row_split=small_row_split(small_v, T, None, largest_group))
+            def small():
+                _call_small(x2, y2, small_v, eff_ids=segments.eff_ids,
+                            row_split=small_row_split(small_v, T, None, largest_group))
+
             if large_v is None:
+                small()
                 return y
-            rest = large_v
+            _split_run(x2.device, lambda: switched_lora_(y, x, segments, large_v, z, path="segments"), small)
+            return y
     zw = packed.num_slices * packed.max_rank
     if z is None:
-        z = torch.empty(max(T, 1), rest.num_slices * rest.max_rank, dtype=x2.dtype, device=x2.device)
+        z = torch.empty(max(T, 1), packed.num_slices * packed.max_rank, dtype=x2.dtype, device=x2.device)
     elif z.stride(-1) != 1 or z.shape[-1] < zw or (T and z.stride(0) != zw):
         raise ValueError("z must be a contiguous [T, S*max_rank] buffer")
-    ws = shrink_workspace(T, H, rest.num_slices, rest.num_adapters, rest.max_rank, x2.device, rest.ranks_host)
+    ws = shrink_workspace(T, H, packed.num_slices, packed.num_adapters, packed.max_rank, x2.device, packed.ranks_host)
     _lib.call("gs_switched_lora", _dtype_code(x2), x2.data_ptr(), x2.stride(0), y2.data_ptr(), y2.stride(0), T, H,
-              rest.out_total, _i32_array(rest.slice_bounds), rest.num_slices, rest.a_pack.data_ptr(),
-              rest.a_off.data_ptr(), rest.b_pack.data_ptr(), rest.b_off.data_ptr(), rest.ranks.data_ptr(),
-              rest.num_adapters, rest.max_rank, _i32_array(rest.ranks_host), segments.seg_offsets.data_ptr(),
+              packed.out_total, _i32_array(packed.slice_bounds), packed.num_slices, packed.a_pack.data_ptr(),
+              packed.a_off.data_ptr(), packed.b_pack.data_ptr(), packed.b_off.data_ptr(), packed.ranks.data_ptr(),
+              packed.num_adapters, packed.max_rank, _i32_array(packed.ranks_host), segments.seg_offsets.data_ptr(),
               segments.perm.data_ptr(), z.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(x2.device))
     return y
 

@@ -8,7 +8,9 @@ per rank class (ranks <= 64 and above), each planned for its own ranks; the
 one-launch decode kernel takes the rank <= 64 class and the segment kernels
 the larger adapters.  Every path is checked against the oracle
 (|got - ref| <= 2e-2 + 2e-2 |ref| in bf16, 1e-5 in fp32) with base rows
-bit-identical.
+bit-identical.  gs_switched_lora runs a two-class module's classes
+concurrently (the large one on a side stream) when its workspace holds both
+classes' partials, and in turn otherwise; both give the same bits.
 """
 
 from __future__ import annotations
@@ -186,3 +188,110 @@ def test_only_large_adapters_and_no_applicable_adapter(dev):
     switched.switched_lora_routed_(y, md.x, torch.tensor(req, device=dev), none, path="segments")
     torch.cuda.synchronize()
     assert torch.equal(y, md.y)
+
+
+def _graph_replays_equal_eager(dev, run, restore, outputs, what):
+    """Eager run, then the same run captured in a HIP graph and replayed three
+    times (with eager work and synchronisations between), every replay
+    bit-identical to the eager result."""
+    run()
+    torch.cuda.synchronize()
+    ref = [o.clone() for o in outputs]
+    restore()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    for replay in range(3):
+        restore()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        same = all(torch.equal(o, r) for o, r in zip(outputs, ref))
+        _say(f"  {what}: replay {replay} {'bit-identical' if same else 'DIFFERS'}")
+        assert same, f"{what}: graph replay {replay} differs from the eager run"
+        _ = torch.ones(1024, device=dev).sum().item()     # eager work between replays
+    return ref
+
+
+def test_concurrent_classes_under_graph_capture(dev):
+    """gs_switched_lora runs a two-class module's large class on the library's
+    side stream, forked from and joined into the caller's stream; the fork and
+    join are captured into a graph with the rest, and every replay equals the
+    eager call.  The one-launch + segments "split" path forks a torch side
+    stream the same way."""
+    ranks = [32] * 6 + [512]
+    NA = len(ranks)
+    spec = workloads.ModuleSpec("qkv", 4096, (4096, 1024, 1024), ranks, 512)
+    T = 400
+    md = workloads.make_module(spec, T, NA, torch.bfloat16, dev, seed=91)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, ranks)
+    req = np.random.default_rng(4).integers(0, NA + 1, size=T)
+    segs = switched.build_segments(torch.tensor(req, device=dev), NA)
+    z = torch.empty(T, spec_zw(pk), dtype=torch.bfloat16, device=dev)
+    y = md.y.clone()
+    y0 = md.y.clone()
+    ref = _graph_replays_equal_eager(dev, lambda: switched.switched_lora_(y, md.x, segs, pk, z, path="segments"),
+                                     lambda: y.copy_(y0), [y], "two classes, segments")
+    _check(md, ref[0], req, torch.bfloat16, "two classes, segments, eager")
+
+    # decode-sized: the split path (one-launch kernel beside the segment kernels)
+    r = workloads.population_routing(1, "r512")
+    NA1 = workloads.population_adapters(1, "r512")
+    spec1 = workloads.population_specs(1, "r512")[0]
+    md1 = workloads.make_module(spec1, r.num_tokens, NA1, torch.bfloat16, dev, seed=92)
+    pk1 = switched.PackedAdapters.from_slices(md1.lora_A_slices, md1.lora_B_slices, spec1.ranks)
+    assert switched.path_plan(pk1, r.num_tokens, r.num_tokens) == "split"
+    args = [torch.tensor(v, device=dev) for v in (r.req_ids, r.positions, r.cu_seqlens, r.act_offsets)]
+    eff = omap.alora_effective_ids(r.req_ids, r.positions, r.cu_seqlens, r.act_offsets)
+    segs1 = switched.build_segments(args[0], NA1, args[1], args[2], args[3])
+    y1 = md1.y.clone()
+    y10 = md1.y.clone()
+    ref1 = _graph_replays_equal_eager(dev, lambda: switched.switched_lora_(y1, md1.x, segs1, pk1, path="auto"),
+                                      lambda: y1.copy_(y10), [y1], "split path")
+    switched.check(dev)
+    _check(md1, ref1[0], eff, torch.bfloat16, "split path, eager")
+
+
+def spec_zw(pk):
+    return pk.num_slices * pk.max_rank
+
+
+def test_two_classes_in_a_one_class_workspace_run_in_turn(dev):
+    """A workspace that holds only the larger class's partials (not both side
+    by side) makes gs_switched_lora run the classes one after the other: the
+    result is bit-identical to the concurrent run."""
+    ranks = [32] * 8 + [256]
+    NA = len(ranks)
+    spec = workloads.ModuleSpec("gate_up", 4096, (2048, 2048), ranks, 256)
+    T = 600
+    md = workloads.make_module(spec, T, NA, torch.bfloat16, dev, seed=93)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, ranks)
+    req = np.random.default_rng(5).integers(0, NA + 1, size=T)
+    segs = switched.build_segments(torch.tensor(req, device=dev), NA)
+    lib = switched._lib.load()
+
+    def ws_bytes(p):
+        return int(lib.gs_shrink_workspace_bytes(T, spec.hidden, pk.num_slices, NA, p.max_rank,
+                                                  switched._i32_array(p.ranks_host)))
+
+    # side by side the classes need align256(small) + large bytes; 256 bytes
+    # fewer still holds either class's partials, but not both
+    both = ws_bytes(pk)
+    one = both - 256
+    _say(f"workspace: both classes {both} B, in turn {one} B")
+    outs = []
+    for nbytes in (both, one):
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        z = torch.empty(T, spec_zw(pk), dtype=torch.bfloat16, device=dev)
+        y = md.y.clone()
+        switched._lib.call("gs_switched_lora", switched._dtype_code(md.x), md.x.data_ptr(), md.x.stride(0),
+                           y.data_ptr(), y.stride(0), T, spec.hidden, pk.out_total,
+                           switched._i32_array(pk.slice_bounds), pk.num_slices, pk.a_pack.data_ptr(),
+                           pk.a_off.data_ptr(), pk.b_pack.data_ptr(), pk.b_off.data_ptr(), pk.ranks.data_ptr(), NA,
+                           pk.max_rank, switched._i32_array(pk.ranks_host), segs.seg_offsets.data_ptr(),
+                           segs.perm.data_ptr(), z.data_ptr(), ws.data_ptr(), nbytes,
+                           switched._lib.stream_ptr(dev))
+        torch.cuda.synchronize()
+        outs.append(y)
+    assert torch.equal(outs[0], outs[1]), "concurrent and in-turn runs differ"
+    _check(md, outs[0], req, torch.bfloat16, "two classes")
