@@ -74,5 +74,42 @@ GS_HD int k_or_zero(int k0, int r) { return k0 < r ? k0 : 0; }
 GS_HD int stage_row(int it, int per_row) { return it / per_row; }
 GS_HD int stage_col(int it, int row, int per_row, int col_base) { return col_base + (it - row * per_row) * 4; }
 
+// ---- reference-semantics ops over x_ext (gs_xext.hip) ----------------------
+// Tier of kernel-local id kid (ids are numbered 1.. across the six tiers in
+// ascending-rank order; tier t holds na[t] adapters of rank 16 << t): its
+// tier t, the tier's first id and the tier's offset in the packed lora_B
+// ([na[t]][N][r] per tier).  False for an id past the last tier.
+GS_HD bool xext_tier(const int* na, int N, int kid, int& t, int& first, int64_t& lb_off) {
+  t = 0;
+  first = 1;
+  lb_off = 0;
+  while (t < 6 && kid >= first + na[t]) {
+    first += na[t];
+    lb_off += static_cast<int64_t>(na[t]) * N * (16 << t);
+    ++t;
+  }
+  return t < 6;
+}
+// First x_ext column of the shrink values of the idx-th adapter of its tier
+// for one slice, from that slice's tier base scr_st (slice_col_r[s][t]).
+GS_HD int64_t xext_zcol(int scr_st, int idx, int S, int r) {
+  return static_cast<int64_t>(scr_st) + static_cast<int64_t>(idx) * S * r;
+}
+// Element of lora_B row n (output column) of the idx-th adapter of a tier.
+GS_HD int64_t xext_brow(int64_t lb_off, int idx, int N, int r, int64_t n) {
+  return lb_off + static_cast<int64_t>(idx) * N * r + n * r;
+}
+// The x_ext row a lane reads: a row past the batch reads row 0.
+GS_HD int64_t xext_row(bool row_ok, int64_t m) { return row_ok ? m : 0; }
+// Read-modify-write piece q of thread tid of a 32 x 128 tile: row
+// (tid + 256 q) / 16, columns 8 ((tid + 256 q) % 16) on.
+GS_HD int xext_piece_row(int tid, int q) { return (tid + 256 * q) >> 4; }
+GS_HD int xext_piece_col(int tid, int q) { return ((tid + 256 * q) & 15) * 8; }
+// Column block of the column-block kernel: piece pc of an adapter's staged
+// lora_B block (r / 8 16-byte pieces per column) lands at column pc >> sh,
+// piece pc & (2^sh - 1) of it (sh = log2(r / 8)).
+GS_HD int xext_stage_colof(int pc, int sh) { return pc >> sh; }
+GS_HD int xext_stage_kof(int pc, int sh) { return pc & ((1 << sh) - 1); }
+
 }  // namespace addr
 }  // namespace gs

@@ -9,8 +9,14 @@
 // the rows of other adapters fed as zeros, so a row only ever receives its own
 // adapter's delta.  The delta goes through LDS to a row-major tile and is
 // added to x_ext in one bf16 read-modify-write per element.
-#include <type_traits>
+#include <stdarg.h>
 
+#include <algorithm>
+#include <array>
+#include <type_traits>
+#include <vector>
+
+#include "gs_addr.h"
 #include "gs_common.h"
 
 namespace gs {
@@ -63,24 +69,18 @@ __device__ f32x16 xext_block_delta(const XextArgs& a, const int* scr, int64_t m0
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) mine |= __shfl_xor(mine, d, 64);
   uint64_t todo = mine & bm;
-  const uint16_t* xrow = static_cast<const uint16_t*>(a.x_ext) + (m0 + i) * a.stride_m;
+  const uint16_t* xrow = static_cast<const uint16_t*>(a.x_ext) + (m0 + i) * a.stride_m;   // read only when sel
   while (todo) {
     const int b = __builtin_amdgcn_readfirstlane(__ffsll(static_cast<long long>(todo)) - 1);   // uniform
     todo &= todo - 1;
     const int kid = b + 1;   // kernel-local id
-    // tier lookup: ids are numbered 1.. across tiers in ascending-rank order
-    int t = 0, first = 1;
-    int64_t lb_off = 0;
-    while (t < 6 && kid >= first + a.na[t]) {
-      first += a.na[t];
-      lb_off += static_cast<int64_t>(a.na[t]) * a.N * (16 << t);   // tier t holds rank 16 << t
-      ++t;
-    }
-    if (t >= 6) break;   // cannot happen: the loop runs only over bits <= total count
+    int t, first;
+    int64_t lb_off;
+    if (!addr::xext_tier(a.na, a.N, kid, t, first, lb_off)) break;   // cannot happen: only valid bits are followed
     const int r = 16 << t;
     const int idx = kid - first;
-    const int64_t c0 = static_cast<int64_t>(scr[s * 6 + t]) + static_cast<int64_t>(idx) * a.S * r;
-    const uint16_t* brow = a.lb + lb_off + static_cast<int64_t>(idx) * a.N * r + static_cast<int64_t>(n0 + i) * r;
+    const int64_t c0 = addr::xext_zcol(scr[s * 6 + t], idx, a.S, r);
+    const uint16_t* brow = a.lb + addr::xext_brow(lb_off, idx, a.N, r, n0 + i);
     const bool sel = row_ok && id == kid;
     for (int kb = 0; kb < r; kb += 16) {
       const int k0 = kb + 8 * h;
@@ -97,15 +97,7 @@ __device__ f32x16 xext_block_delta(const XextArgs& a, const int* scr, int64_t m0
 // id; lb_off = the tier's offset in the packed lora_B.  Returns false for an
 // id past the last tier.
 __device__ __forceinline__ bool xext_tier(const XextArgs& a, int kid, int& t, int& first, int64_t& lb_off) {
-  t = 0;
-  first = 1;
-  lb_off = 0;
-  while (t < 6 && kid >= first + a.na[t]) {
-    first += a.na[t];
-    lb_off += static_cast<int64_t>(a.na[t]) * a.N * (16 << t);
-    ++t;
-  }
-  return t < 6;
+  return addr::xext_tier(a.na, a.N, kid, t, first, lb_off);
 }
 
 // Fast path for modules whose tiers all have rank <= 16 KK.  A row only ever
@@ -150,10 +142,10 @@ __device__ __forceinline__ void xext_own_z(const XextArgs& a, const int* scr, in
   int64_t lb_off = 0;
   ok = xext_tier(a, ok ? id : 1, t, first, lb_off) && ok;
   const int r = 16 << t;
-  const int64_t c0 = static_cast<int64_t>(scr[s * 6 + t]) + static_cast<int64_t>((ok ? id : first) - first) * a.S * r;
+  const int64_t c0 = addr::xext_zcol(scr[s * 6 + t], (ok ? id : first) - first, a.S, r);
   // a row past the batch (row_ok false: also the idle waves of a column-block
   // workgroup, whose whole tile lies past it) reads row 0
-  const uint16_t* xrow = static_cast<const uint16_t*>(a.x_ext) + (row_ok ? m0 + i : 0) * a.stride_m;
+  const uint16_t* xrow = static_cast<const uint16_t*>(a.x_ext) + addr::xext_row(row_ok, m0 + i) * a.stride_m;
   // unmasked (a clamped address when the row's adapter is not followed):
   // a value is only used by the MFMA of the row's own adapter, k-step by
   // k-step within its rank, so the loads need no wait before that
@@ -191,8 +183,7 @@ __device__ void xext_block_delta_fast(const XextArgs& a, const int (&n0)[NS], in
         if (xext_tier(a, bit + 1, t, first, lb_off)) {
           kid[b] = bit + 1;
           rk[b] = 16 << t;
-          bp[b] = a.lb + lb_off + static_cast<int64_t>(bit + 1 - first) * a.N * rk[b] + static_cast<int64_t>(i) * rk[b] +
-                  8 * h;
+          bp[b] = a.lb + addr::xext_brow(lb_off, bit + 1 - first, a.N, rk[b], i) + 8 * h;
         }
       }
     }
@@ -266,7 +257,7 @@ __device__ __forceinline__ void xext_gate_up_general(const XextArgs& a, const in
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) mine |= __shfl_xor(mine, d, 64);
   uint64_t todo = mine & bm;
-  const uint16_t* xrow = static_cast<const uint16_t*>(a.x_ext) + (row_ok ? m0 + i : 0) * a.stride_m;
+  const uint16_t* xrow = static_cast<const uint16_t*>(a.x_ext) + addr::xext_row(row_ok, m0 + i) * a.stride_m;
   while (todo) {
     const int kid = __builtin_amdgcn_readfirstlane(__ffsll(static_cast<long long>(todo)));   // uniform
     todo &= todo - 1;
@@ -275,11 +266,10 @@ __device__ __forceinline__ void xext_gate_up_general(const XextArgs& a, const in
     if (!xext_tier(a, kid, t, first, lb_off)) break;   // cannot happen: only valid bits are followed
     const int r = 16 << t;
     const int idx = kid - first;
-    const int64_t cg = static_cast<int64_t>(scr[t]) + static_cast<int64_t>(idx) * a.S * r;
-    const int64_t cu = static_cast<int64_t>(scr[6 + t]) + static_cast<int64_t>(idx) * a.S * r;
-    const uint16_t* bblk = a.lb + lb_off + static_cast<int64_t>(idx) * a.N * r;
-    const uint16_t* bg = bblk + static_cast<int64_t>(h0 + i) * r;
-    const uint16_t* bu = bblk + static_cast<int64_t>(H + h0 + i) * r;
+    const int64_t cg = addr::xext_zcol(scr[t], idx, a.S, r);
+    const int64_t cu = addr::xext_zcol(scr[6 + t], idx, a.S, r);
+    const uint16_t* bg = a.lb + addr::xext_brow(lb_off, idx, a.N, r, h0 + i);
+    const uint16_t* bu = a.lb + addr::xext_brow(lb_off, idx, a.N, r, H + h0 + i);
     const bool sel = row_ok && id == kid;
     for (int kb = 0; kb < r; kb += 32) {
       // all eight pieces load unconditionally (clamped addresses), so that
@@ -361,8 +351,8 @@ __global__ __launch_bounds__(256) void xext_expand_kernel(XextArgs a, uint16_t* 
   u32x4 in[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    prow[q] = (tid + 256 * q) >> 4;
-    pc[q] = ((tid + 256 * q) & 15) * 8;
+    prow[q] = addr::xext_piece_row(tid, q);
+    pc[q] = addr::xext_piece_col(tid, q);
     const int64_t m = m0 + prow[q];
     out_ok[q] = m < a.M && n_tile0 + pc[q] < a.N;
     p[q] = x_out + (out_ok[q] ? m : m0) * a.stride_m + (out_ok[q] ? n_tile0 + pc[q] : n_tile0);
@@ -453,7 +443,7 @@ __global__ __launch_bounds__(64 * RT) void xext_cols_kernel(XextArgs a, uint16_t
   // loads that depend on nothing: ids, slice tables, this lane's
   // read-modify-write pieces (clamped in-bounds addresses, masked afterwards)
   const bool row_ok = (m0 + i) < a.M;
-  const int id_raw = load_id_t<I64>(a.ids, row_ok ? m0 + i : 0);
+  const int id_raw = load_id_t<I64>(a.ids, addr::xext_row(row_ok, m0 + i));
   const int scr_v = a.slice_col_r[tid < a.S * 6 ? tid : 0];
   int sc[CB];
 #pragma unroll
@@ -470,7 +460,7 @@ __global__ __launch_bounds__(64 * RT) void xext_cols_kernel(XextArgs a, uint16_t
   for (int ps = 0; ps < PASSES; ++ps) {
     const int64_t m = m0 + ps * (64 / LPR) + l / LPR;
     ook[ps] = m < a.M && n_blk0 + cx < a.N;
-    orow[ps] = ook[ps] ? m : 0;
+    orow[ps] = addr::xext_row(ook[ps], m);
     const uint16_t* src = x_out + orow[ps] * a.stride_m + (ook[ps] ? n_blk0 + cx : 0);
     in[ps][0] = ld_row(src);
     in[ps][1] = ld_row(src + 8);
@@ -513,7 +503,7 @@ __global__ __launch_bounds__(64 * RT) void xext_cols_kernel(XextArgs a, uint16_t
         if (xext_tier(a, bit + 1, t, first, lb_off)) {
           my_kid = bit + 1;
           my_r = 16 << t;
-          my_off = lb_off + (static_cast<int64_t>(bit + 1 - first) * a.N + n_blk0) * my_r;
+          my_off = addr::xext_brow(lb_off, bit + 1 - first, a.N, my_r, n_blk0);
         }
       }
     }
@@ -555,8 +545,9 @@ __global__ __launch_bounds__(64 * RT) void xext_cols_kernel(XextArgs a, uint16_t
 #pragma unroll
       for (int q = 0; q < QP; ++q) {
         const int pc = l + 64 * q;
-        char* dst = pc < ncols * r / 8 ? bs + j * ABLK + (pc >> sh) * CST + (pc & ((1 << sh) - 1)) * 16
-                                       : bs + CA * ABLK + l * 16;
+        char* dst = pc < ncols * r / 8
+                        ? bs + j * ABLK + addr::xext_stage_colof(pc, sh) * CST + addr::xext_stage_kof(pc, sh) * 16
+                        : bs + CA * ABLK + l * 16;
         *reinterpret_cast<u32x4*>(dst) = v[jw][q];
       }
     }
@@ -701,14 +692,14 @@ __global__ __launch_bounds__(256) void xext_swiglu_kernel(XextArgs a, uint16_t* 
   int prow[2], pc[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    prow[q] = (tid + 256 * q) >> 4;
-    pc[q] = ((tid + 256 * q) & 15) * 8;
+    prow[q] = addr::xext_piece_row(tid, q);
+    pc[q] = addr::xext_piece_col(tid, q);
   }
   // the ids and the slice table go out first, then the gate and up pieces,
   // then the tile mask (a scalar load: the wait for the kernel arguments
   // before the first vector loads must not include it), so the delta's
   // inputs are one trip away
-  const int id = load_id(a.ids, a.idx_bytes, row_ok ? m0 + i : 0);
+  const int id = load_id(a.ids, a.idx_bytes, addr::xext_row(row_ok, m0 + i));
   const int scr_v = a.slice_col_r[tid < a.S * 6 ? tid : 0];
   __builtin_amdgcn_sched_barrier(0);
   u32x4 gi[2], ui[2];
@@ -787,6 +778,36 @@ int xext_kk(const int32_t* na, int64_t M) {
   return top <= 1 ? 2 : (top == 2 ? 4 : 0);
 }
 
+// Launch form of gs_switch_lora_expand (shared by the launch and the address
+// model): the column-block kernel with CB 32-column blocks over RT row tiles
+// per workgroup, or the per-tile kernel; KK as xext_kk.  The column-block
+// kernel takes 64-column blocks (whole 128-byte row pieces) once they give
+// two workgroups per CU; 32-column blocks otherwise, over eight row tiles
+// when four would take more than one round of workgroups (each column's
+// lora_B is then staged half as often, and no CU runs two workgroups' worth
+// of staging where one would do).
+struct XextForm {
+  int kk;
+  bool cols;
+  int CB, RT;
+  unsigned gx, gy;
+};
+XextForm xext_expand_form(const int32_t* na, int64_t M, int32_t N, int64_t cus) {
+  XextForm f{xext_kk(na, M), false, 0, 0, static_cast<unsigned>((N + 127) / 128), static_cast<unsigned>((M + 31) / 32)};
+  if (f.kk > 0 && GS_XEXT_COLS) {
+    const int64_t tiles = (M + 31) / 32;
+    const unsigned rg4 = static_cast<unsigned>((tiles + 3) / 4), rg8 = static_cast<unsigned>((tiles + 7) / 8);
+    const bool wide = int64_t(N / 64) * rg4 >= 2 * cus;
+    const bool eight = !wide && GS_XEXT_RT8 && int64_t(N / 32) * rg4 > cus;
+    f.cols = true;
+    f.CB = wide ? 2 : 1;
+    f.RT = eight ? 8 : 4;
+    f.gx = static_cast<unsigned>(wide ? (N + 63) / 64 : N / 32);
+    f.gy = eight ? rg8 : rg4;
+  }
+  return f;
+}
+
 int check_xext(const char* who, const void* x_ext, int64_t stride_n, int64_t stride_m, int64_t M, int32_t idx_bytes,
                const int32_t* na, int32_t S, int32_t block_n, int32_t N, const void* lb) {
   GS_CHECK_ARG(idx_bytes == 4 || idx_bytes == 8, "%s: idx_bytes=%d", who, idx_bytes);
@@ -805,6 +826,411 @@ int check_xext(const char* who, const void* x_ext, int64_t stride_n, int64_t str
   return GS_OK;
 }
 
+// ----------------------------------------------------------------------------
+// Address model (test support): replays on the host every global and LDS
+// access the x_ext kernels make for one call -- every workgroup, wave, lane
+// and loop step, with the launch form the call would choose and the addr::
+// formulas the kernels use -- and checks each access against its buffer.
+// It follows the values that steer the kernels (the tile masks, the rows'
+// kernel-local ids, the slice tables), so the caller passes host copies of
+// them.  No HIP call is made.
+// ----------------------------------------------------------------------------
+struct XextModel {
+  // the call
+  int64_t M, stride_m, x_cols;      // x_ext: M rows of x_cols valid elements, stride_m apart
+  const int64_t* ids;               // kernel-local ids [M]
+  int idx_bytes;
+  const int64_t* bm;                // tile masks
+  int64_t stride_bm, bm_elems;
+  int64_t lb_elems;
+  const int32_t* tile_slice;
+  int64_t ts_len;
+  const int32_t* scr;               // slice_col_r [S * 6]
+  int na[6];
+  int S, block_n, N, H;
+  int64_t cus;
+  // outcome
+  int64_t checked = 0, bad = 0;
+  char msg[512] = {0};
+
+  void fail(const char* fmt, ...) {
+    if (++bad > 1) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(msg, sizeof msg, fmt, ap);
+    va_end(ap);
+  }
+  bool in(const char* what, int64_t lo, int64_t len, int64_t size) {
+    ++checked;
+    if (lo < 0 || len < 0 || lo + len > size) {
+      fail("%s: [%lld, %lld) outside [0, %lld)", what, (long long)lo, (long long)(lo + len), (long long)size);
+      return false;
+    }
+    return true;
+  }
+  // an access of n elements at column col of x_ext row `row`
+  void x_at(const char* what, int64_t row, int64_t col, int n) {
+    if (in(what, row, 1, M)) in(what, col, n, x_cols);
+  }
+  void lb_at(const char* what, int64_t elem) { in(what, elem, 8, lb_elems); }
+  // the id of row m as the kernel loads it (an int64 id as its low word)
+  int id_at(int64_t m, bool low_word_form) {
+    if (low_word_form && idx_bytes == 8) in("ids (low words)", 2 * m, 1, 2 * M);
+    else in("ids", m, 1, M);
+    return m >= 0 && m < M ? static_cast<int>(ids[m]) : 0;
+  }
+  int64_t mask_at(int64_t pm) {
+    in("bitmask", pm * stride_bm, 1, bm_elems);
+    const int64_t e = pm * stride_bm;
+    return e >= 0 && e < bm_elems ? bm[e] : 0;
+  }
+  int slice_at(int64_t idx) {
+    in("tile_slice", idx, 1, ts_len);
+    const int v = idx >= 0 && idx < ts_len ? tile_slice[idx] : 0;
+    in("tile_slice value (slice)", v, 1, S);
+    return v >= 0 && v < S ? v : 0;
+  }
+  int scr_at(int idx) {
+    in("slice_col_r (staged)", idx, 1, GS_MAX_SLICES * 6);
+    in("slice_col_r (written part)", idx, 1, S * 6);
+    return idx >= 0 && idx < S * 6 ? scr[idx] : 0;
+  }
+  uint64_t valid() const {
+    int tot = 0;
+    for (int t = 0; t < 6; ++t) tot += na[t];
+    return tot >= 64 ? ~0ull : ((1ull << tot) - 1ull);
+  }
+  static int lowest(uint64_t v) { return __builtin_ctzll(v); }
+
+  // The ids of a 32-row tile's rows as a wave's lanes hold them (0 past the
+  // batch) and the mask of the adapters present in them.
+  uint64_t rows_mask(int64_t m0, int (&id)[32], bool low_word_form, bool conditional) {
+    uint64_t mine = 0;
+    for (int i = 0; i < 32; ++i) {
+      const bool ok = m0 + i < M;
+      id[i] = ok || !conditional ? id_at(addr::xext_row(ok, m0 + i), low_word_form) : 0;
+      if (!ok) id[i] = 0;
+      if (ok && id[i] >= 1 && id[i] <= 64) mine |= 1ull << (id[i] - 1);
+    }
+    return mine;
+  }
+
+  // xext_block_delta: one memory trip per followed adapter
+  void block_delta(int64_t m0, int n0, int s, const int (&id)[32], uint64_t todo) {
+    while (todo) {
+      const int kid = lowest(todo) + 1;
+      todo &= todo - 1;
+      int t, first;
+      int64_t lb_off;
+      if (!addr::xext_tier(na, N, kid, t, first, lb_off)) break;
+      const int r = 16 << t, idx = kid - first;
+      const int64_t c0 = addr::xext_zcol(scr_at(s * 6 + t), idx, S, r);
+      for (int l = 0; l < 64; ++l) {
+        const int i = l & 31, h = l >> 5;
+        const bool sel = m0 + i < M && id[i] == kid;
+        for (int kb = 0; kb < r; kb += 16) {
+          const int k0 = kb + 8 * h;
+          if (sel) x_at("x_ext shrink values (general)", m0 + i, c0 + k0, 8);
+          lb_at("lora_B (general)", addr::xext_brow(lb_off, idx, N, r, n0 + i) + k0);
+        }
+      }
+    }
+  }
+  // xext_own_z: each lane's own row's shrink values of slice s
+  void own_z(int KK, int64_t m0, int s, const int (&id)[32], uint64_t todo) {
+    for (int l = 0; l < 64; ++l) {
+      const int i = l & 31, h = l >> 5;
+      const bool row_ok = m0 + i < M;
+      bool ok = row_ok && id[i] >= 1 && id[i] <= 64 && ((todo >> (id[i] - 1)) & 1ull);
+      int t, first;
+      int64_t lb_off;
+      ok = addr::xext_tier(na, N, ok ? id[i] : 1, t, first, lb_off) && ok;
+      const int r = 16 << t;
+      const int64_t c0 = addr::xext_zcol(scr_at(s * 6 + t), (ok ? id[i] : first) - first, S, r);
+      for (int kk = 0; kk < KK; ++kk) {
+        const bool kin = ok && kk * 16 < r;
+        x_at("x_ext own shrink values", addr::xext_row(row_ok, m0 + i), kin ? c0 + kk * 16 + 8 * h : 0, 8);
+      }
+    }
+  }
+  // xext_block_delta_fast: the lora_B of BA followed adapters per trip
+  void block_delta_fast(int KK, int BA, int NS, const int* n0, uint64_t todo) {
+    while (todo) {
+      std::vector<int> rk(BA, 0);
+      std::vector<int64_t> boff(BA, -1);   // -1: reads the packed array's first line
+      std::vector<int> bidx(BA, 0);
+      std::vector<int64_t> blb(BA, 0);
+      for (int b = 0; b < BA; ++b) {
+        if (!todo) continue;
+        const int bit = lowest(todo);
+        todo &= todo - 1;
+        int t, first;
+        int64_t lb_off;
+        if (addr::xext_tier(na, N, bit + 1, t, first, lb_off)) {
+          rk[b] = 16 << t;
+          bidx[b] = bit + 1 - first;
+          blb[b] = lb_off;
+          boff[b] = 0;
+        }
+      }
+      for (int l = 0; l < 64; ++l) {
+        const int i = l & 31, h = l >> 5;
+        for (int j = 0; j < NS; ++j)
+          for (int b = 0; b < BA; ++b)
+            for (int kk = 0; kk < KK; ++kk) {
+              if (kk * 16 < rk[b])
+                lb_at("lora_B (fast)", addr::xext_brow(blb[b], bidx[b], N, rk[b], i) + 8 * h +
+                                           static_cast<int64_t>(n0[j]) * rk[b] + kk * 16);
+              else
+                lb_at("lora_B (fast, clamped)", 0);
+            }
+      }
+    }
+  }
+  // xext_delta<KK> of one wave (the caller checked n0 < N)
+  void delta(int KK, int64_t m0, int n0, int s, const int (&id)[32], uint64_t bm) {
+    uint64_t mine = 0;
+    for (int i = 0; i < 32; ++i)
+      if (m0 + i < M && id[i] >= 1 && id[i] <= 64) mine |= 1ull << (id[i] - 1);
+    const uint64_t todo = mine & bm;
+    if (KK == 0) {
+      block_delta(m0, n0, s, id, todo);
+      return;
+    }
+    own_z(KK, m0, s, id, todo);
+    block_delta_fast(KK, kXextSlots / KK, 1, &n0, todo);
+  }
+
+  // ---- xext_expand_kernel / xext_shrink_expand_kernel ----------------------
+  // wless: the W-less form (the delta stored into out [M, >= N], stride_om)
+  void tile_kernel(int KK, bool wless, int64_t stride_om, int out_es) {
+    const int64_t gy = (M + 31) / 32, gx = (N + 127) / 128;
+    for (int64_t pm = 0; pm < gy; ++pm) {
+      const int64_t m0 = pm * 32;
+      const int64_t bm_raw = mask_at(pm);
+      int id[32];
+      // the rows' ids: loaded by the lanes whose row is in the batch
+      rows_mask(m0, id, false, true);
+      for (int64_t bx = 0; bx < gx; ++bx) {
+        const int n_tile0 = static_cast<int>(bx * 128);
+        if (!wless) {
+          // the read-modify-write pieces (clamped loads) and their rows' ids
+          for (int tid = 0; tid < 256; ++tid)
+            for (int q = 0; q < 2; ++q) {
+              const int prow = addr::xext_piece_row(tid, q), pc = addr::xext_piece_col(tid, q);
+              const int64_t m = m0 + prow;
+              const bool ok = m < M && n_tile0 + pc < N;
+              x_at("x_ext read-modify-write", ok ? m : m0, ok ? n_tile0 + pc : n_tile0, 8);
+              in("delta tile (LDS)", prow * (128 + 4) + pc, 8, 32 * (128 + 4));
+              if (ok && id_at(m, false) != 0) x_at("x_ext store", m, n_tile0 + pc, 8);
+            }
+        }
+        // the slice tables (the in-place form loads them before its tile
+        // mask test, the W-less form after it)
+        int s_of[4];
+        if (bm_raw != 0 || !wless) {
+          for (int tid = 0; tid < S * 6; ++tid) scr_at(tid);
+          for (int wave = 0; wave < 4; ++wave) {
+            const int n0 = n_tile0 + 32 * wave;
+            s_of[wave] = slice_at((n0 < N ? n0 : n_tile0) / block_n);
+          }
+        }
+        const uint64_t bm = static_cast<uint64_t>(bm_raw) & valid();
+        if (bm_raw != 0) {
+          for (int wave = 0; wave < 4; ++wave) {
+            const int n0 = n_tile0 + 32 * wave;
+            if (n0 < N) delta(KK, m0, n0, s_of[wave], id, bm);
+          }
+        }
+        if (wless) {
+          for (int tid = 0; tid < 256; ++tid) {
+            const int row = tid >> 3, cx = (tid & 7) * 16;
+            const int64_t m = m0 + row;
+            if (m >= M || n_tile0 + cx >= N) continue;
+            in("delta tile (LDS)", row * (128 + 4) + cx, 16, 32 * (128 + 4));
+            if (in("out row", m, 1, M)) in("out store", m * stride_om + n_tile0 + cx, 16, (M - 1) * stride_om + N);
+            (void)out_es;
+          }
+        }
+      }
+    }
+  }
+
+  // ---- xext_swiglu_kernel ----------------------------------------------------
+  void swiglu(int KK, int64_t stride_om) {
+    const int64_t gy = (M + 31) / 32, gx = (H + 127) / 128;
+    for (int64_t pm = 0; pm < gy; ++pm) {
+      const int64_t m0 = pm * 32;
+      int id[32];
+      rows_mask(m0, id, false, false);   // every lane loads (a row past the batch reads row 0)
+      const int64_t bm_raw = mask_at(pm);
+      for (int64_t bx = 0; bx < gx; ++bx) {
+        const int h_tile0 = static_cast<int>(bx * 128);
+        for (int tid = 0; tid < 256; ++tid) {
+          scr_at(tid < S * 6 ? tid : 0);
+          for (int q = 0; q < 2; ++q) {
+            const int prow = addr::xext_piece_row(tid, q), pc = addr::xext_piece_col(tid, q);
+            const int64_t m = m0 + prow;
+            const bool pok = m < M && h_tile0 + pc < H;
+            x_at("x_ext gate", pok ? m : m0, pok ? h_tile0 + pc : h_tile0, 8);
+            x_at("x_ext up", pok ? m : m0, (pok ? h_tile0 + pc : h_tile0) + H, 8);
+            in("gate / up delta (LDS)", prow * (128 + 4) + pc, 8, 32 * (128 + 4));
+            if (pok && in("out row", m, 1, M)) in("out store", m * stride_om + h_tile0 + pc, 8, (M - 1) * stride_om + H);
+          }
+        }
+        if (bm_raw == 0) continue;
+        const uint64_t bm = static_cast<uint64_t>(bm_raw) & valid();
+        uint64_t mine = 0;
+        for (int i = 0; i < 32; ++i)
+          if (m0 + i < M && id[i] >= 1 && id[i] <= 64) mine |= 1ull << (id[i] - 1);
+        const uint64_t todo0 = mine & bm;
+        for (int wave = 0; wave < 4; ++wave) {
+          const int h0 = h_tile0 + 32 * wave;
+          if (h0 >= H) continue;
+          if (KK == 0) {
+            uint64_t todo = todo0;
+            while (todo) {
+              const int kid = lowest(todo) + 1;
+              todo &= todo - 1;
+              int t, first;
+              int64_t lb_off;
+              if (!addr::xext_tier(na, N, kid, t, first, lb_off)) break;
+              const int r = 16 << t, idx = kid - first;
+              const int64_t cg = addr::xext_zcol(scr_at(t), idx, S, r), cu = addr::xext_zcol(scr_at(6 + t), idx, S, r);
+              for (int l = 0; l < 64; ++l) {
+                const int i = l & 31, h = l >> 5;
+                const bool row_ok = m0 + i < M, sel = row_ok && id[i] == kid;
+                const int64_t xr = addr::xext_row(row_ok, m0 + i);
+                for (int kb = 0; kb < r; kb += 32) {
+                  const bool two = kb + 16 < r;
+                  const int k0 = kb + 8 * h, k1 = two ? k0 + 16 : k0;
+                  for (int k : {k0, k1}) {
+                    x_at("x_ext gate shrink values", xr, (sel ? cg : 0) + k, 8);
+                    x_at("x_ext up shrink values", xr, (sel ? cu : 0) + k, 8);
+                    lb_at("gate lora_B", addr::xext_brow(lb_off, idx, N, r, h0 + i) + k);
+                    lb_at("up lora_B", addr::xext_brow(lb_off, idx, N, r, H + h0 + i) + k);
+                  }
+                }
+              }
+            }
+          } else {
+            own_z(KK, m0, 0, id, todo0);
+            own_z(KK, m0, 1, id, todo0);
+            const int n0s[2] = {h0, H + h0};
+            block_delta_fast(KK, kXextSlots / 2 / KK, 2, n0s, todo0);
+          }
+        }
+      }
+    }
+  }
+
+  // ---- xext_cols_kernel ------------------------------------------------------
+  void cols(int KK, int CB, int RT, unsigned gx, unsigned gy) {
+    const int NC = 32 * CB, RMAX = 16 * KK, CST = RMAX * 2 + 16, ABLK = NC * CST, CA = CB == 1 ? 16 : 8;
+    const int CAW = CA / RT, QP = NC * RMAX / 8 / 64, DLD = NC + 4, LPR = NC / 16, PASSES = 32 * LPR / 64;
+    const int64_t bs_bytes = static_cast<int64_t>(CA) * ABLK + 64 * 16;
+    const int64_t n_tiles = (M + 31) / 32;
+    const uint64_t vb = valid();
+    for (unsigned by = 0; by < gy; ++by)
+      for (unsigned bx = 0; bx < gx; ++bx) {
+        const int n_blk0 = static_cast<int>(bx) * NC;
+        const int64_t pm0 = static_cast<int64_t>(by) * RT;
+        const int ncols = std::min(NC, N - n_blk0);
+        std::vector<int64_t> bmt(RT, 0);
+        uint64_t all = 0;
+        for (int w = 0; w < RT; ++w) {
+          bmt[w] = pm0 + w < n_tiles ? mask_at(pm0 + w) : 0;
+          all |= static_cast<uint64_t>(bmt[w]);
+        }
+        all &= vb;
+        std::vector<std::array<int, 32>> wid(RT);
+        std::vector<int> wsc(RT * CB);
+        for (int wave = 0; wave < RT; ++wave) {
+          const int64_t m0 = (pm0 + wave) * 32;
+          for (int l = 0; l < 64; ++l) {
+            const int tid = 64 * wave + l;
+            scr_at(tid < S * 6 ? tid : 0);
+            const int cx = (l % LPR) * 16;
+            for (int ps = 0; ps < PASSES; ++ps) {
+              const int row = ps * (64 / LPR) + l / LPR;
+              const int64_t m = m0 + row;
+              const bool ook = m < M && n_blk0 + cx < N;
+              const int64_t orow = addr::xext_row(ook, m);
+              x_at("x_ext read-modify-write", orow, ook ? n_blk0 + cx : 0, 16);
+              const int oid = id_at(orow, true);
+              in("delta tile (LDS)", (static_cast<int64_t>(wave) * 32 * DLD + row * DLD + cx) * 4, 16 * 4, bs_bytes);
+              if (ook && oid != 0) x_at("x_ext store", orow, n_blk0 + cx, 16);
+            }
+          }
+          for (int i = 0; i < 32; ++i) {
+            const bool row_ok = m0 + i < M;
+            const int v = id_at(addr::xext_row(row_ok, m0 + i), true);
+            wid[wave][i] = row_ok && pm0 + wave < n_tiles ? v : 0;
+          }
+          for (int c = 0; c < CB; ++c) {
+            const int n0 = n_blk0 + 32 * c;
+            wsc[wave * CB + c] = slice_at((n0 < N ? n0 : n_blk0) / block_n);
+          }
+        }
+        bool first_chunk = true;
+        while (all) {
+          // the chunk's adapters (lane j < CA describes the j-th)
+          std::vector<int> my_r(CA, 0);
+          std::vector<int64_t> my_off(CA, 0);
+          uint64_t mm = all;
+          for (int j = 0; j < CA; ++j) {
+            if (mm) {
+              const int bit = lowest(mm);
+              int t, first;
+              int64_t lb_off;
+              if (addr::xext_tier(na, N, bit + 1, t, first, lb_off)) {
+                my_r[j] = 16 << t;
+                my_off[j] = addr::xext_brow(lb_off, bit + 1 - first, N, my_r[j], n_blk0);
+              }
+              mm &= mm - 1;
+            }
+          }
+          for (int k = 0; k < CA; ++k) all &= all - 1;
+          for (int wave = 0; wave < RT; ++wave)
+            for (int jw = 0; jw < CAW; ++jw) {
+              const int j = RT * jw + wave, r = my_r[j];
+              const int sh = 31 - __builtin_clz(r > 0 ? r / 8 : 1);
+              for (int l = 0; l < 64; ++l)
+                for (int q = 0; q < QP; ++q) {
+                  const int pc = l + 64 * q;
+                  const bool real = pc < ncols * r / 8;
+                  lb_at("lora_B block (staged)", real ? my_off[j] + 8 * pc : 0);
+                  if (real) {
+                    const int col = addr::xext_stage_colof(pc, sh), kq = addr::xext_stage_kof(pc, sh);
+                    in("staged block column", col, 1, NC);
+                    in("staged block piece", kq * 16, 16, CST);
+                    in("staging buffer (LDS)", static_cast<int64_t>(j) * ABLK + col * CST + kq * 16, 16, bs_bytes);
+                  } else {
+                    in("staging sink (LDS)", static_cast<int64_t>(CA) * ABLK + l * 16, 16, bs_bytes);
+                  }
+                }
+            }
+          if (first_chunk) {
+            for (int wave = 0; wave < RT; ++wave) {
+              const int64_t m0 = (pm0 + wave) * 32;
+              const uint64_t todo = static_cast<uint64_t>(bmt[wave]) & vb;
+              int id[32];
+              for (int i = 0; i < 32; ++i) id[i] = wid[wave][i];
+              for (int c = 0; c < CB; ++c) own_z(KK, m0, wsc[wave * CB + c], id, todo);
+            }
+            first_chunk = false;
+          }
+          for (int j = 0; j < CA; ++j)
+            for (int l = 0; l < 64; ++l)
+              for (int c = 0; c < CB; ++c)
+                for (int kk = 0; kk < KK; ++kk)
+                  in("staged operand read (LDS)",
+                     static_cast<int64_t>(j) * ABLK + (32 * c + (l & 31)) * CST + (kk * 16 + 8 * (l >> 5)) * 2, 16,
+                     bs_bytes);
+        }
+      }
+  }
+};
 }  // namespace
 
 }  // namespace gs
@@ -836,31 +1262,21 @@ int gs_switch_lora_expand(void* x_ext, int64_t stride_m, int64_t stride_n, int64
   dim3 grid((N + 127) / 128, static_cast<unsigned>((M + 31) / 32));
   hipStream_t st = static_cast<hipStream_t>(stream);
   uint16_t* xo = static_cast<uint16_t*>(x_ext);
-  const int kk = xext_kk(na, M);
-  if (kk > 0 && GS_XEXT_COLS) {
-    // 64-column blocks (whole 128-byte row pieces) once they give two
-    // workgroups per CU; 32-column blocks otherwise, over eight row tiles
-    // when four would take more than one round of workgroups (each column's
-    // lora_B is then staged half as often, and no CU runs two workgroups'
-    // worth of staging where one would do)
-    const int64_t tiles = (M + 31) / 32, cus = device_cus();
-    const unsigned rg4 = static_cast<unsigned>((tiles + 3) / 4), rg8 = static_cast<unsigned>((tiles + 7) / 8);
-    const bool wide = int64_t(N / 64) * rg4 >= 2 * cus;
-    const bool eight = !wide && GS_XEXT_RT8 && int64_t(N / 32) * rg4 > cus;
-    const dim3 g2(static_cast<unsigned>((N + 63) / 64), rg4), g1(static_cast<unsigned>(N / 32), eight ? rg8 : rg4);
-    auto go = [&](auto kern, dim3 g, int rt) {
-      hipLaunchKernelGGL(kern, g, dim3(64 * rt), 0, st, a, xo, tile_slice, block_n);
-    };
+  const XextForm f = xext_expand_form(na, M, N, device_cus());
+  const int kk = f.kk;
+  if (f.cols) {
+    const dim3 g(f.gx, f.gy);
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, g, dim3(64 * f.RT), 0, st, a, xo, tile_slice, block_n); };
     auto pick = [&](auto i64) {
       constexpr bool I64 = decltype(i64)::value;
       if (kk == 2) {
-        if (wide) go(xext_cols_kernel<2, 2, 4, I64>, g2, 4);
-        else if (eight) go(xext_cols_kernel<2, 1, 8, I64>, g1, 8);
-        else go(xext_cols_kernel<2, 1, 4, I64>, g1, 4);
+        if (f.CB == 2) go(xext_cols_kernel<2, 2, 4, I64>);
+        else if (f.RT == 8) go(xext_cols_kernel<2, 1, 8, I64>);
+        else go(xext_cols_kernel<2, 1, 4, I64>);
       } else {
-        if (wide) go(xext_cols_kernel<4, 2, 4, I64>, g2, 4);
-        else if (eight) go(xext_cols_kernel<4, 1, 8, I64>, g1, 8);
-        else go(xext_cols_kernel<4, 1, 4, I64>, g1, 4);
+        if (f.CB == 2) go(xext_cols_kernel<4, 2, 4, I64>);
+        else if (f.RT == 8) go(xext_cols_kernel<4, 1, 8, I64>);
+        else go(xext_cols_kernel<4, 1, 4, I64>);
       }
     };
     if (idx_bytes == 8) pick(std::true_type{});
@@ -954,6 +1370,69 @@ int gs_switch_lora_expand_swiglu(void* out, int64_t stride_om, int64_t stride_on
   }
   GS_CHECK_LAUNCH("gs_switch_lora_expand_swiglu");
   return GS_OK;
+}
+
+int64_t gs_check_xext_addresses(int32_t op, int64_t M, int64_t stride_m, int64_t x_cols, const int64_t* ids,
+                                int32_t idx_bytes, const int64_t* bitmask, int64_t stride_bm, int64_t bitmask_elems,
+                                int64_t lb_elems, const int32_t* tile_slice, int64_t tile_slice_len,
+                                const int32_t* slice_col_r, const int32_t* na, int32_t S, int32_t block_n, int32_t N,
+                                int32_t H, int64_t stride_om, int32_t out_dtype, char* msg, int64_t msg_len,
+                                int64_t* checked) {
+  const char* who = "gs_check_xext_addresses";
+  GS_CHECK_ARG(op >= 0 && op <= 2, "%s: op=%d", who, op);
+  GS_CHECK_ARG(M >= 0 && stride_m >= x_cols && x_cols > 0 && (ids || M == 0) && (bitmask || M == 0) && slice_col_r &&
+                   na && (tile_slice || op == 2),
+               "%s: bad arguments", who);
+  GS_CHECK_ARG(idx_bytes == 4 || idx_bytes == 8, "%s: idx_bytes=%d", who, idx_bytes);
+  GS_CHECK_ARG(S >= 1 && S <= GS_MAX_SLICES && block_n > 0 && N > 0, "%s: S / block_n / N", who);
+  XextModel m{};
+  m.M = M;
+  m.stride_m = stride_m;
+  m.x_cols = x_cols;
+  m.ids = ids;
+  m.idx_bytes = idx_bytes;
+  m.bm = bitmask;
+  m.stride_bm = stride_bm;
+  m.bm_elems = bitmask_elems;
+  m.lb_elems = lb_elems;
+  m.tile_slice = tile_slice;
+  m.ts_len = tile_slice_len;
+  m.scr = slice_col_r;
+  for (int t = 0; t < 6; ++t) m.na[t] = na[t];
+  m.S = S;
+  m.block_n = block_n;
+  m.N = N;
+  m.H = H;
+  m.cus = device_cus();
+  if (M > 0) {
+    const int kk = xext_kk(na, M);
+    if (op == 0) {
+      // the form the launch would take on this device, and every other
+      // column-block shape (they depend on the CU count)
+      const XextForm f = xext_expand_form(na, M, N, m.cus);
+      if (f.cols) {
+        m.cols(f.kk, f.CB, f.RT, f.gx, f.gy);
+        const int64_t tiles = (M + 31) / 32;
+        const unsigned rg4 = static_cast<unsigned>((tiles + 3) / 4), rg8 = static_cast<unsigned>((tiles + 7) / 8);
+        if (!(f.CB == 2)) m.cols(f.kk, 2, 4, static_cast<unsigned>((N + 63) / 64), rg4);
+        if (!(f.CB == 1 && f.RT == 8)) m.cols(f.kk, 1, 8, static_cast<unsigned>(N / 32), rg8);
+        if (!(f.CB == 1 && f.RT == 4)) m.cols(f.kk, 1, 4, static_cast<unsigned>(N / 32), rg4);
+      }
+      m.tile_kernel(kk, false, 0, 2);   // the per-tile form (taken past 1024 rows, or without the fast path)
+      if (kk > 0) m.tile_kernel(0, false, 0, 2);
+    } else if (op == 1) {
+      GS_CHECK_ARG(stride_om >= N, "%s: stride_om", who);
+      m.tile_kernel(kk, true, stride_om, out_dtype == GS_DTYPE_FP32 ? 4 : 2);
+      if (kk > 0) m.tile_kernel(0, true, stride_om, out_dtype == GS_DTYPE_FP32 ? 4 : 2);
+    } else {
+      GS_CHECK_ARG(S == 2 && N == 2 * H && stride_om >= H, "%s: the SwiGLU form needs S == 2, N == 2H", who);
+      m.swiglu(kk, stride_om);
+      if (kk > 0) m.swiglu(0, stride_om);
+    }
+  }
+  if (checked) *checked = m.checked;
+  if (msg && msg_len > 0) snprintf(msg, static_cast<size_t>(msg_len), "%s", m.msg);
+  return m.bad;
 }
 
 }  // extern "C"

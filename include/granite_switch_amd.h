@@ -247,6 +247,26 @@ int64_t gs_check_segment_addresses(int32_t dtype, int64_t num_tokens, int32_t hi
                                    const int32_t* seg_offsets, const int32_t* perm, const int32_t* z_off,
                                    int64_t z_ld, char* msg, int64_t msg_len, int64_t* checked);
 
+/* Test support (no counterpart in the reference; makes no HIP call).  The
+ * same replay for the reference-semantics ops over x_ext: op 0
+ * gs_switch_lora_expand (the launch form this device would take and every
+ * other column-block shape, plus the per-tile forms), op 1
+ * gs_switch_lora_shrink_expand into out [M, >= N] (stride_om, out_dtype),
+ * op 2 gs_switch_lora_expand_swiglu into out [M, H] (stride_om).  x_ext has M
+ * rows of x_cols valid elements, stride_m apart.  Host copies of the values
+ * that steer the kernels: ids [M] (kernel-local, as idx_bytes-wide ids would
+ * hold them), bitmask (bitmask_elems, tile pm at pm * stride_bm),
+ * tile_slice [tile_slice_len] (unused by op 2), slice_col_r [S * 6], na[6];
+ * lb_elems: the packed lora_B's size.  Returns the number of accesses outside
+ * their buffers (0: clean), the first described in msg, *checked the number
+ * checked; a negated GS_* status on bad arguments. */
+int64_t gs_check_xext_addresses(int32_t op, int64_t M, int64_t stride_m, int64_t x_cols, const int64_t* ids,
+                                int32_t idx_bytes, const int64_t* bitmask, int64_t stride_bm, int64_t bitmask_elems,
+                                int64_t lb_elems, const int32_t* tile_slice, int64_t tile_slice_len,
+                                const int32_t* slice_col_r, const int32_t* na, int32_t S, int32_t block_n, int32_t N,
+                                int32_t H, int64_t stride_om, int32_t out_dtype, char* msg, int64_t msg_len,
+                                int64_t* checked);
+
 /* The same op with its scratch (split-K partials and z) in a static device
  * array of GS_NOALLOC_SCRATCH_BYTES per GPU, so it allocates nothing: no
  * workspace, no z, no hipMalloc.  No counterpart in the reference: it is for
