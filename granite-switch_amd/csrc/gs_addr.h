@@ -111,5 +111,31 @@ GS_HD int xext_piece_col(int tid, int q) { return ((tid + 256 * q) & 15) * 8; }
 GS_HD int xext_stage_colof(int pc, int sh) { return pc >> sh; }
 GS_HD int xext_stage_kof(int pc, int sh) { return pc & ((1 << sh) - 1); }
 
+// ---- one-launch small-batch kernel (gs_small.hip) --------------------------
+// Entry a thread loads for routing slot u (tokens / sequences u * 256 + tid),
+// clamped to the last of n (n >= 1).
+GS_HD int small_route_index(int u, int tid, int n) { return imin(u * 256 + tid, n - 1); }
+// Producer workgroup bid: its (k-chunk, adapter) pair q, column block cb and
+// row split rs (the NCB * RS siblings of a pair get ids 8 apart).
+GS_HD void small_producer(int bid, int NCB, int RS, int& q, int& cb, int& rs) {
+  const int inner = (bid >> 3) % (NCB * RS);
+  cb = inner % NCB;
+  rs = inner / NCB;
+  q = ((bid >> 3) / (NCB * RS)) * 8 + (bid & 7);
+}
+// Consumer cid: its (tile group, adapter) item and row split rs.
+GS_HD void small_consumer(int cid, int RS, int& item, int& rs) {
+  item = ((cid >> 3) / RS) * 8 + (cid & 7);
+  rs = (cid >> 3) % RS;
+}
+// A token slot of a row chunk: slots past the adapter's n_g tokens re-read
+// the chunk's first (rt0 < n_g).
+GS_HD int small_slot(int slot, int n_g, int rt0) { return slot < n_g ? slot : rt0; }
+// Tagged partial (g, ks, slot, col) in the workspace: adapter g's region,
+// [KS][cap][zw] 8-byte elements.
+GS_HD int64_t small_part(int64_t region, int g, int ks, int cap, int slot, int zw, int col) {
+  return static_cast<int64_t>(g - 1) * region + (static_cast<int64_t>(ks) * cap + slot) * zw + col;
+}
+
 }  // namespace addr
 }  // namespace gs

@@ -51,6 +51,12 @@
 // Sync buffer (int32 words): [2] error word; [32*g .. 32*g + 1] the 64-bit
 // launch counter of adapter g (one 128-byte line per adapter).  Both buffers
 // are zeroed once before the first call.
+#include <stdarg.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "gs_addr.h"
 #include "gs_common.h"
 
 namespace gs {
@@ -137,30 +143,29 @@ __device__ __forceinline__ int route_nseq(const SmallRoute& r) {
 template <int U>
 __device__ __forceinline__ void route_issue(const SmallRoute& r, RouteRegs<U>& rr) {
   const int tid = threadIdx.x;
-  const int tl = r.T - 1;
   if (r.eff != nullptr) {
     // zero-extended: a negative id becomes a large one, base either way, and
     // no instruction depends on the load before the routing wait
 #pragma unroll
-    for (int u = 0; u < U; ++u) rr.rq[u] = static_cast<uint32_t>(r.eff[min(u * kSmT + tid, tl)]);
+    for (int u = 0; u < U; ++u) rr.rq[u] = static_cast<uint32_t>(r.eff[addr::small_route_index(u, tid, r.T)]);
   } else {
 #pragma unroll
-    for (int u = 0; u < U; ++u) rr.rq[u] = r.req[min(u * kSmT + tid, tl)];
+    for (int u = 0; u < U; ++u) rr.rq[u] = r.req[addr::small_route_index(u, tid, r.T)];
   }
   if (r.eff == nullptr && r.pos != nullptr) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) rr.q[u] = r.pos[min(u * kSmT + tid, tl)];
+    for (int u = 0; u < U; ++u) rr.q[u] = r.pos[addr::small_route_index(u, tid, r.T)];
   } else {
 #pragma unroll
     for (int u = 0; u < U; ++u) rr.q[u] = 0;
   }
   if (route_gated(r)) {
-    const int nl = route_nseq(r) - 1;
+    const int ns = route_nseq(r);
 #pragma unroll
-    for (int u = 0; u < U; ++u) rr.off[u] = r.act_off[min(u * kSmT + tid, nl)];
+    for (int u = 0; u < U; ++u) rr.off[u] = r.act_off[addr::small_route_index(u, tid, ns)];
     if (r.cu != nullptr) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) rr.cu[u] = r.cu[min(u * kSmT + tid, nl)];
+      for (int u = 0; u < U; ++u) rr.cu[u] = r.cu[addr::small_route_index(u, tid, ns)];
     } else {
 #pragma unroll
       for (int u = 0; u < U; ++u) rr.cu[u] = 0;
@@ -389,10 +394,8 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
   // column-block and row-split siblings of one (k-chunk, adapter) -- which
   // read the same x rows or the same lora_A rows -- get ids 8 apart and share
   // an XCD's L2.  Ids past the last (k-chunk, adapter) pair have no work.
-  const int inner = (bid >> 3) % (p.NCB * p.RS);
-  const int cb = inner % p.NCB;
-  const int rs = inner / p.NCB;
-  const int q = ((bid >> 3) / (p.NCB * p.RS)) * 8 + (bid & 7);
+  int q, cb, rs;
+  addr::small_producer(bid, p.NCB, p.RS, q, cb, rs);
   if (q >= p.KS * p.rt.NA) return;
   const int kc = q % p.KS;
   const int g = q / p.KS + 1;
@@ -439,7 +442,7 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
   for (int pp = 0; pp < NPW; ++pp) {
     const int64_t kp = k_lo + pp * KSTEP + q4 * P;
     const bool ok = nok[0] && kp < k_hi;
-    av[0][pp] = ld_a(arow[0] + (ok ? kp : 0) * ES);
+    av[0][pp] = ld_a(arow[0] + addr::reg_x_elem(ok, kp, 0) * ES);
   }
   route_gate<U>(p.rt, g, L.rt, rr);
   if (tid == 0) L.epoch = static_cast<uint32_t>(counter >> kEpochShift);   // visible after route_list's barriers
@@ -447,7 +450,6 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
   const int first = 32 * rs;             // this row split's first chunk
   if (!active || n_g <= first) return;
   const uint64_t tag = static_cast<uint64_t>(L.epoch + 1u) << 32;
-  uint64_t* part = p.part + static_cast<int64_t>(g - 1) * p.region;
 
   // x rows of one 32-token chunk.  Rows past the adapter's tokens re-read its
   // first token (their sums are never stored) and pieces past the k-chunk
@@ -460,12 +462,13 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       const int slot = rt0 + 16 * rt + i16;
-      const char* xrow = static_cast<const char*>(p.x) + static_cast<int64_t>(L.rt.tok[slot < n_g ? slot : rt0]) * p.ldx * ES;
+      const char* xrow =
+          static_cast<const char*>(p.x) + static_cast<int64_t>(L.rt.tok[addr::small_slot(slot, n_g, rt0)]) * p.ldx * ES;
 #pragma unroll
       for (int pp = 0; pp < NPW; ++pp) {
         const int64_t kp = k_lo + pp * KSTEP + q4 * P;
         xk[pp] = kp < k_hi;
-        xv[rt][pp] = ld16(xrow + (xk[pp] ? kp : 0) * ES);
+        xv[rt][pp] = ld16(xrow + addr::reg_x_elem(xk[pp], kp, 0) * ES);
       }
     }
   };
@@ -474,7 +477,7 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
   for (int pp = 0; pp < NPW; ++pp) {
     const int64_t kp = k_lo + pp * KSTEP + q4 * P;
     const bool ok = nok[1] && kp < k_hi;
-    av[1][pp] = ld_a(arow[1] + (ok ? kp : 0) * ES);
+    av[1][pp] = ld_a(arow[1] + addr::reg_x_elem(ok, kp, 0) * ES);
   }
   __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the MFMAs wait
 
@@ -500,7 +503,7 @@ __device__ __forceinline__ void produce(const FusedParams& p, FusedLds<BF16, U>&
       const int rt = wave >> 1;
       const int nw = cb * 32 + 16 * (wave & 1) + i16;
       const f32x4 v = ((L.u.red[0][wave][l] + L.u.red[1][wave][l]) + L.u.red[2][wave][l]) + L.u.red[3][wave][l];
-      uint64_t* dst = part + (static_cast<int64_t>(kc) * p.cap + rt0 + 16 * rt + 4 * q4) * p.zw + nw;
+      uint64_t* dst = p.part + addr::small_part(p.region, g, kc, p.cap, rt0 + 16 * rt + 4 * q4, p.zw, nw);
       const int slots = n_g - (rt0 + 16 * rt + 4 * q4);    // rows of this lane's 4 still in the batch
       if (active && nw < ncols) {
 #pragma unroll
@@ -544,8 +547,8 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
   // (tile group, adapter) items are dealt to the XCDs by the low 3 id bits;
   // the RS row-split siblings of an item, which read the same lora_B rows, get
   // ids 8 apart and share an XCD's L2.  Ids past the last item have no work.
-  const int item = ((cid >> 3) / p.RS) * 8 + (cid & 7);
-  const int rs = (cid >> 3) % p.RS;
+  int item, rs;
+  addr::small_consumer(cid, p.RS, item, rs);
   if (item >= p.NG * p.rt.NA) return;
   const int grp = item % p.NG;
   const int g = item / p.NG + 1;
@@ -575,7 +578,7 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
 #pragma unroll
       for (int kg = 0; kg < KG; ++kg) {
         const int k0 = kg * KSTEP + q4 * P;
-        bv[q][kg] = ld16(brow + (k0 < r ? k0 : 0) * ES);
+        bv[q][kg] = ld16(brow + addr::k_or_zero(k0, r) * ES);
       }
     }
   };
@@ -595,7 +598,6 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
   const int n_g = route_list<U>(g, L.rt, rr);
   if (r == 0 || n_g == 0) return;       // no producer wrote partials for it
   const uint32_t want = L.epoch + 1u;
-  const uint64_t* part = p.part + static_cast<int64_t>(g - 1) * p.region;
   const int64_t kstride = static_cast<int64_t>(p.cap) * p.zw;
   // this consumer's share of the 2^20 that g's NG * RS consumers add per launch
   const int ncons = p.NG * p.RS;
@@ -617,7 +619,7 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
     for (int ps = 0; ps < PASSES; ++ps) {
       const int row = rt0 + ps * RPP + tid / LPR;
       rok[ps] = row < n_g;
-      yoff[ps] = static_cast<int64_t>(L.rt.tok[rok[ps] ? row : rt0]) * p.ldy + nt0 * NT + cx;
+      yoff[ps] = static_cast<int64_t>(L.rt.tok[addr::small_slot(row, n_g, rt0)]) * p.ldy + nt0 * NT + cx;
 #pragma unroll
       for (int hf = 0; hf < NH; ++hf) yv[hf][ps] = ld_y(static_cast<const char*>(p.y) + (yoff[ps] + hf * kHalf) * ES);
     }
@@ -636,7 +638,7 @@ __device__ __forceinline__ void consume(const FusedParams& p, FusedLds<BF16, U>&
         const int row = e / r;
         const int c = e - row * r;
         eok[m] = e < 32 * r && rt0 + row < n_g;
-        src[m] = part + static_cast<int64_t>(rt0 + (eok[m] ? row : 0)) * p.zw + zc0 + (eok[m] ? c : 0);
+        src[m] = p.part + addr::small_part(p.region, g, 0, p.cap, rt0 + (eok[m] ? row : 0), p.zw, zc0 + (eok[m] ? c : 0));
         sum[m] = 0.f;
       }
       for (int ks0 = 0; ks0 < p.KS; ks0 += kKsGrp) {
@@ -905,6 +907,217 @@ void launch_fused(const SmallPlan& pl, const FusedParams& fp, unsigned grid, boo
   else launch_fused_u<BF16, kSmMaxU>(pl, fp, grid, spec, st);
 }
 
+// ----------------------------------------------------------------------------
+// Address model (test support): replays on the host every global and LDS
+// access of small_fused_kernel for one call -- routing, every producer and
+// consumer workgroup, wave, lane and loop step, with the call's own plan and
+// the addr:: formulas the kernel uses -- and checks each access against its
+// buffer.  The adapters' token lists (which the kernel's routing computes)
+// come from the host copy of the gated ids.  No HIP call is made.
+// ----------------------------------------------------------------------------
+struct SmallModel {
+  bool bf16;
+  int64_t T;
+  int H;
+  int64_t ldx;
+  int out_total;
+  int64_t ldy;
+  int S;
+  const int64_t* a_off;
+  const int64_t* b_off;
+  const int32_t* rank;
+  int64_t a_elems, b_elems;
+  int NA;
+  int nseq;
+  bool has_eff, has_pos, has_cu, has_act;
+  int64_t ws_elems;                 // 8-byte elements of the workspace
+  int64_t sync_words;
+  std::vector<std::vector<int>> toks;   // toks[g]: adapter g's tokens, ascending
+  int64_t checked = 0, bad = 0;
+  char msg[512] = {0};
+
+  void fail(const char* fmt, ...) {
+    if (++bad > 1) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(msg, sizeof msg, fmt, ap);
+    va_end(ap);
+  }
+  bool in(const char* what, int64_t lo, int64_t len, int64_t size) {
+    ++checked;
+    if (lo < 0 || len < 0 || lo + len > size) {
+      fail("%s: [%lld, %lld) outside [0, %lld)", what, (long long)lo, (long long)(lo + len), (long long)size);
+      return false;
+    }
+    return true;
+  }
+  int es() const { return bf16 ? 2 : 4; }
+  int P() const { return bf16 ? 8 : 4; }
+  // the routing of one workgroup (route_issue / route_gate / route_list)
+  void routing(int U) {
+    for (int tid = 0; tid < kSmT; ++tid)
+      for (int u = 0; u < U; ++u) {
+        const int k = u * kSmT + tid;
+        if (has_eff) in("eff_ids", addr::small_route_index(u, tid, static_cast<int>(T)), 1, T);
+        else in("req_ids", addr::small_route_index(u, tid, static_cast<int>(T)), 1, T);
+        if (!has_eff && has_pos) in("positions", addr::small_route_index(u, tid, static_cast<int>(T)), 1, T);
+        if (!has_eff && has_act) {
+          in("act_offsets", addr::small_route_index(u, tid, nseq), 1, nseq);
+          if (has_cu) in("cu_seqlens", addr::small_route_index(u, tid, nseq), 1, nseq + 1);
+          if (k < nseq) in("sequence table (LDS)", k, 1, U * kSmT);
+        }
+        in("token list (LDS)", k, 1, U * kSmT);
+      }
+  }
+  void counter(int g) { in("launch counter", static_cast<int64_t>(kSyncLine) * g, 2, sync_words); }
+
+  void produce(const SmallPlan& pl, int RS, int bid, int U) {
+    int q, cb, rs;
+    addr::small_producer(bid, pl.NCB, RS, q, cb, rs);
+    if (q >= pl.KS * NA) return;
+    const int kc = q % pl.KS, g = q / pl.KS + 1;
+    const int r = rank[g], ncols = S * r;
+    const bool active = r > 0 && cb * 32 < ncols;
+    const int KSTEP = 4 * P(), KW = pl.NPW * KSTEP;
+    const std::vector<int>& tk = toks[g];
+    const int n_g = static_cast<int>(tk.size());
+    const int first = 32 * rs;
+    counter(g);
+    routing(U);
+    for (int c2 = 0; c2 < 2; ++c2) {
+      if (c2 == 1 && (!active || n_g <= first)) break;   // the second block goes out with the first x rows
+      for (int wave = 0; wave < 4; ++wave) {
+        const int64_t k_lo = (static_cast<int64_t>(kc) * 4 + wave) * KW;
+        const int64_t k_hi = std::min<int64_t>(H, k_lo + KW);
+        for (int l = 0; l < 64; ++l) {
+          const int i16 = l & 15, q4 = l >> 4;
+          const int n = cb * 32 + 16 * c2 + i16;
+          const bool nok = active && n < ncols;
+          for (int pp = 0; pp < pl.NPW; ++pp) {
+            const int64_t kp = k_lo + pp * KSTEP + q4 * P();
+            const bool ok = nok && kp < k_hi;
+            const int64_t e = a_off[g] + static_cast<int64_t>(nok ? n : 0) * H + addr::reg_x_elem(ok, kp, 0);
+            if (in("lora_A row", nok ? n : 0, 1, std::max(ncols, 1))) in("lora_A", e, P(), a_elems);
+          }
+        }
+      }
+    }
+    if (!active || n_g <= first) return;
+    for (int rt0 = first; rt0 < n_g; rt0 += 32 * RS) {
+      for (int wave = 0; wave < 4; ++wave) {
+        const int64_t k_lo = (static_cast<int64_t>(kc) * 4 + wave) * KW;
+        const int64_t k_hi = std::min<int64_t>(H, k_lo + KW);
+        for (int l = 0; l < 64; ++l) {
+          const int i16 = l & 15, q4 = l >> 4;
+          for (int rt = 0; rt < 2; ++rt) {
+            const int sl = addr::small_slot(rt0 + 16 * rt + i16, n_g, rt0);
+            in("token list read (LDS)", sl, 1, U * kSmT);
+            if (!in("token slot (the adapter's listed tokens)", sl, 1, n_g)) continue;
+            const int tok = tk[sl];
+            for (int pp = 0; pp < pl.NPW; ++pp) {
+              const int64_t kp = k_lo + pp * KSTEP + q4 * P();
+              if (in("x row", tok, 1, T)) in("x", static_cast<int64_t>(tok) * ldx + addr::reg_x_elem(kp < k_hi, kp, 0), P(), (T - 1) * ldx + H);
+            }
+          }
+          // the stores of the tile wave w finishes
+          const int rt = wave >> 1, nw = cb * 32 + 16 * (wave & 1) + i16;
+          const int slot0 = rt0 + 16 * rt + 4 * q4;
+          if (active && nw < ncols)
+            for (int e = 0; e < 4; ++e)
+              if (e < n_g - slot0) {
+                in("partial slot", slot0 + e, 1, pl.cap);
+                in("partial column", nw, 1, pl.zw);
+                in("tagged partials", addr::small_part(pl.region_bytes / 8, g, kc, pl.cap, slot0 + e, pl.zw, nw), 1,
+                   ws_elems);
+              }
+        }
+      }
+    }
+  }
+
+  void consume(const SmallPlan& pl, int RS, int cid, int U, int64_t region) {
+    int item, rs;
+    addr::small_consumer(cid, RS, item, rs);
+    const int NG = pl.NNT / pl.TG;
+    if (item >= NG * NA) return;
+    const int grp = item % NG, g = item / NG + 1, nt0 = grp * pl.TG;
+    const int NQ = pl.NQ, NT = 64 * NQ, NH = NQ / 2;
+    const int r = rank[g];
+    int s = 0;
+    for (int k = 1; k < S; ++k)
+      if (nt0 * NT >= sb[k]) s = k;
+    const int zc0 = s * r;
+    const int KSTEP = 4 * P(), RMAX = pl.zw <= 32 * S ? 32 : 64, KG = RMAX / KSTEP;
+    const int EPL = 16 / es(), LPR = kHalf / EPL, RPP = kSmT / LPR, PASSES = 32 / RPP;
+    const std::vector<int>& tk = toks[g];
+    const int n_g = static_cast<int>(tk.size());
+    counter(g);
+    routing(U);
+    auto load_b = [&](int nt) {
+      in("column tile", nt, 1, pl.NNT);
+      for (int wave = 0; wave < 4; ++wave)
+        for (int l = 0; l < 64; ++l) {
+          const int i16 = l & 15, q4 = l >> 4;
+          for (int q = 0; q < NQ; ++q) {
+            const int64_t n = static_cast<int64_t>(nt) * NT + 16 * (q * 4 + wave) + i16;
+            in("lora_B column", n, 1, out_total);
+            for (int kg = 0; kg < KG; ++kg)
+              in("lora_B", b_off[g] + n * r + addr::k_or_zero(kg * KSTEP + q4 * P(), r), P(), b_elems);
+          }
+        }
+    };
+    load_b(nt0);
+    if (r == 0 || n_g == 0) return;
+    for (int rt0 = 32 * rs; rt0 < n_g; rt0 += 32 * RS) {
+      if (pl.TG > 1 && rt0 != 32 * rs) load_b(nt0);
+      for (int tid = 0; tid < kSmT; ++tid) {
+        const int cx = (tid % LPR) * EPL;
+        for (int ps = 0; ps < PASSES; ++ps) {
+          const int row = rt0 + ps * RPP + tid / LPR;
+          const int sl = addr::small_slot(row, n_g, rt0);
+          in("token list read (LDS)", sl, 1, U * kSmT);
+          if (!in("token slot (the adapter's listed tokens)", sl, 1, n_g)) continue;
+          const int64_t yoff = static_cast<int64_t>(tk[sl]) * ldy + static_cast<int64_t>(nt0) * NT + cx;
+          for (int t = 0; t < pl.TG; ++t)
+            for (int hf = 0; hf < NH; ++hf) {
+              in("y column", static_cast<int64_t>(nt0) * NT + cx + t * NT + hf * kHalf, EPL, out_total);
+              in("y", yoff + t * NT + hf * kHalf, EPL, (T - 1) * ldy + out_total);
+            }
+          in("delta tile read (LDS)", (ps * RPP + tid / LPR) * (kHalf + 4) + cx, EPL, 32 * (kHalf + 4));
+        }
+        // the chunk's shrink rows: partials polled and staged
+        for (int eb = 0; eb < 2; ++eb) {
+          if (kSmT * 4 * eb >= 32 * r) break;
+          for (int m = 0; m < 4; ++m) {
+            const int e = tid + kSmT * (4 * eb + m);
+            const int row = e / r, c = e - row * r;
+            const bool eok = e < 32 * r && rt0 + row < n_g;
+            if (eok)
+              for (int ks = 0; ks < pl.KS; ++ks) {
+                in("partial column (consumer)", zc0 + c, 1, pl.zw);
+                in("tagged partials (consumer)",
+                   addr::small_part(region, g, ks, pl.cap, rt0 + row, pl.zw, zc0 + c), 1, ws_elems);
+              }
+            if (e < 32 * r) in("shrink rows (LDS)", (static_cast<int64_t>(row) * kZld + c) * es(), es(), 32 * kZld * es());
+          }
+        }
+      }
+      // the MFMAs' shrink-row reads
+      for (int l = 0; l < 64; ++l) {
+        const int i16 = l & 15, q4 = l >> 4;
+        for (int kg = 0; kg < KG; ++kg) {
+          if (kg * KSTEP >= r) continue;
+          const int k0 = kg * KSTEP + q4 * P();
+          for (int rt = 0; rt < 2; ++rt)
+            in("shrink rows read (LDS)", ((16 * rt + i16) * kZld + (k0 < r ? k0 : 0)) * es(), 16, 32 * kZld * es());
+        }
+      }
+      for (int t = 1; t < pl.TG; ++t) load_b(nt0 + t);
+    }
+    in("error word", kSyncErrWord, 1, sync_words);
+  }
+  int sb[GS_MAX_SLICES + 1];
+};
 }  // namespace
 
 }  // namespace gs
@@ -1040,6 +1253,67 @@ int gs_switched_lora_small(int32_t dtype, const int64_t* req_ids, const int64_t*
   else launch_fused<false>(pl, fp, grid, speculate != 0, st);
   GS_CHECK_LAUNCH(who);
   return GS_OK;
+}
+
+int64_t gs_check_small_addresses(int32_t dtype, int64_t num_tokens, int32_t hidden, int64_t ldx, int32_t out_total,
+                                 int64_t ldy, const int32_t* slice_bounds, int32_t num_slices, const int64_t* a_off,
+                                 int64_t a_pack_elems, const int64_t* b_off, int64_t b_pack_elems,
+                                 const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* eff_ids,
+                                 int32_t num_seqs, int32_t route_flags, int32_t row_split, char* msg, int64_t msg_len,
+                                 int64_t* checked) {
+  const char* who = "gs_check_small_addresses";
+  GS_CHECK_ARG(dtype == GS_DTYPE_BF16 || dtype == GS_DTYPE_FP32, "%s: dtype=%d", who, dtype);
+  const bool has_cu = (route_flags & 4) != 0;
+  const int nseq = has_cu ? num_seqs : 1;
+  GS_CHECK_ARG(gs_small_eligible(num_tokens, nseq, num_slices, slice_bounds, num_adapters, max_rank),
+               "%s: shape outside the small-batch path", who);
+  GS_CHECK_ARG(row_split >= 1 && row_split <= kSmMaxRowSplit && nseq >= 1, "%s: row_split / num_seqs", who);
+  GS_CHECK_ARG(a_off && b_off && ranks && (eff_ids || num_tokens == 0), "%s: NULL table", who);
+  SmallModel m{};
+  m.bf16 = dtype == GS_DTYPE_BF16;
+  m.T = num_tokens;
+  m.H = hidden;
+  m.ldx = ldx;
+  m.out_total = out_total;
+  m.ldy = ldy;
+  m.S = num_slices;
+  for (int s = 0; s <= num_slices; ++s) m.sb[s] = slice_bounds[s];
+  m.a_off = a_off;
+  m.b_off = b_off;
+  m.rank = ranks;
+  m.a_elems = a_pack_elems;
+  m.b_elems = b_pack_elems;
+  m.NA = num_adapters;
+  m.nseq = nseq;
+  m.has_eff = (route_flags & 1) != 0;
+  m.has_pos = (route_flags & 2) != 0;
+  m.has_cu = has_cu;
+  m.has_act = (route_flags & 8) != 0;
+  m.sync_words = kSyncBytes / 4;
+  m.toks.assign(num_adapters + 1, {});
+  for (int64_t t = 0; t < num_tokens; ++t) {
+    const int v = eff_ids[t];
+    if (v >= 1 && v <= num_adapters) m.toks[v].push_back(static_cast<int>(t));
+  }
+  if (num_tokens > 0) {
+    const int64_t ws_bytes = gs_small_workspace_bytes(dtype, num_tokens, hidden, num_slices, num_adapters, max_rank,
+                                                      out_total, slice_bounds);
+    m.ws_elems = ws_bytes / 8;
+    const SmallPlan pl = plan_small(num_tokens, hidden, num_slices, num_adapters, max_rank, m.bf16, out_total,
+                                    slice_bounds, row_split);
+    const int64_t region = ((ws_bytes / kSmMaxAdapters) & ~int64_t(15)) / 8;   // as the launch derives it
+    if (region < pl.region_bytes / 8) m.fail("%s: adapter region of %lld elements is too small", who, (long long)region);
+    const int U = (num_tokens <= kSmT && nseq <= kSmT) ? 1 : kSmMaxU;
+    const int64_t NP = producer_wgs(pl, num_adapters, row_split);
+    const int64_t NC = consumer_wgs(pl, num_adapters, row_split);
+    SmallPlan plr = pl;
+    plr.region_bytes = region * 8;           // the producers' stride is the launch's region
+    for (int64_t b = 0; b < NP; ++b) m.produce(plr, row_split, static_cast<int>(b), U);
+    for (int64_t c = 0; c < NC; ++c) m.consume(pl, row_split, static_cast<int>(c), U, region);
+  }
+  if (checked) *checked = m.checked;
+  if (msg && msg_len > 0) snprintf(msg, static_cast<size_t>(msg_len), "%s", m.msg);
+  return m.bad;
 }
 
 }  // extern "C"

@@ -267,6 +267,24 @@ int64_t gs_check_xext_addresses(int32_t op, int64_t M, int64_t stride_m, int64_t
                                 int32_t H, int64_t stride_om, int32_t out_dtype, char* msg, int64_t msg_len,
                                 int64_t* checked);
 
+/* Test support (no counterpart in the reference; makes no HIP call).  The
+ * same replay for the one-launch small-batch kernel (gs_switched_lora_small):
+ * the routing loads, every producer and consumer workgroup, wave, lane and
+ * loop step, with the call's own plan (row_split) and the workspace size
+ * gs_small_workspace_bytes gives.  eff_ids [num_tokens]: the gated ids the
+ * kernel's routing produces (host copy; they give each adapter's token
+ * list).  route_flags: which routing inputs the call passes -- 1 eff_ids,
+ * 2 positions, 4 cu_seqlens (num_seqs sequences), 8 act_offsets.  Returns
+ * the number of accesses outside their buffers (0: clean), the first
+ * described in msg, *checked the number checked; a negated GS_* status on
+ * bad arguments. */
+int64_t gs_check_small_addresses(int32_t dtype, int64_t num_tokens, int32_t hidden, int64_t ldx, int32_t out_total,
+                                 int64_t ldy, const int32_t* slice_bounds, int32_t num_slices, const int64_t* a_off,
+                                 int64_t a_pack_elems, const int64_t* b_off, int64_t b_pack_elems,
+                                 const int32_t* ranks, int32_t num_adapters, int32_t max_rank, const int32_t* eff_ids,
+                                 int32_t num_seqs, int32_t route_flags, int32_t row_split, char* msg, int64_t msg_len,
+                                 int64_t* checked);
+
 /* The same op with its scratch (split-K partials and z) in a static device
  * array of GS_NOALLOC_SCRATCH_BYTES per GPU, so it allocates nothing: no
  * workspace, no z, no hipMalloc.  No counterpart in the reference: it is for

@@ -175,3 +175,82 @@ def test_model_catches_a_planted_out_of_range_table():
         _lib.GS_DTYPE_BF16, T, H, H, O, O, i32([0, O]), S, i64(a_off), a_el, i64(b_off_bad), b_el, i32(r8), 2, 16,
         i32(seg), i32(perm), None, 0, msg, 512, ctypes.byref(checked))
     assert bad > 0 and "lora_B" in msg.value.decode()
+
+
+# ---- the one-launch small-batch kernel (gs_check_small_addresses) ----------
+
+def _check_small(T, H, slices, ranks, eff, dtype=_lib.GS_DTYPE_BF16, row_split=1, route_flags=1, num_seqs=1,
+                 ldx=None, ldy=None):
+    S, O = len(slices), int(sum(slices))
+    r8, a_off, b_off, a_el, b_el = _pack_tables(ranks, S, H, O)
+    NA = len(ranks)
+    max_rank = max([8] + r8)
+    bounds = np.concatenate([[0], np.cumsum(slices)]).astype(np.int32)
+    i32 = lambda v: (ctypes.c_int32 * len(v))(*[int(u) for u in v])
+    i64 = lambda v: (ctypes.c_int64 * len(v))(*[int(u) for u in v])
+    msg = ctypes.create_string_buffer(512)
+    checked = ctypes.c_int64(0)
+    bad = _lib.load().gs_check_small_addresses(
+        dtype, T, H, ldx or H, O, ldy or O, i32(bounds), S, i64(a_off), a_el, i64(b_off), b_el, i32(r8), NA, max_rank,
+        i32(np.asarray(eff).tolist() or [0]), num_seqs, route_flags, row_split, msg, 512, ctypes.byref(checked))
+    assert bad >= 0, f"bad arguments: {_lib.last_error()}"
+    assert bad == 0, f"{bad} violations, first: {msg.value.decode()}"
+    return checked.value
+
+
+@pytest.mark.parametrize("config", [0, 1])
+def test_small_kernel_benchmark_workloads(config):
+    r = workloads.routing_for(config)
+    eff = _eff(r)
+    dt = _lib.GS_DTYPE_FP32 if config == 0 else _lib.GS_DTYPE_BF16
+    for spec in workloads.module_specs(config):
+        for flags in (1, 2 | 4 | 8):          # pre-gated ids; the request with positions, sequences, offsets
+            n = _check_small(r.num_tokens, spec.hidden, spec.output_slices, spec.ranks, eff, dt, route_flags=flags,
+                             num_seqs=len(r.cu_seqlens) - 1)
+        print(f"small kernel, config {config} {spec.name}: {n} accesses checked")
+
+
+SMALL = [
+    # T, H, slices, ranks, seed, row splits
+    (1000, 1024, (256, 128), [16, 64, 8], 1, (1, 2, 3, 8, 32)),
+    (333, 1000, (128,), [8, 24, 40, 64, 16], 2, (1,)),
+    (7, 4096, (128, 128, 256), [32, 32], 3, (1,)),
+    (1024, 512, (256,), [32] * 64, 4, (1, 2, 32)),
+    (512, 2048, (2048,), [8, 8, 8, 8], 62, (1, 4, 16)),
+    (1024, 1024, (2560, 2560), [32] * 64, 70, (1, 2, 4)),           # tile groups
+    (256, 4096, (4096, 1024, 1024), [32] * 12, 5, (1, 2)),          # decode QKV
+    (1, 4096, (4096,), [64] * 3, 6, (1,)),
+]
+
+
+@pytest.mark.parametrize("T,H,slices,ranks,seed,splits", SMALL)
+def test_small_kernel_shapes(T, H, slices, ranks, seed, splits):
+    rng = np.random.default_rng(seed)
+    NA = len(ranks)
+    eff = rng.integers(0, NA + 1, size=T)
+    if T >= 128:
+        runs = np.repeat(rng.integers(0, NA + 1, size=T // 256 + 1), 128)      # runs of 128 tokens
+        eff[: T // 2] = runs[: T // 2] if len(runs) >= T // 2 else np.resize(runs, T // 2)
+    for dt in (_lib.GS_DTYPE_BF16, _lib.GS_DTYPE_FP32):
+        for rs in splits:
+            _check_small(T, H, slices, ranks, eff, dt, row_split=rs)
+    _check_small(T, H, slices, ranks, eff, ldx=H + 64, ldy=int(sum(slices)) + 128)
+    _check_small(T, H, slices, ranks, np.zeros(T, dtype=np.int64))
+    if T > 1:
+        _check_small(T, H, slices, ranks, eff, route_flags=2 | 4 | 8, num_seqs=min(T, 40))
+
+
+def test_small_kernel_model_catches_a_short_lora_B_pack():
+    """A lora_B pack one adapter block short is reported."""
+    T, H, slices, ranks = 64, 256, (128,), [16, 16]
+    S, O = 1, 128
+    r8, a_off, b_off, a_el, b_el = _pack_tables(ranks, S, H, O)
+    i32 = lambda v: (ctypes.c_int32 * len(v))(*[int(u) for u in v])
+    i64 = lambda v: (ctypes.c_int64 * len(v))(*[int(u) for u in v])
+    msg = ctypes.create_string_buffer(512)
+    checked = ctypes.c_int64(0)
+    eff = [1, 2] * 32
+    bad = _lib.load().gs_check_small_addresses(
+        _lib.GS_DTYPE_BF16, T, H, H, O, O, i32([0, O]), S, i64(a_off), a_el, i64(b_off), b_el - O * 16, i32(r8), 2, 16,
+        i32(eff), 1, 1, 1, msg, 512, ctypes.byref(checked))
+    assert bad > 0 and "lora_B" in msg.value.decode()
