@@ -131,6 +131,30 @@ GS_HD void small_consumer(int cid, int RS, int& item, int& rs) {
 // A token slot of a row chunk: slots past the adapter's n_g tokens re-read
 // the chunk's first (rt0 < n_g).
 GS_HD int small_slot(int slot, int n_g, int rt0) { return slot < n_g ? slot : rt0; }
+// ---- GEMM (gs_gemm.hip) -----------------------------------------------------
+// Tile (tm, tn) of workgroup bid: tiles are ordered in groups of `group` tile
+// rows (column by column inside a group) and XCD x = bid % 8 takes the
+// contiguous range [x * per, (x + 1) * per) of that order.  False for an id
+// past the last tile.
+GS_HD bool gemm_tile(int bid, int tiles_m, int tiles_n, int group, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  const int per = (total + 7) >> 3;
+  const int t = (bid & 7) * per + (bid >> 3);
+  if (t >= total) return false;
+  const int grp = t / (group * tiles_n);
+  const int first_m = grp * group;
+  const int gm = imin(group, tiles_m - first_m);
+  const int rr = t - grp * group * tiles_n;
+  tm = first_m + rr % gm;
+  tn = rr / gm;
+  return true;
+}
+// An operand row a thread moves: rows past the matrix re-read its last.
+GS_HD int gemm_row(int r, int rows) { return imin(r, rows - 1); }
+// The global 16-byte piece a lane moves into LDS position l % 8 of row r
+// (XOR swizzle by the row).
+GS_HD int gemm_piece(int l, int r) { return (l & 7) ^ (r & 7); }
+
 // Tagged partial (g, ks, slot, col) in the workspace: adapter g's region,
 // [KS][cap][zw] 8-byte elements.
 GS_HD int64_t small_part(int64_t region, int g, int ks, int cap, int slot, int zw, int col) {

@@ -19,6 +19,12 @@
 // into LDS (gemm_bf16_tn_dma_kernel); otherwise they are loaded into
 // registers, zero-filled past K, and written to padded LDS rows
 // (gemm_bf16_tn_kernel).
+#include <stdarg.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "gs_addr.h"
 #include "gs_common.h"
 
 namespace gs {
@@ -58,16 +64,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tn_kernel(GemmParams p
   extern __shared__ __align__(16) char smem[];
 
   // tile of this workgroup: XCD x = id % 8 takes tiles [x*per, (x+1)*per)
-  const int total = p.tiles_m * p.tiles_n;
-  const int per = (total + 7) >> 3;
-  const int t = (static_cast<int>(blockIdx.x) & 7) * per + (static_cast<int>(blockIdx.x) >> 3);
-  if (t >= total) return;
-  const int group = t / (kGGroup * p.tiles_n);
-  const int first_m = group * kGGroup;
-  const int gm = min(kGGroup, p.tiles_m - first_m);
-  const int rr = t - group * kGGroup * p.tiles_n;
-  const int tm = first_m + rr % gm;
-  const int tn = rr / gm;
+  int tm, tn;
+  if (!addr::gemm_tile(static_cast<int>(blockIdx.x), p.tiles_m, p.tiles_n, kGGroup, tm, tn)) return;
 
   const int tid = threadIdx.x;
   // global -> LDS mapping: 8 consecutive threads move one row's 128 bytes
@@ -78,8 +76,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tn_kernel(GemmParams p
   const char* gb[kGPieces];
 #pragma unroll
   for (int j = 0; j < kGPieces; ++j) {
-    const int ra = min(tm * kGBM + lrow + j * kGRowStep, p.M - 1);
-    const int rb = min(tn * kGBN + lrow + j * kGRowStep, p.N - 1);
+    const int ra = addr::gemm_row(tm * kGBM + lrow + j * kGRowStep, p.M);
+    const int rb = addr::gemm_row(tn * kGBN + lrow + j * kGRowStep, p.N);
     ga[j] = p.a + static_cast<int64_t>(ra) * p.lda * 2;
     gb[j] = p.b + static_cast<int64_t>(rb) * p.ldb * 2;
   }
@@ -205,16 +203,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tn_dma_kernel(GemmPara
   constexpr int NJ = kGBN / WN / 32;
   __shared__ __align__(16) char sA0[kDOp], sB0[kDOp], sA1[kDOp], sB1[kDOp];
 
-  const int total = p.tiles_m * p.tiles_n;
-  const int per = (total + 7) >> 3;
-  const int t = (static_cast<int>(blockIdx.x) & 7) * per + (static_cast<int>(blockIdx.x) >> 3);
-  if (t >= total) return;
-  const int group = t / (kGGroup * p.tiles_n);
-  const int first_m = group * kGGroup;
-  const int gm = min(kGGroup, p.tiles_m - first_m);
-  const int rr = t - group * kGGroup * p.tiles_n;
-  const int tm = first_m + rr % gm;
-  const int tn = rr / gm;
+  int tm, tn;
+  if (!addr::gemm_tile(static_cast<int>(blockIdx.x), p.tiles_m, p.tiles_n, kGGroup, tm, tn)) return;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -226,9 +216,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tn_dma_kernel(GemmPara
 #pragma unroll
   for (int i = 0; i < TPO; ++i) {
     const int r = RPW * wave + 8 * i + (l >> 3);
-    const int piece = (l & 7) ^ (r & 7);
-    da[i] = p.a + static_cast<int64_t>(min(tm * kGBM + r, p.M - 1)) * p.lda * 2 + piece * 16;
-    db[i] = p.b + static_cast<int64_t>(min(tn * kGBN + r, p.N - 1)) * p.ldb * 2 + piece * 16;
+    const int piece = addr::gemm_piece(l, r);
+    da[i] = p.a + static_cast<int64_t>(addr::gemm_row(tm * kGBM + r, p.M)) * p.lda * 2 + piece * 16;
+    db[i] = p.b + static_cast<int64_t>(addr::gemm_row(tn * kGBN + r, p.N)) * p.ldb * 2 + piece * 16;
   }
   auto issue = [&](int kt, char* sa, char* sb) {
     const int64_t off = static_cast<int64_t>(kt) * kDRow;
@@ -314,6 +304,136 @@ void launch_gemm(unsigned grid, const GemmParams& p, hipStream_t st) {
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * WM * WN), kGLds, st, p);
 }
 
+// ----------------------------------------------------------------------------
+// Address model (test support): replays on the host every global and LDS
+// access of both GEMM kernels for one shape -- every workgroup, thread and
+// k-tile -- and checks each against its buffer, and that the grid takes
+// every tile exactly once.  No HIP call is made.
+// ----------------------------------------------------------------------------
+struct GemmModel {
+  int64_t M, N, K, lda, ldb, ldc;
+  int tiles_m, tiles_n;
+  int64_t checked = 0, bad = 0;
+  char msg[512] = {0};
+  void fail(const char* fmt, ...) {
+    if (++bad > 1) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(msg, sizeof msg, fmt, ap);
+    va_end(ap);
+  }
+  bool in(const char* what, int64_t lo, int64_t len, int64_t size) {
+    ++checked;
+    if (lo < 0 || len < 0 || lo + len > size) {
+      fail("%s: [%lld, %lld) outside [0, %lld)", what, (long long)lo, (long long)(lo + len), (long long)size);
+      return false;
+    }
+    return true;
+  }
+  int64_t a_elems() const { return (M - 1) * lda + K; }
+  int64_t b_elems() const { return (N - 1) * ldb + K; }
+  // the tiles of the grid, each once
+  template <typename F>
+  void tiles(F&& fn) {
+    const int64_t total = int64_t(tiles_m) * tiles_n, grid = 8 * ((total + 7) / 8);
+    std::vector<char> seen(total, 0);
+    for (int64_t b = 0; b < grid; ++b) {
+      int tm, tn;
+      if (!addr::gemm_tile(static_cast<int>(b), tiles_m, tiles_n, kGGroup, tm, tn)) continue;
+      if (!in("tile row", tm, 1, tiles_m) || !in("tile column", tn, 1, tiles_n)) continue;
+      if (seen[int64_t(tm) * tiles_n + tn]++) fail("tile (%d, %d) taken twice", tm, tn);
+      fn(tm, tn);
+    }
+    for (int64_t t = 0; t < total; ++t)
+      if (!seen[t]) {
+        fail("tile %lld of %lld is never taken", (long long)t, (long long)total);
+        break;
+      }
+  }
+  void stores(int tm, int tn, int WM, int WN) {
+    const int MI = kGBM / WM / 32, NJ = kGBN / WN / 32;
+    for (int wave = 0; wave < WM * WN; ++wave)
+      for (int l = 0; l < 64; ++l) {
+        const int wm = wave / WN, wn = wave % WN;
+        const int row0 = tm * kGBM + wm * MI * 32, col0 = tn * kGBN + wn * NJ * 32 + (l & 31);
+        for (int i = 0; i < MI; ++i)
+          for (int j = 0; j < NJ; ++j) {
+            const int col = col0 + j * 32;
+            if (col >= N) continue;
+            for (int v = 0; v < 16; ++v) {
+              const int row = row0 + i * 32 + ((v >> 2) << 3) + ((l >> 5) << 2) + (v & 3);
+              if (row < M) in("C", int64_t(row) * ldc + col, 1, (M - 1) * ldc + N);
+            }
+          }
+      }
+  }
+  // gemm_bf16_tn_dma_kernel<WM, WN> (K % 64 == 0)
+  void dma(int WM, int WN) {
+    const int NW = WM * WN, RPW = kGBM / NW, TPO = RPW / 8, MI = kGBM / WM / 32, NJ = kGBN / WN / 32;
+    const int nk = static_cast<int>(K / kDBK);
+    tiles([&](int tm, int tn) {
+      for (int wave = 0; wave < NW; ++wave) {
+        for (int l = 0; l < 64; ++l)
+          for (int i = 0; i < TPO; ++i) {
+            const int r = RPW * wave + 8 * i + (l >> 3);
+            const int piece = addr::gemm_piece(l, r);
+            const int64_t ra = addr::gemm_row(tm * kGBM + r, static_cast<int>(M));
+            const int64_t rb = addr::gemm_row(tn * kGBN + r, static_cast<int>(N));
+            in("stage row (LDS)", (RPW * wave + 8 * i) * kDRow + l * 16, 16, kDOp);
+            for (int kt = 0; kt < nk; ++kt) {
+              in("A", ra * lda + int64_t(kt) * kDBK + piece * 8, 8, a_elems());
+              in("B", rb * ldb + int64_t(kt) * kDBK + piece * 8, 8, b_elems());
+            }
+          }
+        const int wm = wave / WN, wn = wave % WN;
+        for (int l = 0; l < 64; ++l)
+          for (int kk = 0; kk < kDBK / 16; ++kk) {
+            const int pos = ((kk * 2 + (l >> 5)) ^ (l & 7)) * 16;
+            for (int i = 0; i < MI; ++i) in("A operand (LDS)", (wm * MI * 32 + (l & 31) + i * 32) * kDRow + pos, 16, kDOp);
+            for (int j = 0; j < NJ; ++j) in("B operand (LDS)", (wn * NJ * 32 + (l & 31) + j * 32) * kDRow + pos, 16, kDOp);
+          }
+      }
+      stores(tm, tn, WM, WN);
+    });
+  }
+  // gemm_bf16_tn_kernel<KTAIL, WM, WN>
+  void reg(bool KTAIL, int WM, int WN) {
+    const int threads = 64 * WM * WN, pieces = kGBM * (kGRowBytes / 16) / threads, step = threads / (kGRowBytes / 16);
+    const int MI = kGBM / WM / 32, NJ = kGBN / WN / 32;
+    const int nk = static_cast<int>((K + kGBK - 1) / kGBK);
+    tiles([&](int tm, int tn) {
+      for (int tid = 0; tid < threads; ++tid) {
+        const int lrow = tid >> 3, lpc = (tid & 7) * 16, kp = (tid & 7) * 8;
+        for (int j = 0; j < pieces; ++j) {
+          const int64_t ra = addr::gemm_row(tm * kGBM + lrow + j * step, static_cast<int>(M));
+          const int64_t rb = addr::gemm_row(tn * kGBN + lrow + j * step, static_cast<int>(N));
+          for (int kt = 0; kt < nk; ++kt) {
+            const bool ok = !KTAIL || kt * kGBK + kp < K;
+            const int64_t off = ok ? int64_t(kt) * kGBK + lpc / 2 : 0;
+            in("A", ra * lda + off, 8, a_elems());
+            in("B", rb * ldb + off, 8, b_elems());
+          }
+          for (int buf = 0; buf < 2; ++buf) {
+            in("A stage (LDS)", buf * kGStage + (lrow + j * step) * kGLd + lpc, 16, kGLds);
+            in("B stage (LDS)", buf * kGStage + kGBM * kGLd + (lrow + j * step) * kGLd + lpc, 16, kGLds);
+          }
+        }
+      }
+      for (int wave = 0; wave < WM * WN; ++wave) {
+        const int wm = wave / WN, wn = wave % WN;
+        for (int l = 0; l < 64; ++l)
+          for (int buf = 0; buf < 2; ++buf)
+            for (int kk = 0; kk < kGBK / 16; ++kk) {
+              const int64_t sa = buf * kGStage + (wm * MI * 32 + (l & 31)) * kGLd + (l >> 5) * 16 + kk * 32;
+              const int64_t sb = buf * kGStage + kGBM * kGLd + (wn * NJ * 32 + (l & 31)) * kGLd + (l >> 5) * 16 + kk * 32;
+              for (int i = 0; i < MI; ++i) in("A operand (LDS)", sa + i * 32 * kGLd, 16, kGLds);
+              for (int j = 0; j < NJ; ++j) in("B operand (LDS)", sb + j * 32 * kGLd, 16, kGLds);
+            }
+      }
+      stores(tm, tn, WM, WN);
+    });
+  }
+};
 }  // namespace
 
 }  // namespace gs
@@ -360,6 +480,30 @@ int gs_gemm_bf16_tn(const void* a, int64_t lda, const void* b, int64_t ldb, void
   else launch_gemm<true>(grid, p, st);
   GS_CHECK_LAUNCH(who);
   return GS_OK;
+}
+
+int64_t gs_check_gemm_addresses(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, char* msg,
+                                int64_t msg_len, int64_t* checked) {
+  const char* who = "gs_check_gemm_addresses";
+  GS_CHECK_ARG(M > 0 && N > 0 && K > 0 && K % 8 == 0 && lda >= K && ldb >= K && ldc >= N, "%s: shape", who);
+  GemmModel m{};
+  m.M = M;
+  m.N = N;
+  m.K = K;
+  m.lda = lda;
+  m.ldb = ldb;
+  m.ldc = ldc;
+  m.tiles_m = static_cast<int>((M + kGBM - 1) / kGBM);
+  m.tiles_n = static_cast<int>((N + kGBN - 1) / kGBN);
+  if (K % kDBK == 0) {
+    m.dma(2, 4);
+    m.reg(false, 2, 4);      // the register-staged form of the same shape
+  } else {
+    m.reg(true, 2, 4);
+  }
+  if (checked) *checked = m.checked;
+  if (msg && msg_len > 0) snprintf(msg, static_cast<size_t>(msg_len), "%s", m.msg);
+  return m.bad;
 }
 
 }  // extern "C"

@@ -1,6 +1,9 @@
 // Metadata kernels: segment builder, latest-wins routing, reference bitmasks.
 #include <stdarg.h>
 
+#include <algorithm>
+#include <vector>
+
 #include "gs_common.h"
 
 namespace gs {
@@ -444,6 +447,113 @@ __global__ __launch_bounds__(256) void split_indices_kernel(const uint8_t* __res
   }
 }
 
+// ---------------------------------------------------------------------------
+// Address model (test support): replays on the host every global and LDS
+// access of the metadata kernels for one call, following the values that
+// steer them (the ids, positions, sequence table and offsets), and checks
+// each against its buffer.  No HIP call is made.
+// ---------------------------------------------------------------------------
+struct MetaModel {
+  int64_t checked = 0, bad = 0;
+  char msg[512] = {0};
+  void fail(const char* fmt, ...) {
+    if (++bad > 1) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(msg, sizeof msg, fmt, ap);
+    va_end(ap);
+  }
+  bool in(const char* what, int64_t lo, int64_t len, int64_t size) {
+    ++checked;
+    if (lo < 0 || len < 0 || lo + len > size) {
+      fail("%s: [%lld, %lld) outside [0, %lld)", what, (long long)lo, (long long)(lo + len), (long long)size);
+      return false;
+    }
+    return true;
+  }
+
+  // ---- the segment builder (both forms) ----------------------------------
+  int T = 0, nseq = 1, NA = 1;
+  const int64_t* req = nullptr;
+  const int64_t* pos = nullptr;
+  const int32_t* cu = nullptr;
+  const int64_t* act = nullptr;
+  // find_seq over the staged or the global table (n entries), as the kernel
+  int seq_of(int t, bool lds) {
+    int lo = 0, hi = nseq - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      in(lds ? "sequence table (LDS)" : "cu_seqlens", mid, 1, lds ? kCuCap : nseq + 1);
+      if (cu[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+  }
+  int gate(int t, bool lds) {
+    int64_t id = req[t];
+    if (act != nullptr) {
+      int sq = 0;
+      if (cu != nullptr) sq = seq_of(t, lds && cu != nullptr);
+      if (cu != nullptr) in(lds ? "sequence table (LDS)" : "cu_seqlens", sq, 1, lds ? kCuCap : nseq + 1);
+      in(lds ? "offsets (LDS)" : "act_offsets", sq, 1, lds ? kCuCap : nseq);
+      const int64_t q = pos != nullptr ? pos[t] : static_cast<int64_t>(t - (cu != nullptr ? cu[sq] : 0));
+      if (q < act[sq]) id = 0;
+    }
+    if (id < 0 || id > NA) id = 0;
+    return static_cast<int>(id);
+  }
+  void build(bool two_launch) {
+    const int chunks = T > 0 ? (T + kBuildThreads - 1) / kBuildThreads : 1;
+    const bool lds = act != nullptr && nseq <= kCuCap;
+    const bool need_pos = pos != nullptr && act != nullptr;
+    // the stable order's slot of every token (what the scatter writes)
+    std::vector<int> eff(T), start(NA + 2, 0), seen(NA + 1, 0);
+    for (int t = 0; t < T; ++t) eff[t] = gate(t, lds);
+    for (int t = 0; t < T; ++t) ++start[eff[t] + 1];
+    for (int g = 1; g <= NA + 1; ++g) start[g] += start[g - 1];
+    const int64_t lds_adapters = GS_MAX_ADAPTERS + 1;
+    for (int b = 0; b < chunks; ++b) {
+      const int c0 = b * kBuildThreads;
+      if (lds)
+        for (int i = 0; i < nseq; ++i) {
+          in("sequence table (LDS)", i, 1, kCuCap);
+          if (cu) in("cu_seqlens", i, 1, nseq + 1);
+          in("act_offsets", i, 1, nseq);
+        }
+      for (int i = 0; i <= NA; ++i) in("per-adapter counts (LDS)", i, 1, lds_adapters);
+      if (!two_launch) {
+        // pass 1: every chunk of the batch, loads clamped
+        const int nch = (T + kBuildThreads - 1) / kBuildThreads;
+        for (int k = 0; k < nch; ++k)
+          for (int tid = 0; tid < kBuildThreads; ++tid) {
+            const int tc = std::min(k * kBuildThreads + tid, T - 1);
+            in("req_ids", tc, 1, T);
+            if (need_pos) in("positions", tc, 1, T);
+          }
+      } else {
+        for (int tid = 0; tid < kBuildThreads; ++tid) {
+          const int tc = std::min(c0 + tid, T - 1);
+          if (T > 0) {
+            in("req_ids", tc, 1, T);
+            if (need_pos) in("positions", tc, 1, T);
+          }
+        }
+        for (int i = 0; i <= NA; ++i) in("histograms", static_cast<int64_t>(b) * (NA + 1) + i, 1, int64_t(chunks) * (NA + 1));
+        for (int i = 0; i < chunks * (NA + 1); ++i) in("histograms (scatter)", i, 1, int64_t(chunks) * (NA + 1));
+      }
+      // the own chunk: eff written, seg by workgroup 0, perm by the scatter
+      if (b == 0)
+        for (int g = 0; g <= NA; ++g) in("seg_offsets", g, 1, NA + 1);
+      for (int tid = 0; tid < kBuildThreads; ++tid) {
+        const int t = c0 + tid;
+        if (t >= T) continue;
+        in("eff_ids", t, 1, T);
+        const int g = eff[t];
+        in("wave counts (LDS)", (tid >> 6) * lds_adapters + g, 1, kBuildWaves * lds_adapters);
+        if (g > 0) in("perm", start[g] + seen[g]++, 1, T);
+      }
+    }
+  }
+};
 }  // namespace gs
 
 using namespace gs;
@@ -545,6 +655,26 @@ int gs_compute_bitmasks(const void* adapter_indices, int32_t idx_bytes, int64_t 
                      static_cast<int>(M), remap_tables_t, na_plus_1, num_modules, block_m, bitmasks, remapped);
   GS_CHECK_LAUNCH("gs_compute_bitmasks");
   return GS_OK;
+}
+
+int64_t gs_check_build_addresses(int64_t num_tokens, int32_t num_seqs, int32_t num_adapters, const int64_t* req_ids,
+                                 const int64_t* positions, const int32_t* cu_seqlens, const int64_t* act_offsets,
+                                 int32_t two_launch, char* msg, int64_t msg_len, int64_t* checked) {
+  GS_CHECK_ARG(num_adapters >= 1 && num_adapters <= GS_MAX_ADAPTERS && num_tokens >= 0 && num_tokens < (1ll << 31),
+               "gs_check_build_addresses: shape");
+  GS_CHECK_ARG(num_tokens == 0 || req_ids, "gs_check_build_addresses: NULL req_ids");
+  MetaModel m{};
+  m.T = static_cast<int>(num_tokens);
+  m.nseq = cu_seqlens ? num_seqs : 1;
+  m.NA = num_adapters;
+  m.req = req_ids;
+  m.pos = positions;
+  m.cu = cu_seqlens;
+  m.act = act_offsets;
+  m.build(two_launch != 0 && num_tokens > 0);
+  if (checked) *checked = m.checked;
+  if (msg && msg_len > 0) snprintf(msg, static_cast<size_t>(msg_len), "%s", m.msg);
+  return m.bad;
 }
 
 }  // extern "C"

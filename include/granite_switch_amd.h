@@ -107,6 +107,18 @@ int gs_build_segments(const int64_t* req_ids, const int64_t* positions, const in
                       int32_t* eff_ids, int32_t* seg_offsets, int32_t* perm, void* workspace, int64_t workspace_bytes,
                       void* stream);
 
+/* Test support (no counterpart in the reference; makes no HIP call).  Replays
+ * on the host every global and LDS access of gs_build_segments for these
+ * inputs (host copies; the same NULL conventions) -- the one-launch form, or
+ * the two-launch form when two_launch is nonzero -- gating every token as the
+ * kernels do and following each token to the perm slot its scatter writes.
+ * Returns the number of accesses outside their buffers (0: clean), the first
+ * described in msg, *checked the number checked; a negated GS_* status on bad
+ * arguments. */
+int64_t gs_check_build_addresses(int64_t num_tokens, int32_t num_seqs, int32_t num_adapters, const int64_t* req_ids,
+                                 const int64_t* positions, const int32_t* cu_seqlens, const int64_t* act_offsets,
+                                 int32_t two_launch, char* msg, int64_t msg_len, int64_t* checked);
+
 /* ------------------------------------------------------------------------
  * Probe-slot split of the per-token index stream (reference ids, 0 = base).
  *
@@ -437,6 +449,16 @@ int gs_switch_lora_shrink_expand(void* out, int32_t out_dtype, int64_t stride_om
  * ---------------------------------------------------------------------- */
 int gs_gemm_bf16_tn(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int64_t ldc, int64_t M,
                     int64_t N, int64_t K, void* stream);
+
+/* Test support (no counterpart in the reference; makes no HIP call).  Replays
+ * on the host every global and LDS access of gs_gemm_bf16_tn's kernels for
+ * this shape (the direct-to-LDS form when K % 64 == 0, plus the
+ * register-staged form) -- every workgroup, thread and k-tile -- and checks
+ * that the grid takes every tile exactly once.  Returns the number of
+ * violations (0: clean), the first described in msg, *checked the number of
+ * accesses checked; a negated GS_* status on bad arguments. */
+int64_t gs_check_gemm_addresses(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, char* msg,
+                                int64_t msg_len, int64_t* checked);
 
 #ifdef __cplusplus
 }

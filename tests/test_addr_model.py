@@ -254,3 +254,71 @@ def test_small_kernel_model_catches_a_short_lora_B_pack():
         _lib.GS_DTYPE_BF16, T, H, H, O, O, i32([0, O]), S, i64(a_off), a_el, i64(b_off), b_el - O * 16, i32(r8), 2, 16,
         i32(eff), 1, 1, 1, msg, 512, ctypes.byref(checked))
     assert bad > 0 and "lora_B" in msg.value.decode()
+
+
+# ---- the segment builder (gs_check_build_addresses) ------------------------
+
+def _check_build(req, NA, pos=None, cu=None, act=None, two_launch=False):
+    T = len(req)
+    arr = lambda a, dt: None if a is None else np.ascontiguousarray(a, dtype=dt)
+    req_a, pos_a, cu_a, act_a = arr(req, np.int64), arr(pos, np.int64), arr(cu, np.int32), arr(act, np.int64)
+    ptr = lambda a: None if a is None or a.size == 0 else a.ctypes.data
+    msg = ctypes.create_string_buffer(512)
+    checked = ctypes.c_int64(0)
+    nseq = len(cu) - 1 if cu is not None else 1
+    bad = _lib.load().gs_check_build_addresses(T, nseq, NA, ptr(req_a), ptr(pos_a), ptr(cu_a), ptr(act_a),
+                                               int(two_launch), msg, 512, ctypes.byref(checked))
+    assert bad >= 0, f"bad arguments: {_lib.last_error()}"
+    assert bad == 0, f"{bad} violations, first: {msg.value.decode()}"
+    return checked.value
+
+
+@pytest.mark.parametrize("config", [0, 1, 2, 3, 4])
+def test_builder_benchmark_workloads(config):
+    r = workloads.routing_for(config)
+    NA = workloads.num_adapters_for(config)
+    for two in (False, True):
+        _check_build(r.req_ids, NA, r.positions, r.cu_seqlens, r.act_offsets, two_launch=two)
+
+
+@pytest.mark.parametrize("T,NA,seed", [(0, 4, 0), (1, 1, 1), (63, 3, 2), (1023, 7, 3), (1024, 64, 4), (1025, 255, 5),
+                                       (5000, 256, 6), (65536, 24, 7)])
+def test_builder_random_batches(T, NA, seed):
+    """The GPU builder tests' batches: out-of-range ids, packed sequences with
+    cached prefixes, activation offsets; with and without positions and
+    sequences, both forms."""
+    rng = np.random.default_rng(seed)
+    req = rng.integers(-3, NA + 4, size=T)
+    nseq = max(1, T // 50)
+    cuts = np.sort(rng.choice(np.arange(1, T), size=min(nseq - 1, max(T - 1, 0)), replace=False)) if T > 1 else []
+    cu = np.concatenate([[0], cuts, [T]]).astype(np.int32)
+    lens = np.diff(cu)
+    cached = rng.integers(0, 100, size=lens.size)
+    pos = np.concatenate([c + np.arange(n) for c, n in zip(cached, lens)]) if T else np.zeros(0, np.int64)
+    offs = rng.integers(0, 160, size=lens.size)
+    for two in (False, True):
+        _check_build(req, NA, pos, cu, offs, two_launch=two)
+        _check_build(req, NA, None, cu, offs, two_launch=two)
+        _check_build(req, NA, two_launch=two)
+    if T > 1:                                     # more sequences than the LDS table holds
+        cu2 = np.arange(0, T + 1, dtype=np.int32)
+        _check_build(req, NA, None, cu2, rng.integers(0, 2, size=T), two_launch=T > 2048)
+
+
+# ---- the layer GEMM (gs_check_gemm_addresses) -------------------------------
+
+@pytest.mark.parametrize("M,N,K,pad", [
+    (1, 7296, 4096, 0),            # one token
+    (256, 7296, 4096, 0),          # decode QKV x . w_ext^T
+    (300, 1000, 72, 0),            # K not a multiple of 64 (register-staged, zero-filled tail), ragged tiles
+    (4144, 4864, 1024, 8),         # step down-projection shape at a shorter K, padded strides
+    (257, 257, 512, 64),
+    (1100, 3000, 8, 0),
+])
+def test_gemm_shapes(M, N, K, pad):
+    msg = ctypes.create_string_buffer(512)
+    checked = ctypes.c_int64(0)
+    bad = _lib.load().gs_check_gemm_addresses(M, N, K, K + pad, K + pad, N + pad, msg, 512, ctypes.byref(checked))
+    assert bad >= 0, f"bad arguments: {_lib.last_error()}"
+    assert bad == 0, f"{bad} violations, first: {msg.value.decode()}"
+    assert checked.value > 0
