@@ -47,6 +47,8 @@ SIGNATURES = {
                                            c_void_p, c_i64, c_void_p, c_i32, c_i32, c_void_p, c_void_p, c_void_p,
                                            c_i64, ctypes.c_char_p, c_i64, c_void_p]),
     "gs_check_gemm_addresses": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_char_p, c_i64, c_void_p]),
+    "gs_check_token_addresses": (c_i64, [c_i64, c_i32, c_void_p, c_i32, c_void_p, c_i32, c_i32, c_i32, c_i32,
+                                         ctypes.c_char_p, c_i64, c_void_p]),
     "gs_check_build_addresses": (c_i64, [c_i64, c_i32, c_i32, c_void_p, c_void_p, c_void_p, c_void_p, c_i32,
                                          ctypes.c_char_p, c_i64, c_void_p]),
     "gs_check_small_addresses": (c_i64, [c_i32, c_i64, c_i32, c_i64, c_i32, c_i64, c_void_p, c_i32, c_void_p, c_i64,

@@ -553,6 +553,69 @@ struct MetaModel {
       }
     }
   }
+
+  // ---- route_latest_wins_kernel: one workgroup per sequence ----------------
+  void route(int num_control) {
+    for (int sq = 0; sq < nseq; ++sq) {
+      for (int i = 0; i < num_control; ++i) {
+        in("control tokens", i, 1, num_control);
+        in("control tokens (LDS)", i, 1, GS_MAX_ADAPTERS + 1);
+      }
+      int lo = 0, hi = T;
+      if (cu != nullptr) {
+        in("cu_seqlens", sq, 2, nseq + 1);
+        lo = cu[sq];
+        hi = cu[sq + 1];
+      }
+      in("start ids (when given)", sq, 1, nseq);
+      for (int base = lo; base < hi; base += kRouteThreads)
+        for (int tid = 0; tid < kRouteThreads; ++tid) {
+          const int t = base + tid;
+          if (t < hi) {
+            in("input_ids", t, 1, T);
+            in("routed ids", t, 1, T);
+          }
+        }
+    }
+  }
+  // ---- bitmask_kernel: grid (ceil(M / 256), num_modules) ---------------------
+  void bitmask(const int64_t* ids, int na_plus_1, int num_modules, int block_m) {
+    const int M = T;
+    const int64_t tiles = (M + block_m - 1) / block_m;
+    const bool pow2 = block_m <= 64 && (block_m & (block_m - 1)) == 0;
+    auto remap_at = [&](int u, int mod) {
+      int64_t id = ids[u];
+      id = id < 0 ? 0 : (id > na_plus_1 - 1 ? na_plus_1 - 1 : id);
+      in("remap table", id * num_modules + mod, 1, int64_t(na_plus_1) * num_modules);
+    };
+    for (int mod = 0; mod < num_modules; ++mod)
+      for (int t = 0; t < M; ++t) {
+        in("adapter ids", t, 1, M);
+        remap_at(t, mod);
+        in("remapped ids", int64_t(mod) * M + t, 1, int64_t(num_modules) * M);
+        if (t % block_m == 0) {
+          in("bitmasks", int64_t(mod) * tiles + t / block_m, 1, int64_t(num_modules) * tiles);
+          if (!pow2)
+            for (int u = t; u < std::min(M, t + block_m); ++u) {
+              in("adapter ids", u, 1, M);
+              remap_at(u, mod);
+            }
+        }
+      }
+  }
+  // ---- split_indices_kernel ----------------------------------------------------
+  void split(const int64_t* ids, int lut_len) {
+    for (int k = 0; k < lut_len; ++k) {
+      in("kind table", k, 1, lut_len);
+      in("kind table (LDS)", k, 1, GS_MAX_ADAPTERS + 1);
+    }
+    for (int t = 0; t < T; ++t) {
+      in("adapter ids", t, 1, T);
+      const int64_t v = ids[t];
+      if (v >= 0 && v < lut_len) in("kind table (LDS)", v, 1, GS_MAX_ADAPTERS + 1);
+      in("split outputs", t, 1, T);
+    }
+  }
 };
 }  // namespace gs
 
@@ -672,6 +735,29 @@ int64_t gs_check_build_addresses(int64_t num_tokens, int32_t num_seqs, int32_t n
   m.cu = cu_seqlens;
   m.act = act_offsets;
   m.build(two_launch != 0 && num_tokens > 0);
+  if (checked) *checked = m.checked;
+  if (msg && msg_len > 0) snprintf(msg, static_cast<size_t>(msg_len), "%s", m.msg);
+  return m.bad;
+}
+
+int64_t gs_check_token_addresses(int64_t num_tokens, int32_t num_seqs, const int32_t* cu_seqlens,
+                                 int32_t num_control, const int64_t* ids, int32_t na_plus_1, int32_t num_modules,
+                                 int32_t block_m, int32_t lut_len, char* msg, int64_t msg_len, int64_t* checked) {
+  const char* who = "gs_check_token_addresses";
+  GS_CHECK_ARG(num_tokens >= 0 && num_tokens < (1ll << 31) && (ids || num_tokens == 0), "%s: tokens", who);
+  GS_CHECK_ARG(num_control >= 0 && num_control <= GS_MAX_ADAPTERS + 1 && (cu_seqlens == nullptr || num_seqs >= 1),
+               "%s: num_control / num_seqs", who);
+  GS_CHECK_ARG(na_plus_1 >= 1 && num_modules >= 1 && block_m >= 1 && block_m <= 1024, "%s: remap shape", who);
+  GS_CHECK_ARG(lut_len >= 1 && lut_len <= GS_MAX_ADAPTERS + 1, "%s: lut_len", who);
+  MetaModel m{};
+  m.T = static_cast<int>(num_tokens);
+  m.nseq = cu_seqlens ? num_seqs : 1;
+  m.cu = cu_seqlens;
+  if (num_tokens > 0) {
+    m.route(num_control);
+    m.bitmask(ids, na_plus_1, num_modules, block_m);
+    m.split(ids, lut_len);
+  }
   if (checked) *checked = m.checked;
   if (msg && msg_len > 0) snprintf(msg, static_cast<size_t>(msg_len), "%s", m.msg);
   return m.bad;

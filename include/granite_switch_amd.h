@@ -119,6 +119,19 @@ int64_t gs_check_build_addresses(int64_t num_tokens, int32_t num_seqs, int32_t n
                                  const int64_t* positions, const int32_t* cu_seqlens, const int64_t* act_offsets,
                                  int32_t two_launch, char* msg, int64_t msg_len, int64_t* checked);
 
+/* Test support (no counterpart in the reference; makes no HIP call).  The
+ * replay of the per-token kernels over one token stream of num_tokens:
+ * gs_route_latest_wins (num_control control tokens, cu_seqlens host copy or
+ * NULL), gs_compute_bitmasks of the ids (host copy; a [na_plus_1,
+ * num_modules] remap table, tiles of block_m) with the remapped output, and
+ * gs_split_adapter_indices of the same ids with a kind table of lut_len.
+ * Returns the number of accesses outside their buffers (0: clean), the first
+ * described in msg, *checked the number checked; a negated GS_* status on bad
+ * arguments. */
+int64_t gs_check_token_addresses(int64_t num_tokens, int32_t num_seqs, const int32_t* cu_seqlens,
+                                 int32_t num_control, const int64_t* ids, int32_t na_plus_1, int32_t num_modules,
+                                 int32_t block_m, int32_t lut_len, char* msg, int64_t msg_len, int64_t* checked);
+
 /* ------------------------------------------------------------------------
  * Probe-slot split of the per-token index stream (reference ids, 0 = base).
  *

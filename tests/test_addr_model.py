@@ -322,3 +322,23 @@ def test_gemm_shapes(M, N, K, pad):
     assert bad >= 0, f"bad arguments: {_lib.last_error()}"
     assert bad == 0, f"{bad} violations, first: {msg.value.decode()}"
     assert checked.value > 0
+
+
+# ---- latest-wins routing, bitmasks, probe split (gs_check_token_addresses) ---
+
+@pytest.mark.parametrize("T,nseq,NA,modules,block_m,seed", [
+    (1, 1, 1, 1, 32, 0), (700, 40, 6, 4, 32, 1), (5000, 1, 64, 128, 32, 2), (333, 7, 10, 3, 24, 3),
+    (1024, 1024, 255, 2, 1, 4), (4144, 304, 24, 128, 64, 5)])
+def test_token_kernels(T, nseq, NA, modules, block_m, seed):
+    rng = np.random.default_rng(seed)
+    ids = rng.integers(-2, NA + 3, size=T).astype(np.int64)     # includes out-of-range ids
+    cuts = np.sort(rng.choice(np.arange(1, T), size=min(nseq - 1, T - 1), replace=False)) if T > 1 else []
+    cu = np.concatenate([[0], cuts, [T]]).astype(np.int32)
+    msg = ctypes.create_string_buffer(512)
+    checked = ctypes.c_int64(0)
+    for with_cu in (True, False):
+        bad = _lib.load().gs_check_token_addresses(
+            T, len(cu) - 1, cu.ctypes.data if with_cu else None, min(NA + 1, 257), ids.ctypes.data, NA + 1, modules,
+            block_m, min(NA + 1, 257), msg, 512, ctypes.byref(checked))
+        assert bad == 0, f"{bad} violations, first: {msg.value.decode()}"
+        assert checked.value > 0
