@@ -165,6 +165,9 @@ def xext_ops(cfg: int, n: int) -> None:
     them (src/granite_switch/vllm/core/lora.py:596-686): switch_lora_expand in
     place on x_ext[:, :N] (src/granite_switch/kernels/switch_lora_kernel.py:171-458)
     and, for gate_up, switch_lora_expand_swiglu into a [T, H] output (:668-857).
+    For the in-place projections the vLLM layer's own expand when segments
+    are built (gs_expand_add reading each row's shrink columns of x_ext by
+    token) is timed beside the reference op, on the same inputs.
     x_ext is computed once per buffer set outside the timed region.  Algorithmic
     bytes: per adapted row its N output values read and written and its S*r
     shrink values read, each used adapter's lora_B tiers once, the ids; the
@@ -229,21 +232,27 @@ def xext_ops(cfg: int, n: int) -> None:
             def call(i):
                 ops.op("switch_lora_expand")(x_exts[i % nsets], loc, bm, layer._lb_packed, layer.tile_to_slice,
                                               layer.slice_col_r, *layer._na, S, layer._block_n, N)
-        call(0)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for i in range(n):
-                call(i)
-        graph.replay()
-        torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record()
-        graph.replay()
-        end.record()
-        end.synchronize()
-        us = start.elapsed_time(end) * 1e3 / n
+        def timed(fn):
+            fn(0)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for i in range(n):
+                    fn(i)
+            graph.replay()
+            torch.cuda.synchronize()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            graph.replay()
+            end.record()
+            end.synchronize()
+            return start.elapsed_time(end) * 1e3 / n
+
+        us = timed(call)
+        # the layer's own expand over x_ext when segments are built: gs_expand_add
+        # reading each row's shrink columns by token (vllm_layers._run_segment_expand)
+        seg_us = None if fuse else timed(lambda i: layer._run_segment_expand(x_exts[i % nsets], segs))
         # adapted rows: an applicable adapter (a token of a non-applicable one stays base)
         rp = [promote_rank(r) for r in ranks]
         adapted = [a for a in range(NA) if ranks[a] > 0]
@@ -259,6 +268,10 @@ def xext_ops(cfg: int, n: int) -> None:
         rows.append({"projection": spec.name, "op": "switch_lora_expand_swiglu" if fuse else "switch_lora_expand",
                      "tokens": T, "adapted_tokens": t_act, "N": N, "us": us, "algorithmic_bytes": alg,
                      "hbm_gbs": alg / us / 1e3, "hbm_frac": alg / us / 1e3 / HBM_PEAK_GBS})
+        if seg_us is not None:
+            rows.append({"projection": spec.name, "op": "segment expand over x_ext (the vLLM layer's path)",
+                         "tokens": T, "adapted_tokens": t_act, "N": N, "us": seg_us, "algorithmic_bytes": alg,
+                         "hbm_gbs": alg / seg_us / 1e3, "hbm_frac": alg / seg_us / 1e3 / HBM_PEAK_GBS})
         del x_exts, out, layer, base
     print(json.dumps({"workload": WORKLOAD_KEY[cfg], "ops": "reference-semantics expand over x_ext (bf16)",
                       "peak_gbs": HBM_PEAK_GBS, "projections": rows}), flush=True)
