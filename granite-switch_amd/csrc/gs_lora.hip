@@ -1933,9 +1933,19 @@ struct ForkState {
 };
 ForkState g_fork[kMaxDevices];
 
-ForkState* fork_state() {
+// nullptr (the classes then run in turn) when `stream` belongs to another
+// device than the current one: the side stream is the current device's, and
+// its kernels must run where the call's memory is.
+ForkState* fork_state(hipStream_t stream) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != dev) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+  }
   ForkState& f = g_fork[dev];
   std::lock_guard<std::mutex> lock(f.mu);
   if (f.side == nullptr && !f.failed) {
@@ -2011,7 +2021,7 @@ int switched_lora_impl(const char* who, int32_t dtype, const void* x, int64_t ld
   }
   const ClassLayout L = class_layout(num_tokens, hidden, num_slices, cls, ncls, bf16, max_part_bytes, concurrent,
                                      workspace_bytes);
-  ForkState* fs = L.concurrent ? fork_state() : nullptr;
+  ForkState* fs = L.concurrent ? fork_state(static_cast<hipStream_t>(stream)) : nullptr;
   auto run_class = [&](const RankClass& k, hipStream_t st, int64_t part_off, int64_t ldz) -> int {
     const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, k, bf16, max_part_bytes);
     void* ws = workspace ? static_cast<void*>(static_cast<char*>(workspace) + part_off) : nullptr;

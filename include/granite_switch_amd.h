@@ -236,7 +236,8 @@ int gs_expand_add(int32_t dtype, void* y, int64_t ldy, int64_t num_tokens, int32
  * split), once per rank class (two launches per class; a sparse large class
  * sums its split-K partials into z in a third).  z [T, S*max_rank] scratch
  * of the same dtype.  With two rank classes and a workspace that holds both
- * classes' partials (gs_shrink_workspace_bytes), the large class runs on the
+ * classes' partials (gs_shrink_workspace_bytes) and `stream` belongs to the
+ * current device, the large class runs on the
  * library's side stream of the current device (default priority, created on
  * the first such call: make it eagerly, outside graph capture), forked from
  * `stream` after the work queued before the call and joined back into it
