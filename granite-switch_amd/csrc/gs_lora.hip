@@ -1100,8 +1100,8 @@ struct ShrinkPlan {
 // The device k-split of a sparse class aims at half the shrink's usual
 // workgroup target: its expand stages the split-K partials of every row for
 // each 128-column item, so fewer, longer k-chunks measured faster overall
-// (decode QKV with one rank-512 adapter: 49.9 -> 43.2 us; a quarter of the
-// target, 45.0 us).
+// (with one rank-512 adapter: decode QKV 46.0 us at the full target, 40.7 at
+// half, 40.2 at a quarter; decoder step 8.87 / 8.85 / 8.90 ms).
 #ifndef GS_SPARSE_KS_DIV
 #define GS_SPARSE_KS_DIV 2
 #endif
@@ -1922,9 +1922,6 @@ int noalloc_scratch(const char* who, char** out) {
 // class of a two-class module runs beside the small one (created on the
 // first such call; default priority, non-blocking).  The mutex makes a call's
 // record / wait / launch sequence atomic against other host threads.
-#ifndef GS_FORK_ORDER
-#define GS_FORK_ORDER 0
-#endif
 struct ForkState {
   std::mutex mu;
   hipStream_t side = nullptr;
@@ -2056,20 +2053,18 @@ int switched_lora_impl(const char* who, int32_t dtype, const void* x, int64_t ld
     return GS_OK;
   }
   // the large class on the side stream once everything before this call on
-  // `stream` is done, issued after the small class's kernels (GS_FORK_ORDER
-  // 0; 1 issues it first); `stream` waits for it before anything after
-  // this call
+  // `stream` is done, issued after the small class's kernels (decoder step
+  // with one rank-512 adapter 9.23 ms; issued first, 9.29 ms); `stream` waits
+  // for it before anything after this call
   const int64_t ldz = static_cast<int64_t>(num_slices) * max_rank;
   std::lock_guard<std::mutex> lock(fs->mu);
   if (hipEventRecord(fs->fork, st) != hipSuccess || hipStreamWaitEvent(fs->side, fs->fork, 0) != hipSuccess) {
     set_error("%s: forking the side stream failed: %s", who, hipGetErrorString(hipGetLastError()));
     return GS_ERR_HIP;
   }
-  int rc0 = GS_OK, rc1 = GS_OK;
-  if (!GS_FORK_ORDER) rc0 = run_class(cls[0], st, L.off[0], ldz);
-  rc1 = run_class(cls[1], fs->side, L.off[1], ldz);
+  const int rc0 = run_class(cls[0], st, L.off[0], ldz);
+  const int rc1 = run_class(cls[1], fs->side, L.off[1], ldz);
   const hipError_t ej = hipEventRecord(fs->join, fs->side);
-  if (GS_FORK_ORDER) rc0 = run_class(cls[0], st, L.off[0], ldz);
   const hipError_t ew = ej == hipSuccess ? hipStreamWaitEvent(st, fs->join, 0) : ej;
   if (rc1 != GS_OK) return rc1;
   if (rc0 != GS_OK) return rc0;
