@@ -564,10 +564,12 @@ def _split_run(device: torch.device, large, small) -> None:
     cur = torch.cuda.current_stream(device)
     side = _side_stream(device)
     side.wait_stream(cur)
-    with torch.cuda.stream(side):
-        large()
-    small()
-    cur.wait_stream(side)
+    try:
+        with torch.cuda.stream(side):
+            large()
+        small()
+    finally:
+        cur.wait_stream(side)     # also when a call raised: nothing queued on the side stream outlives the join
 
 
 def small_sync_buffer(device: torch.device) -> torch.Tensor:
