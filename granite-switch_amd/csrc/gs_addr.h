@@ -35,10 +35,18 @@ GS_HD void dma_kchunk(int H, int ks, int KS, int& s_lo, int& nst) {
   s_lo = (ks * all) / KS;
   nst = ((ks + 1) * all) / KS - s_lo;
 }
+// LDS rows of 128 bytes hold their 16-byte pieces XOR-swizzled: piece p of
+// row r sits at position p ^ lds_swz(r).  A 128-bit LDS read is served 16
+// lanes at a time; an operand read has those lanes on 16 consecutive rows
+// (from a multiple of 16) at one piece, and with this swizzle the 16 rows
+// give 16 distinct (row parity, position) pairs -- all 64 banks once.
+// (r & 7) would put rows r and r + 8 on the same banks.
+GS_HD int lds_swz(int r) { return (r >> 1) & 7; }
 // A wave transfer moves 8 rows of 128 bytes: lane l takes row l / 8 of them
-// and, within it, the 16-byte piece that lands swizzled at LDS position l % 8.
+// and, within it, the 16-byte piece that lands at LDS position l % 8 of LDS
+// row lds_row.
 GS_HD int dma_trow(int l) { return l >> 3; }
-GS_HD int dma_gpiece_bytes(int l) { return ((l & 7) ^ (l >> 3)) * 16; }
+GS_HD int dma_gpiece_bytes(int l, int lds_row) { return ((l & 7) ^ lds_swz(lds_row)) * 16; }
 // Tile row (x) of transfer t of a wave: 16 rows per wave.
 GS_HD int dma_x_row(int wave, int t, int trow) { return 16 * wave + 8 * t + trow; }
 // lora_A row (of the adapter's S*r) of transfer t of a wave: arw rows per
@@ -151,9 +159,8 @@ GS_HD bool gemm_tile(int bid, int tiles_m, int tiles_n, int group, int& tm, int&
 }
 // An operand row a thread moves: rows past the matrix re-read its last.
 GS_HD int gemm_row(int r, int rows) { return imin(r, rows - 1); }
-// The global 16-byte piece a lane moves into LDS position l % 8 of row r
-// (XOR swizzle by the row).
-GS_HD int gemm_piece(int l, int r) { return (l & 7) ^ (r & 7); }
+// The global 16-byte piece a lane moves into LDS position l % 8 of row r.
+GS_HD int gemm_piece(int l, int r) { return (l & 7) ^ lds_swz(r); }
 
 // Tagged partial (g, ks, slot, col) in the workspace: adapter g's region,
 // [KS][cap][zw] 8-byte elements.

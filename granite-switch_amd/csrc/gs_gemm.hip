@@ -184,10 +184,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tn_kernel(GemmParams p
 // L2 request count).  Each wave moves 32 rows of each operand per k-tile.  A
 // transfer fills LDS contiguously, so bank spreading comes from an XOR
 // swizzle instead of padding: the 16-byte piece p of row r sits at position
-// p ^ (r & 7), which puts the operand reads of 8 consecutive rows at one k in
-// distinct banks.  The next k-tile's transfers are issued before the current
-// tile's MFMAs; the waits are explicit (the transfers are written as
-// assembly, so the compiler does not wait for them before every LDS read).
+// p ^ addr::lds_swz(r), which puts the operand reads of 16 consecutive rows at
+// one k (the lanes a 128-bit LDS read serves together) in distinct banks.
+// The next k-tile's transfers are issued before the current tile's MFMAs;
+// the waits are explicit (the transfers are written as assembly, so the
+// compiler does not wait for them before every LDS read).
 // ---------------------------------------------------------------------------
 constexpr int kDBK = 64;                        // k per tile
 constexpr int kDRow = kDBK * 2;                 // bytes of one operand row per tile (one cache line)
@@ -210,7 +211,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tn_dma_kernel(GemmPara
   const int wave = tid >> 6;
   const int l = tid & 63;
   // transfer i of this wave: LDS row RPW*wave + 8*i + l/8, position l % 8,
-  // which holds global piece (l % 8) ^ (row & 7) of that row
+  // which holds global piece (l % 8) ^ lds_swz(row) of that row
   const char* da[TPO];
   const char* db[TPO];
 #pragma unroll
@@ -233,7 +234,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf16_tn_dma_kernel(GemmPara
   const int wn = wave % WN;
   const int i32 = l & 31;
   const int h = l >> 5;
-  const int sw = i32 & 7;                       // swizzle of this lane's rows (blocks start at multiples of 32)
+  const int sw = addr::lds_swz(i32);            // swizzle of this lane's rows (blocks start at multiples of 32)
   f32x16 acc[MI][NJ];
 #pragma unroll
   for (int i = 0; i < MI; ++i)
@@ -350,6 +351,29 @@ struct GemmModel {
         break;
       }
   }
+  // The stage layout a writer mapping produces: slot (row, position) must be
+  // written exactly once and hold the global piece position ^ lds_swz(row),
+  // which is where the operand reads look for it.
+  struct StageLayout {
+    std::vector<int> piece = std::vector<int>(kGBM * 8, -1);
+  };
+  void put(StageLayout& st, int row, int pos, int gpiece) {
+    ++checked;
+    if (row < 0 || row >= kGBM || pos < 0 || pos >= 8) return fail("stage slot (%d, %d) outside the stage", row, pos);
+    int& slot = st.piece[row * 8 + pos];
+    if (slot >= 0) return fail("stage slot (%d, %d) written twice", row, pos);
+    slot = gpiece;
+  }
+  void check_layout(const StageLayout& st, const char* who) {
+    for (int r = 0; r < kGBM; ++r)
+      for (int q = 0; q < 8; ++q) {
+        ++checked;
+        const int g = st.piece[r * 8 + q];
+        if (g != (q ^ addr::lds_swz(r)))
+          return fail("%s: stage slot (%d, %d) holds piece %d, the operand reads expect %d", who, r, q, g,
+                      q ^ addr::lds_swz(r));
+      }
+  }
   void stores(int tm, int tn, int WM, int WN) {
     const int MI = kGBM / WM / 32, NJ = kGBN / WN / 32;
     for (int wave = 0; wave < WM * WN; ++wave)
@@ -371,6 +395,16 @@ struct GemmModel {
   void dma(int WM, int WN) {
     const int NW = WM * WN, RPW = kGBM / NW, TPO = RPW / 8, MI = kGBM / WM / 32, NJ = kGBN / WN / 32;
     const int nk = static_cast<int>(K / kDBK);
+    StageLayout st;
+    for (int wave = 0; wave < NW; ++wave)
+      for (int l = 0; l < 64; ++l)
+        for (int i = 0; i < TPO; ++i) {
+          // a transfer fills 8 rows x 128 bytes of LDS in lane order
+          const int64_t lds = (RPW * wave + 8 * i) * kDRow + l * 16;
+          put(st, static_cast<int>(lds / kDRow), static_cast<int>((lds % kDRow) / 16),
+              addr::gemm_piece(l, RPW * wave + 8 * i + (l >> 3)));
+        }
+    check_layout(st, "dma");
     tiles([&](int tm, int tn) {
       for (int wave = 0; wave < NW; ++wave) {
         for (int l = 0; l < 64; ++l)
@@ -388,7 +422,7 @@ struct GemmModel {
         const int wm = wave / WN, wn = wave % WN;
         for (int l = 0; l < 64; ++l)
           for (int kk = 0; kk < kDBK / 16; ++kk) {
-            const int pos = ((kk * 2 + (l >> 5)) ^ (l & 7)) * 16;
+            const int pos = ((kk * 2 + (l >> 5)) ^ addr::lds_swz(l & 31)) * 16;
             for (int i = 0; i < MI; ++i) in("A operand (LDS)", (wm * MI * 32 + (l & 31) + i * 32) * kDRow + pos, 16, kDOp);
             for (int j = 0; j < NJ; ++j) in("B operand (LDS)", (wn * NJ * 32 + (l & 31) + j * 32) * kDRow + pos, 16, kDOp);
           }

@@ -243,8 +243,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NB <= 
 // 64 k of the tile's 64 x rows and its COLS lora_A rows, one 128-byte line per
 // row (whole-line requests); a wave moves 16 x rows and COLS/4 lora_A rows of
 // every stage (1 KB per transfer: 8 rows, lane l row l/8 position l%8).
-// Pieces are XOR-swizzled (piece p of row r at position p ^ (r & 7)) so the
-// 16 rows an MFMA operand read touches fall in distinct banks.  NST stages
+// Pieces are XOR-swizzled (piece p of row r at position p ^ addr::lds_swz(r))
+// so the 16 rows an MFMA operand read touches fall in distinct banks.  NST stages
 // form a ring with NST - 1 in flight: iteration s waits for its own stage
 // (vmcnt), passes one barrier -- after which every wave is done with stage
 // s - 1, whose slot then receives stage s + NST - 1 -- and runs its MFMAs
@@ -319,21 +319,23 @@ __device__ __forceinline__ void shrink_dma_item(const ShrinkParams& p, const Til
   addr::dma_kchunk(p.H, ks, KS, s_lo, nst);
   const int64_t k_lo = static_cast<int64_t>(s_lo) * kDmaBK;
 
-  // this lane's source in each transfer: row 8t + l/8 of the wave's rows,
-  // global piece (l % 8) ^ (row % 8), so LDS position l % 8 holds it swizzled
+  // this lane's source in each transfer: row 8t + l/8 of the wave's rows, the
+  // global piece that LDS position l % 8 of its LDS row holds swizzled
   const int trow = addr::dma_trow(l);
-  const int gpiece = addr::dma_gpiece_bytes(l);
   const char* xsrc[XT];
 #pragma unroll
   for (int t = 0; t < XT; ++t) {
-    const int token = p.perm[tr.slot0 + addr::tile_row(addr::dma_x_row(wave, t, trow), tr.nrows)];
-    xsrc[t] = static_cast<const char*>(p.x) + (static_cast<int64_t>(token) * p.ldx + k_lo) * 2 + gpiece;
+    const int xrow = addr::dma_x_row(wave, t, trow);    // also its LDS row
+    const int token = p.perm[tr.slot0 + addr::tile_row(xrow, tr.nrows)];
+    xsrc[t] = static_cast<const char*>(p.x) + (static_cast<int64_t>(token) * p.ldx + k_lo) * 2 +
+              addr::dma_gpiece_bytes(l, xrow);
   }
   const char* asrc[AT];
 #pragma unroll
   for (int t = 0; t < AT; ++t) {
     const int arow = addr::dma_a_row(col0, ARW, wave, t, trow, ncols);
-    asrc[t] = static_cast<const char*>(p.a_pack) + (tr.off + static_cast<int64_t>(arow) * p.H + k_lo) * 2 + gpiece;
+    asrc[t] = static_cast<const char*>(p.a_pack) + (tr.off + static_cast<int64_t>(arow) * p.H + k_lo) * 2 +
+              addr::dma_gpiece_bytes(l, kTMS + ARW * wave + 8 * t + trow);
   }
   auto issue = [&](int st) {
     char* slot = ring + (st % NST) * STAGE;
@@ -348,7 +350,7 @@ __device__ __forceinline__ void shrink_dma_item(const ShrinkParams& p, const Til
   f32x4 acc[NC16];
 #pragma unroll
   for (int c = 0; c < NC16; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int sw = i16 & 7;                  // swizzle of every row this lane reads
+  const int sw = addr::lds_swz(i16);      // swizzle of every row this lane reads (blocks start at multiples of 16)
   for (int st = 0; st < NST - 1 && st < nst; ++st) issue(st);
   for (int st = 0; st < nst; ++st) {
     wait_stages<TPW, NST - 2>(min(NST - 2, nst - 1 - st));
@@ -1624,14 +1626,16 @@ struct AddrModel {
       for (int wave = 0; wave < 4; ++wave)
         for (int l = 0; l < 64; ++l) {
           const int trow = addr::dma_trow(l);
-          const int64_t gp = addr::dma_gpiece_bytes(l) / 2;
           for (int t = 0; t < XT; ++t) {
-            const int tok = token_at(tr.slot0 + addr::tile_row(addr::dma_x_row(wave, t, trow), tr.nrows));
+            const int xrow = addr::dma_x_row(wave, t, trow);
+            const int64_t gp = addr::dma_gpiece_bytes(l, xrow) / 2;
+            const int tok = token_at(tr.slot0 + addr::tile_row(xrow, tr.nrows));
             for (int st = 0; st < nst; ++st) row_piece("shrink x", tok, k_lo + st * 64 + gp, 8, H);
             in("shrink x ring", (NST - 1) * stage + (16 * wave + 8 * t) * kDmaRow + 16 * l, 16, ring);
           }
           for (int t = 0; t < AT; ++t) {
             const int arow = addr::dma_a_row(col0, ARW, wave, t, trow, ncols);
+            const int64_t gp = addr::dma_gpiece_bytes(l, kTMS + ARW * wave + 8 * t + trow) / 2;
             for (int st = 0; st < nst; ++st)
               pack_piece("shrink lora_A", tr.off, ncols, H, tr.off + static_cast<int64_t>(arow) * H + k_lo + st * 64 + gp,
                          8, a_elems);
