@@ -879,30 +879,22 @@ void expand_kernel(ExpandParams p) {
 // inside one slice (slice widths are multiples of 128), so only that slice's
 // shrink values are staged.
 // ----------------------------------------------------------------------------
-constexpr int kSpNT = 128;                   // columns per item
+constexpr int kSpNT = 128;                   // columns per item of expand_sparse_kernel
 
-template <int KG>
-__global__ __launch_bounds__(kThreads) void expand_sparse_kernel(ExpandParams p) {
+// One item of the rank-split expand: tile tr, sub-tile `sub` of 32 * QB
+// columns (inside one slice).  red: the waves' partial deltas.  Each output
+// element is the same sum in the same order whatever QB: wave w's k-groups
+// [w*KG, (w+1)*KG) in order, then (w0 + w2) + (w1 + w3).
+template <int KG, int QB>
+__device__ __forceinline__ void expand_sparse_item(const ExpandParams& p, const TileRef& tr, int sub, int nparts,
+                                                   float (&red)[2][kTM][32 * QB + kOutPad], char* zs) {
+  constexpr int NTC = 32 * QB;               // columns per item
   constexpr int KSTEP = 16;                  // bf16 k per MFMA group (both lane halves)
   constexpr int KHALF = 8;
   constexpr int EPL = 8;                     // bf16 elements per 16-byte piece
-  constexpr int LPR = kSpNT / EPL;           // lanes per row
+  constexpr int LPR = NTC / EPL;             // lanes per row
   constexpr int RPI = kThreads / LPR;        // rows per workgroup-wide access
   constexpr int PASSES = kTM / RPI;
-  __shared__ float red[2][kTM][kSpNT + kOutPad];
-  extern __shared__ __align__(16) char zs[];   // [32][max_rank + 8] bf16: one slice's shrink values
-
-  const int n_sub = p.out_total / kSpNT;
-  int lin = static_cast<int>(blockIdx.x);
-  int sub = 0, total = 0;
-  TileRef tr = locate_tile_by<kTM, kExpandBalanced>(p.seg, p.ranks, p.b_off, p.NA, p.rw, lin, true,
-                                                    [&](int) { return n_sub; }, sub, total);
-  int nparts = p.nparts;
-  if (p.ks_target > 0) {
-    const int ks = dyn_ksplit(count_tiles<kTMS>(p.seg, p.ranks, p.NA, p.rw), p.ks_chunks, p.ks_target, p.nparts);
-    nparts = ks > 1 ? ks : 0;
-  }
-  const int items = work_items(total, n_sub, true);
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int l = tid & 63;
@@ -910,168 +902,278 @@ __global__ __launch_bounds__(kThreads) void expand_sparse_kernel(ExpandParams p)
   const int h = l >> 5;
   const int zs_ld = p.max_rank + 8;
   const int cx = (tid % LPR) * EPL;
-  for (;;) {
-    if (tr.g != 0) {
-      const int r = tr.rank;
-      const int n_tile0 = sub * kSpNT;
-      int s = 0;
-      while (s + 1 < p.si.S && n_tile0 >= p.si.bounds[s + 1]) ++s;
-      // the token rows of the item's y pieces (rows past the tile re-read its
-      // first token) and, when z is read by token, of its z pieces: the only
-      // loads the others wait for, so they go first
-      const int zo = (p.z_off != nullptr) ? p.z_off[tr.g] : 0;
-      const int per_row = r >> 2;
-      constexpr int ZIT = kTM * (4 * KG * KSTEP) / 4 / kThreads;   // z pieces per thread at the largest rank
-      int64_t yrow[PASSES];
-      bool rok[PASSES];
+    const int r = tr.rank;
+    const int n_tile0 = sub * NTC;
+    int s = 0;
+    while (s + 1 < p.si.S && n_tile0 >= p.si.bounds[s + 1]) ++s;
+    // the token rows of the item's y pieces (rows past the tile re-read its
+    // first token) and, when z is read by token, of its z pieces: the only
+    // loads the others wait for, so they go first
+    const int zo = (p.z_off != nullptr) ? p.z_off[tr.g] : 0;
+    const int per_row = r >> 2;
+    constexpr int ZIT = kTM * (4 * KG * KSTEP) / 4 / kThreads;   // z pieces per thread at the largest rank
+    int64_t yrow[PASSES];
+    bool rok[PASSES];
 #pragma unroll
-      for (int ps = 0; ps < PASSES; ++ps) {
-        const int row = ps * RPI + tid / LPR;
-        rok[ps] = row < tr.nrows;
-        yrow[ps] = static_cast<int64_t>(p.perm[tr.slot0 + addr::tile_row(row, tr.nrows)]) * p.ldy;
+    for (int ps = 0; ps < PASSES; ++ps) {
+      const int row = ps * RPI + tid / LPR;
+      rok[ps] = row < tr.nrows;
+      yrow[ps] = static_cast<int64_t>(p.perm[tr.slot0 + addr::tile_row(row, tr.nrows)]) * p.ldy;
+    }
+    int32_t zrow[ZIT];                     // slot, or token, indices (widened where they address z)
+#pragma unroll
+    for (int j = 0; j < ZIT; ++j)
+      zrow[j] = tr.slot0 + addr::tile_row(addr::stage_row(tid + j * kThreads, per_row), tr.nrows);
+    if (nparts == 0 && p.z_by_token) {   // uniform
+#pragma unroll
+      for (int j = 0; j < ZIT; ++j) zrow[j] = p.perm[zrow[j]];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // then, all in flight together: the slice's z pieces of the tile's rows
+    // (when z is given; the oldest, so staging them waits for nothing
+    // else; pieces past the rank read clamped addresses and are not
+    // stored), this wave's k-groups of lora_B for the 4 column blocks
+    // (pieces past the rank read the row's first piece and are masked) and
+    // the y pieces
+    uint2 w[ZIT];
+    if (nparts == 0) {
+      const uint16_t* zp = static_cast<const uint16_t*>(p.z) + zo + s * r;
+#pragma unroll
+      for (int j = 0; j < ZIT; ++j) {
+        const int it = tid + j * kThreads;
+        const int c4 = it < kTM * per_row ? addr::stage_col(it, addr::stage_row(it, per_row), per_row, 0) : 0;
+        w[j] = *reinterpret_cast<const uint2*>(zp + static_cast<int64_t>(zrow[j]) * p.ldz + c4);
       }
-      int64_t zrow[ZIT];
+    }
+    u32x4 bv[QB][KG];
 #pragma unroll
-      for (int j = 0; j < ZIT; ++j)
-        zrow[j] = tr.slot0 + addr::tile_row(addr::stage_row(tid + j * kThreads, per_row), tr.nrows);
-      if (nparts == 0 && p.z_by_token) {   // uniform
-#pragma unroll
-        for (int j = 0; j < ZIT; ++j) zrow[j] = p.perm[zrow[j]];
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      // then, all in flight together: the slice's z pieces of the tile's rows
-      // (when z is given; the oldest, so staging them waits for nothing
-      // else; pieces past the rank read clamped addresses and are not
-      // stored), this wave's k-groups of lora_B for the 4 column blocks
-      // (pieces past the rank read the row's first piece and are masked) and
-      // the y pieces
-      uint2 w[ZIT];
-      if (nparts == 0) {
-        const uint16_t* zp = static_cast<const uint16_t*>(p.z) + zo + s * r;
-#pragma unroll
-        for (int j = 0; j < ZIT; ++j) {
-          const int it = tid + j * kThreads;
-          const int c4 = it < kTM * per_row ? addr::stage_col(it, addr::stage_row(it, per_row), per_row, 0) : 0;
-          w[j] = *reinterpret_cast<const uint2*>(zp + zrow[j] * p.ldz + c4);
-        }
-      }
-      u32x4 bv[4][KG];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n_tile0 + 32 * q + i;
-        const char* br = static_cast<const char*>(p.b_pack) + (tr.off + static_cast<int64_t>(n) * r) * 2;
-#pragma unroll
-        for (int kg = 0; kg < KG; ++kg) {
-          const int k0 = (wave * KG + kg) * KSTEP + KHALF * h;
-          bv[q][kg] = sel16(k0 < r, ld16(br + addr::k_or_zero(k0, r) * 2));
-        }
-      }
-      u32x4 yv[PASSES];
-#pragma unroll
-      for (int ps = 0; ps < PASSES; ++ps) yv[ps] = ld16(static_cast<const char*>(p.y) + (yrow[ps] + n_tile0 + cx) * 2);
-      // the slice's shrink values of the tile's rows in LDS: the z pieces
-      // loaded above, or split-K partials summed in ks order (kPartGroup at a
-      // time) and rounded to bf16 as a stored z would be
-      if (nparts == 0) {
-#pragma unroll
-        for (int j = 0; j < ZIT; ++j) {
-          const int it = tid + j * kThreads;
-          const int row = addr::stage_row(it, per_row);
-          if (it < kTM * per_row) {
-            const int c4 = addr::stage_col(it, row, per_row, 0);
-            *reinterpret_cast<uint2*>(zs + (static_cast<int64_t>(row) * zs_ld + c4) * 2) =
-                row < tr.nrows ? w[j] : make_uint2(0u, 0u);
-          }
-        }
-      }
-      // partials: the tile's real rows only (the products of the rows past
-      // them are never stored), UNR passes' pieces in flight per trip (two
-      // at rank > 256, where the kernel holds one wave per SIMD anyway; one
-      // below, which keeps two)
-      constexpr int UNR = KG >= 8 ? 2 : 1;
-      const int npieces = nparts == 0 ? 0 : tr.nrows * per_row;
-      for (int it0 = tid; it0 < npieces; it0 += UNR * kThreads) {
-        float v[UNR][4];
-        const float* src[UNR];
-#pragma unroll
-        for (int w2 = 0; w2 < UNR; ++w2) {
-          const int it = it0 + w2 * kThreads < npieces ? it0 + w2 * kThreads : it0;
-          const int row = addr::stage_row(it, per_row);
-          src[w2] = p.part + static_cast<int64_t>(tr.slot0 + row) * p.zw + s * r +
-                    addr::stage_col(it, row, per_row, 0);
-          v[w2][0] = v[w2][1] = v[w2][2] = v[w2][3] = 0.f;
-        }
-        for (int ks0 = 0; ks0 < nparts; ks0 += kPartGroup) {
-          f32x4 a[UNR][kPartGroup];
-#pragma unroll
-          for (int w2 = 0; w2 < UNR; ++w2)
-#pragma unroll
-            for (int u = 0; u < kPartGroup; ++u)
-              if (ks0 + u < nparts) a[w2][u] = *reinterpret_cast<const f32x4*>(src[w2] + (ks0 + u) * p.part_stride);
-#pragma unroll
-          for (int w2 = 0; w2 < UNR; ++w2)
-#pragma unroll
-            for (int u = 0; u < kPartGroup; ++u) {
-              if (ks0 + u < nparts) {
-                v[w2][0] += a[w2][u].x;
-                v[w2][1] += a[w2][u].y;
-                v[w2][2] += a[w2][u].z;
-                v[w2][3] += a[w2][u].w;
-              }
-            }
-        }
-#pragma unroll
-        for (int w2 = 0; w2 < UNR; ++w2) {
-          const int it = it0 + w2 * kThreads;
-          if (it < npieces) {
-            const int row = addr::stage_row(it, per_row);
-            const int c4 = addr::stage_col(it, row, per_row, 0);
-            *reinterpret_cast<uint2*>(zs + (static_cast<int64_t>(row) * zs_ld + c4) * 2) =
-                make_uint2(pack_bf16x2(v[w2][0], v[w2][1]), pack_bf16x2(v[w2][2], v[w2][3]));
-          }
-        }
-      }
-      lds_barrier();
-      f32x16 acc[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc[q] = f32x16{};
-      const char* zrow_l = zs + static_cast<int64_t>(i) * zs_ld * 2;
+    for (int q = 0; q < QB; ++q) {
+      const int n = n_tile0 + 32 * q + i;
+      const char* br = static_cast<const char*>(p.b_pack) + (tr.off + static_cast<int64_t>(n) * r) * 2;
 #pragma unroll
       for (int kg = 0; kg < KG; ++kg) {
         const int k0 = (wave * KG + kg) * KSTEP + KHALF * h;
-        const bool kin = k0 < r;
-        const u32x4 za = sel16(kin, *reinterpret_cast<const u32x4*>(zrow_l + (kin ? k0 : 0) * 2));
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc[q] = mfma32_bf16(za, bv[q][kg], acc[q]);
-      }
-      // fixed-order sum of the waves' partial deltas
-      if (wave < 2) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) red[wave][mfma32_row(v, l)][32 * q + i] = acc[q][v];
-      }
-      lds_barrier();
-      if (wave >= 2) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) red[wave - 2][mfma32_row(v, l)][32 * q + i] += acc[q][v];
-      }
-      lds_barrier();
-#pragma unroll
-      for (int ps = 0; ps < PASSES; ++ps) {
-        const int row = ps * RPI + tid / LPR;
-        float d[EPL];
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) d[e] = red[0][row][cx + e] + red[1][row][cx + e];
-        if (rok[ps]) add_store_y<true>(p.y, yrow[ps] + n_tile0 + cx, yv[ps], d);
+        bv[q][kg] = sel16(k0 < r, ld16(br + addr::k_or_zero(k0, r) * 2));
       }
     }
+    u32x4 yv[PASSES];
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) yv[ps] = ld16(static_cast<const char*>(p.y) + (yrow[ps] + n_tile0 + cx) * 2);
+    // the slice's shrink values of the tile's rows in LDS: the z pieces
+    // loaded above, or split-K partials summed in ks order (kPartGroup at a
+    // time) and rounded to bf16 as a stored z would be
+    if (nparts == 0) {
+#pragma unroll
+      for (int j = 0; j < ZIT; ++j) {
+        const int it = tid + j * kThreads;
+        const int row = addr::stage_row(it, per_row);
+        if (it < kTM * per_row) {
+          const int c4 = addr::stage_col(it, row, per_row, 0);
+          *reinterpret_cast<uint2*>(zs + (static_cast<int64_t>(row) * zs_ld + c4) * 2) =
+              row < tr.nrows ? w[j] : make_uint2(0u, 0u);
+        }
+      }
+    }
+    // partials: the tile's real rows only (the products of the rows past
+    // them are never stored), UNR passes' pieces in flight per trip (two
+    // for 128-column items at rank > 256, where the kernel holds one wave
+    // per SIMD anyway; one otherwise, which keeps the registers of the
+    // narrower items that share a launch with the small class)
+    constexpr int UNR = KG >= 8 && QB == 4 ? 2 : 1;
+    const int npieces = nparts == 0 ? 0 : tr.nrows * per_row;
+    for (int it0 = tid; it0 < npieces; it0 += UNR * kThreads) {
+      float v[UNR][4];
+      const float* src[UNR];
+#pragma unroll
+      for (int w2 = 0; w2 < UNR; ++w2) {
+        const int it = it0 + w2 * kThreads < npieces ? it0 + w2 * kThreads : it0;
+        const int row = addr::stage_row(it, per_row);
+        src[w2] = p.part + static_cast<int64_t>(tr.slot0 + row) * p.zw + s * r +
+                  addr::stage_col(it, row, per_row, 0);
+        v[w2][0] = v[w2][1] = v[w2][2] = v[w2][3] = 0.f;
+      }
+      for (int ks0 = 0; ks0 < nparts; ks0 += kPartGroup) {
+        f32x4 a[UNR][kPartGroup];
+#pragma unroll
+        for (int w2 = 0; w2 < UNR; ++w2)
+#pragma unroll
+          for (int u = 0; u < kPartGroup; ++u)
+            if (ks0 + u < nparts) a[w2][u] = *reinterpret_cast<const f32x4*>(src[w2] + (ks0 + u) * p.part_stride);
+#pragma unroll
+        for (int w2 = 0; w2 < UNR; ++w2)
+#pragma unroll
+          for (int u = 0; u < kPartGroup; ++u) {
+            if (ks0 + u < nparts) {
+              v[w2][0] += a[w2][u].x;
+              v[w2][1] += a[w2][u].y;
+              v[w2][2] += a[w2][u].z;
+              v[w2][3] += a[w2][u].w;
+            }
+          }
+      }
+#pragma unroll
+      for (int w2 = 0; w2 < UNR; ++w2) {
+        const int it = it0 + w2 * kThreads;
+        if (it < npieces) {
+          const int row = addr::stage_row(it, per_row);
+          const int c4 = addr::stage_col(it, row, per_row, 0);
+          *reinterpret_cast<uint2*>(zs + (static_cast<int64_t>(row) * zs_ld + c4) * 2) =
+              make_uint2(pack_bf16x2(v[w2][0], v[w2][1]), pack_bf16x2(v[w2][2], v[w2][3]));
+        }
+      }
+    }
+    lds_barrier();
+    f32x16 acc[QB];
+#pragma unroll
+    for (int q = 0; q < QB; ++q) acc[q] = f32x16{};
+    const char* zrow_l = zs + static_cast<int64_t>(i) * zs_ld * 2;
+#pragma unroll
+    for (int kg = 0; kg < KG; ++kg) {
+      const int k0 = (wave * KG + kg) * KSTEP + KHALF * h;
+      const bool kin = k0 < r;
+      const u32x4 za = sel16(kin, *reinterpret_cast<const u32x4*>(zrow_l + (kin ? k0 : 0) * 2));
+#pragma unroll
+      for (int q = 0; q < QB; ++q) acc[q] = mfma32_bf16(za, bv[q][kg], acc[q]);
+    }
+    // fixed-order sum of the waves' partial deltas
+    if (wave < 2) {
+#pragma unroll
+      for (int q = 0; q < QB; ++q)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) red[wave][mfma32_row(v, l)][32 * q + i] = acc[q][v];
+    }
+    lds_barrier();
+    if (wave >= 2) {
+#pragma unroll
+      for (int q = 0; q < QB; ++q)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) red[wave - 2][mfma32_row(v, l)][32 * q + i] += acc[q][v];
+    }
+    lds_barrier();
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) {
+      const int row = ps * RPI + tid / LPR;
+      float d[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) d[e] = red[0][row][cx + e] + red[1][row][cx + e];
+      if (rok[ps]) add_store_y<true>(p.y, yrow[ps] + n_tile0 + cx, yv[ps], d);
+    }
+}
+
+// The k-split of a sparse class's partial sums: the shrink's, which it chose
+// on the device from the class's 64-slot tile count when ks_target > 0.
+__device__ __forceinline__ int sparse_nparts(const ExpandParams& p) {
+  if (p.ks_target <= 0) return p.nparts;
+  const int ks = dyn_ksplit(count_tiles<kTMS>(p.seg, p.ranks, p.NA, p.rw), p.ks_chunks, p.ks_target, p.nparts);
+  return ks > 1 ? ks : 0;
+}
+
+template <int KG>
+__global__ __launch_bounds__(kThreads) void expand_sparse_kernel(ExpandParams p) {
+  __shared__ float red[2][kTM][kSpNT + kOutPad];
+  extern __shared__ __align__(16) char zs[];   // [32][max_rank + 8] bf16: one slice's shrink values
+  const int n_sub = p.out_total / kSpNT;
+  int lin = static_cast<int>(blockIdx.x);
+  int sub = 0, total = 0;
+  TileRef tr = locate_tile_by<kTM, kExpandBalanced>(p.seg, p.ranks, p.b_off, p.NA, p.rw, lin, true,
+                                                    [&](int) { return n_sub; }, sub, total);
+  const int nparts = sparse_nparts(p);
+  const int items = work_items(total, n_sub, true);
+  for (;;) {
+    if (tr.g != 0) expand_sparse_item<KG, kSpNT / 32>(p, tr, sub, nparts, red, zs);
     lin += static_cast<int>(gridDim.x);
     if (lin >= items) break;
     lds_barrier();                         // every wave is done with zs and red before the next item
     tr = tile_at<kTM, kExpandBalanced>(p.seg, p.ranks, p.b_off, p.NA, p.rw, lin, true, total, n_sub, sub);
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Both rank classes of a module in the same two launches (bf16, a small class
+// of the one-item forms and a sparse large class).  Run on their own, the
+// large class's few items were a chain of two launches of dependent memory
+// trips (~20 us per projection at the decoder step whatever its bytes) that a
+// second stream hid only in part.  Here the small class's grid carries them:
+//   shrink_dma_pair_kernel: workgroup b shrinks its small-class item, then
+//     the large class's items b, b + grid, ... (its looping form, 32-column
+//     chunks, k-split chosen on the device); workgroup 0 also zeroes the
+//     expand's item counter.
+//   expand_pair_kernel: workgroup b expands its small-class item, then takes
+//     large-class items (64-column sub-tiles of the rank-split form) from that
+//     counter until none are left, so the workgroups that finish first take
+//     them and they fill the launch's end.
+// Every output element is computed as by the separate launches (the same
+// item functions, the same sums in the same order).
+// ----------------------------------------------------------------------------
+constexpr int kPairQB = 2;                     // 32-column blocks per large-class expand item
+
+template <int NB0>
+__global__ __launch_bounds__(kThreads) void shrink_dma_pair_kernel(ShrinkParams p0, ShrinkParams p1, int* claim) {
+  constexpr int R0 = DmaRing<NB0>::NST * (kTMS + 32 * NB0) * kDmaRow;
+  constexpr int R1 = DmaRing<1>::NST * (kTMS + 32) * kDmaRow;
+  __shared__ __align__(16) char ring[R0 > R1 ? R0 : R1];
+  if (blockIdx.x == 0 && threadIdx.x == 0) *claim = 0;   // ordered before the expand launch by the launch boundary
+  int sub = 0, total = 0;
+  {
+    const TileRef tr = locate_tile<kTMS>(p0.seg, p0.ranks, p0.a_off, p0.NA, p0.rw, static_cast<int>(blockIdx.x), false,
+                                         p0.n_chunks * p0.KS, sub, total);
+    if (tr.g != 0) shrink_dma_item<NB0>(p0, tr, sub, p0.KS, ring);
+  }
+  int lin = static_cast<int>(blockIdx.x);
+  int KS = p1.KS;
+  TileRef tr = locate_tile_by<kTMS>(p1.seg, p1.ranks, p1.a_off, p1.NA, p1.rw, lin, true,
+                                    [&](int tot) {
+                                      if (p1.ks_target > 0) KS = dyn_ksplit(tot, p1.n_chunks, p1.ks_target, p1.KS);
+                                      return p1.n_chunks * KS;
+                                    }, sub, total);
+  const int items = work_items(total, p1.n_chunks * KS, true);
+  while (lin < items) {
+    lds_barrier();                         // every wave is done with the ring before the item's transfers
+    if (tr.g != 0) shrink_dma_item<1>(p1, tr, sub, KS, ring);
+    lin += static_cast<int>(gridDim.x);
+    if (lin >= items) break;
+    tr = tile_at<kTMS>(p1.seg, p1.ranks, p1.a_off, p1.NA, p1.rw, lin, true, total, p1.n_chunks * KS, sub);
+  }
+}
+
+template <int NBW, int PRE, int KG>
+__global__ __launch_bounds__(kThreads) void expand_pair_kernel(ExpandParams p0, ExpandParams p1, int* claim) {
+  constexpr int NT = 4 * NBW * 32;
+  constexpr int kD = static_cast<int>(sizeof(float)) * kTM * (NT + kOutPad);
+  constexpr int kR = static_cast<int>(sizeof(float)) * 2 * kTM * (32 * kPairQB + kOutPad);
+  __shared__ __align__(16) char buf[kD > kR ? kD : kR];   // the small item's delta tile, then the large items' partial deltas
+  __shared__ int claimed;
+  extern __shared__ __align__(16) char zs[];   // either class's shrink values
+  auto& dtile = *reinterpret_cast<float(*)[kTM][NT + kOutPad]>(buf);
+  auto& red = *reinterpret_cast<float(*)[2][kTM][32 * kPairQB + kOutPad]>(buf);
+  {
+    const int n_sub = (p0.out_total + NT - 1) / NT;
+    int sub = 0, groups = 1, total = 0;
+    const TileRef tr = locate_tile_by<kTM, kExpandBalanced>(p0.seg, p0.ranks, p0.b_off, p0.NA, p0.rw,
+                                                            static_cast<int>(blockIdx.x), false,
+                                                            [&](int tot) {
+                                                              groups = expand_groups(tot, n_sub, p0.wt);
+                                                              return groups;
+                                                            }, sub, total);
+    if (tr.g != 0) {
+      const int sub0 = (sub * n_sub) / groups;
+      const int nsub = ((sub + 1) * n_sub) / groups - sub0;
+      if (nsub > 0) expand_item<true, NBW, PRE, false>(p0, tr, sub0, nsub, p0.nparts, dtile, zs);
+    }
+  }
+  const int n_sub1 = p1.out_total / (32 * kPairQB);
+  const int total1 = count_tiles<kTM>(p1.seg, p1.ranks, p1.NA, p1.rw);
+  const int items1 = work_items(total1, n_sub1, true);
+  const int nparts1 = sparse_nparts(p1);
+  for (;;) {
+    lds_barrier();                         // zs, buf and `claimed` are free
+    if (threadIdx.x == 0) claimed = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    lds_barrier();
+    const int it = claimed;
+    if (it >= items1) break;
+    int sub = 0;
+    const TileRef tr = tile_at<kTM, kExpandBalanced>(p1.seg, p1.ranks, p1.b_off, p1.NA, p1.rw, it, true, total1, n_sub1, sub);
+    if (tr.g != 0) expand_sparse_item<KG, kPairQB>(p1, tr, sub, nparts1, red, zs);
   }
 }
 
@@ -1502,6 +1604,95 @@ void launch_expand(bool bf16, int64_t T, int adapters, ExpandParams p, hipStream
 }
 
 
+// The pair launches (shrink_dma_pair_kernel, expand_pair_kernel) take a
+// module's two classes when the small class's plans are the one-item ring
+// shrink and column-split expand and the large class's are the sparse ones
+// (bf16): the forms whose item functions the pair kernels run.
+struct PairForm {
+  bool ok = false;
+  int NB0 = 1;            // the small class's shrink column blocks
+  ExpandForm f0{};        // the small class's expand form
+  int KG1 = 0;            // the large class's k-groups per wave
+};
+PairForm pair_form(bool bf16, int64_t T, const ShrinkPlan& pl0, const ShrinkPlan& pl1, const ExpandParams& e0,
+                   const ExpandParams& e1) {
+  PairForm f;
+  if (!bf16 || !pl0.dma || pl0.loop || pl0.flat || !pl1.dma || !pl1.loop || !pl1.flat || pl1.NB != 1) return f;
+  if (e1.max_rank > 4 * 8 * 16) return f;
+  for (int s = 0; s < e1.si.S; ++s)
+    if ((e1.si.bounds[s + 1] - e1.si.bounds[s]) % (32 * kPairQB) != 0) return f;
+  f.f0 = expand_form(true, T, e0);
+  if (f.f0.sparse || e0.flat || f.f0.PRE > 4) return f;
+  f.NB0 = pl0.NB;
+  f.KG1 = e1.max_rank <= 4 * 2 * 16 ? 2 : (e1.max_rank <= 4 * 4 * 16 ? 4 : 8);
+  f.ok = true;
+  return f;
+}
+
+size_t pair_lds_bytes(int S, int max_rank0, int max_rank1) {
+  return std::max(expand_lds_bytes(true, S, max_rank0), static_cast<size_t>(kTM) * (max_rank1 + 8) * 2);
+}
+
+template <int NBW, int PRE, int KG>
+const void* expand_pair_fn() {
+  return reinterpret_cast<const void*>(expand_pair_kernel<NBW, PRE, KG>);
+}
+template <int NBW, int PRE>
+const void* expand_pair_fn_kg(int KG) {
+  return KG == 2 ? expand_pair_fn<NBW, PRE, 2>() : (KG == 4 ? expand_pair_fn<NBW, PRE, 4>() : expand_pair_fn<NBW, PRE, 8>());
+}
+const void* expand_pair_fn_of(const PairForm& f) {
+  if (f.f0.NBW == 2) return expand_pair_fn_kg<2, 2>(f.KG1);
+  return f.f0.PRE <= 2 ? expand_pair_fn_kg<1, 2>(f.KG1) : expand_pair_fn_kg<1, 4>(f.KG1);
+}
+
+// Workgroups of the pair expand resident per CU at `lds` bytes of dynamic LDS
+// (queried once per kernel and size, kept as one word: lds << 16 | count).
+int pair_expand_occupancy(const void* kern, size_t lds) {
+  static std::mutex mu;
+  static std::vector<std::pair<const void*, uint64_t>> memo;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const auto& m : memo)
+    if (m.first == kern && (m.second >> 16) == lds) return static_cast<int>(m.second & 0xffff);
+  if (lds > 64 * 1024) (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kThreads, lds) != hipSuccess || n < 1) n = 1;
+  memo.emplace_back(kern, (static_cast<uint64_t>(lds) << 16) | static_cast<uint64_t>(std::min(n, 0xffff)));
+  return n;
+}
+
+// The pair expand's grid: the small class's one-item grid at the pair
+// kernel's occupancy (sets e0.wt, which its items' column groups follow).
+int64_t pair_expand_grid(const PairForm& f, int64_t T, int adapters0, size_t lds, ExpandParams& e0) {
+  e0.wt = pair_expand_occupancy(expand_pair_fn_of(f), lds) * device_cus();
+  const int NT = 4 * f.f0.NBW * 32;
+  return expand_grid(e0.wt, max_tiles_for(T, adapters0), (e0.out_total + NT - 1) / NT, false);
+}
+
+void launch_shrink_pair(const PairForm& f, int64_t grid, const ShrinkParams& p0, const ShrinkParams& p1, int* claim,
+                        hipStream_t st) {
+  const dim3 g(static_cast<unsigned>(grid));
+  if (f.NB0 == 4) hipLaunchKernelGGL((shrink_dma_pair_kernel<4>), g, dim3(kThreads), 0, st, p0, p1, claim);
+  else if (f.NB0 == 3) hipLaunchKernelGGL((shrink_dma_pair_kernel<3>), g, dim3(kThreads), 0, st, p0, p1, claim);
+  else if (f.NB0 == 2) hipLaunchKernelGGL((shrink_dma_pair_kernel<2>), g, dim3(kThreads), 0, st, p0, p1, claim);
+  else hipLaunchKernelGGL((shrink_dma_pair_kernel<1>), g, dim3(kThreads), 0, st, p0, p1, claim);
+}
+
+template <int NBW, int PRE>
+void launch_expand_pair_kg(int KG, dim3 g, size_t lds, const ExpandParams& e0, const ExpandParams& e1, int* claim,
+                           hipStream_t st) {
+  if (KG == 2) hipLaunchKernelGGL((expand_pair_kernel<NBW, PRE, 2>), g, dim3(kThreads), lds, st, e0, e1, claim);
+  else if (KG == 4) hipLaunchKernelGGL((expand_pair_kernel<NBW, PRE, 4>), g, dim3(kThreads), lds, st, e0, e1, claim);
+  else hipLaunchKernelGGL((expand_pair_kernel<NBW, PRE, 8>), g, dim3(kThreads), lds, st, e0, e1, claim);
+}
+void launch_expand_pair(const PairForm& f, int64_t grid, size_t lds, const ExpandParams& e0, const ExpandParams& e1,
+                        int* claim, hipStream_t st) {
+  const dim3 g(static_cast<unsigned>(grid));
+  if (f.f0.NBW == 2) launch_expand_pair_kg<2, 2>(f.KG1, g, lds, e0, e1, claim, st);
+  else if (f.f0.PRE <= 2) launch_expand_pair_kg<1, 2>(f.KG1, g, lds, e0, e1, claim, st);
+  else launch_expand_pair_kg<1, 4>(f.KG1, g, lds, e0, e1, claim, st);
+}
+
 // ----------------------------------------------------------------------------
 // Address model (test support): replays the global and LDS accesses of the
 // segment kernels on the host, with the launch plans and the addr:: formulas
@@ -1602,7 +1793,12 @@ struct AddrModel {
   }
 
   // ---- shrink_dma_kernel ----------------------------------------------------
-  void shrink_dma(const ShrinkPlan& pl, RankWindow rw, int64_t ldz, int64_t z_elems, int64_t part_elems) {
+  // grid / loop: the launch's (the plan's own unless the pair shrink carries
+  // the items on the small class's grid)
+  void shrink_dma(const ShrinkPlan& pl, RankWindow rw, int64_t ldz, int64_t z_elems, int64_t part_elems,
+                  int64_t grid = -1, int loop = -1) {
+    if (grid < 0) grid = pl.grid;
+    if (loop < 0) loop = pl.loop ? 1 : 0;
     const std::vector<TileRef> tl = tiles<kTMS, false>(rw, a_off);
     const int total = static_cast<int>(tl.size());
     const int KS = pl.ks_target > 0 ? dyn_ksplit(total, pl.n_chunks, pl.ks_target, pl.KS) : pl.KS;
@@ -1612,7 +1808,7 @@ struct AddrModel {
     const int NST = pl.NB == 1 ? GS_DMA_NST1 : (pl.NB == 2 ? GS_DMA_NST2 : (pl.NB == 3 ? GS_DMA_NST3 : GS_DMA_NST4));
     const int64_t stage = static_cast<int64_t>(kTMS + COLS) * kDmaRow, ring = NST * stage;
     const int64_t zw = pl.zw;
-    for_items("shrink_dma_kernel", pl.grid, pl.loop, work_items(total, nsub, flat), [&](int lin) {
+    for_items("shrink_dma_kernel", grid, loop != 0, work_items(total, nsub, flat), [&](int lin) {
       const XcdItem it = work_item(lin, total, nsub, flat);
       if (it.tile < 0) return;
       const TileRef& tr = tl[it.tile];
@@ -1736,8 +1932,11 @@ struct AddrModel {
   // ---- expand_kernel and expand_sparse_kernel --------------------------------
   // z source: partials [nparts][T][zw] (nparts > 0), else z [z_rows, ldz]
   // by slot or by token (z_by_token), columns from z_off[g].
+  // qb: 32-column blocks of a sparse item (the pair expand's are narrower);
+  // claimed: the items are taken from a counter (each exactly once) instead
+  // of by a grid.
   void expand(const ExpandParams& e, const ExpandForm& f, int adapters, int64_t wt, int64_t z_elems,
-              int64_t part_elems, const int32_t* z_off) {
+              int64_t part_elems, const int32_t* z_off, int qb = kSpNT / 32, bool claimed = false) {
     const bool flat = e.flat != 0;
     const int max_tiles = max_tiles_for(T, adapters);
     const std::vector<TileRef> tl = tiles<kTM, kExpandBalanced>(e.rw, b_off);
@@ -1771,22 +1970,24 @@ struct AddrModel {
       }
     };
     if (f.sparse) {
-      const int64_t n_sub = out_total / kSpNT;
+      const int NTC = 32 * qb;
+      const int64_t n_sub = out_total / NTC;
       const int64_t zs_ld = e.max_rank + 8, lds = kTM * zs_ld * 2;
-      const int LPR = kSpNT / 8, RPI = kThreads / LPR, PASSES = kTM / RPI;
-      for_items("expand_sparse_kernel", sparse_grid(wt, max_tiles, n_sub), true,
-                work_items(total, static_cast<int>(n_sub), true), [&](int lin) {
+      const int LPR = NTC / 8, RPI = kThreads / LPR, PASSES = kTM / RPI;
+      const int items = work_items(total, static_cast<int>(n_sub), true);
+      for_items(claimed ? "expand_pair_kernel (claimed items)" : "expand_sparse_kernel",
+                claimed ? items : sparse_grid(wt, max_tiles, n_sub), true, items, [&](int lin) {
         const XcdItem it = work_item(lin, total, static_cast<int>(n_sub), true);
         if (it.tile < 0) return;
         const TileRef& tr = tl[it.tile];
-        const int r = tr.rank, n_tile0 = it.sub * kSpNT;
+        const int r = tr.rank, n_tile0 = it.sub * NTC;
         int s = 0;
         while (s + 1 < si.S && n_tile0 >= si.bounds[s + 1]) ++s;
-        in("sparse sub-tile inside its slice", n_tile0 - si.bounds[s], kSpNT, si.bounds[s + 1] - si.bounds[s]);
+        in("sparse sub-tile inside its slice", n_tile0 - si.bounds[s], NTC, si.bounds[s + 1] - si.bounds[s]);
         for (int wave = 0; wave < 4; ++wave)
           for (int l = 0; l < 64; ++l) {
             const int i = l & 31, h = l >> 5;
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < qb; ++q) {
               const int64_t n = n_tile0 + 32 * q + i;
               in("sparse lora_B column", n, 1, out_total);
               for (int kg = 0; kg < f.KG; ++kg) {
@@ -1969,7 +2170,13 @@ struct ClassLayout {
   int64_t off[2] = {0, 0};
   int64_t bytes = 0;       // the span the call uses
   bool concurrent = false;
+  int64_t claim = -1;      // byte offset of the pair launches' item counter (-1: no room for it)
 };
+// Two classes side by side: class 0's partials, class 1's from the next
+// 256-byte boundary, then one 256-byte line holding the pair expand's item
+// counter (what gs_shrink_workspace_bytes reports).  Without room for the
+// counter but with room for both partials, the classes can still run
+// concurrently on two streams.
 ClassLayout class_layout(int64_t T, int H, int S, const RankClass* cls, int ncls, bool bf16, int64_t max_part_bytes,
                          bool want_concurrent, int64_t workspace_bytes) {
   ClassLayout L;
@@ -1978,7 +2185,13 @@ ClassLayout class_layout(int64_t T, int H, int S, const RankClass* cls, int ncls
   L.bytes = ncls == 2 ? std::max(part[0], part[1]) : part[0];
   if (ncls == 2 && want_concurrent) {
     const int64_t both = part[0] == 0 ? part[1] : align256(part[0]) + part[1];
-    if (both <= workspace_bytes || both == 0) {
+    const int64_t claim = align256(both);
+    if (claim + 256 <= workspace_bytes) {
+      L.concurrent = true;
+      L.off[1] = part[0] == 0 ? 0 : align256(part[0]);
+      L.claim = claim;
+      L.bytes = claim + 256;
+    } else if (both <= workspace_bytes || both == 0) {
       L.concurrent = true;
       L.off[1] = part[0] == 0 ? 0 : align256(part[0]);
       L.bytes = both;
@@ -2022,14 +2235,12 @@ int switched_lora_impl(const char* who, int32_t dtype, const void* x, int64_t ld
   }
   const ClassLayout L = class_layout(num_tokens, hidden, num_slices, cls, ncls, bf16, max_part_bytes, concurrent,
                                      workspace_bytes);
-  ForkState* fs = L.concurrent ? fork_state(static_cast<hipStream_t>(stream)) : nullptr;
-  auto run_class = [&](const RankClass& k, hipStream_t st, int64_t part_off, int64_t ldz) -> int {
-    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, k, bf16, max_part_bytes);
+  auto shrink_params = [&](const RankClass& k, const ShrinkPlan& pl, int64_t part_off, int64_t ldz) {
     void* ws = workspace ? static_cast<void*>(static_cast<char*>(workspace) + part_off) : nullptr;
-    const ShrinkParams sp = make_shrink_params(pl, x, ldx, hidden, a_pack, a_off, ranks, num_slices, num_adapters,
-                                               seg_offsets, perm, z, ldz, ws, num_tokens, k.rw);
-    launch_shrink(bf16, pl, sp, st);
-    GS_CHECK_LAUNCH(who);
+    return make_shrink_params(pl, x, ldx, hidden, a_pack, a_off, ranks, num_slices, num_adapters, seg_offsets, perm, z,
+                              ldz, ws, num_tokens, k.rw);
+  };
+  auto expand_params = [&](const RankClass& k, const ShrinkPlan& pl, const ShrinkParams& sp, int64_t ldz) {
     ExpandParams e = ep;
     e.max_rank = k.max_rank;
     e.rw = k.rw;
@@ -2044,11 +2255,40 @@ int switched_lora_impl(const char* who, int32_t dtype, const void* x, int64_t ld
     e.part_stride = sp.part_stride;
     e.zw = sp.zw;
     e.nparts = pl.KS > 1 ? pl.KS : 0;
-    launch_expand(bf16, num_tokens, k.adapters, e, st);
+    return e;
+  };
+  auto run_class = [&](const RankClass& k, hipStream_t st, int64_t part_off, int64_t ldz) -> int {
+    const ShrinkPlan pl = plan_class(num_tokens, hidden, num_slices, k, bf16, max_part_bytes);
+    const ShrinkParams sp = shrink_params(k, pl, part_off, ldz);
+    launch_shrink(bf16, pl, sp, st);
+    GS_CHECK_LAUNCH(who);
+    launch_expand(bf16, num_tokens, k.adapters, expand_params(k, pl, sp, ldz), st);
     GS_CHECK_LAUNCH(who);
     return GS_OK;
   };
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (L.claim >= 0) {
+    // both classes in the same two launches on `stream` when their forms allow
+    const int64_t ldz = static_cast<int64_t>(num_slices) * max_rank;
+    const ShrinkPlan pl0 = plan_class(num_tokens, hidden, num_slices, cls[0], bf16, max_part_bytes);
+    const ShrinkPlan pl1 = plan_class(num_tokens, hidden, num_slices, cls[1], bf16, max_part_bytes);
+    const ShrinkParams sp0 = shrink_params(cls[0], pl0, L.off[0], ldz);
+    const ShrinkParams sp1 = shrink_params(cls[1], pl1, L.off[1], ldz);
+    ExpandParams e0 = expand_params(cls[0], pl0, sp0, ldz);
+    const ExpandParams e1 = expand_params(cls[1], pl1, sp1, ldz);
+    const PairForm f = pair_form(bf16, num_tokens, pl0, pl1, e0, e1);
+    if (f.ok) {
+      int* claim = reinterpret_cast<int*>(static_cast<char*>(workspace) + L.claim);
+      const size_t lds = pair_lds_bytes(num_slices, cls[0].max_rank, cls[1].max_rank);
+      const int64_t egrid = pair_expand_grid(f, num_tokens, cls[0].adapters, lds, e0);
+      launch_shrink_pair(f, pl0.grid, sp0, sp1, claim, st);
+      GS_CHECK_LAUNCH(who);
+      launch_expand_pair(f, egrid, lds, e0, e1, claim, st);
+      GS_CHECK_LAUNCH(who);
+      return GS_OK;
+    }
+  }
+  ForkState* fs = L.concurrent ? fork_state(st) : nullptr;
   if (fs == nullptr) {
     for (int c = 0; c < ncls; ++c) {
       rc = run_class(cls[c], st, 0, static_cast<int64_t>(num_slices) * cls[c].max_rank);
@@ -2298,6 +2538,41 @@ int64_t gs_check_segment_addresses(int32_t dtype, int64_t num_tokens, int32_t hi
       // gs_switched_lora runs two classes concurrently, their partials side
       // by side (each checked against its own range) and z at one stride
       const ClassLayout L = class_layout(T, hidden, num_slices, cls, ncls, bf16, budget, !noalloc, ws_elems * 4);
+      // the plans and expand parameters of class c as the call makes them
+      auto class_expand = [&](int c, const ShrinkPlan& pl, int64_t zl) {
+        ExpandParams e{};
+        e.out_total = out_total;
+        e.si = m.si;
+        e.ldz = zl;
+        e.part_stride = T * pl.zw;
+        e.zw = pl.zw;
+        e.nparts = pl.KS > 1 ? pl.KS : 0;
+        e.max_rank = cls[c].max_rank;
+        e.rw = cls[c].rw;
+        e.flat = pl.flat ? 1 : 0;
+        e.ks_target = pl.ks_target;
+        e.ks_chunks = pl.n_chunks;
+        return e;
+      };
+      if (L.claim >= 0) {
+        // both classes in the pair launches when their forms allow
+        const int64_t zl = static_cast<int64_t>(num_slices) * max_rank;
+        const ShrinkPlan pl0 = plan_class(T, hidden, num_slices, cls[0], bf16, budget);
+        const ShrinkPlan pl1 = plan_class(T, hidden, num_slices, cls[1], bf16, budget);
+        const ExpandParams e0 = class_expand(0, pl0, zl), e1 = class_expand(1, pl1, zl);
+        const PairForm pf = pair_form(bf16, T, pl0, pl1, e0, e1);
+        if (pf.ok) {
+          m.in("pair item counter", L.claim / 4, 1, ws_elems);
+          const int64_t part0 = L.off[1] > 0 ? L.off[1] / 4 : ws_elems, part1 = L.claim / 4 - L.off[1] / 4;
+          m.shrink_dma(pl0, cls[0].rw, zl, z_elems, part0);
+          m.shrink_dma(pl1, cls[1].rw, zl, z_elems, part1, pl0.grid, 1);
+          for (int occ = 1; occ <= 4; ++occ)
+            m.expand(e0, pf.f0, cls[0].adapters, int64_t(occ) * cus, z_elems, part0, nullptr);
+          const ExpandForm f1{true, 1, 2, pf.KG1};
+          m.expand(e1, f1, cls[1].adapters, cus, z_elems, part1, nullptr, kPairQB, true);
+          continue;
+        }
+      }
       for (int c = 0; c < ncls; ++c) {
         const RankClass& k = cls[c];
         const ShrinkPlan pl = plan_class(T, hidden, num_slices, k, bf16, budget);

@@ -8,9 +8,11 @@ per rank class (ranks <= 64 and above), each planned for its own ranks; the
 one-launch decode kernel takes the rank <= 64 class and the segment kernels
 the larger adapters.  Every path is checked against the oracle
 (|got - ref| <= 2e-2 + 2e-2 |ref| in bf16, 1e-5 in fp32) with base rows
-bit-identical.  gs_switched_lora runs a two-class module's classes
-concurrently (the large one on a side stream) when its workspace holds both
-classes' partials, and in turn otherwise; both give the same bits.
+bit-identical.  gs_switched_lora runs a two-class module in the pair
+launches (the small class's grid carries the sparse large class's items)
+when its workspace holds both classes' partials and the pair's item counter
+and the classes' forms allow; concurrently on two streams when it holds the
+partials only; and in turn otherwise.  All three give the same bits.
 """
 
 from __future__ import annotations
@@ -214,11 +216,11 @@ def _graph_replays_equal_eager(dev, run, restore, outputs, what):
 
 
 def test_concurrent_classes_under_graph_capture(dev):
-    """gs_switched_lora runs a two-class module's large class on the library's
-    side stream, forked from and joined into the caller's stream; the fork and
-    join are captured into a graph with the rest, and every replay equals the
-    eager call.  The one-launch + segments "split" path forks a torch side
-    stream the same way."""
+    """gs_switched_lora runs a two-class module (one rank-512 adapter among
+    rank-32 ones) in the pair launches, whose item counter the shrink zeroes
+    in every launch: captured into a graph, every replay equals the eager
+    call.  The one-launch + segments "split" path forks a torch side stream,
+    captured the same way."""
     ranks = [32] * 6 + [512]
     NA = len(ranks)
     spec = workloads.ModuleSpec("qkv", 4096, (4096, 1024, 1024), ranks, 512)
@@ -233,6 +235,20 @@ def test_concurrent_classes_under_graph_capture(dev):
     ref = _graph_replays_equal_eager(dev, lambda: switched.switched_lora_(y, md.x, segs, pk, z, path="segments"),
                                      lambda: y.copy_(y0), [y], "two classes, segments")
     _check(md, ref[0], req, torch.bfloat16, "two classes, segments, eager")
+
+    # fp32 (no pair launches; the fp32 expand stages S * max_rank <= 952
+    # values per row): the large class on the library's side stream, forked
+    # from and joined into the captured stream
+    ranks_f = [32] * 6 + [256]
+    spec_f = workloads.ModuleSpec("gate_up", 2048, (2048, 2048), ranks_f, 256)
+    mdf = workloads.make_module(spec_f, T, NA, torch.float32, dev, seed=95)
+    pkf = switched.PackedAdapters.from_slices(mdf.lora_A_slices, mdf.lora_B_slices, ranks_f)
+    zf = torch.empty(T, spec_zw(pkf), dtype=torch.float32, device=dev)
+    yf = mdf.y.clone()
+    yf0 = mdf.y.clone()
+    reff = _graph_replays_equal_eager(dev, lambda: switched.switched_lora_(yf, mdf.x, segs, pkf, zf, path="segments"),
+                                      lambda: yf.copy_(yf0), [yf], "two classes, fp32, two streams")
+    _check(mdf, reff[0], req, torch.float32, "two classes, fp32, two streams, eager")
 
     # decode-sized: the split path (one-launch kernel beside the segment kernels)
     r = workloads.population_routing(1, "r512")
@@ -257,9 +273,11 @@ def spec_zw(pk):
 
 
 def test_two_classes_in_a_one_class_workspace_run_in_turn(dev):
-    """A workspace that holds only the larger class's partials (not both side
-    by side) makes gs_switched_lora run the classes one after the other: the
-    result is bit-identical to the concurrent run."""
+    """The workspace decides how gs_switched_lora runs a two-class module: the
+    full size (gs_shrink_workspace_bytes) takes the pair launches, one
+    256-byte line less (both classes' partials but no item counter) the two
+    streams, one more line less (either class's partials, not both) the
+    classes in turn.  The three results are bit-identical."""
     ranks = [32] * 8 + [256]
     NA = len(ranks)
     spec = workloads.ModuleSpec("gate_up", 4096, (2048, 2048), ranks, 256)
@@ -274,13 +292,15 @@ def test_two_classes_in_a_one_class_workspace_run_in_turn(dev):
         return int(lib.gs_shrink_workspace_bytes(T, spec.hidden, pk.num_slices, NA, p.max_rank,
                                                   switched._i32_array(p.ranks_host)))
 
-    # side by side the classes need align256(small) + large bytes; 256 bytes
-    # fewer still holds either class's partials, but not both
-    both = ws_bytes(pk)
+    # side by side the classes need align256(small) + large bytes, then one
+    # 256-byte line for the pair's counter; a line fewer than both still
+    # holds either class's partials
+    full = ws_bytes(pk)
+    both = full - 256
     one = both - 256
-    _say(f"workspace: both classes {both} B, in turn {one} B")
+    _say(f"workspace: pair {full} B, two streams {both} B, in turn {one} B")
     outs = []
-    for nbytes in (both, one):
+    for nbytes in (full, both, one):
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         z = torch.empty(T, spec_zw(pk), dtype=torch.bfloat16, device=dev)
         y = md.y.clone()
@@ -293,5 +313,6 @@ def test_two_classes_in_a_one_class_workspace_run_in_turn(dev):
                            switched._lib.stream_ptr(dev))
         torch.cuda.synchronize()
         outs.append(y)
-    assert torch.equal(outs[0], outs[1]), "concurrent and in-turn runs differ"
+    assert torch.equal(outs[0], outs[1]), "pair launches and two-stream run differ"
+    assert torch.equal(outs[0], outs[2]), "pair launches and in-turn run differ"
     _check(md, outs[0], req, torch.bfloat16, "two classes")
