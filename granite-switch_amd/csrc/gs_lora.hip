@@ -616,9 +616,15 @@ constexpr bool kExpandBalanced = GS_EXPAND_BALANCED;
 // PIPE: ranks above PRE k-groups load lora_B chunk kc + 1 before chunk kc is
 // multiplied (the looping form for large ranks); otherwise each later chunk
 // is loaded where it is used, which keeps the one-item forms' registers.
-template <bool BF16, int NBW, int PRE, bool PIPE>
+// before_last() runs before the last sub-tile's products (the pair expand
+// issues its claim there).
+struct NoHook {
+  __device__ void operator()() const {}
+};
+template <bool BF16, int NBW, int PRE, bool PIPE, typename Hook = NoHook>
 __device__ __forceinline__ void expand_item(const ExpandParams& p, const TileRef& tr, int sub0, int nsub,
-                                            int nparts, float (&dtile)[kTM][4 * NBW * 32 + kOutPad], char* zs) {
+                                            int nparts, float (&dtile)[kTM][4 * NBW * 32 + kOutPad], char* zs,
+                                            Hook before_last = Hook{}) {
   constexpr int NT = 4 * NBW * 32;           // columns per sub-tile
   // read-modify-write mapping: each lane owns one 16-byte piece per row it
   // touches, consecutive lanes consecutive pieces, so every wave access
@@ -811,6 +817,7 @@ __device__ __forceinline__ void expand_item(const ExpandParams& p, const TileRef
 #pragma unroll
       for (int st = 0; st < PRE; ++st) bc[q][st] = bn[q][st];
   }
+  before_last();
   compute(sub0 + nsub - 1, bc, yc);
 }
 
@@ -1107,25 +1114,37 @@ __global__ __launch_bounds__(kThreads) void expand_sparse_kernel(ExpandParams p)
 // ----------------------------------------------------------------------------
 constexpr int kPairQB = 2;                     // 32-column blocks per large-class expand item
 
+// Takes the next item number of the pair expand (agent scope, the counter's
+// old value).  A wrapping increment, which the compiler's atomic combining
+// leaves alone: combined, the returned value is read with a wait right
+// behind the atomic, while here the wait sits where the value is used.
+__device__ __forceinline__ int claim_next(int* counter) {
+  return static_cast<int>(__builtin_amdgcn_atomic_inc32(reinterpret_cast<uint32_t*>(counter), 0xffffffffu,
+                                                        __ATOMIC_RELAXED, "agent"));
+}
+
 template <int NB0>
 __global__ __launch_bounds__(kThreads) void shrink_dma_pair_kernel(ShrinkParams p0, ShrinkParams p1, int* claim) {
   constexpr int R0 = DmaRing<NB0>::NST * (kTMS + 32 * NB0) * kDmaRow;
   constexpr int R1 = DmaRing<1>::NST * (kTMS + 32) * kDmaRow;
   __shared__ __align__(16) char ring[R0 > R1 ? R0 : R1];
   if (blockIdx.x == 0 && threadIdx.x == 0) *claim = 0;   // ordered before the expand launch by the launch boundary
-  int sub = 0, total = 0;
-  {
-    const TileRef tr = locate_tile<kTMS>(p0.seg, p0.ranks, p0.a_off, p0.NA, p0.rw, static_cast<int>(blockIdx.x), false,
-                                         p0.n_chunks * p0.KS, sub, total);
-    if (tr.g != 0) shrink_dma_item<NB0>(p0, tr, sub, p0.KS, ring);
-  }
+  // the large class's first item is looked up before the small item, so its
+  // memory trip overlaps that item
   int lin = static_cast<int>(blockIdx.x);
-  int KS = p1.KS;
+  int KS = p1.KS, sub1 = 0, total = 0;
   TileRef tr = locate_tile_by<kTMS>(p1.seg, p1.ranks, p1.a_off, p1.NA, p1.rw, lin, true,
                                     [&](int tot) {
                                       if (p1.ks_target > 0) KS = dyn_ksplit(tot, p1.n_chunks, p1.ks_target, p1.KS);
                                       return p1.n_chunks * KS;
-                                    }, sub, total);
+                                    }, sub1, total);
+  {
+    int sub = 0, total0 = 0;
+    const TileRef tr0 = locate_tile<kTMS>(p0.seg, p0.ranks, p0.a_off, p0.NA, p0.rw, static_cast<int>(blockIdx.x),
+                                          false, p0.n_chunks * p0.KS, sub, total0);
+    if (tr0.g != 0) shrink_dma_item<NB0>(p0, tr0, sub, p0.KS, ring);
+  }
+  int sub = sub1;
   const int items = work_items(total, p1.n_chunks * KS, true);
   while (lin < items) {
     lds_barrier();                         // every wave is done with the ring before the item's transfers
@@ -1146,6 +1165,8 @@ __global__ __launch_bounds__(kThreads) void expand_pair_kernel(ExpandParams p0, 
   extern __shared__ __align__(16) char zs[];   // either class's shrink values
   auto& dtile = *reinterpret_cast<float(*)[kTM][NT + kOutPad]>(buf);
   auto& red = *reinterpret_cast<float(*)[2][kTM][32 * kPairQB + kOutPad]>(buf);
+  int ticket = 0;
+  bool early = false;                      // uniform: the small item ran and claimed
   {
     const int n_sub = (p0.out_total + NT - 1) / NT;
     int sub = 0, groups = 1, total = 0;
@@ -1155,25 +1176,35 @@ __global__ __launch_bounds__(kThreads) void expand_pair_kernel(ExpandParams p0, 
                                                               groups = expand_groups(tot, n_sub, p0.wt);
                                                               return groups;
                                                             }, sub, total);
+    // the first claim goes out before the small item's last sub-tile, so
+    // its round trip passes while that sub-tile is computed; its result is
+    // written to LDS only afterwards (no wait for it before)
     if (tr.g != 0) {
       const int sub0 = (sub * n_sub) / groups;
       const int nsub = ((sub + 1) * n_sub) / groups - sub0;
-      if (nsub > 0) expand_item<true, NBW, PRE, false>(p0, tr, sub0, nsub, p0.nparts, dtile, zs);
+      if (nsub > 0)
+        expand_item<true, NBW, PRE, false>(p0, tr, sub0, nsub, p0.nparts, dtile, zs, [&]() {
+          if (threadIdx.x == 0) ticket = claim_next(claim);
+          early = true;
+        });
     }
   }
   const int n_sub1 = p1.out_total / (32 * kPairQB);
   const int total1 = count_tiles<kTM>(p1.seg, p1.ranks, p1.NA, p1.rw);
   const int items1 = work_items(total1, n_sub1, true);
   const int nparts1 = sparse_nparts(p1);
-  for (;;) {
-    lds_barrier();                         // zs, buf and `claimed` are free
-    if (threadIdx.x == 0) claimed = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    lds_barrier();
-    const int it = claimed;
-    if (it >= items1) break;
+  if (threadIdx.x == 0)
+    claimed = early ? ticket : claim_next(claim);
+  lds_barrier();                           // every wave is past the small item; `claimed` is written
+  int it = claimed;
+  while (it < items1) {
     int sub = 0;
     const TileRef tr = tile_at<kTM, kExpandBalanced>(p1.seg, p1.ranks, p1.b_off, p1.NA, p1.rw, it, true, total1, n_sub1, sub);
     if (tr.g != 0) expand_sparse_item<KG, kPairQB>(p1, tr, sub, nparts1, red, zs);
+    lds_barrier();                         // zs, buf and `claimed` are free
+    if (threadIdx.x == 0) claimed = claim_next(claim);
+    lds_barrier();
+    it = claimed;
   }
 }
 

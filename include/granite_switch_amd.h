@@ -190,12 +190,14 @@ int gs_route_latest_wins(const int64_t* input_ids, const int32_t* cu_seqlens, in
 /* Workspace for gs_shrink / gs_switched_lora: fp32 split-K partial sums.
  * The hidden dimension is split over several workgroups when there are too
  * few tiles to fill the GPU; each writes its own partial and the consumer adds
- * them in a fixed order (deterministic, no cross-workgroup synchronisation).
- * No initialisation is needed.  Calls that share a workspace must not overlap
- * in time (stream order is enough).  For a module of two rank classes the
- * size holds both classes' partials side by side, which lets
- * gs_switched_lora run the classes concurrently; a workspace that holds only
- * the larger class's partials still works (the classes then run in turn). */
+ * them in a fixed order (deterministic).  No initialisation is needed.  Calls
+ * that share a workspace must not overlap in time (stream order is enough).
+ * For a module of two rank classes the size holds both classes' partials
+ * side by side and then one 256-byte line for the item counter of
+ * gs_switched_lora's pair launches (which the call itself zeroes); a
+ * workspace without that line but with both partials runs the classes on two
+ * streams, and one that holds only the larger class's partials runs them in
+ * turn.  All three give the same bits. */
 int64_t gs_shrink_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t num_slices, int32_t num_adapters,
                                   int32_t max_rank, const int32_t* ranks_host);
 
@@ -233,17 +235,19 @@ int gs_expand_add(int32_t dtype, void* y, int64_t ldy, int64_t num_tokens, int32
 /* The whole switched-LoRA delta added into y in two launches: the shrink,
  * then the expand reading the shrink's output directly (split-K partials are
  * summed while they are staged, so z is only written when the shrink is not
- * split), once per rank class (two launches per class; a sparse large class
- * sums its split-K partials into z in a third).  z [T, S*max_rank] scratch
- * of the same dtype.  With two rank classes and a workspace that holds both
- * classes' partials (gs_shrink_workspace_bytes) and `stream` belongs to the
- * current device, the large class runs on the
- * library's side stream of the current device (default priority, created on
- * the first such call: make it eagerly, outside graph capture), forked from
- * `stream` after the work queued before the call and joined back into it
- * before the work queued after (events; captured into a graph like any other
- * work on `stream`).  The classes write disjoint rows of y and z and
- * disjoint ranges of the workspace. */
+ * split), once per rank class.  z [T, S*max_rank] scratch of the same dtype.
+ * A module of two rank classes with a workspace of gs_shrink_workspace_bytes:
+ *   - bf16 with a sparse large class (e.g. one rank-512 adapter among rank-32
+ *     ones): both classes in the same two launches, the small class's
+ *     workgroups taking the large class's items once their own are done;
+ *   - otherwise, when `stream` belongs to the current device: the large class
+ *     on the library's side stream of the current device (default priority,
+ *     created on the first such call: make it eagerly, outside graph capture),
+ *     forked from `stream` after the work queued before the call and joined
+ *     back into it before the work queued after (events; captured into a graph
+ *     like any other work on `stream`).
+ * The classes write disjoint rows of y and z and disjoint ranges of the
+ * workspace. */
 int gs_switched_lora(int32_t dtype, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t num_tokens,
                      int32_t hidden, int32_t out_total, const int32_t* slice_bounds, int32_t num_slices,
                      const void* a_pack, const int64_t* a_off, const void* b_pack, const int64_t* b_off,
