@@ -43,6 +43,7 @@ SIGNATURES = {
                                      c_void_p]),
     "gs_shrink_workspace_bytes": (c_i64, [c_i64, c_i32, c_i32, c_i32, c_i32, c_void_p]),
     "gs_shrink_ksplits": (c_i32, [c_i32, c_i64, c_i32, c_i32, c_i32, c_i32, c_void_p, c_void_p]),
+    "gs_switched_lora_pair": (c_i32, [c_i32, c_i64, c_i32, c_i32, c_void_p, c_i32, c_i32, c_i32, c_void_p]),
     "gs_check_segment_addresses": (c_i64, [c_i32, c_i64, c_i32, c_i64, c_i32, c_i64, c_void_p, c_i32, c_void_p, c_i64,
                                            c_void_p, c_i64, c_void_p, c_i32, c_i32, c_void_p, c_void_p, c_void_p,
                                            c_i64, ctypes.c_char_p, c_i64, c_void_p]),

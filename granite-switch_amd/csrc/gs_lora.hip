@@ -1660,6 +1660,25 @@ PairForm pair_form(bool bf16, int64_t T, const ShrinkPlan& pl0, const ShrinkPlan
   return f;
 }
 
+// The launch-plan fields of a class's expand parameters (what the form
+// choices read), as a call with these slices makes them.
+ExpandParams class_expand_plan(const SliceInfo& si, int out_total, const RankClass& k, const ShrinkPlan& pl,
+                               int64_t T, int64_t ldz) {
+  ExpandParams e{};
+  e.out_total = out_total;
+  e.si = si;
+  e.ldz = ldz;
+  e.part_stride = T * pl.zw;
+  e.zw = pl.zw;
+  e.nparts = pl.KS > 1 ? pl.KS : 0;
+  e.max_rank = k.max_rank;
+  e.rw = k.rw;
+  e.flat = pl.flat ? 1 : 0;
+  e.ks_target = pl.ks_target;
+  e.ks_chunks = pl.n_chunks;
+  return e;
+}
+
 size_t pair_lds_bytes(int S, int max_rank0, int max_rank1) {
   return std::max(expand_lds_bytes(true, S, max_rank0), static_cast<size_t>(kTM) * (max_rank1 + 8) * 2);
 }
@@ -2383,6 +2402,33 @@ int32_t gs_shrink_ksplits(int32_t dtype, int64_t num_tokens, int32_t hidden, int
   return ncls;
 }
 
+int32_t gs_switched_lora_pair(int32_t dtype, int64_t num_tokens, int32_t hidden, int32_t out_total,
+                              const int32_t* slice_bounds, int32_t num_slices, int32_t num_adapters, int32_t max_rank,
+                              const int32_t* ranks_host) {
+  const char* who = "gs_switched_lora_pair";
+  int rc = check_common(who, dtype, num_tokens, num_slices, num_adapters, max_rank);
+  if (rc != GS_OK) return -rc;
+  GS_CHECK_ARG(hidden > 0 && out_total > 0 && slice_bounds != nullptr, "%s: hidden=%d out_total=%d", who, hidden,
+               out_total);
+  RankClass cls[2];
+  int ncls = 0;
+  rc = rank_classes(who, ranks_host, num_adapters, max_rank, num_tokens, cls, ncls);
+  if (rc != GS_OK) return -rc;
+  if (ncls != 2 || num_tokens == 0) return 0;
+  SliceInfo si{};
+  si.S = num_slices;
+  for (int s = 0; s <= num_slices; ++s) si.bounds[s] = slice_bounds[s];
+  const bool bf16 = dtype == GS_DTYPE_BF16;
+  const int64_t ldz = static_cast<int64_t>(num_slices) * max_rank;
+  const ShrinkPlan pl0 = plan_class(num_tokens, hidden, num_slices, cls[0], bf16);
+  const ShrinkPlan pl1 = plan_class(num_tokens, hidden, num_slices, cls[1], bf16);
+  return pair_form(bf16, num_tokens, pl0, pl1, class_expand_plan(si, out_total, cls[0], pl0, num_tokens, ldz),
+                   class_expand_plan(si, out_total, cls[1], pl1, num_tokens, ldz))
+                 .ok
+             ? 1
+             : 0;
+}
+
 int gs_shrink(int32_t dtype, const void* x, int64_t ldx, int64_t num_tokens, int32_t hidden, const void* a_pack,
               const int64_t* a_off, const int32_t* ranks, int32_t num_slices, int32_t num_adapters,
               int32_t max_rank, const int32_t* ranks_host, const int32_t* seg_offsets, const int32_t* perm, void* z,
@@ -2569,28 +2615,13 @@ int64_t gs_check_segment_addresses(int32_t dtype, int64_t num_tokens, int32_t hi
       // gs_switched_lora runs two classes concurrently, their partials side
       // by side (each checked against its own range) and z at one stride
       const ClassLayout L = class_layout(T, hidden, num_slices, cls, ncls, bf16, budget, !noalloc, ws_elems * 4);
-      // the plans and expand parameters of class c as the call makes them
-      auto class_expand = [&](int c, const ShrinkPlan& pl, int64_t zl) {
-        ExpandParams e{};
-        e.out_total = out_total;
-        e.si = m.si;
-        e.ldz = zl;
-        e.part_stride = T * pl.zw;
-        e.zw = pl.zw;
-        e.nparts = pl.KS > 1 ? pl.KS : 0;
-        e.max_rank = cls[c].max_rank;
-        e.rw = cls[c].rw;
-        e.flat = pl.flat ? 1 : 0;
-        e.ks_target = pl.ks_target;
-        e.ks_chunks = pl.n_chunks;
-        return e;
-      };
       if (L.claim >= 0) {
         // both classes in the pair launches when their forms allow
         const int64_t zl = static_cast<int64_t>(num_slices) * max_rank;
         const ShrinkPlan pl0 = plan_class(T, hidden, num_slices, cls[0], bf16, budget);
         const ShrinkPlan pl1 = plan_class(T, hidden, num_slices, cls[1], bf16, budget);
-        const ExpandParams e0 = class_expand(0, pl0, zl), e1 = class_expand(1, pl1, zl);
+        const ExpandParams e0 = class_expand_plan(m.si, out_total, cls[0], pl0, T, zl);
+        const ExpandParams e1 = class_expand_plan(m.si, out_total, cls[1], pl1, T, zl);
         const PairForm pf = pair_form(bf16, T, pl0, pl1, e0, e1);
         if (pf.ok) {
           m.in("pair item counter", L.claim / 4, 1, ws_elems);

@@ -209,6 +209,17 @@ int64_t gs_shrink_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t nu
 int32_t gs_shrink_ksplits(int32_t dtype, int64_t num_tokens, int32_t hidden, int32_t num_slices,
                           int32_t num_adapters, int32_t max_rank, const int32_t* ranks_host, int32_t* ksplit);
 
+/* Whether gs_switched_lora, with a workspace of gs_shrink_workspace_bytes,
+ * runs this module's two rank classes in its pair launches for this batch
+ * size and dtype: 1 yes, 0 no (one class, fp32, a large class that is not
+ * sparse, or forms the pair kernels do not take), a negated GS_* status on
+ * bad arguments.  No counterpart in the reference; it lets a caller choose
+ * between the segment kernels and the one-launch decode kernel for a module
+ * with a rank above GS_RANK_CLASS_SPLIT (switched.path_plan). */
+int32_t gs_switched_lora_pair(int32_t dtype, int64_t num_tokens, int32_t hidden, int32_t out_total,
+                              const int32_t* slice_bounds, int32_t num_slices, int32_t num_adapters, int32_t max_rank,
+                              const int32_t* ranks_host);
+
 /* z[slot, s*r_g + j] = sum_k x[perm[slot], k] * lora_A_{g,s}[j, k] for every
  * active slot (slot < seg_offsets[num_adapters]) whose adapter is applicable.
  * x [T, hidden] (ld ldx); z [T, ldz] with ldz >= S*max_rank; same dtype.

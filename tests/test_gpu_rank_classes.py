@@ -62,7 +62,9 @@ def test_decode_population_with_a_rank512_adapter(dev, path):
     pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, spec.ranks)
     assert pk.max_rank == 512 and pk.rank_split()[1].ranks_host[NA] == 512
     if path == "auto":
-        assert switched.path_plan(pk, r.num_tokens, r.num_tokens) == "split"
+        # the segment kernels, both classes in the pair launches
+        assert switched.pair_launches(pk, r.num_tokens)
+        assert switched.path_plan(pk, r.num_tokens, r.num_tokens) == "segments"
     args = [torch.tensor(v, device=dev) for v in (r.req_ids, r.positions, r.cu_seqlens, r.act_offsets)]
     eff = omap.alora_effective_ids(r.req_ids, r.positions, r.cu_seqlens, r.act_offsets)
     assert (eff == NA).sum() > 0, "the rank-512 adapter has tokens"
@@ -87,7 +89,8 @@ def test_decode_population_with_a_rank512_adapter(dev, path):
 def test_mixed_ranks_prefill_batch(dev, dtype, path):
     """Sequences of 256 tokens, one adapter each, over ranks 8..512; T = 2048
     (above the one-launch kernel's batch limit, so both rank classes run the
-    segment kernels), and T = 512 (auto: the split)."""
+    segment kernels), and T = 512 (auto: the split, or the segment kernels
+    when they run both classes in the pair launches)."""
     # (fp32 stages its shrink values in LDS at 4 bytes: 2 slices x rank 256 at most)
     top = 512 if dtype == torch.bfloat16 else 256
     ranks = [32, 8, top, 64, 128, 16, 32, 256]
@@ -250,19 +253,20 @@ def test_concurrent_classes_under_graph_capture(dev):
                                       lambda: yf.copy_(yf0), [yf], "two classes, fp32, two streams")
     _check(mdf, reff[0], req, torch.float32, "two classes, fp32, two streams, eager")
 
-    # decode-sized: the split path (one-launch kernel beside the segment kernels)
+    # decode-sized: the split path (one-launch kernel beside the segment
+    # kernels), which path="small" forces for a module with a rank-512 adapter
     r = workloads.population_routing(1, "r512")
     NA1 = workloads.population_adapters(1, "r512")
     spec1 = workloads.population_specs(1, "r512")[0]
     md1 = workloads.make_module(spec1, r.num_tokens, NA1, torch.bfloat16, dev, seed=92)
     pk1 = switched.PackedAdapters.from_slices(md1.lora_A_slices, md1.lora_B_slices, spec1.ranks)
-    assert switched.path_plan(pk1, r.num_tokens, r.num_tokens) == "split"
+    assert switched.path_plan(pk1, r.num_tokens, r.num_tokens) == "segments"
     args = [torch.tensor(v, device=dev) for v in (r.req_ids, r.positions, r.cu_seqlens, r.act_offsets)]
     eff = omap.alora_effective_ids(r.req_ids, r.positions, r.cu_seqlens, r.act_offsets)
     segs1 = switched.build_segments(args[0], NA1, args[1], args[2], args[3])
     y1 = md1.y.clone()
     y10 = md1.y.clone()
-    ref1 = _graph_replays_equal_eager(dev, lambda: switched.switched_lora_(y1, md1.x, segs1, pk1, path="auto"),
+    ref1 = _graph_replays_equal_eager(dev, lambda: switched.switched_lora_(y1, md1.x, segs1, pk1, path="small"),
                                       lambda: y1.copy_(y10), [y1], "split path")
     switched.check(dev)
     _check(md1, ref1[0], eff, torch.bfloat16, "split path, eager")

@@ -439,3 +439,32 @@ def test_population_workloads():
         assert not idle.req_ids.any()
         assert np.array_equal(idle.positions, workloads.routing_for(cfg).positions)
     assert workloads.population_specs(2, "balanced") == workloads.module_specs(2)
+
+
+def _pair_query(dtype, T, H, slices, ranks):
+    i32 = lambda v: (ctypes.c_int32 * len(v))(*[int(u) for u in v])
+    r8 = [0] + [((int(r) + 7) // 8) * 8 if r > 0 else 0 for r in ranks]
+    bounds = [0] + [int(b) for b in np.cumsum(slices)]
+    return _lib.load().gs_switched_lora_pair(dtype, T, H, int(sum(slices)), i32(bounds), len(slices), len(ranks),
+                                             max(r8), i32(r8))
+
+
+def test_pair_launch_query():
+    """gs_switched_lora_pair tells whether gs_switched_lora runs a module's two
+    rank classes in its pair launches (on a 256-CU part; the host plan falls
+    back to 256 without a GPU): the bench's rank-512 populations in bf16 do,
+    their balanced ones (one class) and fp32 do not, nor a large class that
+    holds a prefill batch's worth of tokens (not sparse).  Bad arguments give
+    a negated status."""
+    for cfg in (1, 4):
+        for pop in ("balanced", "r512"):
+            r = workloads.population_routing(cfg, pop)
+            NA = workloads.population_adapters(cfg, pop)
+            for spec in workloads.population_specs(cfg, pop):
+                ranks = spec.ranks[:NA]
+                want = 1 if pop == "r512" else 0
+                assert _pair_query(_lib.GS_DTYPE_BF16, r.num_tokens, spec.hidden, spec.output_slices, ranks) == want
+                assert _pair_query(_lib.GS_DTYPE_FP32, r.num_tokens, spec.hidden, spec.output_slices, ranks) == 0
+    # two adapters, one of rank 512, 8192 tokens: ~4096 expected on it
+    assert _pair_query(_lib.GS_DTYPE_BF16, 8192, 4096, (4096,), [32, 512]) == 0
+    assert _pair_query(7, 256, 4096, (4096,), [32, 512]) < 0
