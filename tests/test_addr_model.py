@@ -98,6 +98,23 @@ def test_rank512_population_with_a_prefill_chunk_on_the_large_adapter():
         _check(r.num_tokens, spec.hidden, spec.output_slices, spec.ranks, eff)
 
 
+@pytest.mark.parametrize("large", [72, 96, 128, 200, 256, 512])
+@pytest.mark.parametrize("T", [1, 64, 600, 4144])
+def test_pair_launches_every_large_rank(large, T):
+    """Two classes in the pair launches (gs_switched_lora_pair says so) at
+    every k-group count of the large class's 64-column items (2, 4 and 8 per
+    wave), odd large ranks, one token to a decoder-step batch: the replay of
+    the pair shrink (large items on a stride of the small class's grid), the
+    pair expand (claimed items) and the counter line."""
+    slices = (2048, 1024, 1024)
+    ranks = [32] * 24 + [large]                    # the large class sparse (its tokens expected: T / 26)
+    rng = np.random.default_rng(large + T)
+    eff = rng.integers(0, len(ranks) + 1, size=T)
+    from test_library import _pair_query
+    assert _pair_query(_lib.GS_DTYPE_BF16, T, 4096, slices, ranks) == 1
+    _check(T, 4096, slices, ranks, eff)
+
+
 EDGE = [
     # T, H, slices, ranks, seed, share of base tokens
     (1, 4096, (4096, 1024, 1024), [32] * 12, 0, 0.0),

@@ -17,6 +17,8 @@ partials only; and in turn otherwise.  All three give the same bits.
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -320,3 +322,55 @@ def test_two_classes_in_a_one_class_workspace_run_in_turn(dev):
     assert torch.equal(outs[0], outs[1]), "pair launches and two-stream run differ"
     assert torch.equal(outs[0], outs[2]), "pair launches and in-turn run differ"
     _check(md, outs[0], req, torch.bfloat16, "two classes")
+
+
+def _run_with_workspace(md, pk, segs, T, spec, nbytes):
+    lib = switched._lib
+    ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=md.y.device)
+    z = torch.empty(T, spec_zw(pk), dtype=md.y.dtype, device=md.y.device)
+    y = md.y.clone()
+    lib.call("gs_switched_lora", switched._dtype_code(md.x), md.x.data_ptr(), md.x.stride(0), y.data_ptr(),
+             y.stride(0), T, spec.hidden, pk.out_total, switched._i32_array(pk.slice_bounds), pk.num_slices,
+             pk.a_pack.data_ptr(), pk.a_off.data_ptr(), pk.b_pack.data_ptr(), pk.b_off.data_ptr(),
+             pk.ranks.data_ptr(), pk.num_adapters, pk.max_rank, switched._i32_array(pk.ranks_host),
+             segs.seg_offsets.data_ptr(), segs.perm.data_ptr(), z.data_ptr(), ws.data_ptr(), nbytes,
+             lib.stream_ptr(md.y.device))
+    torch.cuda.synchronize()
+    return y
+
+
+@pytest.mark.parametrize("large", [72, 96, 128, 256, 512])
+@pytest.mark.parametrize("T", [64, 600])
+def test_pair_launches_every_large_rank(dev, large, T):
+    """The pair launches at every k-group count of the large class's items
+    (ranks 72..128: 2 per wave, ..256: 4, ..512: 8), odd ranks included:
+    bit-identical to the two-stream and in-turn forms, and to the oracle."""
+    ranks = [32] * 24 + [large]
+    NA = len(ranks)
+    spec = workloads.ModuleSpec("qkv", 4096, (2048, 1024, 1024), ranks, large)
+    md = workloads.make_module(spec, T, NA, torch.bfloat16, dev, seed=700 + large + T)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, ranks)
+    assert switched.pair_launches(pk, T)
+    req = np.random.default_rng(large + T).integers(0, NA + 1, size=T)
+    segs = switched.build_segments(torch.tensor(req, device=dev), NA)
+    lib = switched._lib.load()
+    full = int(lib.gs_shrink_workspace_bytes(T, spec.hidden, pk.num_slices, NA, pk.max_rank,
+                                             switched._i32_array(pk.ranks_host)))
+    # the small class's partials (KS x T x S*32 fp32 when split) come first,
+    # the large class's from the next 256-byte boundary (planned at its
+    # largest device k-split), then the counter line; the in-turn form needs
+    # the larger of the two, and exists only when the small class has
+    # partials too
+    ks = (ctypes.c_int32 * 2)()
+    assert lib.gs_shrink_ksplits(switched._lib.GS_DTYPE_BF16, T, spec.hidden, pk.num_slices, NA, pk.max_rank,
+                                 switched._i32_array(pk.ranks_host), ks) == 2
+    part0 = ks[0] * T * pk.num_slices * 32 * 4 if ks[0] > 1 else 0
+    both = full - 256
+    part1 = both - (part0 + 255) // 256 * 256
+    sizes = [full, both] + ([max(part0, part1)] if part0 > 0 else [])
+    outs = [_run_with_workspace(md, pk, segs, T, spec, n) for n in sizes]
+    assert torch.equal(outs[0], outs[1]), "pair launches and two-stream run differ"
+    if len(outs) > 2:
+        assert torch.equal(outs[0], outs[2]), "pair launches and in-turn run differ"
+    err = _check(md, outs[0], req, torch.bfloat16, f"pair launches, large rank {large}, T={T}")
+    _say(f"pair launches, large rank {large}, T={T}: {int((req == NA).sum())} tokens on it, max abs err {err:.3e}")
