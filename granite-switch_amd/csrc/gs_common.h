@@ -335,8 +335,14 @@ __host__ __device__ __forceinline__ void tile_span(int lo, int hi, int jj, int& 
   if constexpr (BAL) {
     const int n = hi - lo;
     const int nt = (n + TM - 1) / TM;
-    slot0 = lo + (jj * n) / nt;
-    nrows = lo + ((jj + 1) * n) / nt - slot0;
+    static_assert(TM >= 32, "the 32-bit products below assume at most n / 32 + 1 tiles");
+    if (n < (1 << 18)) {                   // (jj + 1) * n < 2^13 * 2^18: 32-bit products
+      slot0 = lo + (jj * n) / nt;
+      nrows = lo + ((jj + 1) * n) / nt - slot0;
+    } else {                               // an adapter with 2^18 or more slots
+      slot0 = lo + static_cast<int>((static_cast<int64_t>(jj) * n) / nt);
+      nrows = lo + static_cast<int>((static_cast<int64_t>(jj + 1) * n) / nt) - slot0;
+    }
   } else {
     slot0 = lo + jj * TM;
     nrows = min(TM, hi - slot0);
