@@ -212,6 +212,26 @@ def test_non_applicable_adapter_leaves_rows(dev):
     _check_module(md, y, eff, rows, torch.bfloat16)
 
 
+def test_one_adapter_past_2e18_slots(dev):
+    """An adapter holding 2^18 or more tokens: its 32-slot expand tiles are cut
+    with 64-bit products (tile jj * n passes 2^31 there).  Every row against
+    the oracle; base rows bit-identical."""
+    T = (1 << 18) + 4096
+    spec = workloads.ModuleSpec("t", 128, (256,), [16, 16], 16)
+    md = workloads.make_module(spec, T, 2, torch.bfloat16, dev, seed=11)
+    ids = np.ones(T, dtype=np.int64)
+    ids[::997] = 2
+    ids[::1009] = 0
+    assert int((ids == 1).sum()) >= (1 << 18)
+    _say(f"one adapter past 2^18 slots: T={T} adapter-1 tokens={int((ids == 1).sum())}")
+    segs = switched.build_segments(torch.tensor(ids, device=dev), 2)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, spec.ranks)
+    y = md.y.clone()
+    switched.switched_lora_(y, md.x, segs, pk, path="segments")
+    torch.cuda.synchronize()
+    _check_module(md, y, ids, np.arange(T), torch.bfloat16, hf_too=False)
+
+
 @pytest.mark.parametrize("ranks,slices,H", [([8, 24, 40, 64], (96,), 1000), ([16, 512], (32, 64), 264),
                                             ([128, 8], (4096, 1024, 1024), 4096)])
 def test_odd_shapes(dev, ranks, slices, H):
