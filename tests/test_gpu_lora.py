@@ -212,6 +212,25 @@ def test_non_applicable_adapter_leaves_rows(dev):
     _check_module(md, y, eff, rows, torch.bfloat16)
 
 
+@pytest.mark.parametrize("dtype,T,ranks", [(torch.bfloat16, 5000, [8] * 180 + [32] * 76),
+                                           (torch.float32, 1500, [16] * 100),
+                                           (torch.bfloat16, 3000, [32] * 120 + [256] * 2)])
+def test_more_than_64_adapters(dev, dtype, T, ranks):
+    """Adapter tables past one wave (the kernels' multi-pass tile lookup), up
+    to the builder's 256: every row against the oracle, base rows bit-identical."""
+    NA = len(ranks)
+    spec = workloads.ModuleSpec("t", 512, (256, 128), ranks, max(ranks))
+    md = workloads.make_module(spec, T, NA, dtype, dev, seed=NA + T)
+    ids = np.random.default_rng(NA).integers(0, NA + 1, size=T)
+    _say(f"more than 64 adapters: NA={NA} T={T} {dtype}")
+    segs = switched.build_segments(torch.tensor(ids, device=dev), NA)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, ranks)
+    y = md.y.clone()
+    switched.switched_lora_(y, md.x, segs, pk, path="segments")
+    torch.cuda.synchronize()
+    _check_module(md, y, ids, np.arange(T), dtype)
+
+
 def test_one_adapter_past_2e18_slots(dev):
     """An adapter holding 2^18 or more tokens: its 32-slot expand tiles are cut
     with 64-bit products (tile jj * n passes 2^31 there).  Every row against
