@@ -212,6 +212,26 @@ def test_non_applicable_adapter_leaves_rows(dev):
     _check_module(md, y, eff, rows, torch.bfloat16)
 
 
+@pytest.mark.parametrize("T", [1, 2, 7])
+@pytest.mark.parametrize("path", ["segments", "small"])
+def test_tiny_batches(dev, T, path):
+    """Batches of 1, 2 and 7 tokens on both kernel paths (one tile, part-filled)."""
+    ranks = [32] * 12
+    NA = len(ranks)
+    spec = workloads.ModuleSpec("qkv", 4096, (4096, 1024, 1024), ranks, 32)
+    md = workloads.make_module(spec, T, NA, torch.bfloat16, dev, seed=40 + T)
+    ids = ((np.arange(T) * 5 + 3) % (NA + 1)).astype(np.int64)
+    _say(f"tiny batch T={T} path={path} ids={ids.tolist()}")
+    segs = switched.build_segments(torch.tensor(ids, device=dev), NA)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, ranks)
+    y = md.y.clone()
+    switched.switched_lora_(y, md.x, segs, pk, path=path)
+    torch.cuda.synchronize()
+    if path == "small":
+        switched.check(dev)
+    _check_module(md, y, ids, np.arange(T), torch.bfloat16)
+
+
 @pytest.mark.parametrize("dtype,T,ranks", [(torch.bfloat16, 5000, [8] * 180 + [32] * 76),
                                            (torch.float32, 1500, [16] * 100),
                                            (torch.bfloat16, 3000, [32] * 120 + [256] * 2)])
