@@ -374,3 +374,26 @@ def test_pair_launches_every_large_rank(dev, large, T):
         assert torch.equal(outs[0], outs[2]), "pair launches and in-turn run differ"
     err = _check(md, outs[0], req, torch.bfloat16, f"pair launches, large rank {large}, T={T}")
     _say(f"pair launches, large rank {large}, T={T}: {int((req == NA).sum())} tokens on it, max abs err {err:.3e}")
+
+
+@pytest.mark.parametrize("proj", [0, 1, 2, 3])
+def test_step_population_with_a_rank512_adapter(dev, proj):
+    """The decoder step's shape (T = 4144, chunked prefill plus decode rows)
+    with the rank-512 population: each projection of one layer through the
+    pair launches, every row against the oracle, base rows bit-identical."""
+    r = workloads.population_routing(4, "r512")
+    NA = workloads.population_adapters(4, "r512")
+    spec = workloads.population_specs(4, "r512")[proj]
+    md = workloads.make_module(spec, r.num_tokens, NA, torch.bfloat16, dev, seed=900 + proj)
+    pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, spec.ranks)
+    assert switched.pair_launches(pk, r.num_tokens)
+    eff = omap.alora_effective_ids(r.req_ids, r.positions, r.cu_seqlens, r.act_offsets)
+    assert (eff == NA).sum() > 0, "the rank-512 adapter has tokens"
+    _say(f"step r512 population, {spec.name}: {int((eff > 0).sum())} adapted, {int((eff == NA).sum())} on rank 512")
+    args = [torch.tensor(v, device=dev) for v in (r.req_ids, r.positions, r.cu_seqlens, r.act_offsets)]
+    segs = switched.build_segments(args[0], NA, args[1], args[2], args[3])
+    y = md.y.clone()
+    switched.switched_lora_(y, md.x, segs, pk)
+    torch.cuda.synchronize()
+    err = _check(md, y, eff, torch.bfloat16, f"step r512 {spec.name}")
+    _say(f"  max abs err {err:.3e}")
