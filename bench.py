@@ -314,7 +314,7 @@ def path_choice() -> None:
                     g = torch.Generator(device="cpu").manual_seed(T)
                     ids = torch.randint(1, NA + 1, (T,), generator=g)
                     ids[torch.rand(T, generator=g) < 0.2] = 0
-                    cases.append((spec, NA, T, ids, None, None, None))
+                    cases.append((spec, NA, T, ids, None, None, None, torch.bfloat16))
     for name, H, sl, r, NA, T, L in (("qkv", 4096, (4096, 1024, 1024), 16, 4, 512, 128),
                                      ("qkv", 4096, (4096, 1024, 1024), 16, 12, 512, 128),
                                      ("qkv", 4096, (4096, 1024, 1024), 16, 12, 1024, 128),
@@ -326,20 +326,21 @@ def path_choice() -> None:
         spec = workloads.ModuleSpec(name=name, hidden=H, output_slices=sl, ranks=[r] * NA, max_rank=r)
         g = np.random.default_rng(T + L + NA)
         ids = torch.tensor(np.repeat(g.integers(1, NA + 1, T // L), L))
-        cases.append((spec, NA, T, ids, None, torch.arange(0, T + 1, L, dtype=torch.int32), None))
+        cases.append((spec, NA, T, ids, None, torch.arange(0, T + 1, L, dtype=torch.int32), None, torch.bfloat16))
     r0 = workloads.routing_for(0)
     spec0 = workloads.module_specs(0)[0]
     cases.append((spec0, workloads.num_adapters_for(0), r0.num_tokens, torch.tensor(r0.req_ids),
                    torch.tensor(r0.positions), torch.tensor(r0.cu_seqlens),
-                   None if r0.act_offsets is None else torch.tensor(r0.act_offsets)))
+                   None if r0.act_offsets is None else torch.tensor(r0.act_offsets), workloads.dtype_for(0)))
     rows = []
-    for spec, NA, T, ids, pos, cu, off in cases:
+    for spec, NA, T, ids, pos, cu, off, dtype in cases:
         H, sl = spec.hidden, spec.output_slices
-        per_call = NA * spec.max_rank * (len(sl) * H + sum(sl)) * 2
-        nsets = max(4, min(28, int(2.5e8 // (T * (H + sum(sl)) * 2 + per_call))))
+        e = 4 if dtype == torch.float32 else 2
+        per_call = NA * spec.max_rank * (len(sl) * H + sum(sl)) * e
+        nsets = max(4, min(28, int(2.5e8 // (T * (H + sum(sl)) * e + per_call))))
         sets = []
         for i in range(nsets):
-            md = workloads.make_module(spec, T, NA, torch.bfloat16, dev, seed=50 + i)
+            md = workloads.make_module(spec, T, NA, dtype, dev, seed=50 + i)
             pk = switched.PackedAdapters.from_slices(md.lora_A_slices, md.lora_B_slices, spec.ranks)
             md.lora_A_slices = md.lora_B_slices = None
             sets.append((md, pk))
@@ -371,14 +372,16 @@ def path_choice() -> None:
         auto = "small" if switched.small_preferred(sets[0][1], T, nseq) else "segments"
         auto_hint = "small" if switched.small_preferred(sets[0][1], T, nseq, largest) else "segments"
         rs = switched.small_row_split(sets[0][1], T, nseq)
-        rows.append({"projection": spec.name, "hidden": H, "output_slices": list(sl), "adapters": NA,
+        rows.append({"projection": spec.name, "dtype": "fp32" if dtype == torch.float32 else "bf16",
+                     "hidden": H, "output_slices": list(sl), "adapters": NA,
                      "ranks": sorted(set(spec.ranks)), "tokens": T, "sequences": nseq, "largest_group": largest,
                      "row_split": rs, "small_us": res["small"], "segments_us": res["segments"], "auto": auto,
                      "auto_with_largest_group": auto_hint})
         log(f"{spec.name} H={H} NA={NA} T={T} seqs={nseq} largest={largest} rs={rs}: small {res['small']:.2f} us, "
             f"segments {res['segments']:.2f} us, auto {auto}")
         del sets
-    print(json.dumps({"comparison": "one-launch decode kernel vs segment kernels (bf16)", "rows": rows}), flush=True)
+    print(json.dumps({"comparison": "one-launch decode kernel vs segment kernels (bf16; the last row fp32)",
+                      "rows": rows}), flush=True)
 
 
 WL_NAMES = {0: "switched-LoRA single op fp32 2048->2048 T=512 (4x128) 4 adapters r8 aLoRA",
